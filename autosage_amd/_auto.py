@@ -1,0 +1,622 @@
+"""Input-aware scheduling of the sparse kernels.
+
+Behaviour follows ``autosage/_auto.py`` of the reference: the same public
+functions and private helpers, the same sampling, shortlist, probing,
+guardrail, cache replay and result dictionaries (``:266-441``, ``:544-741``),
+so cached schedules and telemetry read the same.  The SpMM and SDDMM
+schedulers share one probe engine here (``_probe_and_choose``).
+
+gfx950 changes:
+* candidates keep the reference's ``[tile, warps, threshold]`` shape; on
+  MI355X ``tile`` is the light-row features per pass, ``warps`` the waves per
+  hub workgroup and ``threshold`` the hub degree;
+* a sampled "autosage" decision is confirmed once on the full graph against
+  the PyTorch-ROCm baseline (``SchedulerConfig.full_graph_check``) before it is
+  cached, so a replayed schedule is never slower than the baseline on the
+  graph it was made for;
+* the CSR row softmax and the attention pipeline run as native kernels on the
+  GPU (``csr_attention_forward`` can fuse all three stages into one launch).
+"""
+
+from __future__ import annotations
+
+import os
+import statistics
+import time
+from typing import Any, Callable, Optional
+
+import torch
+
+from ._cache import ScheduleCache, device_signature, graph_signature, log_probe
+from .config import SchedulerConfig
+from .ops import _normalize_csr, load_native, native_op, spmm_csr
+
+AUTOTUNE_SCHEMA_VERSION = 3
+
+
+def _time_cuda(
+    function: Callable[[], torch.Tensor],
+    *,
+    warmup: int,
+    iterations: int,
+    cap_ms: Optional[float] = None,
+) -> dict[str, Any]:
+    """Event timing of ``_auto.py:18-54``: warmups, then per-iteration events
+    with a sync, stopping early once ``cap_ms`` of kernel time is spent."""
+    torch.cuda.synchronize()
+    wall_start = time.perf_counter()
+    for _ in range(max(0, warmup)):
+        function()
+    torch.cuda.synchronize()
+    samples: list[float] = []
+    output = None
+    spent = 0.0
+    for _ in range(max(1, iterations)):
+        begin = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        begin.record()
+        output = function()
+        end.record()
+        end.synchronize()
+        elapsed = float(begin.elapsed_time(end))
+        samples.append(elapsed)
+        spent += elapsed
+        if cap_ms is not None and spent >= max(0.0, cap_ms):
+            break
+    torch.cuda.synchronize()
+    return {
+        "best_ms": min(samples),
+        "mean_ms": statistics.fmean(samples),
+        "std_ms": statistics.pstdev(samples) if len(samples) > 1 else 0.0,
+        "iterations": len(samples),
+        "total_ms": spent,
+        "wall_ms": (time.perf_counter() - wall_start) * 1000.0,
+        "output": output,
+    }
+
+
+def _prepare_spmm_baseline(crow, col, val, x) -> tuple[Callable[[], torch.Tensor], str]:
+    """PyTorch CSR SpMM (hipSPARSE on ROCm), ``_auto.py:57-76``."""
+    weights = torch.ones(col.numel(), device=x.device, dtype=x.dtype) if val is None else val
+    matrix = torch.sparse_csr_tensor(
+        crow, col, weights.to(dtype=x.dtype), size=(crow.numel() - 1, x.size(0)), device=x.device, dtype=x.dtype
+    )
+    return (lambda: torch.sparse.mm(matrix, x)), "torch.sparse.mm(csr)"
+
+
+def _edge_rows(crow: torch.Tensor) -> torch.Tensor:
+    counts = (crow[1:] - crow[:-1]).to(torch.long)
+    return torch.repeat_interleave(torch.arange(crow.numel() - 1, device=crow.device, dtype=torch.long), counts)
+
+
+def _prepare_sddmm_baseline(crow, col, query, key) -> tuple[Callable[[], torch.Tensor], str]:
+    """Gather-dot baseline, ``_auto.py:79-92``."""
+    rows = _edge_rows(crow)
+    return (lambda: (query.index_select(0, rows) * key.index_select(0, col)).sum(dim=1)), "gather-dot"
+
+
+def _induced_sample_csr(crow, col, val, *, fraction: float, minimum_rows: int, seed: int):
+    """Induced sub-graph on a seeded row sample (``_auto.py:95-154``): rows
+    ``randperm(N)[:S]`` sorted, S = min(max(int(N·fraction), minimum_rows, 1), N);
+    an edge survives when its column is also sampled; columns are renumbered."""
+    rows = crow.numel() - 1
+    size = min(max(int(rows * fraction), minimum_rows, 1), rows)
+    device = crow.device
+    generator = torch.Generator(device=device)
+    generator.manual_seed(seed)
+    selected = torch.randperm(rows, generator=generator, device=device)[:size].sort().values
+
+    remap = torch.full((rows,), -1, dtype=torch.long, device=device)
+    remap[selected] = torch.arange(size, device=device)
+    starts = crow.index_select(0, selected)
+    counts = crow.index_select(0, selected + 1) - starts
+    total = int(counts.sum().item())
+    if total == 0:
+        empty_val = None if val is None else torch.empty(0, dtype=val.dtype, device=val.device)
+        return (
+            torch.zeros(size + 1, dtype=torch.long, device=device),
+            torch.empty(0, dtype=torch.long, device=col.device),
+            empty_val,
+            selected,
+        )
+    owner = torch.repeat_interleave(torch.arange(size, device=device, dtype=torch.long), counts)
+    first = torch.repeat_interleave(torch.cumsum(counts, dim=0) - counts, counts)
+    positions = starts.index_select(0, owner) + torch.arange(total, device=device, dtype=torch.long) - first
+    mapped = remap.index_select(0, col.index_select(0, positions))
+    keep = mapped.ge(0)
+    kept_counts = torch.bincount(owner[keep], minlength=size)
+    new_crow = torch.cat((torch.zeros(1, dtype=torch.long, device=device), kept_counts.cumsum(0)))
+    new_col = mapped[keep].contiguous()
+    new_val = None if val is None else val.index_select(0, positions)[keep].contiguous()
+    return new_crow, new_col, new_val, selected
+
+
+def _quantile_ints(degrees: torch.Tensor, points: list[float]) -> list[int]:
+    q = torch.tensor(points, dtype=torch.float64, device=degrees.device)
+    return torch.quantile(degrees.to(torch.float64), q).round().clamp_min(1).to(torch.long).cpu().tolist()
+
+
+def _degree_quantiles(crow: torch.Tensor) -> tuple[int, int, int]:
+    """Rounded q90/q95/q99 of the row degrees, at least 1 (``_auto.py:157-172``)."""
+    degrees = crow[1:] - crow[:-1]
+    if degrees.numel() == 0:
+        return 1, 1, 1
+    q90, q95, q99 = _quantile_ints(degrees, [0.9, 0.95, 0.99])
+    return int(q90), int(q95), int(q99)
+
+
+def _spmm_candidates(crow: torch.Tensor, feature_width: int, config: SchedulerConfig) -> list[tuple[int, int, int]]:
+    """Shortlist of ``(tile, waves, threshold)`` (``_auto.py:175-216``).
+
+    The preferred point is tile 64 for F <= 64 else 128, waves 8/4/2 for
+    degree skew q99/q50 >= 4 / >= 2 / otherwise, threshold q95; candidates are
+    ranked by |Δtile|/64 + |Δwaves|/6 + |Δthreshold|/threshold, ties broken by
+    the tuple, and the first ``candidate_count`` are kept."""
+    q90, q95, q99 = _degree_quantiles(crow)
+    degrees = crow[1:] - crow[:-1]
+    q50 = int(torch.quantile(degrees.to(torch.float64), 0.5).round().item()) if degrees.numel() else 1
+    skew = q99 / max(q50, 1)
+    want_waves = 8 if skew >= 4 else 4 if skew >= 2 else 2
+    want_tile = 64 if feature_width <= 64 else 128
+    want_threshold = q95
+
+    tiles = [config.feature_tile] if config.feature_tile is not None else [64, 128]
+    waves = [config.warps_per_block] if config.warps_per_block is not None else [2, 4, 8]
+    thresholds = [config.hub_threshold] if config.hub_threshold is not None else list(dict.fromkeys((q95, q90, q99)))
+
+    def rank(candidate: tuple[int, int, int]):
+        tile, wave_count, threshold = candidate
+        distance = abs(tile - want_tile) / 64 + abs(wave_count - want_waves) / 6
+        distance += abs(threshold - want_threshold) / max(want_threshold, 1)
+        return distance, candidate
+
+    pool = {(int(t), int(w), max(1, int(h))) for t in tiles for w in waves for h in thresholds}
+    return sorted(pool, key=rank)[: max(1, config.candidate_count)]
+
+
+def _cache_hit_allowed(result: dict[str, Any], config: SchedulerConfig) -> bool:
+    if result.get("schema_version") != AUTOTUNE_SCHEMA_VERSION:
+        return False
+    return True if config.replay_only else result.get("configuration") == config.tuning_signature()
+
+
+def _cached_native_available(operation: str, choice: str, candidate: Optional[list[int]]) -> bool:
+    if choice != "autosage":
+        return True
+    return native_op(operation + ("_split" if candidate is not None else "")) is not None
+
+
+def _cpu_info(operation: str) -> dict[str, Any]:
+    return {
+        "operation": operation,
+        "schema_version": AUTOTUNE_SCHEMA_VERSION,
+        "choice": "baseline",
+        "baseline": "torch CPU",
+        "from_cache": False,
+        "reason": "AutoSAGE scheduling is CUDA-only",
+    }
+
+
+def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
+    if choice == "autosage":
+        split, core = native_op("spmm_csr_split"), native_op("spmm_csr")
+        if split is not None and candidate is not None:
+            return split(crow, col, val, x, *map(int, candidate))
+        if core is not None:
+            return core(crow, col, val, x)
+    baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
+    return baseline()
+
+
+def _run_sddmm_choice(choice, candidate, crow, col, query, key) -> torch.Tensor:
+    if choice == "autosage":
+        split, core = native_op("sddmm_csr_split"), native_op("sddmm_csr")
+        if split is not None and candidate is not None:
+            return split(crow, col, query, key, *map(int, candidate))
+        if core is not None:
+            return core(crow, col, query, key)
+    baseline, _ = _prepare_sddmm_baseline(crow, col, query, key)
+    return baseline()
+
+
+def _strip_output(timing: dict[str, Any]) -> dict[str, Any]:
+    return {k: v for k, v in timing.items() if k != "output"}
+
+
+def _probe_and_choose(
+    *,
+    operation: str,
+    config: SchedulerConfig,
+    sampled_crow: torch.Tensor,
+    sampled_col: torch.Tensor,
+    baseline: Callable[[], torch.Tensor],
+    split_calls: list[tuple[list[int], Callable[[], torch.Tensor]]],
+    core_call: Optional[Callable[[], torch.Tensor]],
+) -> dict[str, Any]:
+    """Probe loop shared by SpMM and SDDMM (``_auto.py:338-401``, ``:632-704``):
+    the baseline, then the shortlisted split candidates while the probe budget
+    lasts (the first always runs), or the core kernel when no split op exists;
+    the guardrail picks the native variant only with enough sampled work and
+    ``best <= guardrail · baseline``."""
+    baseline_timing = _time_cuda(baseline, warmup=1, iterations=config.probe_iterations)
+    timings: list[dict[str, Any]] = []
+    chosen: Optional[list[int]] = None
+    best = float("inf")
+    budget = config.probe_cap_ms
+    if split_calls:
+        for index, (candidate, call) in enumerate(split_calls):
+            if index > 0 and budget <= 0.0:
+                break
+            timing = _time_cuda(call, warmup=1, iterations=config.probe_iterations, cap_ms=max(0.0, budget))
+            budget = max(0.0, budget - timing["total_ms"])
+            timings.append({"candidate": list(candidate), **_strip_output(timing)})
+            if timing["best_ms"] < best:
+                best = timing["best_ms"]
+                chosen = list(candidate)
+    elif core_call is not None:
+        timing = _time_cuda(core_call, warmup=1, iterations=config.probe_iterations, cap_ms=config.probe_cap_ms)
+        best = timing["best_ms"]
+        timings.append({"candidate": None, **_strip_output(timing)})
+    enough = (
+        sampled_crow.numel() - 1 >= config.minimum_probe_rows and sampled_col.numel() >= config.minimum_probe_nonzeros
+    )
+    use_native = enough and best <= config.guardrail * baseline_timing["best_ms"]
+    return {
+        "baseline_timing": baseline_timing,
+        "timings": timings,
+        "chosen": chosen,
+        "best": best,
+        "use_native": use_native,
+    }
+
+
+def _full_graph_confirmation(
+    native: Callable[[], torch.Tensor], baseline: Callable[[], torch.Tensor]
+) -> dict[str, float]:
+    native_t = _time_cuda(native, warmup=1, iterations=3)["best_ms"]
+    baseline_t = _time_cuda(baseline, warmup=1, iterations=3)["best_ms"]
+    return {"autosage_ms": native_t, "baseline_ms": baseline_t}
+
+
+def _result_dict(operation, config, probe, baseline_name, sampled_crow, sampled_col, sample_ms) -> dict[str, Any]:
+    baseline_best = probe["baseline_timing"]["best_ms"]
+    best = probe["best"]
+    choice = "autosage" if probe["use_native"] else "baseline"
+    return {
+        "operation": operation,
+        "schema_version": AUTOTUNE_SCHEMA_VERSION,
+        "choice": choice,
+        "candidate": probe["chosen"] if probe["use_native"] else None,
+        "baseline": baseline_name,
+        "guardrail": config.guardrail,
+        "configuration": config.tuning_signature(),
+        "probe_rows": int(sampled_crow.numel() - 1),
+        "probe_nonzeros": int(sampled_col.numel()),
+        "sampling_ms": sample_ms,
+        "probe_ms": sample_ms
+        + probe["baseline_timing"]["wall_ms"]
+        + sum(entry["wall_ms"] for entry in probe["timings"]),
+        "baseline_probe_ms": baseline_best,
+        "autosage_probe_ms": None if best == float("inf") else best,
+        "sampled_speedup": baseline_best / best if best not in (0.0, float("inf")) else None,
+        "candidates": probe["timings"],
+        "from_cache": False,
+    }
+
+
+def _replay_miss(operation: str, baseline_name: str) -> dict[str, Any]:
+    return {
+        "operation": operation,
+        "schema_version": AUTOTUNE_SCHEMA_VERSION,
+        "choice": "baseline",
+        "baseline": baseline_name,
+        "from_cache": False,
+        "replay_only": True,
+        "reason": "cache miss",
+    }
+
+
+def _verbose(tag: str, result: dict[str, Any], verbose: bool) -> None:
+    if verbose or os.getenv("AUTOSAGE_VERBOSE") == "1":
+        print(
+            f"[autosage:{tag}] rows={result['probe_rows']} nnz={result['probe_nonzeros']} "
+            f"baseline={result['baseline_probe_ms']:.4f} ms auto={result['autosage_probe_ms']} "
+            f"choice={result['choice']}"
+        )
+
+
+def spmm_csr_auto(
+    crow: torch.Tensor,
+    col: torch.Tensor,
+    val: Optional[torch.Tensor],
+    x: torch.Tensor,
+    *,
+    guardrail: float = 0.95,
+    k: int = 6,
+    seed: int = 0,
+    verbose: bool = False,
+) -> tuple[torch.Tensor, dict[str, Any]]:
+    crow, col, val, x = _normalize_csr(crow, col, val, x)
+    if not x.is_cuda:
+        return spmm_csr(crow, col, val, x), _cpu_info("spmm")
+    if x.dtype != torch.float32:
+        run, name = _prepare_spmm_baseline(crow, col, val, x)
+        return run(), {**_cpu_info("spmm"), "baseline": name, "reason": "AutoSAGE CUDA kernels require float32 features"}
+
+    load_native()
+    config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=k)
+    device = device_signature()
+    graph = graph_signature(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
+    cache = ScheduleCache()
+    if config.cache:
+        record = cache.lookup(device, graph)
+        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
+            result = record["result"]
+            choice, candidate = result.get("choice", "baseline"), result.get("candidate")
+            if _cached_native_available("spmm_csr", choice, candidate):
+                return _run_spmm_choice(choice, candidate, crow, col, val, x), {**result, "from_cache": True}
+    if config.replay_only:
+        return _run_spmm_choice("baseline", None, crow, col, val, x), _replay_miss("spmm", "torch.sparse.mm(csr)")
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s_crow, s_col, s_val, selected = _induced_sample_csr(
+        crow, col, val, fraction=config.probe_fraction, minimum_rows=config.probe_min_rows, seed=seed
+    )
+    s_x = x.index_select(0, selected).contiguous()
+    torch.cuda.synchronize()
+    sample_ms = (time.perf_counter() - t0) * 1000.0
+
+    baseline, baseline_name = _prepare_spmm_baseline(s_crow, s_col, s_val, s_x)
+    split = native_op("spmm_csr_split") if config.hub_split else None
+    core = native_op("spmm_csr")
+    split_calls = []
+    if split is not None:
+        for tile, waves, threshold in _spmm_candidates(s_crow, x.size(1), config):
+            split_calls.append(
+                ([tile, waves, threshold], lambda t=tile, w=waves, h=threshold: split(s_crow, s_col, s_val, s_x, t, w, h))
+            )
+    core_call = (lambda: core(s_crow, s_col, s_val, s_x)) if (split is None and core is not None) else None
+    probe = _probe_and_choose(
+        operation="spmm",
+        config=config,
+        sampled_crow=s_crow,
+        sampled_col=s_col,
+        baseline=baseline,
+        split_calls=split_calls,
+        core_call=core_call,
+    )
+    result = _result_dict("spmm", config, probe, baseline_name, s_crow, s_col, sample_ms)
+    if result["choice"] == "autosage" and config.full_graph_check:
+        full_baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
+        confirm = _full_graph_confirmation(
+            lambda: _run_spmm_choice("autosage", result["candidate"], crow, col, val, x), full_baseline
+        )
+        result["full_graph"] = confirm
+        if confirm["autosage_ms"] > confirm["baseline_ms"]:
+            result["choice"] = "baseline"
+            result["candidate"] = None
+            result["reason"] = "slower than the baseline on the full graph"
+    output = _run_spmm_choice(result["choice"], result["candidate"], crow, col, val, x)
+    if config.cache:
+        cache.store(device, graph, result)
+    log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})
+    _verbose("spmm", result, verbose)
+    return output, result
+
+
+def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dict[str, Any]]:
+    """Full-graph calibration of every shortlisted candidate (``_auto.py:444-522``)."""
+    crow, col, val, x = _normalize_csr(crow, col, val, x)
+    if not x.is_cuda:
+        return "baseline", _cpu_info("spmm")
+    if x.dtype != torch.float32:
+        return "baseline", {
+            **_cpu_info("spmm"),
+            "baseline": "torch.sparse.mm(csr)",
+            "reason": "AutoSAGE CUDA kernels require float32 features",
+        }
+    load_native()
+    config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=6)
+    baseline, baseline_name = _prepare_spmm_baseline(crow, col, val, x)
+    baseline_timing = _time_cuda(baseline, warmup=2, iterations=5)
+    split = native_op("spmm_csr_split") if config.hub_split else None
+    core = native_op("spmm_csr")
+    best, selected = float("inf"), None
+    timings: list[dict[str, Any]] = []
+    if split is not None:
+        for tile, waves, threshold in _spmm_candidates(crow, x.size(1), config):
+            t = _time_cuda(lambda a=tile, b=waves, c=threshold: split(crow, col, val, x, a, b, c), warmup=2, iterations=5)
+            timings.append({"candidate": [tile, waves, threshold], "best_ms": t["best_ms"]})
+            if t["best_ms"] < best:
+                best, selected = t["best_ms"], [tile, waves, threshold]
+    elif core is not None:
+        best = _time_cuda(lambda: core(crow, col, val, x), warmup=2, iterations=5)["best_ms"]
+        timings.append({"candidate": None, "best_ms": best})
+    choice = "autosage" if best <= guardrail * baseline_timing["best_ms"] else "baseline"
+    result = {
+        "operation": "spmm",
+        "schema_version": AUTOTUNE_SCHEMA_VERSION,
+        "choice": choice,
+        "candidate": selected if choice == "autosage" else None,
+        "baseline": baseline_name,
+        "guardrail": guardrail,
+        "configuration": config.tuning_signature(),
+        "calibration": "full_graph",
+        "baseline_ms": baseline_timing["best_ms"],
+        "autosage_ms": None if best == float("inf") else best,
+        "speedup": baseline_timing["best_ms"] / best if best not in (0.0, float("inf")) else None,
+        "candidates": timings,
+        "from_cache": False,
+    }
+    device = device_signature()
+    graph = graph_signature(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
+    if config.cache:
+        ScheduleCache().store(device, graph, result)
+    log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})
+    return choice, result
+
+
+def _normalize_sddmm(crow, col, query, key):
+    """Checks of ``_auto.py:554-570``."""
+    if crow.dtype not in (torch.int32, torch.int64) or col.dtype not in (torch.int32, torch.int64):
+        raise TypeError("crow and col must use integer indices")
+    crow = crow.to(dtype=torch.long).contiguous()
+    col = col.to(dtype=torch.long).contiguous()
+    query, key = query.contiguous(), key.contiguous()
+    if query.shape != key.shape or query.ndim != 2:
+        raise ValueError("query and key must have the same [N, F] shape")
+    if not query.is_floating_point() or query.dtype != key.dtype:
+        raise TypeError("query and key must use the same floating-point dtype")
+    if crow.ndim != 1 or col.ndim != 1:
+        raise ValueError("crow and col must be one-dimensional")
+    if crow.numel() != query.size(0) + 1:
+        raise ValueError("crow must contain N + 1 entries")
+    if not (crow.device == col.device == query.device == key.device):
+        raise ValueError("all SDDMM inputs must be on the same device")
+    return crow, col, query, key
+
+
+def sddmm_csr_auto(
+    crow: torch.Tensor,
+    col: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    *,
+    guardrail: float = 0.95,
+    seed: int = 0,
+    verbose: bool = False,
+) -> tuple[torch.Tensor, dict[str, Any]]:
+    crow, col, query, key = _normalize_sddmm(crow, col, query, key)
+    if not query.is_cuda:
+        run, name = _prepare_sddmm_baseline(crow, col, query, key)
+        return run(), {**_cpu_info("sddmm"), "baseline": name}
+    if query.dtype != torch.float32:
+        run, name = _prepare_sddmm_baseline(crow, col, query, key)
+        return run(), {**_cpu_info("sddmm"), "baseline": name, "reason": "AutoSAGE CUDA kernels require float32 features"}
+
+    load_native()
+    config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=6)
+    device = device_signature()
+    graph = graph_signature(crow, col, query.size(1), "sddmm", dtype=query.dtype)
+    cache = ScheduleCache()
+    if config.cache:
+        record = cache.lookup(device, graph)
+        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
+            result = record["result"]
+            choice, candidate = result.get("choice", "baseline"), result.get("candidate")
+            if _cached_native_available("sddmm_csr", choice, candidate):
+                return _run_sddmm_choice(choice, candidate, crow, col, query, key), {**result, "from_cache": True}
+    if config.replay_only:
+        return _run_sddmm_choice("baseline", None, crow, col, query, key), _replay_miss("sddmm", "gather-dot")
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s_crow, s_col, _, selected = _induced_sample_csr(
+        crow, col, None, fraction=config.probe_fraction, minimum_rows=config.probe_min_rows, seed=seed
+    )
+    s_q = query.index_select(0, selected).contiguous()
+    s_k = key.index_select(0, selected).contiguous()
+    torch.cuda.synchronize()
+    sample_ms = (time.perf_counter() - t0) * 1000.0
+
+    baseline, baseline_name = _prepare_sddmm_baseline(s_crow, s_col, s_q, s_k)
+    split = native_op("sddmm_csr_split") if config.hub_split else None
+    core = native_op("sddmm_csr")
+    split_calls = []
+    if split is not None:
+        pairs = dict.fromkeys((w, h) for _, w, h in _spmm_candidates(s_crow, query.size(1), config))
+        for waves, threshold in pairs:
+            split_calls.append(([waves, threshold], lambda w=waves, h=threshold: split(s_crow, s_col, s_q, s_k, w, h)))
+    core_call = (lambda: core(s_crow, s_col, s_q, s_k)) if (split is None and core is not None) else None
+    probe = _probe_and_choose(
+        operation="sddmm",
+        config=config,
+        sampled_crow=s_crow,
+        sampled_col=s_col,
+        baseline=baseline,
+        split_calls=split_calls,
+        core_call=core_call,
+    )
+    result = _result_dict("sddmm", config, probe, baseline_name, s_crow, s_col, sample_ms)
+    output = _run_sddmm_choice(result["choice"], result["candidate"], crow, col, query, key)
+    if config.cache:
+        cache.store(device, graph, result)
+    log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})
+    _verbose("sddmm", result, verbose)
+    return output, result
+
+
+def _torch_row_softmax(crow: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+    """The reference composition (``_auto.py:744-759``): per-row amax,
+    exp(s - max), scatter_add denominators, divide."""
+    rows = _edge_rows(crow)
+    if scores.numel() == 0:
+        return scores.clone()
+    maxima = torch.full((crow.numel() - 1,), -torch.inf, dtype=scores.dtype, device=scores.device)
+    maxima.scatter_reduce_(0, rows, scores, reduce="amax", include_self=True)
+    exps = (scores - maxima.index_select(0, rows)).exp()
+    sums = torch.zeros_like(maxima)
+    sums.scatter_add_(0, rows, exps)
+    return exps / sums.index_select(0, rows)
+
+
+def _csr_row_softmax(crow: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+    """CSR row softmax: the native kernel on the GPU (float32), the reference
+    torch composition on the CPU."""
+    if scores.is_cuda and scores.dtype == torch.float32:
+        if not load_native() or native_op("csr_row_softmax") is None:
+            raise RuntimeError("AutoSAGE native csr_row_softmax is unavailable")
+        return native_op("csr_row_softmax")(crow.to(torch.long).contiguous(), scores.contiguous())
+    return _torch_row_softmax(crow, scores)
+
+
+def _fused_default() -> bool:
+    return os.getenv("AUTOSAGE_FUSED_ATTENTION", "1") == "1"
+
+
+def csr_attention_forward(
+    crow: torch.Tensor,
+    col: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    guardrail: float = 0.95,
+    seed: int = 0,
+    verbose: bool = False,
+    scale: float = 1.0,
+    fused: Optional[bool] = None,
+) -> tuple[torch.Tensor, dict[str, Any]]:
+    """softmax_row(scale · SDDMM(query, key)) · value (``_auto.py:762-780``;
+    the reference has no scale, i.e. scale = 1).
+
+    On the GPU with float32 inputs and ``fused`` (default: the
+    ``AUTOSAGE_FUSED_ATTENTION`` switch, on) the three stages run as one
+    native kernel; otherwise as the scheduled SDDMM, the row softmax and the
+    scheduled SpMM, as in the reference."""
+    use_fused = _fused_default() if fused is None else bool(fused)
+    if use_fused and query.is_cuda and query.dtype == torch.float32 and value.dtype == torch.float32:
+        crow_n, col_n, q, k = _normalize_sddmm(crow, col, query, key)
+        if not load_native() or native_op("csr_attention") is None:
+            raise RuntimeError("AutoSAGE native csr_attention is unavailable")
+        out = native_op("csr_attention")(crow_n, col_n, q, k, value.contiguous(), float(scale))
+        info = {"operation": "attention", "schema_version": AUTOTUNE_SCHEMA_VERSION, "choice": "fused",
+                "from_cache": False}
+        return out, {"sddmm": {**info, "operation": "sddmm"}, "spmm": {**info, "operation": "spmm"}, "fused": True}
+    scores, sddmm_info = sddmm_csr_auto(crow, col, query, key, guardrail=guardrail, seed=seed, verbose=verbose)
+    scores = scores.to(query.dtype)
+    if scale != 1.0:
+        scores = scores * scale
+    probabilities = _csr_row_softmax(crow, scores)
+    output, spmm_info = spmm_csr_auto(crow, col, probabilities, value, guardrail=guardrail, seed=seed, verbose=verbose)
+    return output, {"sddmm": sddmm_info, "spmm": spmm_info}
+
+
+__all__ = [
+    "AUTOTUNE_SCHEMA_VERSION",
+    "calibrate_full",
+    "csr_attention_forward",
+    "sddmm_csr_auto",
+    "spmm_csr_auto",
+]

@@ -1,0 +1,157 @@
+"""Schedule keys and the on-disk schedule cache.
+
+Follows ``autosage/_cache.py`` of the reference so that keys and files are
+interchangeable: the device dictionary (``:24-37``), the graph dictionary with
+rounded linear degree quantiles (``:57-93``), the 24-hex-digit structure hash
+over the raw little-endian bytes of at most the first and last 1024 entries of
+``crow`` and ``col`` (``:40-54``), the key as canonical JSON of
+``{"device", "graph"}`` (``:103-107``), the schema-1 JSON file replaced
+atomically (``:126-148``) and the JSONL probe log (``:151-157``).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import tempfile
+import time
+from pathlib import Path
+from typing import Any, Optional
+
+import torch
+
+CACHE_SCHEMA_VERSION = 1
+_HASH_EDGE = 1024  # entries hashed from each end of a long index vector
+
+
+def cache_directory() -> Path:
+    configured = os.getenv("AUTOSAGE_CACHE_DIR")
+    return Path(configured).expanduser() if configured else Path.home() / ".cache" / "autosage"
+
+
+def device_signature(device: Optional[int] = None) -> dict[str, Any]:
+    if not torch.cuda.is_available():
+        return {"type": "cpu", "torch": torch.__version__}
+    index = torch.cuda.current_device() if device is None else device
+    props = torch.cuda.get_device_properties(index)
+    return {
+        "type": "cuda",
+        "name": props.name,
+        "compute_capability": [props.major, props.minor],
+        "multiprocessors": props.multi_processor_count,
+        "total_memory": int(props.total_memory),
+        "cuda": torch.version.cuda,
+        "torch": torch.__version__,
+    }
+
+
+def _hash_slice(tensor: torch.Tensor) -> torch.Tensor:
+    count = tensor.numel()
+    if count <= 2 * _HASH_EDGE:
+        return tensor
+    return torch.cat((tensor[:_HASH_EDGE], tensor[-_HASH_EDGE:]))
+
+
+def _sample_hash(crow: torch.Tensor, col: torch.Tensor) -> str:
+    digest = hashlib.sha256()
+    for tensor in (crow, col):
+        if tensor.numel() == 0:
+            continue
+        raw = _hash_slice(tensor).detach().contiguous().cpu()
+        digest.update(raw.numpy().tobytes())
+    return digest.hexdigest()[:24]
+
+
+def _rounded_quantiles(degrees: torch.Tensor, qs: list[float]) -> list[int]:
+    points = torch.tensor(qs, dtype=torch.float64, device=degrees.device)
+    values = torch.quantile(degrees.to(torch.float64), points).round().to(torch.long)
+    return [int(v) for v in values.cpu().tolist()]
+
+
+def graph_signature(
+    crow: torch.Tensor,
+    col: torch.Tensor,
+    feature_width: int,
+    operation: str,
+    *,
+    weighted: bool = False,
+    dtype: Optional[torch.dtype] = None,
+) -> dict[str, Any]:
+    degrees = crow[1:] - crow[:-1]
+    q50, q90, q99 = _rounded_quantiles(degrees, [0.5, 0.9, 0.99]) if degrees.numel() else (0, 0, 0)
+    return {
+        "operation": operation,
+        "feature_width": int(feature_width),
+        "dtype": None if dtype is None else str(dtype),
+        "weighted": bool(weighted),
+        "rows": int(crow.numel() - 1),
+        "nonzeros": int(col.numel()),
+        "degree_q50": q50,
+        "degree_q90": q90,
+        "degree_q99": q99,
+        "structure_hash": _sample_hash(crow, col),
+    }
+
+
+class ScheduleCache:
+    def __init__(self, path: Optional[os.PathLike[str] | str] = None):
+        self.path = Path(path) if path is not None else cache_directory() / "schedules.json"
+        self._records = self._load()
+
+    @staticmethod
+    def _key(device: dict[str, Any], graph: dict[str, Any]) -> str:
+        return json.dumps({"device": device, "graph": graph}, sort_keys=True, separators=(",", ":"))
+
+    def _load(self) -> dict[str, dict[str, Any]]:
+        try:
+            payload = json.loads(self.path.read_text(encoding="utf-8"))
+        except FileNotFoundError:
+            return {}
+        except (OSError, json.JSONDecodeError):
+            return {}
+        if not isinstance(payload, dict) or payload.get("schema_version") != CACHE_SCHEMA_VERSION:
+            return {}
+        records = payload.get("records", {})
+        return records if isinstance(records, dict) else {}
+
+    def lookup(self, device: dict[str, Any], graph: dict[str, Any]) -> Optional[dict[str, Any]]:
+        return self._records.get(self._key(device, graph))
+
+    def store(self, device: dict[str, Any], graph: dict[str, Any], result: dict[str, Any]) -> None:
+        self.path.parent.mkdir(parents=True, exist_ok=True)
+        self._records[self._key(device, graph)] = {
+            "timestamp": int(time.time()),
+            "device": device,
+            "graph": graph,
+            "result": result,
+        }
+        payload = {"schema_version": CACHE_SCHEMA_VERSION, "records": self._records}
+        fd, temporary = tempfile.mkstemp(prefix="schedules-", suffix=".json", dir=self.path.parent)
+        try:
+            with os.fdopen(fd, "w", encoding="utf-8") as stream:
+                json.dump(payload, stream, indent=2, sort_keys=True)
+                stream.write("\n")
+            os.replace(temporary, self.path)
+        finally:
+            if os.path.exists(temporary):
+                os.unlink(temporary)
+
+
+def log_probe(event: dict[str, Any]) -> None:
+    if os.getenv("AUTOSAGE_LOG_PROBES", "1") != "1":
+        return
+    path = cache_directory() / "probe_logs.jsonl"
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with path.open("a", encoding="utf-8") as stream:
+        stream.write(json.dumps(event, sort_keys=True) + "\n")
+
+
+__all__ = [
+    "CACHE_SCHEMA_VERSION",
+    "ScheduleCache",
+    "cache_directory",
+    "device_signature",
+    "graph_signature",
+    "log_probe",
+]

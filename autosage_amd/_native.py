@@ -1,0 +1,355 @@
+"""ctypes binding of ``libautosage_hip.so`` and the ``autosage::*`` operators.
+
+The reference registers its CUDA kernels as torch operators from C++
+(``csrc/spmm_binding.cpp:65-75``, ``csrc/sddmm_csr_op.cu:191-201``).  Here the
+kernels live behind the plain C ABI of ``include/autosage_hip.h`` and this
+module registers the same operator schemas under the same ``autosage``
+namespace with ``torch.library``, implemented for the CUDA dispatch key (HIP
+devices on PyTorch-ROCm).  Callers that use ``torch.ops.autosage.spmm_csr``,
+``spmm_csr_split``, ``sddmm_csr`` or ``sddmm_csr_split`` keep working.  Two
+operators are new: ``csr_row_softmax`` and ``csr_attention``.
+
+Input checks and their messages follow ``check_inputs``
+(``csrc/spmm_binding.cpp:9-29``) and ``check_sddmm_inputs``
+(``csrc/sddmm_csr_op.cu:85-106``); a failing check raises ``RuntimeError``
+as ``TORCH_CHECK`` does.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIBRARY_NAME = "libautosage_hip.so"
+ABI_VERSION = 1
+HUB_EXACT = 0
+HUB_SPLIT64 = 1
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_ptr = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+
+_SIGNATURES = {
+    "as_last_error": (ctypes.c_char_p, []),
+    "as_abi_version": (_c_int, []),
+    "as_spmm_csr_f32": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr]),
+    "as_bin_workspace_bytes": (_c_size, [_c_i64]),
+    "as_bin_rows_by_degree": (_c_int, [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "as_spmm_split_workspace_bytes": (_c_size, [_c_i64]),
+    "as_spmm_csr_split_f32": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_int, _c_int,
+         _c_ptr, _c_size, _c_ptr],
+    ),
+    "as_sddmm_csr_f32": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr]),
+    "as_sddmm_split_workspace_bytes": (_c_size, [_c_i64]),
+    "as_sddmm_csr_split_f32": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_ptr, _c_size, _c_ptr],
+    ),
+    "as_csr_row_softmax_f32": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr]),
+    "as_csr_attention_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
+    "as_csr_attention_f32": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr,
+         _c_size, _c_ptr],
+    ),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_LIB: Optional[ctypes.CDLL] = None
+_LIB_PATH: Optional[Path] = None
+_OPS_LIBRARY: Optional[torch.library.Library] = None
+
+
+def package_library_path() -> Path:
+    return Path(__file__).resolve().parent / "lib" / LIBRARY_NAME
+
+
+def open_library(path: os.PathLike[str] | str) -> ctypes.CDLL:
+    """dlopens the C-ABI library and declares every exported signature.
+
+    torch is imported first so that its HIP runtime is the one the library
+    binds to (both use the soname ``libamdhip64.so.7``)."""
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.as_abi_version()
+    if version != ABI_VERSION:
+        raise OSError(f"{path}: ABI version {version}, expected {ABI_VERSION}")
+    return lib
+
+
+def library() -> ctypes.CDLL:
+    if _LIB is None:
+        raise RuntimeError("AutoSAGE HIP library is not loaded")
+    return _LIB
+
+
+def loaded_path() -> Optional[Path]:
+    return _LIB_PATH
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _raise(status: int, what: str) -> None:
+    if status != 0:
+        message = library().as_last_error().decode("utf-8", "replace")
+        raise RuntimeError(f"{what}: {message} (status {status})")
+
+
+def _env_vec4() -> bool:
+    value = os.getenv("AUTOSAGE_VEC4")
+    if value is None:
+        return True
+    return value.strip().lower() not in {"0", "false", "no", "off"}
+
+
+def _env_hub_mode() -> int:
+    value = (os.getenv("AUTOSAGE_HUB_MODE") or "exact").strip().lower()
+    if value in {"exact", "0"}:
+        return HUB_EXACT
+    if value in {"split64", "1"}:
+        return HUB_SPLIT64
+    raise ValueError("AUTOSAGE_HUB_MODE must be 'exact' or 'split64'")
+
+
+def _check(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError(message)
+
+
+def check_spmm_inputs(crow, col, val, x) -> None:
+    _check(crow.is_cuda and col.is_cuda and x.is_cuda, "crow, col, and x must be CUDA tensors")
+    _check(crow.dtype == torch.long and col.dtype == torch.long, "crow and col must use torch.long indices")
+    _check(crow.dim() == 1 and col.dim() == 1, "crow and col must be one-dimensional")
+    _check(x.dim() == 2 and x.is_contiguous(), "x must be contiguous with shape [N, F]")
+    _check(crow.is_contiguous() and col.is_contiguous(), "crow and col must be contiguous")
+    _check(crow.device == x.device and col.device == x.device, "crow, col, and x must be on the same CUDA device")
+    _check(crow.numel() == x.size(0) + 1, "crow must contain N + 1 entries")
+    _check(x.dtype == torch.float32, "x must be float32")
+    if val is not None:
+        _check(val.is_cuda and val.device == x.device, "val must be on the same CUDA device as x")
+        _check(val.dtype == torch.float32 and val.is_contiguous(), "val must be contiguous float32")
+        _check(val.numel() == col.numel(), "val must contain one weight per nonzero")
+
+
+def check_sddmm_inputs(crow, col, query, key) -> None:
+    _check(crow.is_cuda and col.is_cuda and query.is_cuda and key.is_cuda, "all SDDMM inputs must be CUDA tensors")
+    _check(crow.dtype == torch.long and col.dtype == torch.long, "crow and col must use torch.long indices")
+    _check(query.dtype == torch.float32 and key.dtype == torch.float32, "query and key must be float32")
+    _check(query.dim() == 2 and query.shape == key.shape, "query and key must have the same [N, F] shape")
+    _check(crow.numel() == query.size(0) + 1, "crow must contain N + 1 entries")
+    _check(
+        crow.device == query.device and col.device == query.device and key.device == query.device,
+        "all SDDMM inputs must be on the same CUDA device",
+    )
+    _check(
+        crow.is_contiguous() and col.is_contiguous() and query.is_contiguous() and key.is_contiguous(),
+        "all SDDMM inputs must be contiguous",
+    )
+    _check(query.size(0) <= 2**31 - 1 and query.size(1) <= 2**31 - 1, "SDDMM dimensions exceed the kernel index range")
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# Operator implementations (CUDA dispatch key)
+
+
+def spmm_csr_impl(crow, col, val, x):
+    check_spmm_inputs(crow, col, val, x)
+    y = torch.empty_like(x)
+    n, f = x.shape
+    if n == 0 or f == 0:
+        return y
+    with torch.cuda.device(x.device):
+        status = library().as_spmm_csr_f32(
+            _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, int(_env_vec4()), _stream(x.device)
+        )
+    _raise(status, "autosage::spmm_csr")
+    return y
+
+
+def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_threshold):
+    check_spmm_inputs(crow, col, val, x)
+    _check(feature_tile in (64, 128), "feature_tile must be 64 or 128")
+    _check(warps_per_block in (2, 4, 8), "warps_per_block must be 2, 4, or 8")
+    _check(hub_threshold > 0, "hub_threshold must be positive")
+    y = torch.empty_like(x)
+    n, f = x.shape
+    if n == 0 or f == 0:
+        return y
+    lib = library()
+    ws = _workspace(lib.as_spmm_split_workspace_bytes(n), x.device)
+    with torch.cuda.device(x.device):
+        status = lib.as_spmm_csr_split_f32(
+            _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, int(feature_tile),
+            int(warps_per_block), int(hub_threshold), int(_env_vec4()), _env_hub_mode(), _ptr(ws), ws.numel(),
+            _stream(x.device),
+        )
+    _raise(status, "autosage::spmm_csr_split")
+    return y
+
+
+def sddmm_csr_impl(crow, col, query, key):
+    check_sddmm_inputs(crow, col, query, key)
+    nnz = col.numel()
+    n, f = query.shape
+    if f == 0:
+        return torch.zeros(nnz, dtype=query.dtype, device=query.device)
+    out = torch.empty(nnz, dtype=query.dtype, device=query.device)
+    if n == 0 or nnz == 0:
+        return out
+    with torch.cuda.device(query.device):
+        status = library().as_sddmm_csr_f32(
+            _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, _stream(query.device)
+        )
+    _raise(status, "autosage::sddmm_csr")
+    return out
+
+
+def sddmm_csr_split_impl(crow, col, query, key, warps_per_block, hub_threshold):
+    check_sddmm_inputs(crow, col, query, key)
+    _check(warps_per_block in (2, 4, 8), "warps_per_block must be 2, 4, or 8")
+    _check(0 < hub_threshold <= 2**31 - 1, "hub_threshold must be a positive 32-bit integer")
+    nnz = col.numel()
+    n, f = query.shape
+    if f == 0:
+        return torch.zeros(nnz, dtype=query.dtype, device=query.device)
+    out = torch.empty(nnz, dtype=query.dtype, device=query.device)
+    if n == 0 or nnz == 0:
+        return out
+    lib = library()
+    ws = _workspace(lib.as_sddmm_split_workspace_bytes(n), query.device)
+    with torch.cuda.device(query.device):
+        status = lib.as_sddmm_csr_split_f32(
+            _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, int(warps_per_block),
+            int(hub_threshold), _ptr(ws), ws.numel(), _stream(query.device),
+        )
+    _raise(status, "autosage::sddmm_csr_split")
+    return out
+
+
+def csr_row_softmax_impl(crow, scores):
+    _check(crow.is_cuda and scores.is_cuda, "crow and scores must be CUDA tensors")
+    _check(crow.dtype == torch.long and crow.dim() == 1 and crow.is_contiguous(), "crow must be contiguous torch.long")
+    _check(scores.dtype == torch.float32 and scores.dim() == 1, "scores must be one-dimensional float32")
+    _check(crow.device == scores.device, "crow and scores must be on the same CUDA device")
+    scores = scores.contiguous()
+    probs = torch.empty_like(scores)
+    n = crow.numel() - 1
+    if n <= 0 or scores.numel() == 0:
+        return probs
+    with torch.cuda.device(scores.device):
+        status = library().as_csr_row_softmax_f32(
+            _ptr(crow), _ptr(scores), _ptr(probs), n, scores.numel(), _stream(scores.device)
+        )
+    _raise(status, "autosage::csr_row_softmax")
+    return probs
+
+
+def csr_attention_impl(crow, col, query, key, value, scale):
+    check_sddmm_inputs(crow, col, query, key)
+    _check(value.is_cuda and value.device == query.device, "value must be on the same CUDA device as query")
+    _check(value.dtype == torch.float32 and value.dim() == 2 and value.is_contiguous(),
+           "value must be contiguous float32 with shape [N, F_v]")
+    _check(value.size(0) == query.size(0), "value must have one row per node")
+    n, fqk = query.shape
+    fv = value.size(1)
+    nnz = col.numel()
+    out = torch.empty((n, fv), dtype=value.dtype, device=value.device)
+    if n == 0 or fv == 0:
+        return out
+    if fqk == 0 and nnz > 0:
+        # all scores are zero: the softmax of each row is uniform
+        scores = torch.zeros(nnz, dtype=query.dtype, device=query.device)
+        return spmm_csr_impl(crow, col, csr_row_softmax_impl(crow, scores), value)
+    lib = library()
+    ws = _workspace(lib.as_csr_attention_workspace_bytes(n, nnz), query.device)
+    with torch.cuda.device(query.device):
+        status = lib.as_csr_attention_f32(
+            _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv, float(scale),
+            _ptr(ws), ws.numel(), _stream(query.device),
+        )
+    _raise(status, "autosage::csr_attention")
+    return out
+
+
+def bin_rows_by_degree(crow: torch.Tensor, threshold: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(heavy rows ascending, light rows ascending) as int32, computed on the
+    device (``csrc/launcher_spmm.cu:49-59``).  Synchronises to split the lists."""
+    _check(crow.is_cuda and crow.dtype == torch.long and crow.dim() == 1, "crow must be a CUDA torch.long vector")
+    _check(threshold > 0, "hub_threshold must be positive")
+    crow = crow.contiguous()
+    n = crow.numel() - 1
+    order = torch.empty(max(n, 1), dtype=torch.int32, device=crow.device)
+    counts = torch.zeros(4, dtype=torch.int32, device=crow.device)
+    lib = library()
+    ws = _workspace(lib.as_bin_workspace_bytes(n), crow.device)
+    with torch.cuda.device(crow.device):
+        status = lib.as_bin_rows_by_degree(
+            _ptr(crow), n, int(threshold), _ptr(order), _ptr(counts), _ptr(ws), ws.numel(), _stream(crow.device)
+        )
+    _raise(status, "bin_rows_by_degree")
+    heavy = int(counts[0].item())
+    return order[:heavy].clone(), order[heavy:n].clone()
+
+
+_SCHEMAS = {
+    "spmm_csr": ("spmm_csr(Tensor crow, Tensor col, Tensor? val, Tensor x) -> Tensor", spmm_csr_impl),
+    "spmm_csr_split": (
+        "spmm_csr_split(Tensor crow, Tensor col, Tensor? val, Tensor x, int feature_tile, int warps_per_block, "
+        "int hub_threshold) -> Tensor",
+        spmm_csr_split_impl,
+    ),
+    "sddmm_csr": ("sddmm_csr(Tensor crow, Tensor col, Tensor query, Tensor key) -> Tensor", sddmm_csr_impl),
+    "sddmm_csr_split": (
+        "sddmm_csr_split(Tensor crow, Tensor col, Tensor query, Tensor key, int warps_per_block, "
+        "int hub_threshold) -> Tensor",
+        sddmm_csr_split_impl,
+    ),
+    "csr_row_softmax": ("csr_row_softmax(Tensor crow, Tensor scores) -> Tensor", csr_row_softmax_impl),
+    "csr_attention": (
+        "csr_attention(Tensor crow, Tensor col, Tensor query, Tensor key, Tensor value, float scale=1.0) -> Tensor",
+        csr_attention_impl,
+    ),
+}
+
+OPERATOR_NAMES = tuple(_SCHEMAS)
+
+
+def _register_operators() -> None:
+    global _OPS_LIBRARY
+    if _OPS_LIBRARY is not None:
+        return
+    lib = torch.library.Library("autosage", "DEF")
+    for name, (schema, impl) in _SCHEMAS.items():
+        lib.define(schema)
+        lib.impl(name, impl, "CUDA")
+    _OPS_LIBRARY = lib
+
+
+def load(path: os.PathLike[str] | str) -> None:
+    """Loads the library at ``path`` and registers the ``autosage::*`` ops."""
+    global _LIB, _LIB_PATH
+    if _LIB is None:
+        _LIB = open_library(path)
+        _LIB_PATH = Path(path)
+    _register_operators()

@@ -1,0 +1,41 @@
+// Host-side internals shared by the kernel translation units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/autosage_hip.h"
+
+namespace as {
+
+constexpr int kWave = 64;        // CDNA wavefront width
+constexpr int kBlock = 256;      // default workgroup: 4 waves
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+// Largest number of workgroups one launch may use along x (grid work-items
+// must stay below 2^32 on AMD hardware).
+constexpr int64_t kMaxBlocksPerLaunch = int64_t(1) << 22;
+
+// Error reporting: format into the thread-local message and return `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Converts the last HIP launch error (if any) into an as_status.
+int check_launch(const char* what);
+// Clears the thread-local message (called at the start of every entry point).
+void clear_error();
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Degree binning (binning.hip).
+constexpr int kBinRowsPerThread = 4;
+constexpr int kBinTile = kBlock * kBinRowsPerThread;
+inline int64_t bin_tiles(int64_t n) { return (n + kBinTile - 1) / kBinTile; }
+size_t bin_workspace_bytes(int64_t n);
+// order[n], counts[4] (counts[0]=heavy, counts[1]=light, counts[2..3] free
+// for callers) are written; workspace holds per-tile counts and offsets.
+int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold,
+                    int32_t* order, int32_t* counts, void* workspace,
+                    hipStream_t stream);
+
+}  // namespace as

@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the sparse hot path on one MI355X.
+
+Default workload: configuration 3 of the benchmark contract — fp32 SpMM,
+F = 128, on the seeded skewed graph (N = 232,965, nnz = 114,615,892, max
+degree 21,000).  A step is one call of the scheduled native SpMM
+(``torch.ops.autosage.spmm_csr_split`` with the candidate chosen by a
+full-graph calibration, or the whole-graph kernel when that is faster) with
+inputs resident in HBM.  Prints one JSON line.
+
+Other workloads (``--workload cfg1|cfg2|cfg3|cfg4|cfg5``) are for the
+builder's own measurements.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "SpMM/SDDMM GFLOP/s (2·nnz·F) + achieved HBM GB/s vs ~8 TB/s peak, F=128"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def spmm_bytes(n: int, nnz: int, f: int, weighted: bool) -> int:
+    """Algorithmic bytes of one SpMM: X-row gathers, Y write, col, crow, val."""
+    return 4 * f * nnz + 4 * f * n + 8 * nnz + 8 * (n + 1) + (4 * nnz if weighted else 0)
+
+
+def sddmm_bytes(n: int, nnz: int, f: int) -> int:
+    return 4 * f * nnz + 4 * f * n + 4 * nnz + 8 * nnz + 8 * (n + 1)
+
+
+def attention_bytes(n: int, nnz: int, fqk: int, fv: int) -> int:
+    return 4 * fqk * nnz + 4 * fqk * n + 4 * fv * nnz + 4 * fv * n + 8 * nnz + 8 * (n + 1)
+
+
+def time_steps(fn, steps: int, warmup: int) -> tuple[float, list[float]]:
+    """Warmup, then ``steps`` back-to-back calls between two events on the
+    current stream (the stream the kernels are launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    end.synchronize()
+    total = float(start.elapsed_time(end))
+    # per-call samples for the spread
+    samples = []
+    for _ in range(min(steps, 5)):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        samples.append(float(s.elapsed_time(e)))
+    return total / steps, samples
+
+
+def cpu_baseline_spmm(crow: np.ndarray, col: np.ndarray, val, x: np.ndarray, target_nnz: int) -> dict:
+    """The reference CPU path (torch.sparse.mm on a CSR tensor, restated in
+    oracle/) on the leading rows of the graph holding about ``target_nnz``
+    nonzeros, timed on this host's cores."""
+    import oracle
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    rows = int(np.searchsorted(crow, min(target_nnz, int(crow[-1])), side="left"))
+    rows = max(1, min(rows, crow.size - 1))
+    s_crow = torch.from_numpy(crow[: rows + 1].copy())
+    nnz = int(s_crow[-1])
+    s_col = torch.from_numpy(col[:nnz].copy())
+    s_val = None if val is None else torch.from_numpy(val[:nnz].copy())
+    xt = torch.from_numpy(x)
+    f = x.shape[1]
+    # the sample's rows gather from the full X: build an N_sample x N matrix
+    weights = torch.ones(nnz, dtype=torch.float32) if s_val is None else s_val
+    matrix = torch.sparse_csr_tensor(s_crow, s_col, weights, size=(rows, x.shape[0]))
+    torch.sparse.mm(matrix, xt)  # warmup
+    reps, times = 3, []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        torch.sparse.mm(matrix, xt)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    del oracle
+    return {
+        "value": 2.0 * nnz * f / t / 1e9,
+        "unit": "GFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"torch.sparse.mm CPU CSR SpMM (reference ops.py:124-143 path) on rows [0,{rows}) = "
+        f"{nnz} nnz of the same graph, F={f}, median of {reps} after 1 warmup, {t * 1e3:.1f} ms/call",
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--workload", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    parser.add_argument("--features", type=int, default=None)
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--variant", default="calibrated",
+                        help="calibrated | whole | t,w,h (split candidate)")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-gpu-baseline", action="store_true")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the row-sharded design is described in DESIGN.md)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    import autosage_amd
+    from autosage_amd import synth
+    from autosage_amd._auto import _prepare_spmm_baseline, _spmm_candidates
+    from autosage_amd.config import SchedulerConfig
+
+    if not autosage_amd.load_native():
+        raise RuntimeError(f"HIP library failed to load: {autosage_amd.ops.native_load_error()}")
+    device = torch.device("cuda:0")
+    t0 = time.time()
+    if args.workload in ("cfg1", "cfg2", "cfg3"):
+        f = args.features or {"cfg1": 64, "cfg2": 128, "cfg3": 128}[args.workload]
+        w = {"cfg1": synth.config1, "cfg2": synth.config2, "cfg3": synth.config3}[args.workload](
+            seed=args.seed, features=f)
+        log(f"generated {args.workload}: {w.degree_stats()} in {time.time() - t0:.1f}s")
+        n, nnz = w.rows, w.nnz
+        crow = torch.from_numpy(w.crow).to(device)
+        col = torch.from_numpy(w.col).to(device)
+        val = None if w.val is None else torch.from_numpy(w.val).to(device)
+        x = torch.from_numpy(w.dense["x"]).to(device)
+        weighted = val is not None
+
+        variants = {"whole": lambda: torch.ops.autosage.spmm_csr(crow, col, val, x)}
+        for cand in _spmm_candidates(crow, f, SchedulerConfig(candidate_count=6)):
+            variants[",".join(map(str, cand))] = (
+                lambda c=cand: torch.ops.autosage.spmm_csr_split(crow, col, val, x, *c))
+        calib = {}
+        if args.variant == "calibrated":
+            for name, fn in variants.items():
+                ms, _ = time_steps(fn, 3, 1)
+                calib[name] = round(ms, 4)
+            chosen = min(calib, key=calib.get)
+        else:
+            chosen = args.variant
+            if chosen not in variants:
+                t_, w_, h_ = map(int, chosen.split(","))
+                variants[chosen] = lambda: torch.ops.autosage.spmm_csr_split(crow, col, val, x, t_, w_, h_)
+        log(f"calibration (ms): {calib}; chosen {chosen}")
+        step = variants[chosen]
+        ms, samples = time_steps(step, args.steps, args.warmup)
+        flops = 2.0 * nnz * f
+        algo = spmm_bytes(n, nnz, f, weighted)
+        result = {
+            "metric": METRIC,
+            "value": round(flops / (ms * 1e-3) / 1e9, 2),
+            "unit": "GFLOP/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f32",
+            "data": "synthetic",
+            "config": {
+                "workload": f"{args.workload} SpMM fp32 F={f}" + (" weighted" if weighted else " unweighted"),
+                "rows": n,
+                "nnz": nnz,
+                "features": f,
+                "variant": chosen,
+                "graph_fingerprint": w.fingerprint(),
+                "degree_stats": w.degree_stats(),
+            },
+            "roofline": {
+                "bound": "hbm",
+                "achieved": round(algo / (ms * 1e-3) / 1e9, 1),
+                "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s",
+                "frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                "traffic": None,
+                "algorithmic_bytes": algo,
+            },
+            "per_call_ms": [round(s, 4) for s in samples],
+            "calibration_ms": calib,
+        }
+        if not args.no_gpu_baseline:
+            base, name = _prepare_spmm_baseline(crow, col, val, x)
+            bms, _ = time_steps(base, 3, 1)
+            result["gpu_baseline"] = {"name": f"{name} (PyTorch-ROCm)", "ms": round(bms, 4),
+                                      "speedup": round(bms / ms, 3)}
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = cpu_baseline_spmm(w.crow, w.col, w.val, w.dense["x"], target_nnz=nnz // 8)
+        else:
+            result["cpu_baseline"] = None
+    else:
+        result = bench_other(args, device)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def bench_other(args, device) -> dict:
+    """SDDMM (cfg4) and fused attention (cfg5) lines for the builder's tables."""
+    from autosage_amd import synth
+
+    t0 = time.time()
+    if args.workload == "cfg4":
+        f = args.features or 128
+        w = synth.config4(seed=args.seed, features=f)
+        log(f"generated cfg4: {w.degree_stats()} in {time.time() - t0:.1f}s")
+        crow = torch.from_numpy(w.crow).to(device)
+        col = torch.from_numpy(w.col).to(device)
+        q = torch.from_numpy(w.dense["q"]).to(device)
+        k = torch.from_numpy(w.dense["k"]).to(device)
+        calib = {"whole": time_steps(lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k), 3, 1)[0]}
+        for waves in (2, 4, 8):
+            for thr in (256, 1024, 4096):
+                calib[f"{waves},{thr}"] = time_steps(
+                    lambda a=waves, b=thr: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b), 3, 1)[0]
+        chosen = min(calib, key=calib.get)
+        if chosen == "whole":
+            step = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)  # noqa: E731
+        else:
+            a, b = map(int, chosen.split(","))
+            step = lambda: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b)  # noqa: E731
+        ms, samples = time_steps(step, args.steps, args.warmup)
+        flops = 2.0 * w.nnz * f
+        algo = sddmm_bytes(w.rows, w.nnz, f)
+        name = f"cfg4 SDDMM fp32 F={f}"
+    else:
+        w = synth.config5(seed=args.seed)
+        log(f"generated cfg5: {w.degree_stats()} in {time.time() - t0:.1f}s")
+        crow = torch.from_numpy(w.crow).to(device)
+        col = torch.from_numpy(w.col).to(device)
+        q = torch.from_numpy(w.dense["q"]).to(device)
+        k = torch.from_numpy(w.dense["k"]).to(device)
+        v = torch.from_numpy(w.dense["v"]).to(device)
+        step = lambda: torch.ops.autosage.csr_attention(crow, col, q, k, v, 0.125)  # noqa: E731
+        calib = {}
+        chosen = "fused"
+        ms, samples = time_steps(step, args.steps, args.warmup)
+        flops = 2.0 * w.nnz * (64 + 128)
+        algo = attention_bytes(w.rows, w.nnz, 64, 128)
+        name = "cfg5 fused CSR attention fp32 Fqk=64 Fv=128 scale=1/8"
+    return {
+        "metric": METRIC,
+        "value": round(flops / (ms * 1e-3) / 1e9, 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": name, "rows": w.rows, "nnz": w.nnz, "variant": chosen,
+                   "degree_stats": w.degree_stats()},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(algo / (ms * 1e-3) / 1e9, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes": algo,
+        },
+        "per_call_ms": [round(s, 4) for s in samples],
+        "calibration_ms": {k_: round(v_, 4) for k_, v_ in calib.items()},
+        "cpu_baseline": None,
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

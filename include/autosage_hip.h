@@ -1,0 +1,146 @@
+/*
+ * autosage_hip.h — C ABI of the MI355X (gfx950) sparse hot path.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a HIP stream
+ * (passed as `void*`, a hipStream_t; NULL means the default stream).  The
+ * library never allocates device memory: outputs and workspaces are owned by
+ * the caller (the Python host layer allocates them with torch), and the
+ * library keeps no per-call state.  All launches are asynchronous on the given
+ * stream; no entry point synchronises the host.
+ *
+ * Return value: AS_OK (0) or a positive as_status; as_last_error() then
+ * returns a thread-local message describing the failure.
+ *
+ * Data layout (all row-major, contiguous):
+ *   crow  int64[n + 1]   CSR row pointer, crow[0] == 0, crow[n] == nnz
+ *   col   int64[nnz]     column of each nonzero, 0 <= col < n (square graph)
+ *   val   float[nnz]     optional per-nonzero weight (NULL = unweighted)
+ *   x     float[n, f]    dense features; y float[n, f] output
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the AutoSAGE reference tree).
+ */
+#ifndef AUTOSAGE_HIP_H
+#define AUTOSAGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AS_ABI_VERSION 1
+
+typedef enum as_status {
+  AS_OK = 0,
+  AS_ERR_INVALID_ARGUMENT = 1,
+  AS_ERR_LAUNCH = 2,
+  AS_ERR_UNSUPPORTED = 3,
+  AS_ERR_WORKSPACE = 4
+} as_status;
+
+/* Hub-row strategy for as_spmm_csr_split_f32 (no reference counterpart; the
+ * reference always reassociates, csrc/spmm_hub.cu:40-47,81-90). */
+enum {
+  AS_HUB_EXACT = 0,   /* wave per hub row, edge order preserved: bit-exact   */
+  AS_HUB_SPLIT64 = 1  /* waves split the row's edges, fp64 partials reduced
+                         in LDS in wave order: deterministic, reassociated   */
+};
+
+/* Thread-local text of the last error (empty string when none). */
+const char* as_last_error(void);
+
+/* AS_ABI_VERSION of the loaded library. */
+int as_abi_version(void);
+
+/* Y = A·X over all rows.  Replaces autosage::spmm_csr_cuda
+ * (csrc/spmm_csr_vec4.cu:97-176) behind the op
+ * `spmm_csr(Tensor crow, Tensor col, Tensor? val, Tensor x) -> Tensor`
+ * (csrc/spmm_binding.cpp:66).  `vec4` != 0 allows float4 lanes (the
+ * reference's AUTOSAGE_VEC4 switch, csrc/spmm_csr_vec4.cu:135-148).
+ * Per output element the sum runs in CSR edge order with fmaf, so the result
+ * is bit-identical to the sequential CPU CSR product. */
+int as_spmm_csr_f32(const int64_t* crow, const int64_t* col, const float* val,
+                    const float* x, float* y, int64_t n, int64_t nnz,
+                    int64_t f, int vec4, void* stream);
+
+/* Bytes of workspace as_bin_rows_by_degree needs for n rows. */
+size_t as_bin_workspace_bytes(int64_t n);
+
+/* Degree binning of csrc/launcher_spmm.cu:49-59: rows with
+ * crow[r+1]-crow[r] >= threshold are heavy.  Writes order[0..H) = heavy rows
+ * ascending and order[H..n) = light rows ascending (the two at::nonzero lists
+ * concatenated), counts[0] = H, counts[1] = n - H.  threshold must be > 0. */
+int as_bin_rows_by_degree(const int64_t* crow, int64_t n, int64_t threshold,
+                          int32_t* order, int32_t* counts, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace as_spmm_csr_split_f32 needs for n rows. */
+size_t as_spmm_split_workspace_bytes(int64_t n);
+
+/* Degree-split SpMM.  Replaces autosage::spmm_csr_split_cuda
+ * (csrc/launcher_spmm.cu:22-72) behind the op
+ * `spmm_csr_split(Tensor crow, Tensor col, Tensor? val, Tensor x,
+ *  int feature_tile, int warps_per_block, int hub_threshold) -> Tensor`
+ * (csrc/spmm_binding.cpp:67-69, argument checks :49-52).
+ * feature_tile in {64,128}: features per pass of the light-row kernel;
+ * waves_per_block in {2,4,8}: waves per workgroup of the hub kernel;
+ * hub_threshold > 0: rows with degree >= it are hub rows;
+ * hub_mode: AS_HUB_EXACT or AS_HUB_SPLIT64. */
+int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col,
+                          const float* val, const float* x, float* y,
+                          int64_t n, int64_t nnz, int64_t f, int feature_tile,
+                          int waves_per_block, int64_t hub_threshold, int vec4,
+                          int hub_mode, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* out[e] = <query[row(e)], key[col[e]]> for every nonzero, CSR order.
+ * Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134), op schema :192.
+ * The dot product uses the reference kernel's summation order
+ * (32 lane-strided fma chains, then a 16/8/4/2/1 tree,
+ * csrc/sddmm_csr_op.cu:12-17,39-49). */
+int as_sddmm_csr_f32(const int64_t* crow, const int64_t* col,
+                     const float* query, const float* key, float* out,
+                     int64_t n, int64_t nnz, int64_t f, void* stream);
+
+/* Bytes of workspace as_sddmm_csr_split_f32 needs for n rows. */
+size_t as_sddmm_split_workspace_bytes(int64_t n);
+
+/* Degree-split SDDMM.  Replaces sddmm_csr_split
+ * (csrc/sddmm_csr_op.cu:136-187), op schema :193-195: rows with degree
+ * < hub_threshold go to the row kernel, the rest are cut into edge chunks
+ * spread over workgroups of waves_per_block waves.  Bit-identical to
+ * as_sddmm_csr_f32. */
+int as_sddmm_csr_split_f32(const int64_t* crow, const int64_t* col,
+                           const float* query, const float* key, float* out,
+                           int64_t n, int64_t nnz, int64_t f,
+                           int waves_per_block, int64_t hub_threshold,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Row softmax over CSR values: p_e = exp(s_e - max_row) / sum_row.
+ * Replaces the torch composition _csr_row_softmax (autosage/_auto.py:744-759). */
+int as_csr_row_softmax_f32(const int64_t* crow, const float* scores,
+                           float* probs, int64_t n, int64_t nnz, void* stream);
+
+/* Bytes of workspace as_csr_attention_f32 needs. */
+size_t as_csr_attention_workspace_bytes(int64_t n, int64_t nnz);
+
+/* Fused out = SpMM(softmax_row(scale * SDDMM(query, key)), value).
+ * Replaces csr_attention_forward (autosage/_auto.py:762-780), which runs the
+ * three stages separately and has no scale (scale = 1 reproduces it).
+ * Bit-identical to as_sddmm_csr_f32 -> as_csr_row_softmax_f32 ->
+ * as_spmm_csr_f32 when scale is 1 or a power of two. */
+int as_csr_attention_f32(const int64_t* crow, const int64_t* col,
+                         const float* query, const float* key,
+                         const float* value, float* out, int64_t n,
+                         int64_t nnz, int64_t f_qk, int64_t f_v, float scale,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AUTOSAGE_HIP_H */

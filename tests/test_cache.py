@@ -1,0 +1,116 @@
+"""Schedule keys and cache file (mirrors the reference tests/test_cache.py)."""
+
+from __future__ import annotations
+
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from autosage_amd._cache import ScheduleCache, cache_directory, device_signature, graph_signature, log_probe
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_cache_directory_is_resolved_at_call_time(tmp_path, monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    assert cache_directory() == tmp_path
+    cache = ScheduleCache()
+    device = {"type": "cpu", "torch": torch.__version__}
+    graph = {"operation": "spmm", "rows": 2}
+    result = {"choice": "baseline"}
+    cache.store(device, graph, result)
+    assert ScheduleCache().lookup(device, graph)["result"] == result
+    payload = json.loads((tmp_path / "schedules.json").read_text(encoding="utf-8"))
+    assert payload["schema_version"] == 1
+
+
+def test_graph_signature_preserves_large_integer_counts():
+    crow = torch.tensor([0, 1, 3, 3], dtype=torch.long)
+    col = torch.tensor([0, 1, 2], dtype=torch.long)
+    signature = graph_signature(crow, col, 64, "spmm")
+    assert signature["rows"] == 3
+    assert signature["nonzeros"] == 3
+    assert signature["operation"] == "spmm"
+    assert len(signature["structure_hash"]) == 24
+
+
+def test_graph_signature_separates_weighted_and_dtype_variants():
+    crow = torch.tensor([0, 1], dtype=torch.long)
+    col = torch.tensor([0], dtype=torch.long)
+    unweighted = graph_signature(crow, col, 64, "spmm", dtype=torch.float32)
+    weighted = graph_signature(crow, col, 64, "spmm", weighted=True, dtype=torch.float32)
+    double = graph_signature(crow, col, 64, "spmm", dtype=torch.float64)
+    assert unweighted != weighted
+    assert unweighted != double
+
+
+def test_structure_hash_closed_form():
+    # sha256 over little-endian int64 bytes of crow then col, each cut to its
+    # first and last 1024 entries when longer than 2048.
+    crow = torch.arange(0, 3001, dtype=torch.long)
+    col = torch.arange(3000, dtype=torch.long) % 7
+    h = hashlib.sha256()
+    for arr in (crow.numpy(), col.numpy()):
+        part = np.concatenate([arr[:1024], arr[-1024:]]) if arr.size > 2048 else arr
+        h.update(part.astype("<i8").tobytes())
+    assert graph_signature(crow, col, 8, "spmm")["structure_hash"] == h.hexdigest()[:24]
+
+
+def test_degree_quantiles_in_signature():
+    crow = torch.tensor([0, 1, 3, 3, 10], dtype=torch.long)  # degrees 1 2 0 7
+    sig = graph_signature(crow, torch.zeros(10, dtype=torch.long), 4, "sddmm")
+    # linear quantiles: q50 = 1.5 -> 2, q90 = 5.5 -> 6, q99 = 6.85 -> 7
+    assert (sig["degree_q50"], sig["degree_q90"], sig["degree_q99"]) == (2, 6, 7)
+
+
+def test_corrupt_or_foreign_cache_file_is_empty(tmp_path):
+    path = tmp_path / "schedules.json"
+    path.write_text("{not json")
+    assert ScheduleCache(path).lookup({}, {}) is None
+    path.write_text(json.dumps({"schema_version": 99, "records": {"x": 1}}))
+    assert ScheduleCache(path)._records == {}
+
+
+def test_store_is_atomic_and_sorted(tmp_path):
+    path = tmp_path / "schedules.json"
+    cache = ScheduleCache(path)
+    cache.store({"type": "cpu"}, {"rows": 1}, {"choice": "baseline"})
+    assert [p.name for p in tmp_path.iterdir()] == ["schedules.json"]
+    text = path.read_text()
+    assert text.endswith("\n")
+    key = json.dumps({"device": {"type": "cpu"}, "graph": {"rows": 1}}, sort_keys=True, separators=(",", ":"))
+    assert key in json.loads(text)["records"]
+
+
+def test_probe_log_can_be_disabled(tmp_path, monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    monkeypatch.setenv("AUTOSAGE_LOG_PROBES", "0")
+    log_probe({"a": 1})
+    assert not (tmp_path / "probe_logs.jsonl").exists()
+    monkeypatch.setenv("AUTOSAGE_LOG_PROBES", "1")
+    log_probe({"a": 1})
+    assert (tmp_path / "probe_logs.jsonl").read_text() == '{"a": 1}\n'
+
+
+def test_cpu_device_signature():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    assert device_signature() == {"type": "cpu", "torch": torch.__version__}
+
+
+def test_signatures_match_golden_vectors():
+    path = GOLDEN / "scheduler_golden.json"
+    if not path.exists():
+        pytest.skip("golden signature vectors not generated")
+    cases = json.loads(path.read_text())
+    for case in cases["signatures"]:
+        crow = torch.tensor(case["crow"], dtype=torch.long)
+        col = torch.tensor(case["col"], dtype=torch.long)
+        dtype = None if case["dtype"] is None else getattr(torch, case["dtype"].split(".")[-1])
+        got = graph_signature(crow, col, case["feature_width"], case["operation"], weighted=case["weighted"],
+                              dtype=dtype)
+        assert got == case["expected"], case["name"]

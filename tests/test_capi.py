@@ -1,0 +1,75 @@
+"""The C-ABI library: builds for gfx950, loads, and exports exactly what
+include/autosage_hip.h declares.  No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from autosage_amd import _native
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "autosage_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(as_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    path = _native.package_library_path()
+    if not path.exists():
+        pytest.skip("HIP library not built")
+    return _native.open_library(path)
+
+
+def test_header_declares_the_bound_symbols():
+    assert declared_functions() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_abi_version_and_empty_error(lib):
+    assert lib.as_abi_version() == _native.ABI_VERSION
+    assert lib.as_last_error() == b""
+
+
+def test_workspace_sizes_are_host_only_and_monotone(lib):
+    for fn in (lib.as_bin_workspace_bytes, lib.as_spmm_split_workspace_bytes, lib.as_sddmm_split_workspace_bytes):
+        sizes = [fn(n) for n in (0, 1, 1023, 1024, 10**6)]
+        assert all(s > 0 for s in sizes)
+        assert sizes == sorted(sizes)
+    assert lib.as_spmm_split_workspace_bytes(10**6) >= 4 * 10**6
+    assert lib.as_csr_attention_workspace_bytes(10, 1000) >= 4000
+
+
+def test_argument_errors_are_reported_without_a_launch(lib):
+    # Invalid arguments are rejected on the host before any HIP call.
+    status = lib.as_spmm_csr_split_f32(None, None, None, None, None, 4, 0, 8, 32, 4, 1, 1, 0, None, 0, None)
+    assert status == 1
+    assert lib.as_last_error() == b"feature_tile must be 64 or 128"
+    status = lib.as_spmm_csr_split_f32(None, None, None, None, None, 4, 0, 8, 64, 3, 1, 1, 0, None, 0, None)
+    assert lib.as_last_error() == b"warps_per_block must be 2, 4, or 8"
+    status = lib.as_bin_rows_by_degree(None, 4, 0, None, None, None, 0, None)
+    assert status == 1 and lib.as_last_error() == b"hub_threshold must be positive"
+    status = lib.as_sddmm_csr_split_f32(None, None, None, None, None, 4, 0, 8, 4, 0, None, 0, None)
+    assert lib.as_last_error() == b"hub_threshold must be a positive 32-bit integer"
+    # n == 0 is a no-op success
+    assert lib.as_spmm_csr_f32(None, None, None, None, None, 0, 0, 8, 1, None) == 0
+
+
+def test_library_targets_gfx950_only():
+    data = _native.package_library_path().read_bytes() if _native.package_library_path().exists() else b""
+    if not data:
+        pytest.skip("HIP library not built")
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"sm_"):
+        assert b"amdgcn-amd-amdhsa--" + other not in data

@@ -1,0 +1,177 @@
+"""GPU parity of the SpMM kernels against the CPU oracle.
+
+Bar: the order-preserving kernels (whole graph, split with exact hub rows)
+are bit-identical to the oracle's sequential fmaf product, which is itself
+bit-identical to torch.sparse.mm on the CPU (tests/test_oracle.py).  The
+reassociating split64 hub path is checked against the fp64 oracle:
+|gpu - fp64| <= 1e-6·|fp64| + 1e-9.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from autosage_amd import _native, synth
+from tests.gpu_common import bitwise_equal, case_graph, mismatch_report, require_gpu, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def _inputs(features, weighted, seed=0, rows=700, hubs=3, hub_degree=500):
+    crow, col = case_graph(rows, 9, seed=seed, hubs=hubs, hub_degree=hub_degree, empty=0.08)
+    rng = np.random.default_rng(seed + 100)
+    val = rng.standard_normal(col.size).astype(np.float32) if weighted else None
+    x = rng.standard_normal((rows, features)).astype(np.float32)
+    return crow, col, val, x
+
+
+@pytest.mark.parametrize("vec4", ["1", "0"])
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("features", [1, 3, 32, 64, 100, 128, 200, 256, 300])
+def test_spmm_csr_bitwise(features, weighted, vec4, monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_VEC4", vec4)
+    crow, col, val, x = _inputs(features, weighted, seed=features)
+    ref = oracle.spmm_seq(crow, col, val, x)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    got = torch.ops.autosage.spmm_csr(d_crow, d_col, d_val, d_x)
+    torch.cuda.synchronize()
+    assert bitwise_equal(got, ref), mismatch_report(got, ref)
+
+
+@pytest.mark.parametrize("vec4", ["1", "0"])
+@pytest.mark.parametrize("tile", [64, 128])
+@pytest.mark.parametrize("waves", [2, 4, 8])
+@pytest.mark.parametrize("threshold", [1, 10, 400, 10**6])
+def test_spmm_split_exact_bitwise(tile, waves, threshold, vec4, monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_VEC4", vec4)
+    monkeypatch.setenv("AUTOSAGE_HUB_MODE", "exact")
+    for features, weighted in ((64, False), (128, True), (256, False), (33, True)):
+        crow, col, val, x = _inputs(features, weighted, seed=threshold + features)
+        ref = oracle.spmm_seq(crow, col, val, x)
+        d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+        got = torch.ops.autosage.spmm_csr_split(d_crow, d_col, d_val, d_x, tile, waves, threshold)
+        torch.cuda.synchronize()
+        assert bitwise_equal(got, ref), (features, weighted, mismatch_report(got, ref))
+
+
+@pytest.mark.parametrize("waves", [2, 4, 8])
+@pytest.mark.parametrize("features,weighted", [(64, False), (128, True), (256, False), (45, True)])
+def test_spmm_split64_against_fp64(waves, features, weighted, monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_HUB_MODE", "split64")
+    crow, col, val, x = _inputs(features, weighted, seed=waves * 7 + features, hub_degree=650)
+    exact = oracle.spmm_f64(crow, col, val, x)
+    seq = oracle.spmm_seq(crow, col, val, x)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    got = torch.ops.autosage.spmm_csr_split(d_crow, d_col, d_val, d_x, 128, waves, 300).cpu().numpy()
+    assert np.all(np.abs(got - exact) <= 1e-6 * np.abs(exact) + 1e-9)
+    light = np.diff(crow) < 300
+    assert np.array_equal(got[light], seq[light])
+
+
+@pytest.mark.parametrize("threshold", [1, 2, 9, 500, 10**9])
+def test_bin_rows_bitwise(threshold):
+    crow, _ = case_graph(5000, 8, seed=threshold % 97, hubs=20, hub_degree=600, empty=0.05)
+    heavy_ref, light_ref = oracle.bin_rows(crow, threshold)
+    (d_crow,) = to_dev(crow)
+    heavy, light = _native.bin_rows_by_degree(d_crow, threshold)
+    assert np.array_equal(heavy.cpu().numpy(), heavy_ref)
+    assert np.array_equal(light.cpu().numpy(), light_ref)
+
+
+def test_bin_rows_many_tiles():
+    rng = np.random.default_rng(3)
+    deg = rng.integers(0, 40, size=300_001)
+    crow = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    heavy_ref, light_ref = oracle.bin_rows(crow, 20)
+    (d_crow,) = to_dev(crow)
+    heavy, light = _native.bin_rows_by_degree(d_crow, 20)
+    assert np.array_equal(heavy.cpu().numpy(), heavy_ref)
+    assert np.array_equal(light.cpu().numpy(), light_ref)
+
+
+def test_config1_bitwise_against_oracle_and_torch_cpu():
+    w = synth.config1(seed=0)
+    x = w.dense["x"]
+    ref = oracle.spmm_seq(w.crow, w.col, None, x)
+    cpu = oracle.torch_cpu_spmm(torch.from_numpy(w.crow), torch.from_numpy(w.col), None, torch.from_numpy(x))
+    assert np.array_equal(ref, cpu.numpy())
+    d_crow, d_col, d_x = to_dev(w.crow, w.col, x)
+    assert bitwise_equal(torch.ops.autosage.spmm_csr(d_crow, d_col, None, d_x), ref)
+    for cand in ((64, 2, 9), (64, 8, 12), (128, 4, 10)):
+        got = torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, *cand)
+        assert bitwise_equal(got, ref), cand
+
+
+def test_degenerate_shapes():
+    # no nonzeros: zero output; single row; zero features
+    crow = np.zeros(5, dtype=np.int64)
+    col = np.zeros(0, dtype=np.int64)
+    x = np.ones((4, 8), dtype=np.float32)
+    d_crow, d_col, d_x = to_dev(crow, col, x)
+    y = torch.ops.autosage.spmm_csr(d_crow, d_col, None, d_x)
+    assert torch.count_nonzero(y).item() == 0
+    y = torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, 64, 4, 1)
+    assert torch.count_nonzero(y).item() == 0
+    d_crow, d_col, d_x = to_dev(np.array([0, 1]), np.array([0]), np.array([[2.5, -1.0]], dtype=np.float32))
+    assert torch.equal(torch.ops.autosage.spmm_csr(d_crow, d_col, None, d_x).cpu(), torch.tensor([[2.5, -1.0]]))
+    empty_x = torch.empty((1, 0), device="cuda")
+    assert torch.ops.autosage.spmm_csr(d_crow, d_col, None, empty_x).shape == (1, 0)
+
+
+def test_input_checks_raise_runtime_error():
+    d_crow, d_col, d_x = to_dev(np.array([0, 1]), np.array([0]), np.ones((1, 4), dtype=np.float32))
+    with pytest.raises(RuntimeError, match="feature_tile must be 64 or 128"):
+        torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, 32, 4, 1)
+    with pytest.raises(RuntimeError, match="warps_per_block must be 2, 4, or 8"):
+        torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, 64, 3, 1)
+    with pytest.raises(RuntimeError, match="hub_threshold must be positive"):
+        torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, 64, 4, 0)
+    with pytest.raises(RuntimeError, match="crow must contain N \\+ 1 entries"):
+        torch.ops.autosage.spmm_csr(d_crow[:1], d_col, None, d_x)
+    with pytest.raises(RuntimeError, match="x must be contiguous"):
+        torch.ops.autosage.spmm_csr(d_crow, d_col, None, torch.ones((4, 1), device="cuda").t())
+
+
+# Reference tests/test_cuda.py:32-57 at the reference tolerance, against
+# PyTorch-ROCm's CSR product on the GPU.
+def _random_csr_ref_style(rows, degree, seed=0):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    counts = torch.randint(0, 2 * degree + 1, (rows,), generator=g, device="cuda")
+    crow = torch.cat((torch.zeros(1, device="cuda", dtype=torch.long), counts.cumsum(0)))
+    col = torch.randint(0, rows, (int(crow[-1].item()),), generator=g, device="cuda")
+    return crow, col
+
+
+@pytest.mark.parametrize("features", [32, 64, 113, 128, 256])
+def test_spmm_native_matches_torch(features):
+    crow, col = _random_csr_ref_style(256, 12)
+    x = torch.randn(256, features, device="cuda")
+    values = torch.rand(col.numel(), device="cuda")
+    expected = torch.sparse.mm(torch.sparse_csr_tensor(crow, col, values, size=(256, 256)), x)
+    actual = torch.ops.autosage.spmm_csr(crow, col, values, x)
+    assert torch.allclose(actual, expected, rtol=1e-4, atol=3e-3)
+    ref = oracle.spmm_seq(crow.cpu(), col.cpu(), values.cpu(), x.cpu())
+    assert bitwise_equal(actual, ref)
+
+
+def test_split_matches_torch_on_hub_graph():
+    rows = 512
+    counts = torch.full((rows,), 8, device="cuda", dtype=torch.long)
+    counts[0] = 400
+    crow = torch.cat((torch.zeros(1, device="cuda", dtype=torch.long), counts.cumsum(0)))
+    col = torch.randint(0, rows, (int(crow[-1].item()),), device="cuda")
+    x = torch.randn(rows, 128, device="cuda")
+    matrix = torch.sparse_csr_tensor(crow, col, torch.ones(col.numel(), device="cuda"), size=(rows, rows))
+    expected = torch.sparse.mm(matrix, x)
+    actual = torch.ops.autosage.spmm_csr_split(crow, col, None, x, 128, 8, 128)
+    assert torch.allclose(actual, expected, rtol=1e-4, atol=3e-3)
+    assert bitwise_equal(actual, oracle.spmm_seq(crow.cpu(), col.cpu(), None, x.cpu()))

@@ -1,0 +1,233 @@
+"""Pins the CPU oracle (oracle/) against independent references.
+
+Each oracle function is checked against something that does not share its
+code: PyTorch's own CSR product (the reference CPU path), brute-force dense
+products in float64, reference known answers, numpy restatements and
+closed forms — chosen so that a dropped term, a wrong index or a transposed
+operand fails at least one check.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from autosage_amd import synth
+
+
+def _graph(rows, degree, seed, hubs=0, hub_degree=0, empty=0.0):
+    crow, col = synth.random_csr(rows, degree, seed=seed, hub_rows=hubs, hub_degree=hub_degree,
+                                 empty_fraction=empty)
+    return crow, col
+
+
+def _dense(crow, col, val, n):
+    a = np.zeros((n, n), dtype=np.float64)
+    for r in range(n):
+        for e in range(crow[r], crow[r + 1]):
+            a[r, col[e]] += 1.0 if val is None else float(val[e])
+    return a
+
+
+# --- SpMM -------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("features", [1, 7, 64, 128])
+def test_spmm_seq_is_bit_identical_to_torch_cpu(weighted, features):
+    crow, col = _graph(300, 9, seed=features, hubs=2, hub_degree=250, empty=0.1)
+    rng = np.random.default_rng(1)
+    val = rng.standard_normal(col.size).astype(np.float32) if weighted else None
+    x = rng.standard_normal((300, features)).astype(np.float32)
+    expect = oracle.torch_cpu_spmm(torch.from_numpy(crow), torch.from_numpy(col),
+                                   None if val is None else torch.from_numpy(val), torch.from_numpy(x))
+    got = oracle.spmm_seq(crow, col, val, x)
+    assert np.array_equal(got, expect.numpy())
+
+
+@pytest.mark.parametrize("threads", [1, 4])
+def test_spmm_seq_matches_torch_cpu_across_thread_counts(threads):
+    old = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        crow, col = _graph(2000, 30, seed=5, hubs=3, hub_degree=1500)
+        x = np.random.default_rng(2).standard_normal((2000, 64)).astype(np.float32)
+        val = np.random.default_rng(3).random(col.size).astype(np.float32)
+        expect = oracle.torch_cpu_spmm(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(val),
+                                       torch.from_numpy(x))
+        assert np.array_equal(oracle.spmm_seq(crow, col, val, x), expect.numpy())
+    finally:
+        torch.set_num_threads(old)
+
+
+def test_spmm_reference_known_answers():
+    # reference tests/test_cpu.py:25-32 (weights and an empty row)
+    crow = np.array([0, 2, 2, 3])
+    col = np.array([1, 2, 0])
+    val = np.array([0.5, 2.0, -1.0], dtype=np.float32)
+    x = np.array([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], dtype=np.float32)
+    assert np.array_equal(oracle.spmm_seq(crow, col, val, x), [[11.5, 14.0], [0.0, 0.0], [-1.0, -2.0]])
+    # reference tests/test_cpu.py:16-22 (destination rows)
+    crow, col = oracle.numpy_edge_index_to_csr(np.array([[0, 1, 2, 3], [1, 2, 3, 0]]), 4)
+    x = np.arange(12, dtype=np.float32).reshape(4, 3)
+    y = oracle.spmm_seq(crow, col, None, x)
+    assert np.array_equal(y[0], x[3]) and np.array_equal(y[1], x[0])
+
+
+def test_spmm_order_is_sequential_not_pairwise():
+    # 1e8 followed by eight 1s: a left-to-right fp32 chain keeps 1e8 (each +1
+    # is below half an ulp), a pairwise or reassociated sum gives 1e8 + 8.
+    crow = np.array([0, 9, 9])
+    col = np.array([0] + [1] * 8)
+    x = np.array([[1e8], [1.0]], dtype=np.float32)
+    got = oracle.spmm_seq(crow, col, None, x)
+    assert got[0, 0] == np.float32(1e8)
+    assert np.float32(1e8) + np.float32(8.0) != np.float32(1e8)
+    expect = oracle.torch_cpu_spmm(torch.from_numpy(crow), torch.from_numpy(col), None, torch.from_numpy(x))
+    assert np.array_equal(got, expect.numpy())
+
+
+def test_spmm_f64_matches_dense_brute_force():
+    crow, col = _graph(40, 6, seed=11, hubs=1, hub_degree=30)
+    rng = np.random.default_rng(4)
+    val = rng.standard_normal(col.size).astype(np.float32)
+    x = rng.standard_normal((40, 5)).astype(np.float32)
+    expect = _dense(crow, col, val, 40) @ x.astype(np.float64)
+    assert np.allclose(oracle.spmm_f64(crow, col, val, x), expect, rtol=1e-13, atol=1e-13)
+    rows = np.array([3, 0, 39])
+    assert np.allclose(oracle.spmm_f64(crow, col, val, x, rows=rows), expect[rows], rtol=1e-13, atol=1e-13)
+
+
+def test_spmm_seq_row_subset_matches_full():
+    crow, col = _graph(500, 12, seed=9)
+    x = np.random.default_rng(0).standard_normal((500, 33)).astype(np.float32)
+    full = oracle.spmm_seq(crow, col, None, x)
+    rows = np.array([499, 0, 17, 17, 250])
+    assert np.array_equal(oracle.spmm_seq(crow, col, None, x, rows=rows), full[rows])
+
+
+# --- binning ------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("threshold", [1, 2, 9, 100, 10**9])
+def test_bin_rows_matches_flatnonzero(threshold):
+    crow, _ = _graph(1000, 8, seed=3, hubs=5, hub_degree=120, empty=0.05)
+    deg = np.diff(crow)
+    heavy, light = oracle.bin_rows(crow, threshold)
+    assert np.array_equal(heavy, np.flatnonzero(deg >= threshold).astype(np.int32))
+    assert np.array_equal(light, np.flatnonzero(deg < threshold).astype(np.int32))
+
+
+def test_bin_rows_known_answer():
+    crow = np.array([0, 3, 3, 10, 11, 16])  # degrees 3 0 7 1 5
+    heavy, light = oracle.bin_rows(crow, 3)
+    assert heavy.tolist() == [0, 2, 4] and light.tolist() == [1, 3]
+
+
+# --- SDDMM --------------------------------------------------------------------
+
+
+def test_sddmm_reference_known_answer():
+    # reference tests/test_cpu.py:45-53
+    crow = np.array([0, 2, 3])
+    col = np.array([0, 1, 0])
+    q = np.array([[1.0, 2.0], [3.0, 4.0]], dtype=np.float32)
+    k = np.array([[2.0, 1.0], [1.0, 3.0]], dtype=np.float32)
+    assert oracle.sddmm_ref(crow, col, q, k).tolist() == [4.0, 7.0, 10.0]
+
+
+@pytest.mark.parametrize("features", [1, 17, 32, 64, 100, 128, 256])
+def test_sddmm_ref_against_fp64_and_gather_dot(features):
+    crow, col = _graph(200, 7, seed=features, hubs=2, hub_degree=150)
+    rng = np.random.default_rng(features)
+    q = rng.standard_normal((200, features)).astype(np.float32)
+    k = rng.standard_normal((200, features)).astype(np.float32)
+    got = oracle.sddmm_ref(crow, col, q, k)
+    exact = oracle.sddmm_f64(crow, col, q, k)
+    rows = np.repeat(np.arange(200), np.diff(crow))
+    bound = 2 * features * np.finfo(np.float32).eps * (np.abs(q[rows]) * np.abs(k[col])).sum(1)
+    assert np.all(np.abs(got - exact) <= bound + 1e-30)
+    gd = oracle.torch_gather_dot(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(q),
+                                 torch.from_numpy(k)).numpy()
+    assert np.all(np.abs(got - gd) <= 2 * bound + 1e-30)
+
+
+def test_sddmm_f64_matches_brute_force():
+    crow, col = _graph(30, 5, seed=1)
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((30, 9)).astype(np.float32)
+    k = rng.standard_normal((30, 9)).astype(np.float32)
+    rows = np.repeat(np.arange(30), np.diff(crow))
+    expect = np.einsum("ef,ef->e", q[rows].astype(np.float64), k[col].astype(np.float64))
+    assert np.allclose(oracle.sddmm_f64(crow, col, q, k), expect, rtol=1e-14, atol=1e-14)
+
+
+def test_sddmm_tree_order_differs_from_sequential():
+    # Feature 0 carries a large value and features 1..32 small ones: the
+    # reference order adds partial 0 (q0k0 + q32k32) last in its tree, so the
+    # result differs from a left-to-right fp32 sum; the oracle must give the
+    # tree value.
+    f = 33
+    q = np.ones((1, f), dtype=np.float32)
+    k = np.full((1, f), 2.0 ** -24, dtype=np.float32)
+    k[0, 0] = 1.0
+    crow, col = np.array([0, 1]), np.array([0])
+    got = oracle.sddmm_ref(crow, col, q, k)[0]
+    # partials: p0 = 1 + 2^-24 -> 1 (rounds to even), p1..p31 = 2^-24; tree of
+    # p1..p31 is exact (31·2^-24) and added to p0 in the final steps.
+    seq = np.float32(0)
+    for j in range(f):
+        seq = np.float32(seq + q[0, j] * k[0, j])
+    p = [np.float32(1.0)] + [np.float32(2.0 ** -24)] * 31
+    for o in (16, 8, 4, 2, 1):
+        for lane in range(o):
+            p[lane] = np.float32(p[lane] + p[lane + o])
+    assert got == p[0]
+    assert got != seq
+
+
+# --- softmax / attention --------------------------------------------------------
+
+
+def test_row_softmax_known_answers():
+    crow = np.array([0, 2, 3, 3])
+    s = np.array([4.0, 7.0, 10.0], dtype=np.float32)
+    p = oracle.row_softmax(crow, s)
+    assert abs(p[:2].sum() - 1.0) < 1e-7
+    assert p[2] == 1.0
+    assert np.isclose(p[1] / p[0], np.exp(3.0), rtol=1e-6)
+
+
+def test_row_softmax_against_torch_and_fp64():
+    crow, col = _graph(400, 10, seed=21, hubs=3, hub_degree=300, empty=0.1)
+    s = (np.random.default_rng(5).standard_normal(col.size) * 4).astype(np.float32)
+    got = oracle.row_softmax(crow, s)
+    ref = oracle.torch_row_softmax(torch.from_numpy(crow), torch.from_numpy(s)).numpy()
+    exact = oracle.row_softmax_f64(crow, s.astype(np.float64))
+    assert np.allclose(got, ref, rtol=2e-6, atol=1e-9)
+    assert np.allclose(got, exact, rtol=2e-6, atol=1e-9)
+    sums = np.add.reduceat(got, crow[:-1][np.diff(crow) > 0])
+    assert np.allclose(sums, 1.0, atol=1e-5)
+
+
+def test_attention_composition_against_fp64():
+    crow, col = _graph(120, 6, seed=2, hubs=1, hub_degree=100)
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((120, 64)).astype(np.float32)
+    k = rng.standard_normal((120, 64)).astype(np.float32)
+    v = rng.standard_normal((120, 32)).astype(np.float32)
+    got = oracle.attention_ref(crow, col, q, k, v, scale=0.125)
+    exact = oracle.attention_f64(crow, col, q, k, v, scale=0.125)
+    assert np.allclose(got, exact, rtol=1e-4, atol=1e-5)
+
+
+def test_edge_index_to_csr_restatement_matches_package():
+    from autosage_amd.utils.csr import edge_index_to_csr
+
+    rng = np.random.default_rng(0)
+    ei = rng.integers(0, 50, size=(2, 400))
+    crow, col = oracle.numpy_edge_index_to_csr(ei, 50)
+    t_crow, t_col = edge_index_to_csr(torch.from_numpy(ei), 50)
+    assert np.array_equal(crow, t_crow.numpy()) and np.array_equal(col, t_col.numpy())

@@ -1,0 +1,107 @@
+"""Scheduler configuration and candidate shortlist (mirrors the reference
+tests/test_scheduler.py, plus exact-order checks)."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import pytest
+import torch
+
+from autosage_amd._auto import _degree_quantiles, _spmm_candidates
+from autosage_amd.config import SchedulerConfig
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_candidates_only_contain_effective_parameters():
+    crow = torch.tensor([0, 1, 3, 3, 10], dtype=torch.long)
+    candidates = _spmm_candidates(crow, 64, SchedulerConfig(candidate_count=18))
+    assert candidates
+    assert len(candidates) == len(set(candidates))
+    assert all(tile in {64, 128} for tile, _, _ in candidates)
+    assert all(warps in {2, 4, 8} for _, warps, _ in candidates)
+    assert all(threshold > 0 for _, _, threshold in candidates)
+
+
+def test_environment_overrides_are_read_for_each_configuration(monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_FTILE", "64")
+    monkeypatch.setenv("AUTOSAGE_WPB", "8")
+    monkeypatch.setenv("AUTOSAGE_HUB_T", "16")
+    first = SchedulerConfig.from_env()
+    monkeypatch.setenv("AUTOSAGE_HUB_T", "32")
+    second = SchedulerConfig.from_env()
+    assert first.hub_threshold == 16
+    assert second.hub_threshold == 32
+
+
+def test_tuning_signature_tracks_kernel_policy(monkeypatch):
+    first = SchedulerConfig.from_env().tuning_signature()
+    monkeypatch.setenv("AUTOSAGE_VEC4", "false")
+    second = SchedulerConfig.from_env().tuning_signature()
+    assert first["vec4"] is True
+    assert second["vec4"] is False
+    assert first != second
+
+
+def test_hub_mode_is_part_of_the_signature(monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_HUB_MODE", "split64")
+    assert SchedulerConfig.from_env().tuning_signature()["hub_mode"] == "split64"
+    monkeypatch.setenv("AUTOSAGE_HUB_MODE", "bogus")
+    with pytest.raises(ValueError, match="hub_mode"):
+        SchedulerConfig.from_env()
+
+
+@pytest.mark.parametrize(
+    "kwargs, message",
+    [
+        ({"guardrail": 0.0}, "guardrail"),
+        ({"probe_fraction": 1.5}, "probe_fraction"),
+        ({"probe_iterations": 0}, "positive"),
+        ({"probe_cap_ms": -1.0}, "negative"),
+        ({"feature_tile": 32}, "feature_tile"),
+        ({"warps_per_block": 3}, "warps_per_block"),
+        ({"hub_threshold": 0}, "hub_threshold"),
+    ],
+)
+def test_invalid_configuration_is_rejected(kwargs, message):
+    with pytest.raises(ValueError, match=message):
+        SchedulerConfig(**kwargs)
+
+
+def test_bad_boolean_environment_value(monkeypatch):
+    monkeypatch.setenv("AUTOSAGE_VEC4", "maybe")
+    with pytest.raises(ValueError, match="AUTOSAGE_VEC4 must be a boolean value"):
+        SchedulerConfig.from_env()
+
+
+def test_candidate_order_closed_form():
+    # degrees 1, 2, 0, 7: q90/q95/q99 (linear) = 5.5/6.25/6.85 -> 6, 6, 7;
+    # q50 = 1.5 -> 2 (half to even); skew 7/2 = 3.5 -> preferred waves 4;
+    # F = 64 -> preferred tile 64; preferred threshold 6.
+    crow = torch.tensor([0, 1, 3, 3, 10], dtype=torch.long)
+    assert _degree_quantiles(crow) == (6, 6, 7)
+    got = _spmm_candidates(crow, 64, SchedulerConfig(candidate_count=18))
+    want_tile, want_waves, want_thr = 64, 4, 6
+
+    def dist(c):
+        return abs(c[0] - want_tile) / 64 + abs(c[1] - want_waves) / 6 + abs(c[2] - want_thr) / want_thr
+
+    brute = sorted(
+        ((t, w, h) for t in (64, 128) for w in (2, 4, 8) for h in (6, 7)), key=lambda c: (dist(c), c)
+    )
+    assert got == brute
+    assert got[0] == (64, 4, 6)
+
+
+def test_candidates_match_golden_vectors():
+    path = GOLDEN / "scheduler_golden.json"
+    if not path.exists():
+        pytest.skip("golden scheduler vectors not generated")
+    cases = json.loads(path.read_text())
+    for case in cases["candidates"]:
+        crow = torch.tensor(case["crow"], dtype=torch.long)
+        config = SchedulerConfig(candidate_count=case["k"])
+        got = [list(c) for c in _spmm_candidates(crow, case["feature_width"], config)]
+        assert got == case["expected"], case["name"]
