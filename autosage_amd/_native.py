@@ -265,7 +265,7 @@ def csr_row_softmax_impl(crow, scores):
     return probs
 
 
-def csr_attention_impl(crow, col, query, key, value, scale):
+def csr_attention_impl(crow, col, query, key, value, scale=1.0):
     check_sddmm_inputs(crow, col, query, key)
     _check(value.is_cuda and value.device == query.device, "value must be on the same CUDA device as query")
     _check(value.dtype == torch.float32 and value.dim() == 2 and value.is_contiguous(),

@@ -31,11 +31,14 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 constexpr int kBinRowsPerThread = 4;
 constexpr int kBinTile = kBlock * kBinRowsPerThread;
 inline int64_t bin_tiles(int64_t n) { return (n + kBinTile - 1) / kBinTile; }
+constexpr int kMaxHeavyBuckets = 8;
 size_t bin_workspace_bytes(int64_t n);
-// order[n], counts[4] (counts[0]=heavy, counts[1]=light, counts[2..3] free
-// for callers) are written; workspace holds per-tile counts and offsets.
+// Writes order[n] = heavy rows (in `buckets` degree buckets, longest bucket
+// first, ascending inside a bucket) then light rows ascending, and
+// counts[0] = heavy, counts[1] = light (counts[2..3] are left to callers).
+// The workspace holds the per-tile bin table and offsets.
 int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold,
-                    int32_t* order, int32_t* counts, void* workspace,
-                    hipStream_t stream);
+                    int buckets, int32_t* order, int32_t* counts,
+                    void* workspace, hipStream_t stream);
 
 }  // namespace as

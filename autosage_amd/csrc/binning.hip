@@ -1,14 +1,22 @@
-// Degree binning: stable partition of the rows into heavy (degree >= T) and
-// light rows, both ascending — the integer work of the reference split
-// launcher (csrc/launcher_spmm.cu:13-18 degrees, :49-59 nonzero lists),
-// done on the device without a host synchronisation.
+// Degree binning on the device, without a host synchronisation.
 //
-// Three small kernels over tiles of kBinTile rows:
-//   count   — heavy rows per tile;
-//   scan    — one workgroup turns tile counts into tile offsets and writes
-//             counts[0] = H, counts[1] = n - H;
-//   scatter — each row goes to order[heavy_before(r)] if heavy, else to
-//             order[H + r - heavy_before(r)].
+// Reference integer work: csrc/launcher_spmm.cu:13-18 (degrees) and :49-59
+// (heavy = degree >= T, heavy and light row lists ascending via at::nonzero).
+//
+// Generalised to K heavy buckets (1 <= K <= kMaxHeavyBuckets): a heavy row of
+// degree d goes to bucket K-1-min(K-1, floor(log2(d / T))), so bucket 0 holds
+// the longest rows.  The output is one permutation
+//   order = [bucket 0 rows, ..., bucket K-1 rows, light rows]
+// with each group ascending by row id, plus counts[0] = H (heavy rows) and
+// counts[1] = n - H.  With K = 1 this is exactly the reference's heavy list
+// followed by its light list.
+//
+// Three kernels over tiles of kBinTile rows:
+//   hist    — per-tile count of every bin (bin-major table);
+//   scan    — one workgroup: exclusive prefix over the bin-major table, which
+//             yields each (bin, tile) output offset; writes counts[];
+//   scatter — each row is written at its (bin, tile) offset plus its rank
+//             among the tile's earlier rows of the same bin.
 #include "as_device.h"
 #include "as_internal.h"
 
@@ -16,9 +24,16 @@ namespace as {
 
 namespace {
 
-// Exclusive prefix sum over a workgroup of up to 1024 threads.
-// `lds` needs blockDim.x / 64 ints.  Returns the exclusive prefix; *total
-// receives the workgroup sum.
+__device__ __forceinline__ int bin_of(int64_t deg, int64_t threshold, int buckets) {
+  if (deg < threshold) return buckets;  // light
+  const uint64_t q = static_cast<uint64_t>(deg / threshold);  // >= 1
+  int level = 63 - __clzll(static_cast<long long>(q));
+  if (level > buckets - 1) level = buckets - 1;
+  return buckets - 1 - level;
+}
+
+// Exclusive prefix sum over a workgroup of up to 1024 threads; `lds` needs
+// blockDim.x / 64 ints; *total receives the workgroup sum.
 __device__ __forceinline__ int block_excl_scan(int v, int* lds, int* total) {
   const int lane = lane_id();
   const int wave = wave_in_block();
@@ -38,78 +53,82 @@ __device__ __forceinline__ int block_excl_scan(int v, int* lds, int* total) {
   return before + incl - v;
 }
 
-__device__ __forceinline__ int heavy_flags(const int64_t* __restrict__ crow, int64_t n,
-                                           int64_t threshold, int64_t first, bool (&flag)[kBinRowsPerThread]) {
-  int count = 0;
+__device__ __forceinline__ void row_bins(const int64_t* __restrict__ crow, int64_t n, int64_t threshold,
+                                         int buckets, int64_t first, int (&bin)[kBinRowsPerThread]) {
 #pragma unroll
   for (int i = 0; i < kBinRowsPerThread; ++i) {
     const int64_t r = first + i;
-    flag[i] = false;
-    if (r < n) flag[i] = (crow[r + 1] - crow[r]) >= threshold;
-    count += flag[i] ? 1 : 0;
+    bin[i] = r < n ? bin_of(crow[r + 1] - crow[r], threshold, buckets) : -1;
   }
-  return count;
 }
 
-__global__ __launch_bounds__(kBlock) void bin_count_kernel(const int64_t* __restrict__ crow, int64_t n,
-                                                           int64_t threshold,
-                                                           int32_t* __restrict__ tile_counts) {
+__global__ __launch_bounds__(kBlock) void bin_hist_kernel(const int64_t* __restrict__ crow, int64_t n,
+                                                          int64_t threshold, int buckets, int64_t tiles,
+                                                          int32_t* __restrict__ table) {
   __shared__ int lds[kBlock / kWave];
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kBinTile + threadIdx.x * kBinRowsPerThread;
-  bool flag[kBinRowsPerThread];
-  const int count = heavy_flags(crow, n, threshold, first, flag);
-  int total = 0;
-  block_excl_scan(count, lds, &total);
-  if (threadIdx.x == 0) tile_counts[blockIdx.x] = total;
+  int bin[kBinRowsPerThread];
+  row_bins(crow, n, threshold, buckets, first, bin);
+  for (int b = 0; b <= buckets; ++b) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < kBinRowsPerThread; ++i) c += bin[i] == b ? 1 : 0;
+    int total = 0;
+    block_excl_scan(c, lds, &total);
+    if (threadIdx.x == 0) table[b * tiles + blockIdx.x] = total;
+  }
 }
 
 constexpr int kScanThreads = 1024;
 
-__global__ __launch_bounds__(kScanThreads) void bin_scan_kernel(const int32_t* __restrict__ tile_counts,
-                                                                int64_t tiles, int64_t n,
-                                                                int32_t* __restrict__ tile_offsets,
+__global__ __launch_bounds__(kScanThreads) void bin_scan_kernel(const int32_t* __restrict__ table, int64_t entries,
+                                                                int64_t heavy_entries, int64_t n,
+                                                                int32_t* __restrict__ offsets,
                                                                 int32_t* __restrict__ counts) {
   __shared__ int lds[kScanThreads / kWave];
-  const int64_t per = (tiles + kScanThreads - 1) / kScanThreads;
+  __shared__ int heavy_part[kScanThreads / kWave];
+  const int64_t per = (entries + kScanThreads - 1) / kScanThreads;
   const int64_t begin = static_cast<int64_t>(threadIdx.x) * per;
-  const int64_t end = begin + per < tiles ? begin + per : tiles;
+  const int64_t end = begin + per < entries ? begin + per : entries;
   int local = 0;
-  for (int64_t t = begin; t < end; ++t) local += tile_counts[t];
+  int local_heavy = 0;
+  for (int64_t t = begin; t < end; ++t) {
+    local += table[t];
+    if (t < heavy_entries) local_heavy += table[t];
+  }
   int total = 0;
   int running = block_excl_scan(local, lds, &total);
   for (int64_t t = begin; t < end; ++t) {
-    tile_offsets[t] = running;
-    running += tile_counts[t];
+    offsets[t] = running;
+    running += table[t];
   }
+  int heavy_total = 0;
+  block_excl_scan(local_heavy, heavy_part, &heavy_total);
   if (threadIdx.x == 0) {
-    counts[0] = total;
-    counts[1] = static_cast<int32_t>(n - total);
+    counts[0] = heavy_total;
+    counts[1] = static_cast<int32_t>(n - heavy_total);
   }
 }
 
 __global__ __launch_bounds__(kBlock) void bin_scatter_kernel(const int64_t* __restrict__ crow, int64_t n,
-                                                             int64_t threshold,
-                                                             const int32_t* __restrict__ tile_offsets,
-                                                             const int32_t* __restrict__ counts,
+                                                             int64_t threshold, int buckets, int64_t tiles,
+                                                             const int32_t* __restrict__ offsets,
                                                              int32_t* __restrict__ order) {
   __shared__ int lds[kBlock / kWave];
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kBinTile + threadIdx.x * kBinRowsPerThread;
-  bool flag[kBinRowsPerThread];
-  const int count = heavy_flags(crow, n, threshold, first, flag);
-  int total = 0;
-  const int excl = block_excl_scan(count, lds, &total);
-  const int64_t heavy_total = counts[0];
-  int64_t heavy_before = static_cast<int64_t>(tile_offsets[blockIdx.x]) + excl;
+  int bin[kBinRowsPerThread];
+  row_bins(crow, n, threshold, buckets, first, bin);
+  for (int b = 0; b <= buckets; ++b) {
+    int c = 0;
 #pragma unroll
-  for (int i = 0; i < kBinRowsPerThread; ++i) {
-    const int64_t r = first + i;
-    if (r < n) {
-      if (flag[i]) {
-        order[heavy_before] = static_cast<int32_t>(r);
-        ++heavy_before;
-      } else {
-        order[heavy_total + (r - heavy_before)] = static_cast<int32_t>(r);
-      }
+    for (int i = 0; i < kBinRowsPerThread; ++i) c += bin[i] == b ? 1 : 0;
+    int total = 0;
+    const int excl = block_excl_scan(c, lds, &total);
+    if (total == 0) continue;  // workgroup-uniform
+    int64_t pos = static_cast<int64_t>(offsets[b * tiles + blockIdx.x]) + excl;
+#pragma unroll
+    for (int i = 0; i < kBinRowsPerThread; ++i) {
+      if (bin[i] == b) order[pos++] = static_cast<int32_t>(first + i);
     }
   }
 }
@@ -117,25 +136,27 @@ __global__ __launch_bounds__(kBlock) void bin_scatter_kernel(const int64_t* __re
 }  // namespace
 
 size_t bin_workspace_bytes(int64_t n) {
-  const int64_t tiles = bin_tiles(n);
-  return 2 * align_up(static_cast<size_t>(tiles > 0 ? tiles : 1) * sizeof(int32_t), 256);
+  const int64_t tiles = bin_tiles(n) > 0 ? bin_tiles(n) : 1;
+  return 2 * align_up(static_cast<size_t>(tiles) * (kMaxHeavyBuckets + 1) * sizeof(int32_t), 256);
 }
 
-int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold, int32_t* order, int32_t* counts,
+int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold, int buckets, int32_t* order, int32_t* counts,
                     void* workspace, hipStream_t stream) {
+  if (buckets < 1 || buckets > kMaxHeavyBuckets) return fail(AS_ERR_INVALID_ARGUMENT, "bad bucket count %d", buckets);
   const int64_t tiles = bin_tiles(n);
-  int32_t* tile_counts = static_cast<int32_t*>(workspace);
-  int32_t* tile_offsets = reinterpret_cast<int32_t*>(
-      static_cast<char*>(workspace) + align_up(static_cast<size_t>(tiles > 0 ? tiles : 1) * sizeof(int32_t), 256));
+  const size_t half = bin_workspace_bytes(n) / 2;
+  int32_t* table = static_cast<int32_t*>(workspace);
+  int32_t* offsets = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + half);
+  const int64_t entries = (buckets + 1) * tiles;
   if (tiles > 0) {
-    hipLaunchKernelGGL(bin_count_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kBlock), 0, stream, crow, n,
-                       threshold, tile_counts);
+    hipLaunchKernelGGL(bin_hist_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kBlock), 0, stream, crow, n,
+                       threshold, buckets, tiles, table);
   }
-  hipLaunchKernelGGL(bin_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, tile_counts, tiles, n, tile_offsets,
-                     counts);
+  hipLaunchKernelGGL(bin_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, table, entries, buckets * tiles, n,
+                     offsets, counts);
   if (tiles > 0) {
     hipLaunchKernelGGL(bin_scatter_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kBlock), 0, stream, crow, n,
-                       threshold, tile_offsets, counts, order);
+                       threshold, buckets, tiles, offsets, order);
   }
   return check_launch("bin_rows_by_degree");
 }
@@ -156,7 +177,7 @@ int as_bin_rows_by_degree(const int64_t* crow, int64_t n, int64_t threshold, int
   if (workspace == nullptr || workspace_bytes < as::bin_workspace_bytes(n))
     return as::fail(AS_ERR_WORKSPACE, "binning needs %zu workspace bytes, got %zu", as::bin_workspace_bytes(n),
                     workspace_bytes);
-  return as::launch_bin_rows(crow, n, threshold, order, counts, workspace, static_cast<hipStream_t>(stream));
+  return as::launch_bin_rows(crow, n, threshold, 1, order, counts, workspace, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

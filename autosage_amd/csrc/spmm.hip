@@ -4,23 +4,33 @@
 // csrc/spmm_rows.cu:11-157 (light rows), csrc/spmm_hub.cu:13-182 (hub rows),
 // csrc/launcher_spmm.cu:22-72 (split launcher).
 //
-// Every kernel except the SPLIT64 hub kernel keeps, for each output element
-// Y[r, f], one fp32 accumulator updated in CSR edge order with fmaf
-// (acc + x when unweighted, which is the same value).  That is the order of
-// the sequential CPU CSR product, so these kernels are bit-identical to it
-// whatever the row-to-wave mapping, feature tiling or vector width.
+// Exactness.  Except in the SPLIT64 hub mode, every output element Y[r, f]
+// is one fp32 accumulator updated in CSR edge order with fmaf (acc + x when
+// unweighted, which is the same value).  That is the order of the
+// sequential CPU CSR product, so the result is bit-identical to it whatever
+// the row-to-wave mapping, feature slicing or vector width.
 //
-// Layouts (all one row per lane group, lanes own consecutive features):
-//   wave-row  one wave64 per row, lane owns V in {1,2,4} consecutive
-//             features, a pass covers 64·V features.  Column indices and
-//             weights of 64 edges are loaded cooperatively (one coalesced
-//             load) and broadcast with v_readlane, so the X-row address is
-//             wave-uniform.  U gathers are in flight per wave.
+// Row layouts:
+//   wave-row  one wave64 owns a row (or a feature slice of it); lane owns V in
+//             {1,2,4} consecutive features; a pass covers 64·V features.
+//             Column indices and weights of 64 edges are loaded with one
+//             coalesced load, one chunk ahead, and broadcast with v_readlane,
+//             so the X-row address is wave-uniform.  U gathers in flight.
 //   sub-wave  float4 lanes, LPR in {16,32} lanes per row, 64/LPR rows per
-//             wave; for short uniform rows where a whole wave per row idles.
-//   split64   one workgroup per hub row; its W waves take contiguous slices
-//             of the row's edges, accumulate in fp64 and the slices are
-//             summed in LDS in wave order (deterministic, reassociated).
+//             wave, for short rows where a whole wave per row would idle.
+//
+// Split schedule (one launch after the degree binning): workgroups of W
+// waves; the first H workgroups take the heavy rows, longest degree bucket
+// first, and split each heavy row's FEATURES across their W waves (no
+// reassociation: W times the memory parallelism on long rows without
+// changing any sum); the remaining workgroups take the light rows, one (or
+// 64/LPR) per wave.  Workgroups are dispatched in index order, so hub rows
+// start first and light rows fill the machine behind them.
+//
+// SPLIT64 hub mode: the W waves split the hub row's EDGES into contiguous
+// slices accumulated in fp64; the slices are added in LDS in wave order and
+// rounded to fp32 once (deterministic; reassociated, within about one fp32
+// rounding of the exact sum).
 #include "as_device.h"
 #include "as_internal.h"
 
@@ -28,51 +38,40 @@ namespace as {
 
 namespace {
 
-enum RowSource : int { kAllRows = 0, kHeavyRows = 1, kLightRows = 2 };
+enum Layout : int { kWaveV1 = 0, kWaveV2 = 1, kWaveV4 = 2, kSub16 = 3, kSub32 = 4 };
 
-// Maps the idx-th work item of a launch to a CSR row.
-template <int SRC>
-__device__ __forceinline__ bool pick_row(int64_t idx, int64_t n, const int32_t* __restrict__ order,
-                                         const int32_t* __restrict__ counts, int64_t* row) {
-  if constexpr (SRC == kAllRows) {
-    *row = idx;
-    return idx < n;
-  } else if constexpr (SRC == kHeavyRows) {
-    const int64_t heavy = counts[0];
-    if (idx >= heavy) return false;
-    *row = order[idx];
-    return true;
-  } else {
-    const int64_t heavy = counts[0];
-    if (idx >= n - heavy) return false;
-    *row = order[heavy + idx];
-    return true;
-  }
-}
+template <int L>
+struct LayoutInfo;
+template <>
+struct LayoutInfo<kWaveV1> { static constexpr int V = 1, LPR = 64; };
+template <>
+struct LayoutInfo<kWaveV2> { static constexpr int V = 2, LPR = 64; };
+template <>
+struct LayoutInfo<kWaveV4> { static constexpr int V = 4, LPR = 64; };
+template <>
+struct LayoutInfo<kSub16> { static constexpr int V = 4, LPR = 16; };
+template <>
+struct LayoutInfo<kSub32> { static constexpr int V = 4, LPR = 32; };
 
-// One wave per row; see the file comment.
-template <int V, bool HAS_VAL, int U, int SRC>
-__global__ __launch_bounds__(kBlock) void spmm_wave_row_kernel(
-    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const float* __restrict__ val,
-    const float* __restrict__ x, float* __restrict__ y, int64_t n, int64_t F,
-    const int32_t* __restrict__ order, const int32_t* __restrict__ counts, int64_t idx_base) {
+constexpr int kHubUnroll = 16;
+constexpr int kRowUnroll = 8;
+constexpr int kLongRow = 1024;  // rows at least this long use the deep unroll
+
+// One wave computes Y[row, fbeg:fend) in edge order.  V | (fend - fbeg) and
+// V | F are guaranteed by the host.
+template <int V, bool HAS_VAL, int U>
+__device__ __forceinline__ void wave_row_exact(const int64_t* __restrict__ col, const float* __restrict__ val,
+                                               const float* __restrict__ x, float* __restrict__ y, int64_t F,
+                                               int64_t row, int64_t rs, int64_t re, int64_t fbeg, int64_t fend) {
   const int lane = lane_id();
-  const int64_t idx = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
-  int64_t row = 0;
-  if (!pick_row<SRC>(idx, n, order, counts, &row)) return;
-  const int64_t rs = crow[row];
-  const int64_t re = crow[row + 1];
-  constexpr int P = kWave * V;
-
-  for (int64_t f0 = 0; f0 < F; f0 += P) {
+  for (int64_t f0 = fbeg; f0 < fend; f0 += kWave * V) {
     const int64_t fl = f0 + static_cast<int64_t>(lane) * V;
-    const bool active = fl < F;
+    const bool active = fl < fend;
     const float* xf = x + fl;
     float acc[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.f;
 
-    // Column/weight chunk of the next 64 edges, loaded one chunk ahead.
     int next_col = 0;
     float next_w = 1.f;
     if (rs < re && lane < re - rs) {
@@ -126,24 +125,15 @@ __global__ __launch_bounds__(kBlock) void spmm_wave_row_kernel(
   }
 }
 
-// float4 lanes, LPR lanes per row, 64/LPR rows per wave.
-template <int LPR, bool HAS_VAL, int U, int SRC>
-__global__ __launch_bounds__(kBlock) void spmm_subwave_kernel(
-    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const float* __restrict__ val,
-    const float* __restrict__ x, float* __restrict__ y, int64_t n, int64_t F,
-    const int32_t* __restrict__ order, const int32_t* __restrict__ counts, int64_t idx_base) {
-  constexpr int RPW = kWave / LPR;
+// Sub-wave rows: this lane group computes the whole of `row` (valid) with
+// float4 lanes; rows of one wave may differ in length (the loop runs to the
+// longest, shorter groups idle).
+template <int LPR, bool HAS_VAL, int U>
+__device__ __forceinline__ void subwave_row_exact(const int64_t* __restrict__ col, const float* __restrict__ val,
+                                                  const float* __restrict__ x, float* __restrict__ y, int64_t F,
+                                                  int64_t row, bool valid, int64_t rs, int64_t re) {
   constexpr int P = LPR * 4;
-  const int lane = lane_id();
-  const int sub = lane / LPR;
-  const int sl = lane % LPR;
-  const int64_t wave_idx = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
-  const int64_t idx = wave_idx * RPW + sub;
-  int64_t row = 0;
-  const bool valid = pick_row<SRC>(idx, n, order, counts, &row);
-  const int64_t rs = valid ? crow[row] : 0;
-  const int64_t re = valid ? crow[row + 1] : 0;
-
+  const int sl = lane_id() % LPR;
   for (int64_t f0 = 0; f0 < F; f0 += P) {
     const int64_t fl = f0 + static_cast<int64_t>(sl) * 4;
     const bool active = valid && fl < F;
@@ -186,29 +176,63 @@ __global__ __launch_bounds__(kBlock) void spmm_subwave_kernel(
   }
 }
 
-// One workgroup of W waves per heavy row.  Wave w sums the contiguous edge
-// slice [rs + w·S, rs + (w+1)·S) in fp64 (S = ceil(deg / W)), the W partial
-// tiles meet in LDS and are added in wave order 0..W-1 in fp64, and the
-// result is rounded to fp32 once.
-template <int V, bool HAS_VAL, int W>
-__global__ __launch_bounds__(512) void spmm_hub_split64_kernel(
-    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const float* __restrict__ val,
-    const float* __restrict__ x, float* __restrict__ y, int64_t n, int64_t F,
-    const int32_t* __restrict__ order, const int32_t* __restrict__ counts, int64_t idx_base) {
+// Light work of one wave: entry `wave_index` (times the rows per wave) of
+// `rows` (nullptr = identity); `limit` is the number of valid entries.
+template <int LAYOUT, bool HAS_VAL>
+__device__ __forceinline__ void light_wave(const int64_t* __restrict__ crow, const int64_t* __restrict__ col,
+                                           const float* __restrict__ val, const float* __restrict__ x,
+                                           float* __restrict__ y, int64_t F, const int32_t* __restrict__ rows,
+                                           int64_t wave_index, int64_t limit) {
+  using LI = LayoutInfo<LAYOUT>;
+  if constexpr (LI::LPR == kWave) {
+    if (wave_index >= limit) return;
+    const int64_t row = rows ? static_cast<int64_t>(rows[wave_index]) : wave_index;
+    const int64_t rs = crow[row];
+    const int64_t re = crow[row + 1];
+    if (re - rs >= kLongRow) {
+      wave_row_exact<LI::V, HAS_VAL, kHubUnroll>(col, val, x, y, F, row, rs, re, 0, F);
+    } else {
+      wave_row_exact<LI::V, HAS_VAL, kRowUnroll>(col, val, x, y, F, row, rs, re, 0, F);
+    }
+  } else {
+    constexpr int RPW = kWave / LI::LPR;
+    const int64_t idx = wave_index * RPW + lane_id() / LI::LPR;
+    const bool valid = idx < limit;
+    int64_t row = 0;
+    if (valid) row = rows ? static_cast<int64_t>(rows[idx]) : idx;
+    const int64_t rs = valid ? crow[row] : 0;
+    const int64_t re = valid ? crow[row + 1] : 0;
+    subwave_row_exact<LI::LPR, HAS_VAL, kRowUnroll>(col, val, x, y, F, row, valid, rs, re);
+  }
+}
+
+// Whole graph in row order: each wave takes one row (wave-row layouts) or
+// 64/LPR consecutive rows (sub-wave layouts).
+template <int LAYOUT, bool HAS_VAL>
+__global__ __launch_bounds__(kBlock) void spmm_rows_kernel(const int64_t* __restrict__ crow,
+                                                           const int64_t* __restrict__ col,
+                                                           const float* __restrict__ val,
+                                                           const float* __restrict__ x, float* __restrict__ y,
+                                                           int64_t n, int64_t F, int64_t wave_base) {
+  const int64_t wave_index = wave_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
+  light_wave<LAYOUT, HAS_VAL>(crow, col, val, x, y, F, nullptr, wave_index, n);
+}
+
+// SPLIT64 hub row: W waves, contiguous edge slices, fp64 partials, LDS
+// reduction in wave order, one rounding.
+template <int V, bool HAS_VAL>
+__device__ __forceinline__ void hub_row_split64(const int64_t* __restrict__ col, const float* __restrict__ val,
+                                                const float* __restrict__ x, float* __restrict__ y, int64_t F,
+                                                int64_t row, int64_t rs, int64_t re) {
   constexpr int P = kWave * V;
   constexpr int U = 8;
-  __shared__ double partial[W][P];
+  __shared__ double partial[8 * P];
   const int lane = lane_id();
   const int wave = wave_in_block();
-  const int64_t idx = idx_base + blockIdx.x;
-  int64_t row = 0;
-  if (!pick_row<kHeavyRows>(idx, n, order, counts, &row)) return;  // workgroup-uniform
-  const int64_t rs = crow[row];
-  const int64_t re = crow[row + 1];
+  const int W = static_cast<int>(blockDim.x >> 6);
   const int64_t slice = (re - rs + W - 1) / W;
   const int64_t ws = rs + wave * slice < re ? rs + wave * slice : re;
   const int64_t we = ws + slice < re ? ws + slice : re;
-
   for (int64_t f0 = 0; f0 < F; f0 += P) {
     const int64_t fl = f0 + static_cast<int64_t>(lane) * V;
     const bool active = fl < F;
@@ -250,19 +274,55 @@ __global__ __launch_bounds__(512) void spmm_hub_split64_kernel(
       }
     }
 #pragma unroll
-    for (int v = 0; v < V; ++v) partial[wave][lane * V + v] = acc[v];
+    for (int v = 0; v < V; ++v) partial[wave * P + lane * V + v] = acc[v];
     __syncthreads();
     for (int t = static_cast<int>(threadIdx.x); t < P; t += static_cast<int>(blockDim.x)) {
       if (f0 + t < F) {
-        double s = partial[0][t];
-#pragma unroll
-        for (int w2 = 1; w2 < W; ++w2) s += partial[w2][t];
+        double s = partial[t];
+        for (int w2 = 1; w2 < W; ++w2) s += partial[w2 * P + t];
         y[row * F + f0 + t] = static_cast<float>(s);
       }
     }
     __syncthreads();
   }
 }
+
+// Split schedule; see the file comment.  Work item = workgroup index.
+template <int HV, int LAYOUT, bool HAS_VAL, bool SPLIT64>
+__global__ __launch_bounds__(512) void spmm_scheduled_kernel(const int64_t* __restrict__ crow,
+                                                             const int64_t* __restrict__ col,
+                                                             const float* __restrict__ val,
+                                                             const float* __restrict__ x, float* __restrict__ y,
+                                                             int64_t n, int64_t F,
+                                                             const int32_t* __restrict__ order,
+                                                             const int32_t* __restrict__ counts,
+                                                             int64_t item_base) {
+  const int W = static_cast<int>(blockDim.x >> 6);
+  const int wave = wave_in_block();
+  const int64_t item = item_base + blockIdx.x;
+  const int64_t heavy = counts[0];
+  if (item < heavy) {
+    const int64_t row = order[item];
+    const int64_t rs = crow[row];
+    const int64_t re = crow[row + 1];
+    if constexpr (SPLIT64) {
+      hub_row_split64<HV, HAS_VAL>(col, val, x, y, F, row, rs, re);
+    } else {
+      // feature slice of this wave, a multiple of HV
+      int64_t slice = (F + W - 1) / W;
+      slice = (slice + HV - 1) / HV * HV;
+      const int64_t fbeg = wave * slice;
+      const int64_t fend = fbeg + slice < F ? fbeg + slice : F;
+      if (fbeg < F) wave_row_exact<HV, HAS_VAL, kHubUnroll>(col, val, x, y, F, row, rs, re, fbeg, fend);
+    }
+    return;
+  }
+  const int64_t light_wave_index = (item - heavy) * W + wave;
+  light_wave<LAYOUT, HAS_VAL>(crow, col, val, x, y, F, order + heavy, light_wave_index, n - heavy);
+}
+
+// ----------------------------------------------------------------------------
+// Host side
 
 struct SpmmArgs {
   const int64_t* crow;
@@ -272,99 +332,89 @@ struct SpmmArgs {
   float* y;
   int64_t n;
   int64_t f;
+};
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int rows_per_wave(int layout) { return layout == kSub16 ? 4 : layout == kSub32 ? 2 : 1; }
+
+// Layout of the whole-graph kernel and of the light rows.
+int pick_layout(const SpmmArgs& a, int feature_tile, bool vec4) {
+  const bool v4 = vec4 && a.f % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
+  const bool v2 = a.f % 2 == 0 && aligned(a.x, 8) && aligned(a.y, 8);
+  if (v4) {
+    if (a.f <= 64 || feature_tile == 64) return kSub16;
+    if (a.f <= 128) return kSub32;
+    return kWaveV4;
+  }
+  if (v2 && feature_tile == 128 && a.f > 64) return kWaveV2;
+  return kWaveV1;
+}
+
+// Lane vector width for a hub row slice of `slice` features.
+int pick_hub_vector(const SpmmArgs& a, int64_t slice, bool vec4) {
+  if (vec4 && slice > 128 && a.f % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16)) return 4;
+  if (slice > 64 && a.f % 2 == 0 && aligned(a.x, 8) && aligned(a.y, 8)) return 2;
+  return 1;
+}
+
+template <int LAYOUT, bool HAS_VAL>
+void launch_rows_t(const SpmmArgs& a, hipStream_t s) {
+  const int64_t waves = (a.n + rows_per_wave(LAYOUT) - 1) / rows_per_wave(LAYOUT);
+  const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
+    const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
+    hipLaunchKernelGGL((spmm_rows_kernel<LAYOUT, HAS_VAL>), dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0, s,
+                       a.crow, a.col, a.val, a.x, a.y, a.n, a.f, b0 * kWavesPerBlock);
+  }
+}
+
+template <bool HAS_VAL>
+void launch_rows(const SpmmArgs& a, int layout, hipStream_t s) {
+  switch (layout) {
+    case kWaveV1: launch_rows_t<kWaveV1, HAS_VAL>(a, s); break;
+    case kWaveV2: launch_rows_t<kWaveV2, HAS_VAL>(a, s); break;
+    case kWaveV4: launch_rows_t<kWaveV4, HAS_VAL>(a, s); break;
+    case kSub16: launch_rows_t<kSub16, HAS_VAL>(a, s); break;
+    default: launch_rows_t<kSub32, HAS_VAL>(a, s); break;
+  }
+}
+
+struct SchedLaunch {
+  int64_t blocks;
+  int waves;
   const int32_t* order;
   const int32_t* counts;
 };
 
-enum Layout : int { kWaveV1, kWaveV2, kWaveV4, kSub16, kSub32 };
-
-// Launches `rows` row work items (upper bound) with the given layout.
-template <int SRC, int U>
-int launch_rows(const SpmmArgs& a, Layout layout, int64_t rows, bool has_val, hipStream_t stream) {
-  if (rows <= 0) return AS_OK;
-  const int waves_per_block = kWavesPerBlock;
-  int64_t waves = rows;
-  if (layout == kSub16) waves = (rows + 3) / 4;
-  if (layout == kSub32) waves = (rows + 1) / 2;
-  const int64_t blocks = (waves + waves_per_block - 1) / waves_per_block;
-  for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
-    const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
-    const int64_t wave_base = b0 * waves_per_block;
-    const dim3 grid(static_cast<unsigned>(nb));
-    const dim3 block(kBlock);
-#define AS_LAUNCH(K)                                                                                        \
-  hipLaunchKernelGGL(K, grid, block, 0, stream, a.crow, a.col, a.val, a.x, a.y, a.n, a.f, a.order, a.counts, \
-                     wave_base)
-    switch (layout) {
-      case kWaveV1:
-        if (has_val) AS_LAUNCH((spmm_wave_row_kernel<1, true, U, SRC>));
-        else AS_LAUNCH((spmm_wave_row_kernel<1, false, U, SRC>));
-        break;
-      case kWaveV2:
-        if (has_val) AS_LAUNCH((spmm_wave_row_kernel<2, true, U, SRC>));
-        else AS_LAUNCH((spmm_wave_row_kernel<2, false, U, SRC>));
-        break;
-      case kWaveV4:
-        if (has_val) AS_LAUNCH((spmm_wave_row_kernel<4, true, U, SRC>));
-        else AS_LAUNCH((spmm_wave_row_kernel<4, false, U, SRC>));
-        break;
-      case kSub16:
-        if (has_val) AS_LAUNCH((spmm_subwave_kernel<16, true, 8, SRC>));
-        else AS_LAUNCH((spmm_subwave_kernel<16, false, 8, SRC>));
-        break;
-      case kSub32:
-        if (has_val) AS_LAUNCH((spmm_subwave_kernel<32, true, 8, SRC>));
-        else AS_LAUNCH((spmm_subwave_kernel<32, false, 8, SRC>));
-        break;
-    }
-#undef AS_LAUNCH
-  }
-  return AS_OK;
-}
-
-template <int V, bool HAS_VAL>
-void launch_split64_w(int waves, const SpmmArgs& a, int64_t blocks, int64_t base, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(blocks));
-  switch (waves) {
-    case 2:
-      hipLaunchKernelGGL((spmm_hub_split64_kernel<V, HAS_VAL, 2>), grid, dim3(2 * kWave), 0, stream, a.crow, a.col,
-                         a.val, a.x, a.y, a.n, a.f, a.order, a.counts, base);
-      break;
-    case 4:
-      hipLaunchKernelGGL((spmm_hub_split64_kernel<V, HAS_VAL, 4>), grid, dim3(4 * kWave), 0, stream, a.crow, a.col,
-                         a.val, a.x, a.y, a.n, a.f, a.order, a.counts, base);
-      break;
-    default:
-      hipLaunchKernelGGL((spmm_hub_split64_kernel<V, HAS_VAL, 8>), grid, dim3(8 * kWave), 0, stream, a.crow, a.col,
-                         a.val, a.x, a.y, a.n, a.f, a.order, a.counts, base);
-      break;
+template <int HV, int LAYOUT, bool HAS_VAL, bool SPLIT64>
+void launch_sched_t(const SpmmArgs& a, const SchedLaunch& l, hipStream_t s) {
+  for (int64_t b0 = 0; b0 < l.blocks; b0 += kMaxBlocksPerLaunch) {
+    const int64_t nb = l.blocks - b0 < kMaxBlocksPerLaunch ? l.blocks - b0 : kMaxBlocksPerLaunch;
+    hipLaunchKernelGGL((spmm_scheduled_kernel<HV, LAYOUT, HAS_VAL, SPLIT64>), dim3(static_cast<unsigned>(nb)),
+                       dim3(static_cast<unsigned>(l.waves * kWave)), 0, s, a.crow, a.col, a.val, a.x, a.y, a.n, a.f,
+                       l.order, l.counts, b0);
   }
 }
 
-int launch_hub_split64(const SpmmArgs& a, int v, int waves, int64_t rows, bool has_val, hipStream_t stream) {
-  for (int64_t b0 = 0; b0 < rows; b0 += kMaxBlocksPerLaunch) {
-    const int64_t nb = rows - b0 < kMaxBlocksPerLaunch ? rows - b0 : kMaxBlocksPerLaunch;
-    if (v == 4) {
-      if (has_val) launch_split64_w<4, true>(waves, a, nb, b0, stream);
-      else launch_split64_w<4, false>(waves, a, nb, b0, stream);
-    } else if (v == 2) {
-      if (has_val) launch_split64_w<2, true>(waves, a, nb, b0, stream);
-      else launch_split64_w<2, false>(waves, a, nb, b0, stream);
-    } else {
-      if (has_val) launch_split64_w<1, true>(waves, a, nb, b0, stream);
-      else launch_split64_w<1, false>(waves, a, nb, b0, stream);
-    }
+template <int HV, bool HAS_VAL, bool SPLIT64>
+void launch_sched_l(int layout, const SpmmArgs& a, const SchedLaunch& l, hipStream_t s) {
+  switch (layout) {
+    case kWaveV1: launch_sched_t<HV, kWaveV1, HAS_VAL, SPLIT64>(a, l, s); break;
+    case kWaveV2: launch_sched_t<HV, kWaveV2, HAS_VAL, SPLIT64>(a, l, s); break;
+    case kWaveV4: launch_sched_t<HV, kWaveV4, HAS_VAL, SPLIT64>(a, l, s); break;
+    case kSub16: launch_sched_t<HV, kSub16, HAS_VAL, SPLIT64>(a, l, s); break;
+    default: launch_sched_t<HV, kSub32, HAS_VAL, SPLIT64>(a, l, s); break;
   }
-  return AS_OK;
 }
 
-bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
-
-// Widest lane vector the feature width and pointer alignment allow, capped at cap.
-int lane_vector(const float* x, const float* y, int64_t F, bool vec4, int cap) {
-  if (vec4 && cap >= 4 && F % 4 == 0 && aligned(x, 16) && aligned(y, 16)) return 4;
-  if (cap >= 2 && F % 2 == 0 && aligned(x, 8) && aligned(y, 8)) return 2;
-  return 1;
+template <bool HAS_VAL, bool SPLIT64>
+void launch_sched_v(int hv, int layout, const SpmmArgs& a, const SchedLaunch& l, hipStream_t s) {
+  switch (hv) {
+    case 4: launch_sched_l<4, HAS_VAL, SPLIT64>(layout, a, l, s); break;
+    case 2: launch_sched_l<2, HAS_VAL, SPLIT64>(layout, a, l, s); break;
+    default: launch_sched_l<1, HAS_VAL, SPLIT64>(layout, a, l, s); break;
+  }
 }
 
 int validate_spmm(const int64_t* crow, const int64_t* col, const float* x, float* y, int64_t n, int64_t nnz,
@@ -379,6 +429,8 @@ int validate_spmm(const int64_t* crow, const int64_t* col, const float* x, float
 }
 
 }  // namespace
+
+constexpr int kSplitBuckets = 8;
 
 size_t spmm_split_workspace_bytes(int64_t n) {
   const size_t order_bytes = align_up(static_cast<size_t>(n > 0 ? n : 1) * sizeof(int32_t), 256);
@@ -396,16 +448,10 @@ int as_spmm_csr_f32(const int64_t* crow, const int64_t* col, const float* val, c
   if (st != AS_OK) return st;
   if (n == 0 || f == 0) return AS_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  as::SpmmArgs a{crow, col, val, x, y, n, f, nullptr, nullptr};
-  const int v = as::lane_vector(x, y, f, vec4 != 0, 4);
-  as::Layout layout;
-  if (v == 4 && f <= 64) layout = as::kSub16;
-  else if (v == 4 && f <= 128) layout = as::kSub32;
-  else if (v == 4) layout = as::kWaveV4;
-  else if (v == 2) layout = as::kWaveV2;
-  else layout = as::kWaveV1;
-  st = as::launch_rows<as::kAllRows, 8>(a, layout, n, val != nullptr, s);
-  if (st != AS_OK) return st;
+  const as::SpmmArgs a{crow, col, val, x, y, n, f};
+  const int layout = as::pick_layout(a, 128, vec4 != 0);
+  if (val != nullptr) as::launch_rows<true>(a, layout, s);
+  else as::launch_rows<false>(a, layout, s);
   return as::check_launch("spmm_csr");
 }
 
@@ -435,32 +481,27 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col, const float* 
   const size_t order_bytes = as::align_up(static_cast<size_t>(n) * sizeof(int32_t), 256);
   int32_t* counts = reinterpret_cast<int32_t*>(ws + order_bytes);
   void* bin_ws = ws + order_bytes + 256;
-  st = as::launch_bin_rows(crow, n, hub_threshold, order, counts, bin_ws, s);
+  const bool split64 = hub_mode == AS_HUB_SPLIT64;
+  st = as::launch_bin_rows(crow, n, hub_threshold, split64 ? 1 : as::kSplitBuckets, order, counts, bin_ws, s);
   if (st != AS_OK) return st;
 
-  as::SpmmArgs a{crow, col, val, x, y, n, f, order, counts};
-  const bool has_val = val != nullptr;
-  // Hub rows: at most min(n, nnz / T) of them.
+  const as::SpmmArgs a{crow, col, val, x, y, n, f};
+  const int layout = as::pick_layout(a, feature_tile, vec4 != 0);
+  const int64_t slice = split64 ? f : (f + waves_per_block - 1) / waves_per_block;
+  const int hv = as::pick_hub_vector(a, slice, vec4 != 0);
+  // At most min(n, nnz / T) hub rows; light rows need ceil(n / (W·rows per wave)) workgroups.
   int64_t heavy_upper = nnz / hub_threshold;
   if (heavy_upper > n) heavy_upper = n;
-  const int hub_v = as::lane_vector(x, y, f, vec4 != 0, f > 128 ? 4 : 2);
-  if (heavy_upper > 0) {
-    if (hub_mode == AS_HUB_SPLIT64) {
-      st = as::launch_hub_split64(a, hub_v, waves_per_block, heavy_upper, has_val, s);
-    } else {
-      const as::Layout hub_layout = hub_v == 4 ? as::kWaveV4 : hub_v == 2 ? as::kWaveV2 : as::kWaveV1;
-      st = as::launch_rows<as::kHeavyRows, 16>(a, hub_layout, heavy_upper, has_val, s);
-    }
-    if (st != AS_OK) return st;
+  const int64_t per_group = static_cast<int64_t>(waves_per_block) * as::rows_per_wave(layout);
+  const as::SchedLaunch l{heavy_upper + (n + per_group - 1) / per_group, waves_per_block, order, counts};
+  const bool has_val = val != nullptr;
+  if (has_val) {
+    if (split64) as::launch_sched_v<true, true>(hv, layout, a, l, s);
+    else as::launch_sched_v<true, false>(hv, layout, a, l, s);
+  } else {
+    if (split64) as::launch_sched_v<false, true>(hv, layout, a, l, s);
+    else as::launch_sched_v<false, false>(hv, layout, a, l, s);
   }
-  // Light rows: feature_tile features per pass.
-  as::Layout light;
-  const int lv = as::lane_vector(x, y, f, vec4 != 0, 4);
-  if (lv == 4) light = feature_tile == 64 ? as::kSub16 : as::kSub32;
-  else if (lv == 2 && feature_tile == 128) light = as::kWaveV2;
-  else light = as::kWaveV1;
-  st = as::launch_rows<as::kLightRows, 8>(a, light, n, has_val, s);
-  if (st != AS_OK) return st;
   return as::check_launch("spmm_csr_split");
 }
 

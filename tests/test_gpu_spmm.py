@@ -71,9 +71,12 @@ def test_spmm_split64_against_fp64(waves, features, weighted, monkeypatch):
     seq = oracle.spmm_seq(crow, col, val, x)
     d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
     got = torch.ops.autosage.spmm_csr_split(d_crow, d_col, d_val, d_x, 128, waves, 300).cpu().numpy()
-    assert np.all(np.abs(got - exact) <= 1e-6 * np.abs(exact) + 1e-9)
-    light = np.diff(crow) < 300
-    assert np.array_equal(got[light], seq[light])
+    heavy = np.diff(crow) >= 300
+    assert heavy.sum() >= 3
+    # hub rows: fp64 partials rounded once, so within 1e-6 relative of fp64
+    assert np.all(np.abs(got[heavy] - exact[heavy]) <= 1e-6 * np.abs(exact[heavy]) + 1e-9)
+    # light rows: the exact kernel
+    assert np.array_equal(got[~heavy], seq[~heavy])
 
 
 @pytest.mark.parametrize("threshold", [1, 2, 9, 500, 10**9])
@@ -137,7 +140,7 @@ def test_input_checks_raise_runtime_error():
     with pytest.raises(RuntimeError, match="crow must contain N \\+ 1 entries"):
         torch.ops.autosage.spmm_csr(d_crow[:1], d_col, None, d_x)
     with pytest.raises(RuntimeError, match="x must be contiguous"):
-        torch.ops.autosage.spmm_csr(d_crow, d_col, None, torch.ones((4, 1), device="cuda").t())
+        torch.ops.autosage.spmm_csr(d_crow, d_col, None, torch.ones((4, 2), device="cuda").t())
 
 
 # Reference tests/test_cuda.py:32-57 at the reference tolerance, against
