@@ -52,9 +52,9 @@ def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-def _compile(source: Path) -> Path:
-    obj = BUILDDIR / (source.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(source), "-o", str(obj)]
+def _compile(source: Path, builddir: Path, defines: tuple[str, ...]) -> Path:
+    obj = builddir / (source.stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, *(f"-D{d}" for d in defines), "-c", str(source), "-o", str(obj)]
     if source.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     result = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,22 +63,26 @@ def _compile(source: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    BUILDDIR.mkdir(exist_ok=True)
-    LIBDIR.mkdir(exist_ok=True)
+def build(verbose: bool = False, output: Path = LIBRARY, defines: tuple[str, ...] = ()) -> Path:
+    """Compiles every source for gfx950 and links ``output``; ``defines``
+    are extra preprocessor definitions (tuning constants)."""
+    output = Path(output)
+    builddir = BUILDDIR if output == LIBRARY else output.parent / ("_build_" + output.stem)
+    builddir.mkdir(parents=True, exist_ok=True)
+    output.parent.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, srcs))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+        objects = list(pool.map(lambda src: _compile(src, builddir, tuple(defines)), srcs))
+    tmp = output.with_suffix(".so.tmp")
     cmd = [hipcc(), "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objects), "-o", str(tmp)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
-        raise RuntimeError(f"linking {LIBRARY.name} failed:\n{result.stdout}\n{result.stderr}")
-    os.replace(tmp, LIBRARY)
+        raise RuntimeError(f"linking {output.name} failed:\n{result.stdout}\n{result.stderr}")
+    os.replace(tmp, output)
     if verbose:
-        print(f"built {LIBRARY}")
-    return LIBRARY
+        print(f"built {output}")
+    return output
 
 
 if __name__ == "__main__":

@@ -53,9 +53,17 @@ struct LayoutInfo<kSub16> { static constexpr int V = 4, LPR = 16; };
 template <>
 struct LayoutInfo<kSub32> { static constexpr int V = 4, LPR = 32; };
 
-constexpr int kHubUnroll = 16;
-constexpr int kRowUnroll = 8;
-constexpr int kLongRow = 1024;  // rows at least this long use the deep unroll
+// Gathers in flight per wave: hub rows, ordinary rows, and the degree from
+// which an ordinary row uses the hub depth.
+#ifndef AS_HUB_UNROLL
+#define AS_HUB_UNROLL 16
+#endif
+#ifndef AS_ROW_UNROLL
+#define AS_ROW_UNROLL 8
+#endif
+constexpr int kHubUnroll = AS_HUB_UNROLL;
+constexpr int kRowUnroll = AS_ROW_UNROLL;
+constexpr int kLongRow = 1024;
 
 // One wave computes Y[row, fbeg:fend) in edge order.  V | (fend - fbeg) and
 // V | F are guaranteed by the host.
@@ -338,15 +346,21 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 int rows_per_wave(int layout) { return layout == kSub16 ? 4 : layout == kSub32 ? 2 : 1; }
 
-// Layout of the whole-graph kernel and of the light rows.
-int pick_layout(const SpmmArgs& a, int feature_tile, bool vec4) {
+// Mean degree below which float4 sub-wave rows beat one wave per row.
+constexpr int64_t kSubwaveMaxMeanDegree = 48;
+
+// Layout of the whole-graph kernel and of the light rows: float4 sub-wave
+// rows when vec4 is allowed and rows are short on average, otherwise one
+// wave per row (column broadcast through SGPRs).
+int pick_layout(const SpmmArgs& a, int64_t nnz, int feature_tile, bool vec4) {
+  const bool short_rows = nnz < kSubwaveMaxMeanDegree * a.n;
   const bool v4 = vec4 && a.f % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
   const bool v2 = a.f % 2 == 0 && aligned(a.x, 8) && aligned(a.y, 8);
-  if (v4) {
+  if (v4 && short_rows) {
     if (a.f <= 64 || feature_tile == 64) return kSub16;
     if (a.f <= 128) return kSub32;
-    return kWaveV4;
   }
+  if (v4 && a.f > 128 && feature_tile == 128) return kWaveV4;
   if (v2 && feature_tile == 128 && a.f > 64) return kWaveV2;
   return kWaveV1;
 }
@@ -449,7 +463,7 @@ int as_spmm_csr_f32(const int64_t* crow, const int64_t* col, const float* val, c
   if (n == 0 || f == 0) return AS_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const as::SpmmArgs a{crow, col, val, x, y, n, f};
-  const int layout = as::pick_layout(a, 128, vec4 != 0);
+  const int layout = as::pick_layout(a, nnz, 128, vec4 != 0);
   if (val != nullptr) as::launch_rows<true>(a, layout, s);
   else as::launch_rows<false>(a, layout, s);
   return as::check_launch("spmm_csr");
@@ -486,7 +500,7 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col, const float* 
   if (st != AS_OK) return st;
 
   const as::SpmmArgs a{crow, col, val, x, y, n, f};
-  const int layout = as::pick_layout(a, feature_tile, vec4 != 0);
+  const int layout = as::pick_layout(a, nnz, feature_tile, vec4 != 0);
   const int64_t slice = split64 ? f : (f + waves_per_block - 1) / waves_per_block;
   const int hv = as::pick_hub_vector(a, slice, vec4 != 0);
   // At most min(n, nnz / T) hub rows; light rows need ceil(n / (W·rows per wave)) workgroups.

@@ -126,6 +126,9 @@ def main() -> int:
                         help="calibrated | whole | t,w,h (split candidate)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gpu-baseline", action="store_true")
+    parser.add_argument("--copy-calibration-mib", type=int, default=0,
+                        help="also run one device-to-device copy of this many MiB (known-size kernel for scaling "
+                             "FETCH_SIZE/WRITE_SIZE counters)")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -144,6 +147,14 @@ def main() -> int:
     if not autosage_amd.load_native():
         raise RuntimeError(f"HIP library failed to load: {autosage_amd.ops.native_load_error()}")
     device = torch.device("cuda:0")
+    if args.copy_calibration_mib > 0:
+        count = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(count, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {count * 4} bytes read and written")
+        del src, dst
     t0 = time.time()
     if args.workload in ("cfg1", "cfg2", "cfg3"):
         f = args.features or {"cfg1": 64, "cfg2": 128, "cfg3": 128}[args.workload]

@@ -119,9 +119,15 @@ def test_attention_forward_api_fused_and_unfused(monkeypatch):
     unfused, info2 = csr_attention_forward(d_crow, d_col, d_q, d_k, d_v, fused=False)
     assert set(info2) == {"sddmm", "spmm"}
     ref = oracle.attention_ref(crow, col, q, k, v)
-    for out in (fused, unfused):
-        got = out.cpu().numpy()
-        assert np.all(np.abs(got - ref) <= ATOL + RTOL * np.abs(ref))
+    got = fused.cpu().numpy()
+    assert np.all(np.abs(got - ref) <= ATOL + RTOL * np.abs(ref))
+    # The unfused path runs whatever the schedulers chose; the native choices
+    # are held to the native bar, a PyTorch baseline choice (different
+    # summation order) to the reference suite's tolerance.
+    native = info2["sddmm"]["choice"] == "autosage" and info2["spmm"]["choice"] == "autosage"
+    rtol, atol = (RTOL, ATOL) if native else (1e-4, 1e-4)
+    got = unfused.cpu().numpy()
+    assert np.all(np.abs(got - ref) <= atol + rtol * np.abs(ref)), (info2["sddmm"]["choice"], info2["spmm"]["choice"])
 
 
 def test_auto_schedulers_on_gpu():
