@@ -346,8 +346,12 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 int rows_per_wave(int layout) { return layout == kSub16 ? 4 : layout == kSub32 ? 2 : 1; }
 
-// Mean degree below which float4 sub-wave rows beat one wave per row.
-constexpr int64_t kSubwaveMaxMeanDegree = 48;
+// Mean degree below which float4 sub-wave rows are used for short rows
+// (when vec4 is allowed).
+#ifndef AS_SUBWAVE_MAX_MEAN_DEGREE
+#define AS_SUBWAVE_MAX_MEAN_DEGREE 48
+#endif
+constexpr int64_t kSubwaveMaxMeanDegree = AS_SUBWAVE_MAX_MEAN_DEGREE;
 
 // Layout of the whole-graph kernel and of the light rows: float4 sub-wave
 // rows when vec4 is allowed and rows are short on average, otherwise one

@@ -113,15 +113,44 @@ int synth_union_rows(const int64_t* crow, const int64_t* col, const int64_t* t_c
 }
 
 // Transpose of a square CSR A: t_crow[n+1], t_col[nnz]; rows of the
-// transpose list their columns in ascending order.
+// transpose list their columns in ascending order.  Threads own contiguous
+// source-row ranges; per-thread column histograms give each thread its write
+// offsets, so the output is the same for every thread count.
 int synth_transpose(const int64_t* crow, const int64_t* col, int64_t n, int64_t* t_crow, int64_t* t_col) {
-  std::vector<int64_t> fill(static_cast<size_t>(n) + 1, 0);
-  const int64_t nnz = crow[n];
-  for (int64_t e = 0; e < nnz; ++e) ++fill[static_cast<size_t>(col[e]) + 1];
-  for (int64_t r = 0; r < n; ++r) fill[r + 1] += fill[r];
-  std::copy(fill.begin(), fill.end(), t_crow);
-  for (int64_t r = 0; r < n; ++r)
-    for (int64_t e = crow[r]; e < crow[r + 1]; ++e) t_col[fill[col[e]]++] = r;
+  const int parts = 16;
+  std::vector<std::vector<int64_t>> hist(parts, std::vector<int64_t>(static_cast<size_t>(n), 0));
+  auto range = [&](int p, int64_t* b, int64_t* e) {
+    *b = n * p / parts;
+    *e = n * (p + 1) / parts;
+  };
+#pragma omp parallel for schedule(static, 1)
+  for (int p = 0; p < parts; ++p) {
+    int64_t b, e;
+    range(p, &b, &e);
+    auto& h = hist[p];
+    for (int64_t k = crow[b]; k < crow[e]; ++k) ++h[static_cast<size_t>(col[k])];
+  }
+  t_crow[0] = 0;
+  for (int64_t c = 0; c < n; ++c) {
+    int64_t total = 0;
+    for (int p = 0; p < parts; ++p) {
+      const int64_t v = hist[p][c];
+      hist[p][c] = total;  // exclusive offset of part p inside column c
+      total += v;
+    }
+    t_crow[c + 1] = t_crow[c] + total;
+  }
+#pragma omp parallel for schedule(static, 1)
+  for (int p = 0; p < parts; ++p) {
+    int64_t b, e;
+    range(p, &b, &e);
+    auto& h = hist[p];
+    for (int64_t r = b; r < e; ++r)
+      for (int64_t k = crow[r]; k < crow[r + 1]; ++k) {
+        const int64_t c = col[k];
+        t_col[t_crow[c] + h[static_cast<size_t>(c)]++] = r;
+      }
+  }
   return 0;
 }
 

@@ -1,0 +1,116 @@
+"""Parity at the benchmark configurations' full sizes.
+
+The GPU runs the whole graph; the CPU oracle checks a seeded sample of rows
+(always including the longest ones), through sub-CSRs of those rows.  Bars as
+in the small-size tests: bit-identical for SpMM (exact modes) and SDDMM,
+|Δ| <= 1e-6 + 1e-5·|ref| for softmax/attention, fp64 bound for split64.
+Size-independent properties are checked on the full outputs: every split
+variant equals the whole-graph kernel bit for bit, fused attention equals
+the unfused stages bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from autosage_amd import synth
+from tests.gpu_common import bitwise_equal, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+ATOL = 1e-6
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def sample_rows(crow: np.ndarray, count: int, seed: int, longest: int = 8) -> np.ndarray:
+    deg = np.diff(crow)
+    rng = np.random.default_rng(seed)
+    picked = rng.choice(deg.size, size=min(count, deg.size), replace=False)
+    top = np.argsort(deg)[-longest:]
+    return np.unique(np.concatenate([picked, top]))
+
+
+def sub_csr(crow: np.ndarray, col: np.ndarray, rows: np.ndarray):
+    starts, ends = crow[rows], crow[rows + 1]
+    sub_crow = np.concatenate([[0], np.cumsum(ends - starts)]).astype(np.int64)
+    edges = np.concatenate([np.arange(s, e) for s, e in zip(starts, ends)]).astype(np.int64)
+    return sub_crow, col[edges], edges
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def test_config2_weighted_spmm():
+    w = synth.config2(seed=0)
+    d_crow, d_col, d_val, d_x = dev(w.crow), dev(w.col), dev(w.val), dev(w.dense["x"])
+    whole = torch.ops.autosage.spmm_csr(d_crow, d_col, d_val, d_x)
+    split = torch.ops.autosage.spmm_csr_split(d_crow, d_col, d_val, d_x, 128, 2, 16)
+    assert torch.equal(whole, split)
+    rows = sample_rows(w.crow, 3000, seed=1)
+    ref = oracle.spmm_seq(w.crow, w.col, w.val, w.dense["x"], rows=rows)
+    assert bitwise_equal(whole[torch.from_numpy(rows).cuda()], ref)
+
+
+@pytest.mark.parametrize("features", [64, 128, 256])
+def test_config3_skewed_spmm(features, monkeypatch):
+    w = synth.config3(seed=0, features=features)
+    d_crow, d_col, d_x = dev(w.crow), dev(w.col), dev(w.dense["x"])
+    deg = np.diff(w.crow)
+    q95 = int(np.rint(np.quantile(deg, 0.95)))
+    whole = torch.ops.autosage.spmm_csr(d_crow, d_col, None, d_x)
+    for cand in ((128, 2, q95), (64, 4, 512), (128, 8, 2048)):
+        assert torch.equal(torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, *cand), whole), cand
+    rows = sample_rows(w.crow, 1500, seed=features)
+    ref = oracle.spmm_seq(w.crow, w.col, None, w.dense["x"], rows=rows)
+    d_rows = torch.from_numpy(rows).cuda()
+    assert bitwise_equal(whole[d_rows], ref)
+    # reassociating hub mode: hub rows within 1e-6 of fp64, light rows exact
+    monkeypatch.setenv("AUTOSAGE_HUB_MODE", "split64")
+    s64 = torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, 128, 4, q95)[d_rows].cpu().numpy()
+    exact = oracle.spmm_f64(w.crow, w.col, None, w.dense["x"], rows=rows)
+    heavy = deg[rows] >= q95
+    assert heavy.sum() >= 8
+    assert np.all(np.abs(s64[heavy] - exact[heavy]) <= 1e-6 * np.abs(exact[heavy]) + 1e-9)
+    assert np.array_equal(s64[~heavy], ref[~heavy])
+
+
+@pytest.mark.parametrize("features", [64, 128])
+def test_config4_sddmm(features):
+    w = synth.config4(seed=0, features=features)
+    d_crow, d_col, d_q, d_k = dev(w.crow), dev(w.col), dev(w.dense["q"]), dev(w.dense["k"])
+    whole = torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, d_k)
+    for waves, threshold in ((4, 256), (8, 4096), (2, 60000)):
+        assert torch.equal(torch.ops.autosage.sddmm_csr_split(d_crow, d_col, d_q, d_k, waves, threshold), whole)
+    rows = sample_rows(w.crow, 2000, seed=features, longest=6)
+    s_crow, s_col, edges = sub_csr(w.crow, w.col, rows)
+    ref = oracle.sddmm_ref(s_crow, s_col, w.dense["q"][rows], w.dense["k"])
+    assert bitwise_equal(whole[torch.from_numpy(edges).cuda()], ref)
+
+
+def test_config5_attention():
+    w = synth.config5(seed=0)
+    q, k, v = w.dense["q"], w.dense["k"], w.dense["v"]
+    d_crow, d_col, d_q, d_k, d_v = dev(w.crow), dev(w.col), dev(q), dev(k), dev(v)
+    fused = torch.ops.autosage.csr_attention(d_crow, d_col, d_q, d_k, d_v, 0.125)
+    scores = torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, d_k) * 0.125
+    probs = torch.ops.autosage.csr_row_softmax(d_crow, scores)
+    del scores
+    unfused = torch.ops.autosage.spmm_csr(d_crow, d_col, probs, d_v)
+    assert torch.equal(fused, unfused)
+    rows = sample_rows(w.crow, 1500, seed=5)
+    s_crow, s_col, edges = sub_csr(w.crow, w.col, rows)
+    ref = oracle.attention_ref(s_crow, s_col, q[rows], k, v, scale=0.125)
+    got = fused[torch.from_numpy(rows).cuda()].cpu().numpy()
+    assert np.all(np.abs(got - ref) <= ATOL + RTOL * np.abs(ref)), float(np.max(np.abs(got - ref)))
+    p_ref = oracle.row_softmax(s_crow, oracle.sddmm_ref(s_crow, s_col, q[rows], k) * np.float32(0.125))
+    p_got = probs[torch.from_numpy(edges).cuda()].cpu().numpy()
+    assert np.all(np.abs(p_got - p_ref) <= ATOL + RTOL * np.abs(p_ref))
