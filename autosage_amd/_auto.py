@@ -145,18 +145,28 @@ def _degree_quantiles(crow: torch.Tensor) -> tuple[int, int, int]:
     return int(q90), int(q95), int(q99)
 
 
+def _preferred_waves(feature_width: int) -> int:
+    """Waves per hub workgroup to rank first.
+
+    The reference prefers 8/4/2 warps for degree skew q99/q50 >= 4 / >= 2 /
+    otherwise (``_auto.py:187-188``), because its warps split a hub row's
+    edges.  Here the waves of a hub workgroup split the row's features (the
+    sum keeps its order), and a slice narrower than 64 features leaves lanes
+    idle: on the skewed 115M-nnz graph 2 waves beat 4 and 8 at F = 64, 128
+    and 256 (6.29 / 8.19 / 13.7 ms at F = 128).  Two waves are preferred up
+    to F = 128, four above."""
+    return 2 if feature_width <= 128 else 4
+
+
 def _spmm_candidates(crow: torch.Tensor, feature_width: int, config: SchedulerConfig) -> list[tuple[int, int, int]]:
     """Shortlist of ``(tile, waves, threshold)`` (``_auto.py:175-216``).
 
-    The preferred point is tile 64 for F <= 64 else 128, waves 8/4/2 for
-    degree skew q99/q50 >= 4 / >= 2 / otherwise, threshold q95; candidates are
-    ranked by |Δtile|/64 + |Δwaves|/6 + |Δthreshold|/threshold, ties broken by
-    the tuple, and the first ``candidate_count`` are kept."""
+    The preferred point is tile 64 for F <= 64 else 128, the waves of
+    ``_preferred_waves`` and threshold q95; candidates are ranked by
+    |Δtile|/64 + |Δwaves|/6 + |Δthreshold|/threshold, ties broken by the
+    tuple, and the first ``candidate_count`` are kept."""
     q90, q95, q99 = _degree_quantiles(crow)
-    degrees = crow[1:] - crow[:-1]
-    q50 = int(torch.quantile(degrees.to(torch.float64), 0.5).round().item()) if degrees.numel() else 1
-    skew = q99 / max(q50, 1)
-    want_waves = 8 if skew >= 4 else 4 if skew >= 2 else 2
+    want_waves = _preferred_waves(feature_width)
     want_tile = 64 if feature_width <= 64 else 128
     want_threshold = q95
 

@@ -61,9 +61,21 @@ struct LayoutInfo<kSub32> { static constexpr int V = 4, LPR = 32; };
 #ifndef AS_ROW_UNROLL
 #define AS_ROW_UNROLL 8
 #endif
+#ifndef AS_NT_STREAMS
+#define AS_NT_STREAMS 0
+#endif
 constexpr int kHubUnroll = AS_HUB_UNROLL;
 constexpr int kRowUnroll = AS_ROW_UNROLL;
 constexpr int kLongRow = 1024;
+
+// Loads of data read exactly once (column indices, weights); with
+// AS_NT_STREAMS they carry the non-temporal hint so they do not displace X
+// rows from the caches.
+template <typename T>
+__device__ __forceinline__ T stream_load(const T* p) {
+  if constexpr (AS_NT_STREAMS != 0) return __builtin_nontemporal_load(p);
+  else return *p;
+}
 
 // One wave computes Y[row, fbeg:fend) in edge order.  V | (fend - fbeg) and
 // V | F are guaranteed by the host.
@@ -83,8 +95,8 @@ __device__ __forceinline__ void wave_row_exact(const int64_t* __restrict__ col, 
     int next_col = 0;
     float next_w = 1.f;
     if (rs < re && lane < re - rs) {
-      next_col = static_cast<int>(col[rs + lane]);
-      if constexpr (HAS_VAL) next_w = val[rs + lane];
+      next_col = static_cast<int>(stream_load(col + rs + lane));
+      if constexpr (HAS_VAL) next_w = stream_load(val + rs + lane);
     }
     for (int64_t base = rs; base < re; base += kWave) {
       const int cnt = static_cast<int>((re - base) < kWave ? (re - base) : kWave);
@@ -92,8 +104,8 @@ __device__ __forceinline__ void wave_row_exact(const int64_t* __restrict__ col, 
       const float my_w = next_w;
       const int64_t nb = base + kWave;
       if (nb < re && lane < re - nb) {
-        next_col = static_cast<int>(col[nb + lane]);
-        if constexpr (HAS_VAL) next_w = val[nb + lane];
+        next_col = static_cast<int>(stream_load(col + nb + lane));
+        if constexpr (HAS_VAL) next_w = stream_load(val + nb + lane);
       }
       for (int j = 0; j < cnt; j += U) {
         FVec<V> xv[U];

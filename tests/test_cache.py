@@ -102,14 +102,15 @@ def test_cpu_device_signature():
     assert device_signature() == {"type": "cpu", "torch": torch.__version__}
 
 
-def test_signatures_match_golden_vectors():
-    path = GOLDEN / "scheduler_golden.json"
-    if not path.exists():
-        pytest.skip("golden signature vectors not generated")
-    cases = json.loads(path.read_text())
-    for case in cases["signatures"]:
-        crow = torch.tensor(case["crow"], dtype=torch.long)
-        col = torch.tensor(case["col"], dtype=torch.long)
+def test_signatures_match_reference_golden():
+    """graph_signature dictionaries, structure hash included, equal the
+    reference's for the same inputs."""
+    g = json.loads((GOLDEN / "scheduler_golden.json").read_text())
+    assert len(g["signatures"]) >= 12
+    for case in g["signatures"]:
+        gr = g["graphs"][case["graph"]]
+        crow = torch.tensor(gr["crow"], dtype=torch.long)
+        col = torch.tensor(gr["col"], dtype=torch.long)
         dtype = None if case["dtype"] is None else getattr(torch, case["dtype"].split(".")[-1])
         got = graph_signature(crow, col, case["feature_width"], case["operation"], weighted=case["weighted"],
                               dtype=dtype)
