@@ -50,6 +50,21 @@ def attention_bytes(n: int, nnz: int, fqk: int, fv: int) -> int:
     return 4 * fqk * nnz + 4 * fqk * n + 4 * fv * nnz + 4 * fv * n + 8 * nnz + 8 * (n + 1)
 
 
+def profiled_traffic(workload: str, variant: str):
+    """Per-launch HBM-side traffic (bytes) measured with rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs for this exact workload and variant, read from the
+    ``<!-- traffic: {...} -->`` record of a summary under profiles/; None when
+    no record matches."""
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text(encoding="utf-8").splitlines():
+            line = line.strip()
+            if line.startswith("<!-- traffic:") and line.endswith("-->"):
+                record = json.loads(line[len("<!-- traffic:"):-3])
+                if record.get("workload") == workload and record.get("variant") == variant:
+                    return record
+    return None
+
+
 def time_steps(fn, steps: int, warmup: int) -> tuple[float, list[float]]:
     """Warmup, then ``steps`` back-to-back calls between two events on the
     current stream (the stream the kernels are launched on)."""
@@ -188,6 +203,8 @@ def main() -> int:
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * nnz * f
         algo = spmm_bytes(n, nnz, f, weighted)
+        workload_name = f"{args.workload} SpMM fp32 F={f}" + (" weighted" if weighted else " unweighted")
+        traffic = profiled_traffic(workload_name, chosen)
         result = {
             "metric": METRIC,
             "value": round(flops / (ms * 1e-3) / 1e9, 2),
@@ -202,7 +219,7 @@ def main() -> int:
             "dtype": "f32",
             "data": "synthetic",
             "config": {
-                "workload": f"{args.workload} SpMM fp32 F={f}" + (" weighted" if weighted else " unweighted"),
+                "workload": workload_name,
                 "rows": n,
                 "nnz": nnz,
                 "features": f,
@@ -216,8 +233,11 @@ def main() -> int:
                 "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s",
                 "frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                "traffic": None,
+                "traffic": None if traffic is None else traffic["bytes"],
                 "algorithmic_bytes": algo,
+                "traffic_source": None if traffic is None else traffic["source"],
+                "traffic_gbps_at_this_step_time": None if traffic is None
+                else round(traffic["bytes"] / (ms * 1e-3) / 1e9, 1),
             },
             "per_call_ms": [round(s, 4) for s in samples],
             "calibration_ms": calib,
