@@ -20,6 +20,20 @@ __device__ __forceinline__ float bcast_f32(float v, int src) {
 __device__ __forceinline__ int uniform_i32(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
+// A 64-bit value every lane holds identically, moved to SGPRs so that
+// control flow and address arithmetic on it stay scalar.
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+// Element offset of row c in a row-major [*, F] matrix, for c < 2^31 and
+// F < 2^31 (one 32x32->64 multiply).
+__device__ __forceinline__ int64_t row_offset(int c, int64_t F) {
+  return static_cast<int64_t>(static_cast<uint64_t>(static_cast<uint32_t>(c)) *
+                              static_cast<uint64_t>(static_cast<uint32_t>(F)));
+}
 
 // V consecutive floats owned by one lane.  Component-wise arithmetic is
 // written out so that no packed-fp32 instruction is needed.
@@ -31,6 +45,12 @@ struct alignas(4 * V) FVec {
 template <int V>
 __device__ __forceinline__ FVec<V> load_vec(const float* p) {
   return *reinterpret_cast<const FVec<V>*>(p);
+}
+// Load from a wave-uniform base plus a per-lane byte offset below 2^32, the
+// shape of the SGPR-base global load.
+template <int V>
+__device__ __forceinline__ FVec<V> load_vec_off(const float* base, uint32_t byte_offset) {
+  return *reinterpret_cast<const FVec<V>*>(reinterpret_cast<const char*>(base) + byte_offset);
 }
 template <int V>
 __device__ __forceinline__ void store_vec(float* p, const FVec<V>& a) {

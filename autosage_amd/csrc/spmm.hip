@@ -78,16 +78,22 @@ __device__ __forceinline__ T stream_load(const T* p) {
 }
 
 // One wave computes Y[row, fbeg:fend) in edge order.  V | (fend - fbeg) and
-// V | F are guaranteed by the host.
+// V | F are guaranteed by the host; row, rs, re, fbeg, fend are wave-uniform.
+// Lanes past fend load a valid in-row address and store nothing, so the
+// gathers carry no per-lane branches; full batches of U edges run without
+// bound checks and the remainder one edge at a time.
 template <int V, bool HAS_VAL, int U>
 __device__ __forceinline__ void wave_row_exact(const int64_t* __restrict__ col, const float* __restrict__ val,
                                                const float* __restrict__ x, float* __restrict__ y, int64_t F,
                                                int64_t row, int64_t rs, int64_t re, int64_t fbeg, int64_t fend) {
   const int lane = lane_id();
+  rs = uniform_i64(rs);
+  re = uniform_i64(re);
   for (int64_t f0 = fbeg; f0 < fend; f0 += kWave * V) {
     const int64_t fl = f0 + static_cast<int64_t>(lane) * V;
     const bool active = fl < fend;
-    const float* xf = x + fl;
+    // byte offset of this lane's features inside an X row (< 2^32 since F < 2^29)
+    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : fbeg) * 4);
     float acc[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.f;
@@ -107,31 +113,38 @@ __device__ __forceinline__ void wave_row_exact(const int64_t* __restrict__ col, 
         next_col = static_cast<int>(stream_load(col + nb + lane));
         if constexpr (HAS_VAL) next_w = stream_load(val + nb + lane);
       }
-      for (int j = 0; j < cnt; j += U) {
+      int j = 0;
+      for (; j + U <= cnt; j += U) {
         FVec<V> xv[U];
         float w[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) xv[u].v[v] = 0.f;
-          w[u] = 1.f;
-          if (j + u < cnt) {
-            const int c = bcast_i32(my_col, j + u);
-            if constexpr (HAS_VAL) w[u] = bcast_f32(my_w, j + u);
-            if (active) xv[u] = load_vec<V>(xf + static_cast<int64_t>(c) * F);
-          }
+          const int c = bcast_i32(my_col, j + u);
+          w[u] = HAS_VAL ? bcast_f32(my_w, j + u) : 1.f;
+          xv[u] = load_vec_off<V>(x + row_offset(c, F), lane_bytes);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          if (j + u < cnt) {
 #pragma unroll
-            for (int v = 0; v < V; ++v) {
-              if constexpr (HAS_VAL) {
-                acc[v] = __builtin_fmaf(w[u], xv[u].v[v], acc[v]);
-              } else {
-                acc[v] = acc[v] + xv[u].v[v];
-              }
+          for (int v = 0; v < V; ++v) {
+            if constexpr (HAS_VAL) {
+              acc[v] = __builtin_fmaf(w[u], xv[u].v[v], acc[v]);
+            } else {
+              acc[v] = acc[v] + xv[u].v[v];
             }
+          }
+        }
+      }
+      for (; j < cnt; ++j) {
+        const int c = bcast_i32(my_col, j);
+        const FVec<V> xv = load_vec_off<V>(x + row_offset(c, F), lane_bytes);
+        const float w = HAS_VAL ? bcast_f32(my_w, j) : 1.f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (HAS_VAL) {
+            acc[v] = __builtin_fmaf(w, xv.v[v], acc[v]);
+          } else {
+            acc[v] = acc[v] + xv.v[v];
           }
         }
       }
@@ -206,9 +219,9 @@ __device__ __forceinline__ void light_wave(const int64_t* __restrict__ crow, con
   using LI = LayoutInfo<LAYOUT>;
   if constexpr (LI::LPR == kWave) {
     if (wave_index >= limit) return;
-    const int64_t row = rows ? static_cast<int64_t>(rows[wave_index]) : wave_index;
-    const int64_t rs = crow[row];
-    const int64_t re = crow[row + 1];
+    const int64_t row = uniform_i64(rows ? static_cast<int64_t>(rows[wave_index]) : wave_index);
+    const int64_t rs = uniform_i64(crow[row]);
+    const int64_t re = uniform_i64(crow[row + 1]);
     if (re - rs >= kLongRow) {
       wave_row_exact<LI::V, HAS_VAL, kHubUnroll>(col, val, x, y, F, row, rs, re, 0, F);
     } else {
@@ -322,9 +335,9 @@ __global__ __launch_bounds__(512) void spmm_scheduled_kernel(const int64_t* __re
   const int64_t item = item_base + blockIdx.x;
   const int64_t heavy = counts[0];
   if (item < heavy) {
-    const int64_t row = order[item];
-    const int64_t rs = crow[row];
-    const int64_t re = crow[row + 1];
+    const int64_t row = uniform_i64(order[item]);
+    const int64_t rs = uniform_i64(crow[row]);
+    const int64_t re = uniform_i64(crow[row + 1]);
     if constexpr (SPLIT64) {
       hub_row_split64<HV, HAS_VAL>(col, val, x, y, F, row, rs, re);
     } else {
@@ -359,9 +372,12 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 int rows_per_wave(int layout) { return layout == kSub16 ? 4 : layout == kSub32 ? 2 : 1; }
 
 // Mean degree below which float4 sub-wave rows are used for short rows
-// (when vec4 is allowed).
+// (when vec4 is allowed).  Off by default: one wave per row with SGPR column
+// broadcast measured faster on every graph tried, including 16 nonzeros per
+// row (1.21 vs 1.30 ms on 2^20 rows, F = 128), because the sub-wave form
+// needs one vector load of the column index per edge.
 #ifndef AS_SUBWAVE_MAX_MEAN_DEGREE
-#define AS_SUBWAVE_MAX_MEAN_DEGREE 48
+#define AS_SUBWAVE_MAX_MEAN_DEGREE 0
 #endif
 constexpr int64_t kSubwaveMaxMeanDegree = AS_SUBWAVE_MAX_MEAN_DEGREE;
 
@@ -369,6 +385,9 @@ constexpr int64_t kSubwaveMaxMeanDegree = AS_SUBWAVE_MAX_MEAN_DEGREE;
 // rows when vec4 is allowed and rows are short on average, otherwise one
 // wave per row (column broadcast through SGPRs).
 int pick_layout(const SpmmArgs& a, int64_t nnz, int feature_tile, bool vec4) {
+#ifdef AS_FORCE_LAYOUT
+  return AS_FORCE_LAYOUT;
+#endif
   const bool short_rows = nnz < kSubwaveMaxMeanDegree * a.n;
   const bool v4 = vec4 && a.f % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
   const bool v2 = a.f % 2 == 0 && aligned(a.x, 8) && aligned(a.y, 8);
