@@ -30,8 +30,8 @@ __global__ __launch_bounds__(kBlock) void csr_row_softmax_kernel(const int64_t* 
   const int lane = lane_id();
   const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
   if (row >= n) return;
-  const int64_t rs = crow[row];
-  const int64_t re = crow[row + 1];
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
   if (rs == re) return;
   float m = -INFINITY;
   for (int64_t e = rs + lane; e < re; e += kWave) m = fmaxf(m, scores[e]);
@@ -75,8 +75,8 @@ __global__ __launch_bounds__(kBlock) void csr_attention_kernel(
   const int j = lane % G;
   const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
   if (row >= n) return;
-  const int64_t rs = crow[row];
-  const int64_t re = crow[row + 1];
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
 
   float m = -INFINITY;
   float d = 0.f;
@@ -103,8 +103,8 @@ __global__ __launch_bounds__(kBlock) void csr_attention_kernel(
           e[u] = base + u * NG + g;
           ok[u] = e[u] < re;
           const int64_t ee = ok[u] ? e[u] : re - 1;
-          const int64_t c = static_cast<int>(col[ee]);
-          const float* kr = key + c * Fqk + S * j;
+          const int c = static_cast<int>(col[ee]);
+          const float* kr = key + row_offset(c, Fqk) + S * j;
 #pragma unroll
           for (int mm = 0; mm < MF; ++mm) kv[u][mm] = load_vec<S>(kr + 32 * mm);
         }
@@ -128,8 +128,8 @@ __global__ __launch_bounds__(kBlock) void csr_attention_kernel(
         const int64_t e = base + g;
         const bool ok = e < re;
         const int64_t ee = ok ? e : re - 1;
-        const int64_t c = static_cast<int>(col[ee]);
-        const float* kr = key + c * Fqk;
+        const int c = static_cast<int>(col[ee]);
+        const float* kr = key + row_offset(c, Fqk);
         float p[1] = {0.f};
         for (int64_t f = j; f < Fqk; f += 32) p[0] = __builtin_fmaf(qrow[f], kr[f], p[0]);
         const float sc = ref_tree_a<1>(p) * scale;
@@ -147,12 +147,14 @@ __global__ __launch_bounds__(kBlock) void csr_attention_kernel(
     d = wave_sum_f32(d);
   }
 
-  // Pass C: out = sum_e p_e · V[col_e] in edge order (wave-row SpMM layout).
+  // Pass C: out = sum_e p_e · V[col_e] in edge order (wave-row SpMM layout:
+  // unchecked full batches of U edges, then the remainder; lanes past Fv load
+  // a valid address and store nothing).
   constexpr int P = kWave * VV;
   for (int64_t f0 = 0; f0 < Fv; f0 += P) {
     const int64_t fl = f0 + static_cast<int64_t>(lane) * VV;
     const bool active = fl < Fv;
-    const float* vf = value + fl;
+    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : 0) * 4);
     float acc[VV];
 #pragma unroll
     for (int v = 0; v < VV; ++v) acc[v] = 0.f;
@@ -164,27 +166,28 @@ __global__ __launch_bounds__(kBlock) void csr_attention_kernel(
         my_col = static_cast<int>(col[base + lane]);
         my_p = expf(scratch[base + lane] - m) / d;
       }
-      for (int jj = 0; jj < cnt; jj += U) {
+      int jj = 0;
+      for (; jj + U <= cnt; jj += U) {
         FVec<VV> xv[U];
         float w[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-#pragma unroll
-          for (int v = 0; v < VV; ++v) xv[u].v[v] = 0.f;
-          w[u] = 0.f;
-          if (jj + u < cnt) {
-            const int c = bcast_i32(my_col, jj + u);
-            w[u] = bcast_f32(my_p, jj + u);
-            if (active) xv[u] = load_vec<VV>(vf + static_cast<int64_t>(c) * Fv);
-          }
+          const int c = bcast_i32(my_col, jj + u);
+          w[u] = bcast_f32(my_p, jj + u);
+          xv[u] = load_vec_off<VV>(value + row_offset(c, Fv), lane_bytes);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          if (jj + u < cnt) {
 #pragma unroll
-            for (int v = 0; v < VV; ++v) acc[v] = __builtin_fmaf(w[u], xv[u].v[v], acc[v]);
-          }
+          for (int v = 0; v < VV; ++v) acc[v] = __builtin_fmaf(w[u], xv[u].v[v], acc[v]);
         }
+      }
+      for (; jj < cnt; ++jj) {
+        const int c = bcast_i32(my_col, jj);
+        const float w = bcast_f32(my_p, jj);
+        const FVec<VV> xv = load_vec_off<VV>(value + row_offset(c, Fv), lane_bytes);
+#pragma unroll
+        for (int v = 0; v < VV; ++v) acc[v] = __builtin_fmaf(w, xv.v[v], acc[v]);
       }
     }
     if (active) {

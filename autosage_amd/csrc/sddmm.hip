@@ -55,8 +55,8 @@ __device__ __forceinline__ void dot_edges_vec(const int64_t* __restrict__ col, c
     e[u] = first + u * stride + g;
     ok[u] = e[u] < end;
     const int64_t ee = ok[u] ? e[u] : end - 1;
-    const int64_t c = static_cast<int>(col[ee]);
-    const float* kr = key + c * F + S * j;
+    const int c = static_cast<int>(col[ee]);
+    const float* kr = key + row_offset(c, F) + S * j;
 #pragma unroll
     for (int m = 0; m < MF; ++m) kv[u][m] = load_vec<S>(kr + 32 * m);
   }
@@ -83,8 +83,8 @@ __device__ __forceinline__ void dot_edges_scalar(const int64_t* __restrict__ col
   const int64_t e = first + g;
   const bool ok = e < end;
   const int64_t ee = ok ? e : end - 1;
-  const int64_t c = static_cast<int>(col[ee]);
-  const float* kr = key + c * F;
+  const int c = static_cast<int>(col[ee]);
+  const float* kr = key + row_offset(c, F);
   float p[1] = {0.f};
   for (int64_t f = j; f < F; f += 32) p[0] = __builtin_fmaf(qrow[f], kr[f], p[0]);
   const float d = ref_tree<1>(p);
@@ -119,8 +119,8 @@ __global__ __launch_bounds__(kBlock) void sddmm_rows_vec_kernel(const int64_t* _
   const int j = lane % G;
   const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
   if (row >= n) return;
-  const int64_t rs = crow[row];
-  const int64_t re = crow[row + 1];
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
   if (re - rs >= hub_threshold || re == rs) return;
   float qv[MF][32 / G];
   load_query<G, MF>(query + row * F, j, qv);
@@ -140,8 +140,8 @@ __global__ __launch_bounds__(kBlock) void sddmm_rows_scalar_kernel(const int64_t
   const int j = lane % 32;
   const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
   if (row >= n) return;
-  const int64_t rs = crow[row];
-  const int64_t re = crow[row + 1];
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
   if (re - rs >= hub_threshold || re == rs) return;
   const float* qrow = query + row * F;
   for (int64_t base = rs; base < re; base += 2) dot_edges_scalar(col, qrow, key, out, F, base, 2, re, g, j);
@@ -213,10 +213,10 @@ __global__ __launch_bounds__(512) void sddmm_hub_chunks_kernel(const int64_t* __
       if (chunk_off[mid] <= item) lo = mid;
       else hi = mid - 1;
     }
-    const int64_t row = order[lo];
-    const int64_t rs = crow[row];
-    const int64_t re = crow[row + 1];
-    const int64_t cs = rs + (item - chunk_off[lo]) * kChunkEdges;
+    const int64_t row = uniform_i64(order[lo]);
+    const int64_t rs = uniform_i64(crow[row]);
+    const int64_t re = uniform_i64(crow[row + 1]);
+    const int64_t cs = rs + (item - uniform_i64(chunk_off[lo])) * kChunkEdges;
     const int64_t ce = cs + kChunkEdges < re ? cs + kChunkEdges : re;
     if constexpr (VEC) {
       float qv[MF][32 / G];
