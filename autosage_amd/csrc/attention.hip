@@ -11,11 +11,13 @@
 //   p_e = exp(s_e - m) / d             (IEEE division)
 //
 // The fused kernel computes, per row, the same scores as the SDDMM kernels
-// (reference dot order) times `scale`, stores them in a caller-provided
+// (reference dot order) times `scale`, stores them in the workspace's
 // nnz-float scratch, derives m and d exactly as above and then accumulates
 // out[r, :] = sum_e p_e · V[col_e, :] in edge order with fmaf, as the SpMM
 // kernels do.  With scale 1 (or a power of two) it is therefore
-// bit-identical to the three unfused stages.
+// bit-identical to the three unfused stages.  Rows of degree >= 1024 are
+// binned (longest bucket first, as for the split SpMM) and each gets a
+// workgroup whose waves share the scoring and split the value features.
 #include "as_device.h"
 #include "as_internal.h"
 
@@ -57,104 +59,117 @@ __device__ __forceinline__ float ref_tree_a(float (&p)[S]) {
   return p[0];
 }
 
-// QVEC: query/key rows as 8 lanes × float4 per 32 features (MF blocks);
-// otherwise 32 lanes per edge with scalar loads (any F_qk).
-// VV: value floats per lane, a pass covers 64·VV value features.
-template <bool QVEC, int MF, int VV>
-__global__ __launch_bounds__(kBlock) void csr_attention_kernel(
-    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const float* __restrict__ query,
-    const float* __restrict__ key, const float* __restrict__ value, float* __restrict__ out,
-    float* __restrict__ scratch, int64_t n, int64_t Fqk, int64_t Fv, float scale, int64_t idx_base) {
+// Rows at least this long are hub rows of the fused kernel: a workgroup of
+// kAttWaves waves takes each of them, longest degree bucket first.
+#ifndef AS_ATT_HUB_DEGREE
+#define AS_ATT_HUB_DEGREE 1024
+#endif
+constexpr int64_t kAttHubDegree = AS_ATT_HUB_DEGREE;
+constexpr int kAttWaves = 4;
+constexpr int kAttBuckets = 8;
+
+// Pass A for one wave: scores of the edge groups starting at `first`,
+// `first + step`, ... (each group = UE·NG consecutive edges) into scratch,
+// returning this wave's running max over the edges it scored.
+// QVEC: 8 lanes × float4 per 32 query/key features (MF blocks); otherwise
+// 32 lanes per edge with scalar loads (any F_qk).
+template <bool QVEC, int MF>
+__device__ __forceinline__ float att_scores(const int64_t* __restrict__ col, const float* __restrict__ key,
+                                            float* __restrict__ scratch, const float* __restrict__ qrow,
+                                            int64_t Fqk, float scale, int64_t first, int64_t step, int64_t re) {
   constexpr int G = QVEC ? 8 : 32;
   constexpr int S = 32 / G;
   constexpr int NG = kWave / G;
   constexpr int UE = QVEC ? (MF <= 2 ? 4 : 2) : 1;
-  constexpr int U = 8;
   const int lane = lane_id();
   const int g = lane / G;
   const int j = lane % G;
-  const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
-  if (row >= n) return;
-  const int64_t rs = uniform_i64(crow[row]);
-  const int64_t re = uniform_i64(crow[row + 1]);
-
-  float m = -INFINITY;
-  float d = 0.f;
-  if (rs < re) {
-    // Pass A: scores (reference SDDMM order) into scratch, running max.
-    float qv[QVEC ? MF : 1][S];
-    const float* qrow = query + row * Fqk;
-    if constexpr (QVEC) {
+  float qv[QVEC ? MF : 1][S];
+  if constexpr (QVEC) {
 #pragma unroll
-      for (int mm = 0; mm < MF; ++mm) {
-        const FVec<S> t = load_vec<S>(qrow + 32 * mm + S * j);
+    for (int mm = 0; mm < MF; ++mm) {
+      const FVec<S> t = load_vec<S>(qrow + 32 * mm + S * j);
 #pragma unroll
-        for (int s = 0; s < S; ++s) qv[mm][s] = t.v[s];
-      }
+      for (int s = 0; s < S; ++s) qv[mm][s] = t.v[s];
     }
-    float mloc = -INFINITY;
-    for (int64_t base = rs; base < re; base += NG * UE) {
-      if constexpr (QVEC) {
-        FVec<S> kv[UE][MF];
-        bool ok[UE];
-        int64_t e[UE];
-#pragma unroll
-        for (int u = 0; u < UE; ++u) {
-          e[u] = base + u * NG + g;
-          ok[u] = e[u] < re;
-          const int64_t ee = ok[u] ? e[u] : re - 1;
-          const int c = static_cast<int>(col[ee]);
-          const float* kr = key + row_offset(c, Fqk) + S * j;
-#pragma unroll
-          for (int mm = 0; mm < MF; ++mm) kv[u][mm] = load_vec<S>(kr + 32 * mm);
-        }
-#pragma unroll
-        for (int u = 0; u < UE; ++u) {
-          float p[S];
-#pragma unroll
-          for (int s = 0; s < S; ++s) p[s] = 0.f;
-#pragma unroll
-          for (int mm = 0; mm < MF; ++mm) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) p[s] = __builtin_fmaf(qv[mm][s], kv[u][mm].v[s], p[s]);
-          }
-          const float sc = ref_tree_a<S>(p) * scale;
-          if (ok[u]) {
-            mloc = fmaxf(mloc, sc);
-            if (j == 0) scratch[e[u]] = sc;
-          }
-        }
-      } else {
-        const int64_t e = base + g;
-        const bool ok = e < re;
-        const int64_t ee = ok ? e : re - 1;
-        const int c = static_cast<int>(col[ee]);
-        const float* kr = key + row_offset(c, Fqk);
-        float p[1] = {0.f};
-        for (int64_t f = j; f < Fqk; f += 32) p[0] = __builtin_fmaf(qrow[f], kr[f], p[0]);
-        const float sc = ref_tree_a<1>(p) * scale;
-        if (ok) {
-          mloc = fmaxf(mloc, sc);
-          if (j == 0) scratch[e] = sc;
-        }
-      }
-    }
-    m = wave_max_f32(mloc);
-    // The scratch scores were written by other lanes of this wave.
-    __threadfence_block();
-    // Pass B: denominator in the row-softmax order.
-    for (int64_t e = rs + lane; e < re; e += kWave) d += expf(scratch[e] - m);
-    d = wave_sum_f32(d);
   }
+  float mloc = -INFINITY;
+  for (int64_t base = first; base < re; base += step) {
+    if constexpr (QVEC) {
+      FVec<S> kv[UE][MF];
+      bool ok[UE];
+      int64_t e[UE];
+#pragma unroll
+      for (int u = 0; u < UE; ++u) {
+        e[u] = base + u * NG + g;
+        ok[u] = e[u] < re;
+        const int64_t ee = ok[u] ? e[u] : re - 1;
+        const int c = static_cast<int>(col[ee]);
+        const float* kr = key + row_offset(c, Fqk) + S * j;
+#pragma unroll
+        for (int mm = 0; mm < MF; ++mm) kv[u][mm] = load_vec<S>(kr + 32 * mm);
+      }
+#pragma unroll
+      for (int u = 0; u < UE; ++u) {
+        float p[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) p[s] = 0.f;
+#pragma unroll
+        for (int mm = 0; mm < MF; ++mm) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) p[s] = __builtin_fmaf(qv[mm][s], kv[u][mm].v[s], p[s]);
+        }
+        const float sc = ref_tree_a<S>(p) * scale;
+        if (ok[u]) {
+          mloc = fmaxf(mloc, sc);
+          if (j == 0) scratch[e[u]] = sc;
+        }
+      }
+    } else {
+      const int64_t e = base + g;
+      const bool ok = e < re;
+      const int64_t ee = ok ? e : re - 1;
+      const int c = static_cast<int>(col[ee]);
+      const float* kr = key + row_offset(c, Fqk);
+      float p[1] = {0.f};
+      for (int64_t f = j; f < Fqk; f += 32) p[0] = __builtin_fmaf(qrow[f], kr[f], p[0]);
+      const float sc = ref_tree_a<1>(p) * scale;
+      if (ok) {
+        mloc = fmaxf(mloc, sc);
+        if (j == 0) scratch[e] = sc;
+      }
+    }
+  }
+  return mloc;
+}
 
-  // Pass C: out = sum_e p_e · V[col_e] in edge order (wave-row SpMM layout:
-  // unchecked full batches of U edges, then the remainder; lanes past Fv load
-  // a valid address and store nothing).
-  constexpr int P = kWave * VV;
-  for (int64_t f0 = 0; f0 < Fv; f0 += P) {
+template <bool QVEC, int MF>
+constexpr int64_t att_group_edges() {
+  return QVEC ? (kWave / 8) * (MF <= 2 ? 4 : 2) : 2;
+}
+
+// Pass B: the row softmax denominator in the canonical order.
+__device__ __forceinline__ float att_denominator(const float* __restrict__ scratch, float m, int64_t rs, int64_t re) {
+  float d = 0.f;
+  for (int64_t e = rs + lane_id(); e < re; e += kWave) d += expf(scratch[e] - m);
+  return wave_sum_f32(d);
+}
+
+// Pass C for one wave: out[row, fbeg:fend) = sum_e p_e · V[col_e, fbeg:fend)
+// in edge order (wave-row SpMM layout: unchecked full batches of U edges,
+// then the remainder; lanes past fend load a valid address and store
+// nothing).  VV | (fend - fbeg).
+template <int VV>
+__device__ __forceinline__ void att_accumulate(const int64_t* __restrict__ col, const float* __restrict__ value,
+                                               const float* __restrict__ scratch, float* __restrict__ out,
+                                               int64_t Fv, int64_t row, int64_t rs, int64_t re, float m, float d,
+                                               int64_t fbeg, int64_t fend) {
+  constexpr int U = 8;
+  const int lane = lane_id();
+  for (int64_t f0 = fbeg; f0 < fend; f0 += kWave * VV) {
     const int64_t fl = f0 + static_cast<int64_t>(lane) * VV;
-    const bool active = fl < Fv;
-    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : 0) * 4);
+    const bool active = fl < fend;
+    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : fbeg) * 4);
     float acc[VV];
 #pragma unroll
     for (int v = 0; v < VV; ++v) acc[v] = 0.f;
@@ -199,26 +214,114 @@ __global__ __launch_bounds__(kBlock) void csr_attention_kernel(
   }
 }
 
+// Fused attention.  Workgroups of kAttWaves waves; work item = workgroup
+// index.  Items [0, H): hub row order[item] — the waves split the row's
+// edges for the scores, combine their maxima in LDS, each computes the
+// denominator in the canonical order, and they split the value features
+// for the weighted sum.  Items >= H: groups of kAttWaves light rows, one per
+// wave, all passes on that wave.  Both give the same bits as the unfused
+// SDDMM -> softmax -> SpMM stages.
+template <bool QVEC, int MF, int VV, int HV>
+__global__ __launch_bounds__(kAttWaves * kWave) void csr_attention_kernel(
+    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const float* __restrict__ query,
+    const float* __restrict__ key, const float* __restrict__ value, float* __restrict__ out,
+    float* __restrict__ scratch, int64_t n, int64_t Fqk, int64_t Fv, float scale,
+    const int32_t* __restrict__ order, const int32_t* __restrict__ counts, int64_t item_base) {
+  __shared__ float wave_max[kAttWaves];
+  constexpr int64_t GE = att_group_edges<QVEC, MF>();
+  const int wave = wave_in_block();
+  const int64_t item = item_base + blockIdx.x;
+  const int64_t heavy = counts[0];
+  if (item < heavy) {
+    const int64_t row = uniform_i64(order[item]);
+    const int64_t rs = uniform_i64(crow[row]);
+    const int64_t re = uniform_i64(crow[row + 1]);
+    const float mw = att_scores<QVEC, MF>(col, key, scratch, query + row * Fqk, Fqk, scale, rs + wave * GE,
+                                          kAttWaves * GE, re);
+    const float mwave = wave_max_f32(mw);
+    if (lane_id() == 0) wave_max[wave] = mwave;
+    __threadfence_block();
+    __syncthreads();
+    float m = wave_max[0];
+#pragma unroll
+    for (int w = 1; w < kAttWaves; ++w) m = fmaxf(m, wave_max[w]);
+    const float d = att_denominator(scratch, m, rs, re);
+    int64_t slice = (Fv + kAttWaves - 1) / kAttWaves;
+    slice = (slice + HV - 1) / HV * HV;
+    const int64_t fbeg = wave * slice;
+    const int64_t fend = fbeg + slice < Fv ? fbeg + slice : Fv;
+    if (fbeg < Fv) att_accumulate<HV>(col, value, scratch, out, Fv, row, rs, re, m, d, fbeg, fend);
+    return;
+  }
+  const int64_t light_index = (item - heavy) * kAttWaves + wave;
+  if (light_index >= n - heavy) return;
+  const int64_t row = uniform_i64(order[heavy + light_index]);
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
+  float m = -INFINITY;
+  float d = 0.f;
+  if (rs < re) {
+    m = wave_max_f32(att_scores<QVEC, MF>(col, key, scratch, query + row * Fqk, Fqk, scale, rs, GE, re));
+    // The scratch scores were written by other lanes of this wave.
+    __threadfence_block();
+    d = att_denominator(scratch, m, rs, re);
+  }
+  att_accumulate<VV>(col, value, scratch, out, Fv, row, rs, re, m, d, 0, Fv);
+}
+
 bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-template <bool QVEC, int MF>
-void launch_attention_vv(int vv, dim3 grid, hipStream_t s, const int64_t* crow, const int64_t* col, const float* q,
-                         const float* k, const float* v, float* out, float* scratch, int64_t n, int64_t fqk,
-                         int64_t fv, float scale, int64_t base) {
-  switch (vv) {
-    case 4:
-      hipLaunchKernelGGL((csr_attention_kernel<QVEC, MF, 4>), grid, dim3(kBlock), 0, s, crow, col, q, k, v, out,
-                         scratch, n, fqk, fv, scale, base);
-      break;
-    case 2:
-      hipLaunchKernelGGL((csr_attention_kernel<QVEC, MF, 2>), grid, dim3(kBlock), 0, s, crow, col, q, k, v, out,
-                         scratch, n, fqk, fv, scale, base);
-      break;
-    default:
-      hipLaunchKernelGGL((csr_attention_kernel<QVEC, MF, 1>), grid, dim3(kBlock), 0, s, crow, col, q, k, v, out,
-                         scratch, n, fqk, fv, scale, base);
-      break;
+struct AttArgs {
+  const int64_t* crow;
+  const int64_t* col;
+  const float* q;
+  const float* k;
+  const float* v;
+  float* out;
+  float* scratch;
+  int64_t n;
+  int64_t fqk;
+  int64_t fv;
+  float scale;
+  const int32_t* order;
+  const int32_t* counts;
+};
+
+template <bool QVEC, int MF, int VV, int HV>
+void launch_att_t(const AttArgs& a, int64_t blocks, hipStream_t s) {
+  for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
+    const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
+    hipLaunchKernelGGL((csr_attention_kernel<QVEC, MF, VV, HV>), dim3(static_cast<unsigned>(nb)),
+                       dim3(kAttWaves * kWave), 0, s, a.crow, a.col, a.q, a.k, a.v, a.out, a.scratch, a.n, a.fqk,
+                       a.fv, a.scale, a.order, a.counts, b0);
   }
+}
+
+template <bool QVEC, int MF>
+void launch_att_vv(int vv, int hv, const AttArgs& a, int64_t blocks, hipStream_t s) {
+  if (vv == 4) {
+    if (hv == 4) launch_att_t<QVEC, MF, 4, 4>(a, blocks, s);
+    else if (hv == 2) launch_att_t<QVEC, MF, 4, 2>(a, blocks, s);
+    else launch_att_t<QVEC, MF, 4, 1>(a, blocks, s);
+  } else if (vv == 2) {
+    if (hv == 2) launch_att_t<QVEC, MF, 2, 2>(a, blocks, s);
+    else launch_att_t<QVEC, MF, 2, 1>(a, blocks, s);
+  } else {
+    launch_att_t<QVEC, MF, 1, 1>(a, blocks, s);
+  }
+}
+
+// Lane vector width for `width` value features per wave.
+int value_vector(const float* v, const float* out, int64_t fv, int64_t width) {
+  if (fv % 4 == 0 && width > 128 && al(v, 16) && al(out, 16)) return 4;
+  if (fv % 2 == 0 && width > 64 && al(v, 8) && al(out, 8)) return 2;
+  return 1;
+}
+
+size_t attention_workspace(int64_t n, int64_t nnz) {
+  const size_t scratch = align_up(static_cast<size_t>(nnz > 0 ? nnz : 1) * sizeof(float), 256);
+  const size_t order = align_up(static_cast<size_t>(n > 0 ? n : 1) * sizeof(int32_t), 256);
+  return scratch + order + 256 + bin_workspace_bytes(n);
 }
 
 }  // namespace
@@ -245,8 +348,7 @@ int as_csr_row_softmax_f32(const int64_t* crow, const float* scores, float* prob
 }
 
 size_t as_csr_attention_workspace_bytes(int64_t n, int64_t nnz) {
-  (void)n;
-  return as::align_up(static_cast<size_t>(nnz > 0 ? nnz : 1) * sizeof(float), 256);
+  return as::attention_workspace(n < 0 ? 0 : n, nnz < 0 ? 0 : nnz);
 }
 
 int as_csr_attention_f32(const int64_t* crow, const int64_t* col, const float* query, const float* key,
@@ -261,37 +363,40 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col, const float* q
     return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (f_qk == 0 && nnz > 0)
     return as::fail(AS_ERR_UNSUPPORTED, "attention with zero query/key features is handled by the caller");
-  if (workspace == nullptr || workspace_bytes < as_csr_attention_workspace_bytes(n, nnz))
-    return as::fail(AS_ERR_WORKSPACE, "attention needs %zu workspace bytes, got %zu",
-                    as_csr_attention_workspace_bytes(n, nnz), workspace_bytes);
+  if (workspace == nullptr || workspace_bytes < as::attention_workspace(n, nnz))
+    return as::fail(AS_ERR_WORKSPACE, "attention needs %zu workspace bytes, got %zu", as::attention_workspace(n, nnz),
+                    workspace_bytes);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  float* scratch = static_cast<float*>(workspace);
+  char* ws = static_cast<char*>(workspace);
+  float* scratch = reinterpret_cast<float*>(ws);
+  ws += as::align_up(static_cast<size_t>(nnz > 0 ? nnz : 1) * sizeof(float), 256);
+  int32_t* order = reinterpret_cast<int32_t*>(ws);
+  ws += as::align_up(static_cast<size_t>(n) * sizeof(int32_t), 256);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws);
+  void* bin_ws = ws + 256;
+  int st = as::launch_bin_rows(crow, n, as::kAttHubDegree, as::kAttBuckets, order, counts, bin_ws, s);
+  if (st != AS_OK) return st;
+
   const bool qvec = f_qk > 0 && f_qk % 32 == 0 && f_qk / 32 <= 8 && as::al(query, 16) && as::al(key, 16);
-  int vv = 1;
-  if (f_v % 4 == 0 && f_v > 128 && as::al(value, 16) && as::al(out, 16)) vv = 4;
-  else if (f_v % 2 == 0 && f_v > 64 && as::al(value, 8) && as::al(out, 8)) vv = 2;
-  const int64_t blocks = (n + as::kWavesPerBlock - 1) / as::kWavesPerBlock;
-  for (int64_t b0 = 0; b0 < blocks; b0 += as::kMaxBlocksPerLaunch) {
-    const int64_t nb = blocks - b0 < as::kMaxBlocksPerLaunch ? blocks - b0 : as::kMaxBlocksPerLaunch;
-    const dim3 grid(static_cast<unsigned>(nb));
-    const int64_t base = b0 * as::kWavesPerBlock;
-#define AS_ATT(QV, MF) \
-  as::launch_attention_vv<QV, MF>(vv, grid, s, crow, col, query, key, value, out, scratch, n, f_qk, f_v, scale, base)
-    if (!qvec) {
-      AS_ATT(false, 1);
-    } else {
-      switch (static_cast<int>(f_qk / 32)) {
-        case 1: AS_ATT(true, 1); break;
-        case 2: AS_ATT(true, 2); break;
-        case 3: AS_ATT(true, 3); break;
-        case 4: AS_ATT(true, 4); break;
-        case 5: AS_ATT(true, 5); break;
-        case 6: AS_ATT(true, 6); break;
-        case 7: AS_ATT(true, 7); break;
-        default: AS_ATT(true, 8); break;
-      }
+  const int vv = as::value_vector(value, out, f_v, f_v);
+  const int hv = as::value_vector(value, out, f_v, (f_v + as::kAttWaves - 1) / as::kAttWaves);
+  int64_t heavy_upper = nnz / as::kAttHubDegree;
+  if (heavy_upper > n) heavy_upper = n;
+  const int64_t blocks = heavy_upper + (n + as::kAttWaves - 1) / as::kAttWaves;
+  const as::AttArgs a{crow, col, query, key, value, out, scratch, n, f_qk, f_v, scale, order, counts};
+  if (!qvec) {
+    as::launch_att_vv<false, 1>(vv, hv, a, blocks, s);
+  } else {
+    switch (static_cast<int>(f_qk / 32)) {
+      case 1: as::launch_att_vv<true, 1>(vv, hv, a, blocks, s); break;
+      case 2: as::launch_att_vv<true, 2>(vv, hv, a, blocks, s); break;
+      case 3: as::launch_att_vv<true, 3>(vv, hv, a, blocks, s); break;
+      case 4: as::launch_att_vv<true, 4>(vv, hv, a, blocks, s); break;
+      case 5: as::launch_att_vv<true, 5>(vv, hv, a, blocks, s); break;
+      case 6: as::launch_att_vv<true, 6>(vv, hv, a, blocks, s); break;
+      case 7: as::launch_att_vv<true, 7>(vv, hv, a, blocks, s); break;
+      default: as::launch_att_vv<true, 8>(vv, hv, a, blocks, s); break;
     }
-#undef AS_ATT
   }
   return as::check_launch("csr_attention");
 }
