@@ -27,7 +27,7 @@ from typing import Any, Callable, Optional
 
 import torch
 
-from ._cache import ScheduleCache, device_signature, graph_signature, log_probe
+from ._cache import ScheduleCache, device_signature, graph_signature_memo, log_probe
 from .config import SchedulerConfig
 from .ops import _normalize_csr, load_native, native_op, spmm_csr
 
@@ -356,7 +356,7 @@ def spmm_csr_auto(
     load_native()
     config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=k)
     device = device_signature()
-    graph = graph_signature(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
+    graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
     cache = ScheduleCache()
     if config.cache:
         record = cache.lookup(device, graph)
@@ -460,7 +460,7 @@ def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dic
         "from_cache": False,
     }
     device = device_signature()
-    graph = graph_signature(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
+    graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
     if config.cache:
         ScheduleCache().store(device, graph, result)
     log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})
@@ -508,7 +508,7 @@ def sddmm_csr_auto(
     load_native()
     config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=6)
     device = device_signature()
-    graph = graph_signature(crow, col, query.size(1), "sddmm", dtype=query.dtype)
+    graph = graph_signature_memo(crow, col, query.size(1), "sddmm", dtype=query.dtype)
     cache = ScheduleCache()
     if config.cache:
         record = cache.lookup(device, graph)

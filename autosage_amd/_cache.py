@@ -11,11 +11,14 @@ atomically (``:126-148``) and the JSONL probe log (``:151-157``).
 
 from __future__ import annotations
 
+import collections
 import hashlib
 import json
 import os
 import tempfile
+import threading
 import time
+import weakref
 from pathlib import Path
 from typing import Any, Optional
 
@@ -23,6 +26,14 @@ import torch
 
 CACHE_SCHEMA_VERSION = 1
 _HASH_EDGE = 1024  # entries hashed from each end of a long index vector
+
+# Steady-state memos that keep the per-call host work of the schedulers small
+# (no quantile sort, hash, device->host sync or JSON parse on a repeated
+# call).  Both cache values the functions below would recompute identically.
+_MEMO_LOCK = threading.Lock()
+_SIGNATURE_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+_SIGNATURE_MEMO_SIZE = 64
+_FILE_MEMO: dict[str, tuple[int, int, dict]] = {}
 
 
 def cache_directory() -> Path:
@@ -94,10 +105,66 @@ def graph_signature(
     }
 
 
+def graph_signature_memo(
+    crow: torch.Tensor,
+    col: torch.Tensor,
+    feature_width: int,
+    operation: str,
+    *,
+    weighted: bool = False,
+    dtype: Optional[torch.dtype] = None,
+) -> dict[str, Any]:
+    """``graph_signature`` memoised per live (crow, col) tensor pair.
+
+    The memo holds weak references to the two tensor objects and their
+    in-place version counters: a hit needs the very same objects, still
+    alive and unmodified, so the signature cannot be stale.  Saves the two
+    device->host syncs, the quantile sort and the hash on repeated calls."""
+    key = (id(crow), crow._version, id(col), col._version, int(feature_width), operation, bool(weighted), str(dtype))
+    with _MEMO_LOCK:
+        entry = _SIGNATURE_MEMO.get(key)
+        if entry is not None and entry[0]() is crow and entry[1]() is col:
+            _SIGNATURE_MEMO.move_to_end(key)
+            return dict(entry[2])
+    signature = graph_signature(crow, col, feature_width, operation, weighted=weighted, dtype=dtype)
+    try:
+        refs = (weakref.ref(crow), weakref.ref(col))
+    except TypeError:
+        return signature
+    with _MEMO_LOCK:
+        _SIGNATURE_MEMO[key] = (*refs, dict(signature))
+        while len(_SIGNATURE_MEMO) > _SIGNATURE_MEMO_SIZE:
+            _SIGNATURE_MEMO.popitem(last=False)
+    return signature
+
+
+def _file_stamp(path: Path) -> Optional[tuple[int, int]]:
+    try:
+        st = path.stat()
+    except OSError:
+        return None
+    return st.st_mtime_ns, st.st_size
+
+
 class ScheduleCache:
     def __init__(self, path: Optional[os.PathLike[str] | str] = None):
         self.path = Path(path) if path is not None else cache_directory() / "schedules.json"
-        self._records = self._load()
+        self._records = self._load_memo()
+
+    def _load_memo(self) -> dict[str, dict[str, Any]]:
+        """``_load`` unless the file is unchanged (same mtime and size) since
+        this process last parsed or wrote it."""
+        stamp = _file_stamp(self.path)
+        key = str(self.path)
+        with _MEMO_LOCK:
+            memo = _FILE_MEMO.get(key)
+            if stamp is not None and memo is not None and memo[:2] == stamp:
+                return dict(memo[2])
+        records = self._load()
+        if stamp is not None:
+            with _MEMO_LOCK:
+                _FILE_MEMO[key] = (*stamp, dict(records))
+        return records
 
     @staticmethod
     def _key(device: dict[str, Any], graph: dict[str, Any]) -> str:
@@ -136,6 +203,10 @@ class ScheduleCache:
         finally:
             if os.path.exists(temporary):
                 os.unlink(temporary)
+        stamp = _file_stamp(self.path)
+        if stamp is not None:
+            with _MEMO_LOCK:
+                _FILE_MEMO[str(self.path)] = (*stamp, dict(self._records))
 
 
 def log_probe(event: dict[str, Any]) -> None:
@@ -153,5 +224,6 @@ __all__ = [
     "cache_directory",
     "device_signature",
     "graph_signature",
+    "graph_signature_memo",
     "log_probe",
 ]

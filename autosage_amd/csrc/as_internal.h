@@ -33,12 +33,14 @@ constexpr int kBinTile = kBlock * kBinRowsPerThread;
 inline int64_t bin_tiles(int64_t n) { return (n + kBinTile - 1) / kBinTile; }
 constexpr int kMaxHeavyBuckets = 8;
 size_t bin_workspace_bytes(int64_t n);
-// Writes order[n] = heavy rows (in `buckets` degree buckets, longest bucket
-// first, ascending inside a bucket) then light rows ascending, and
-// counts[0] = heavy, counts[1] = light (counts[2..3] are left to callers).
-// The workspace holds the per-tile bin table and offsets.
+// Writes order[n] = heavy rows (degree >= threshold) in `buckets` log2
+// degree buckets, longest bucket first, then light rows in `light_buckets`
+// buckets, longest first; rows ascending inside a bucket.  counts[0] = heavy,
+// counts[1] = light (counts[2..3] are left to callers).  The workspace holds
+// the per-tile bin table and offsets.  buckets = light_buckets = 1 gives the
+// reference's two ascending lists.
 int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold,
-                    int buckets, int32_t* order, int32_t* counts,
-                    void* workspace, hipStream_t stream);
+                    int buckets, int light_buckets, int32_t* order,
+                    int32_t* counts, void* workspace, hipStream_t stream);
 
 }  // namespace as

@@ -3,13 +3,16 @@
 // Reference integer work: csrc/launcher_spmm.cu:13-18 (degrees) and :49-59
 // (heavy = degree >= T, heavy and light row lists ascending via at::nonzero).
 //
-// Generalised to K heavy buckets (1 <= K <= kMaxHeavyBuckets): a heavy row of
-// degree d goes to bucket K-1-min(K-1, floor(log2(d / T))), so bucket 0 holds
-// the longest rows.  The output is one permutation
-//   order = [bucket 0 rows, ..., bucket K-1 rows, light rows]
-// with each group ascending by row id, plus counts[0] = H (heavy rows) and
-// counts[1] = n - H.  With K = 1 this is exactly the reference's heavy list
-// followed by its light list.
+// Generalised to K heavy and L light buckets (1 <= K, L <= kMaxHeavyBuckets):
+// a heavy row of degree d goes to bucket K-1-min(K-1, floor(log2(d / T))), so
+// bucket 0 holds the longest rows; a light row (d < T) goes to bucket
+// K + min(L-1, floor(log2((T-1) / d))) (empty rows to the last bucket), so
+// light rows are also ordered from long to short.  The output is one
+// permutation
+//   order = [bucket 0 rows, ..., bucket K+L-1 rows]
+// with each bucket ascending by row id, plus counts[0] = H (heavy rows) and
+// counts[1] = n - H.  With K = L = 1 this is exactly the reference's heavy
+// list followed by its light list.
 //
 // Three kernels over tiles of kBinTile rows:
 //   hist    — per-tile count of every bin (bin-major table);
@@ -24,8 +27,14 @@ namespace as {
 
 namespace {
 
-__device__ __forceinline__ int bin_of(int64_t deg, int64_t threshold, int buckets) {
-  if (deg < threshold) return buckets;  // light
+__device__ __forceinline__ int bin_of(int64_t deg, int64_t threshold, int buckets, int light_buckets) {
+  if (deg < threshold) {
+    if (deg == 0) return buckets + light_buckets - 1;
+    const uint64_t q = static_cast<uint64_t>((threshold - 1) / deg);  // >= 1
+    int level = 63 - __clzll(static_cast<long long>(q));
+    if (level > light_buckets - 1) level = light_buckets - 1;
+    return buckets + level;
+  }
   const uint64_t q = static_cast<uint64_t>(deg / threshold);  // >= 1
   int level = 63 - __clzll(static_cast<long long>(q));
   if (level > buckets - 1) level = buckets - 1;
@@ -54,22 +63,23 @@ __device__ __forceinline__ int block_excl_scan(int v, int* lds, int* total) {
 }
 
 __device__ __forceinline__ void row_bins(const int64_t* __restrict__ crow, int64_t n, int64_t threshold,
-                                         int buckets, int64_t first, int (&bin)[kBinRowsPerThread]) {
+                                         int buckets, int light_buckets, int64_t first,
+                                         int (&bin)[kBinRowsPerThread]) {
 #pragma unroll
   for (int i = 0; i < kBinRowsPerThread; ++i) {
     const int64_t r = first + i;
-    bin[i] = r < n ? bin_of(crow[r + 1] - crow[r], threshold, buckets) : -1;
+    bin[i] = r < n ? bin_of(crow[r + 1] - crow[r], threshold, buckets, light_buckets) : -1;
   }
 }
 
 __global__ __launch_bounds__(kBlock) void bin_hist_kernel(const int64_t* __restrict__ crow, int64_t n,
-                                                          int64_t threshold, int buckets, int64_t tiles,
-                                                          int32_t* __restrict__ table) {
+                                                          int64_t threshold, int buckets, int light_buckets,
+                                                          int64_t tiles, int32_t* __restrict__ table) {
   __shared__ int lds[kBlock / kWave];
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kBinTile + threadIdx.x * kBinRowsPerThread;
   int bin[kBinRowsPerThread];
-  row_bins(crow, n, threshold, buckets, first, bin);
-  for (int b = 0; b <= buckets; ++b) {
+  row_bins(crow, n, threshold, buckets, light_buckets, first, bin);
+  for (int b = 0; b < buckets + light_buckets; ++b) {
     int c = 0;
 #pragma unroll
     for (int i = 0; i < kBinRowsPerThread; ++i) c += bin[i] == b ? 1 : 0;
@@ -111,14 +121,14 @@ __global__ __launch_bounds__(kScanThreads) void bin_scan_kernel(const int32_t* _
 }
 
 __global__ __launch_bounds__(kBlock) void bin_scatter_kernel(const int64_t* __restrict__ crow, int64_t n,
-                                                             int64_t threshold, int buckets, int64_t tiles,
-                                                             const int32_t* __restrict__ offsets,
+                                                             int64_t threshold, int buckets, int light_buckets,
+                                                             int64_t tiles, const int32_t* __restrict__ offsets,
                                                              int32_t* __restrict__ order) {
   __shared__ int lds[kBlock / kWave];
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kBinTile + threadIdx.x * kBinRowsPerThread;
   int bin[kBinRowsPerThread];
-  row_bins(crow, n, threshold, buckets, first, bin);
-  for (int b = 0; b <= buckets; ++b) {
+  row_bins(crow, n, threshold, buckets, light_buckets, first, bin);
+  for (int b = 0; b < buckets + light_buckets; ++b) {
     int c = 0;
 #pragma unroll
     for (int i = 0; i < kBinRowsPerThread; ++i) c += bin[i] == b ? 1 : 0;
@@ -137,26 +147,27 @@ __global__ __launch_bounds__(kBlock) void bin_scatter_kernel(const int64_t* __re
 
 size_t bin_workspace_bytes(int64_t n) {
   const int64_t tiles = bin_tiles(n) > 0 ? bin_tiles(n) : 1;
-  return 2 * align_up(static_cast<size_t>(tiles) * (kMaxHeavyBuckets + 1) * sizeof(int32_t), 256);
+  return 2 * align_up(static_cast<size_t>(tiles) * (2 * kMaxHeavyBuckets) * sizeof(int32_t), 256);
 }
 
-int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold, int buckets, int32_t* order, int32_t* counts,
-                    void* workspace, hipStream_t stream) {
-  if (buckets < 1 || buckets > kMaxHeavyBuckets) return fail(AS_ERR_INVALID_ARGUMENT, "bad bucket count %d", buckets);
+int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold, int buckets, int light_buckets,
+                    int32_t* order, int32_t* counts, void* workspace, hipStream_t stream) {
+  if (buckets < 1 || buckets > kMaxHeavyBuckets || light_buckets < 1 || light_buckets > kMaxHeavyBuckets)
+    return fail(AS_ERR_INVALID_ARGUMENT, "bad bucket counts %d/%d", buckets, light_buckets);
   const int64_t tiles = bin_tiles(n);
   const size_t half = bin_workspace_bytes(n) / 2;
   int32_t* table = static_cast<int32_t*>(workspace);
   int32_t* offsets = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + half);
-  const int64_t entries = (buckets + 1) * tiles;
+  const int64_t entries = (buckets + light_buckets) * tiles;
   if (tiles > 0) {
     hipLaunchKernelGGL(bin_hist_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kBlock), 0, stream, crow, n,
-                       threshold, buckets, tiles, table);
+                       threshold, buckets, light_buckets, tiles, table);
   }
   hipLaunchKernelGGL(bin_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, table, entries, buckets * tiles, n,
                      offsets, counts);
   if (tiles > 0) {
     hipLaunchKernelGGL(bin_scatter_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kBlock), 0, stream, crow, n,
-                       threshold, buckets, tiles, offsets, order);
+                       threshold, buckets, light_buckets, tiles, offsets, order);
   }
   return check_launch("bin_rows_by_degree");
 }
@@ -177,7 +188,7 @@ int as_bin_rows_by_degree(const int64_t* crow, int64_t n, int64_t threshold, int
   if (workspace == nullptr || workspace_bytes < as::bin_workspace_bytes(n))
     return as::fail(AS_ERR_WORKSPACE, "binning needs %zu workspace bytes, got %zu", as::bin_workspace_bytes(n),
                     workspace_bytes);
-  return as::launch_bin_rows(crow, n, threshold, 1, order, counts, workspace, static_cast<hipStream_t>(stream));
+  return as::launch_bin_rows(crow, n, threshold, 1, 1, order, counts, workspace, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -367,7 +367,7 @@ int as_sddmm_csr_split_f32(const int64_t* crow, const int64_t* col, const float*
   int64_t heavy_upper = nnz / hub_threshold;
   if (heavy_upper > n) heavy_upper = n;
   if (heavy_upper > 0) {
-    st = as::launch_bin_rows(crow, n, hub_threshold, 1, order, counts, bin_ws, s);
+    st = as::launch_bin_rows(crow, n, hub_threshold, 1, 1, order, counts, bin_ws, s);
     if (st != AS_OK) return st;
     hipLaunchKernelGGL(as::hub_chunk_scan_kernel, dim3(1), dim3(1024), 0, s, crow, order, counts, chunk_off);
     const int64_t item_upper = nnz / as::kChunkEdges + heavy_upper;

@@ -531,7 +531,8 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col, const float* 
   int32_t* counts = reinterpret_cast<int32_t*>(ws + order_bytes);
   void* bin_ws = ws + order_bytes + 256;
   const bool split64 = hub_mode == AS_HUB_SPLIT64;
-  st = as::launch_bin_rows(crow, n, hub_threshold, split64 ? 1 : as::kSplitBuckets, order, counts, bin_ws, s);
+  st = as::launch_bin_rows(crow, n, hub_threshold, split64 ? 1 : as::kSplitBuckets, as::kSplitBuckets, order,
+                           counts, bin_ws, s);
   if (st != AS_OK) return st;
 
   const as::SpmmArgs a{crow, col, val, x, y, n, f};

@@ -147,8 +147,9 @@ def main() -> int:
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the row-sharded design is described in DESIGN.md)", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path; the ops are row-independent "
+              "and would shard by nnz-balanced row ranges with one all-gather of the dense operand",
+              file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

@@ -115,3 +115,30 @@ def test_signatures_match_reference_golden():
         got = graph_signature(crow, col, case["feature_width"], case["operation"], weighted=case["weighted"],
                               dtype=dtype)
         assert got == case["expected"], case["name"]
+
+
+def test_signature_memo_hits_only_for_the_same_unmodified_tensors():
+    from autosage_amd._cache import graph_signature_memo
+
+    crow = torch.tensor([0, 1, 3, 3], dtype=torch.long)
+    col = torch.tensor([0, 1, 2], dtype=torch.long)
+    first = graph_signature_memo(crow, col, 8, "spmm")
+    assert first == graph_signature(crow, col, 8, "spmm")
+    assert graph_signature_memo(crow, col, 8, "spmm") == first
+    col[0] = 2  # in-place change bumps the version: recomputed
+    changed = graph_signature_memo(crow, col, 8, "spmm")
+    assert changed == graph_signature(crow, col, 8, "spmm")
+    assert changed["structure_hash"] != first["structure_hash"]
+    other = col.clone()  # equal content, other object: recomputed, same value
+    assert graph_signature_memo(crow, other, 8, "spmm") == changed
+
+
+def test_schedule_file_memo_sees_external_writes(tmp_path):
+    path = tmp_path / "schedules.json"
+    ScheduleCache(path).store({"type": "cpu"}, {"rows": 1}, {"choice": "baseline"})
+    assert ScheduleCache(path).lookup({"type": "cpu"}, {"rows": 1})["result"] == {"choice": "baseline"}
+    payload = json.loads(path.read_text())
+    key = next(iter(payload["records"]))
+    payload["records"][key]["result"] = {"choice": "autosage", "note": "written by another process"}
+    path.write_text(json.dumps(payload, indent=2))
+    assert ScheduleCache(path).lookup({"type": "cpu"}, {"rows": 1})["result"]["choice"] == "autosage"
