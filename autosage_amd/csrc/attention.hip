@@ -374,8 +374,9 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col, const float* q
   ws += as::align_up(static_cast<size_t>(n) * sizeof(int32_t), 256);
   int32_t* counts = reinterpret_cast<int32_t*>(ws);
   void* bin_ws = ws + 256;
-  int st = as::launch_bin_rows(crow, n, as::kAttHubDegree, as::kAttBuckets, as::kAttBuckets, order, counts,
-                               bin_ws, s);
+  // Light rows stay in row order (one bucket): ordering them by degree measured
+  // slower here (13.4 vs 12.8 ms on the 124M-nnz attention graph).
+  int st = as::launch_bin_rows(crow, n, as::kAttHubDegree, as::kAttBuckets, 1, order, counts, bin_ws, s);
   if (st != AS_OK) return st;
 
   const bool qvec = f_qk > 0 && f_qk % 32 == 0 && f_qk / 32 <= 8 && as::al(query, 16) && as::al(key, 16);

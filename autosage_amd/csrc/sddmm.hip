@@ -103,48 +103,41 @@ __device__ __forceinline__ void load_query(const float* __restrict__ qrow, int j
   }
 }
 
-// One wave per row; rows of degree >= hub_threshold are left to the hub
-// kernel (csrc/sddmm_csr_op.cu:35-37).
-template <int G, int MF>
-__global__ __launch_bounds__(kBlock) void sddmm_rows_vec_kernel(const int64_t* __restrict__ crow,
-                                                                const int64_t* __restrict__ col,
-                                                                const float* __restrict__ query,
-                                                                const float* __restrict__ key,
-                                                                float* __restrict__ out, int64_t n, int64_t F,
-                                                                int64_t hub_threshold, int64_t idx_base) {
-  constexpr int NG = kWave / G;
-  constexpr int UE = MF <= 2 ? 4 : 2;
+// One wave computes every edge of `row` (vector or scalar path).
+template <int G, int MF, bool VEC>
+__device__ __forceinline__ void sddmm_row(const int64_t* __restrict__ col, const float* __restrict__ query,
+                                          const float* __restrict__ key, float* __restrict__ out, int64_t F,
+                                          int64_t row, int64_t rs, int64_t re) {
   const int lane = lane_id();
   const int g = lane / G;
   const int j = lane % G;
-  const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
-  if (row >= n) return;
-  const int64_t rs = uniform_i64(crow[row]);
-  const int64_t re = uniform_i64(crow[row + 1]);
-  if (re - rs >= hub_threshold || re == rs) return;
-  float qv[MF][32 / G];
-  load_query<G, MF>(query + row * F, j, qv);
-  for (int64_t base = rs; base < re; base += NG * UE) {
-    dot_edges_vec<G, MF, UE>(col, key, out, F, qv, base, NG, re, g, j);
+  if constexpr (VEC) {
+    constexpr int NG = kWave / G;
+    constexpr int UE = MF <= 2 ? 4 : 2;
+    float qv[MF][32 / G];
+    load_query<G, MF>(query + row * F, j, qv);
+    for (int64_t base = rs; base < re; base += NG * UE) dot_edges_vec<G, MF, UE>(col, key, out, F, qv, base, NG, re, g, j);
+  } else {
+    const float* qrow = query + row * F;
+    for (int64_t base = rs; base < re; base += 2) dot_edges_scalar(col, qrow, key, out, F, base, 2, re, g, j);
   }
 }
 
-__global__ __launch_bounds__(kBlock) void sddmm_rows_scalar_kernel(const int64_t* __restrict__ crow,
-                                                                   const int64_t* __restrict__ col,
-                                                                   const float* __restrict__ query,
-                                                                   const float* __restrict__ key,
-                                                                   float* __restrict__ out, int64_t n, int64_t F,
-                                                                   int64_t hub_threshold, int64_t idx_base) {
-  const int lane = lane_id();
-  const int g = lane / 32;
-  const int j = lane % 32;
+// One wave per row; rows of degree >= hub_threshold are left to the hub
+// kernel (csrc/sddmm_csr_op.cu:35-37).
+template <int G, int MF, bool VEC>
+__global__ __launch_bounds__(kBlock) void sddmm_rows_kernel(const int64_t* __restrict__ crow,
+                                                            const int64_t* __restrict__ col,
+                                                            const float* __restrict__ query,
+                                                            const float* __restrict__ key, float* __restrict__ out,
+                                                            int64_t n, int64_t F, int64_t hub_threshold,
+                                                            int64_t idx_base) {
   const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
   if (row >= n) return;
   const int64_t rs = uniform_i64(crow[row]);
   const int64_t re = uniform_i64(crow[row + 1]);
   if (re - rs >= hub_threshold || re == rs) return;
-  const float* qrow = query + row * F;
-  for (int64_t base = rs; base < re; base += 2) dot_edges_scalar(col, qrow, key, out, F, base, 2, re, g, j);
+  sddmm_row<G, MF, VEC>(col, query, key, out, F, row, rs, re);
 }
 
 // Work items of the hub kernel: hub h (order[h], h < counts[0]) is cut into
@@ -185,52 +178,58 @@ __global__ __launch_bounds__(1024) void hub_chunk_scan_kernel(const int64_t* __r
   if (threadIdx.x == 0) counts[2] = total;
 }
 
-// Persistent hub kernel: workgroups of W waves stride over the chunk items.
-// Every wave reads the same item total, so all waves leave the loop.
+// Split SDDMM in one launch.  Workgroups [0, hub_blocks) are persistent and
+// stride over the hub chunk items (2048-edge pieces of hub rows); the rest take
+// the light rows in row order, one per wave, skipping hub and empty rows.
+// Hub workgroups have the lowest indices, so they are dispatched first.
 template <int G, int MF, bool VEC>
-__global__ __launch_bounds__(512) void sddmm_hub_chunks_kernel(const int64_t* __restrict__ crow,
-                                                               const int64_t* __restrict__ col,
-                                                               const float* __restrict__ query,
-                                                               const float* __restrict__ key,
-                                                               float* __restrict__ out, int64_t F,
-                                                               const int32_t* __restrict__ order,
-                                                               const int32_t* __restrict__ counts,
-                                                               const int32_t* __restrict__ chunk_off) {
-  constexpr int NG = kWave / G;
+__global__ __launch_bounds__(512) void sddmm_scheduled_kernel(
+    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const float* __restrict__ query,
+    const float* __restrict__ key, float* __restrict__ out, int64_t n, int64_t F, int64_t hub_threshold,
+    const int32_t* __restrict__ order, const int32_t* __restrict__ counts, const int32_t* __restrict__ chunk_off,
+    int64_t hub_blocks, int64_t block_base) {
+  constexpr int NG = VEC ? kWave / G : 2;
   const int lane = lane_id();
-  const int g = lane / G;
-  const int j = lane % G;
+  const int g = lane / (VEC ? G : 32);
+  const int j = lane % (VEC ? G : 32);
   const int wave = wave_in_block();
   const int waves = static_cast<int>(blockDim.x >> 6);
-  const int64_t hubs = counts[0];
-  const int64_t items = counts[2];
-  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-    // largest h with chunk_off[h] <= item
-    int64_t lo = 0;
-    int64_t hi = hubs - 1;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi + 1) >> 1;
-      if (chunk_off[mid] <= item) lo = mid;
-      else hi = mid - 1;
-    }
-    const int64_t row = uniform_i64(order[lo]);
-    const int64_t rs = uniform_i64(crow[row]);
-    const int64_t re = uniform_i64(crow[row + 1]);
-    const int64_t cs = rs + (item - uniform_i64(chunk_off[lo])) * kChunkEdges;
-    const int64_t ce = cs + kChunkEdges < re ? cs + kChunkEdges : re;
-    if constexpr (VEC) {
-      float qv[MF][32 / G];
-      load_query<G, MF>(query + row * F, j, qv);
-      for (int64_t base = cs + static_cast<int64_t>(wave) * NG; base < ce; base += static_cast<int64_t>(waves) * NG) {
-        dot_edges_vec<G, MF, 1>(col, key, out, F, qv, base, NG, ce, g, j);
+  const int64_t block = block_base + blockIdx.x;
+  if (block < hub_blocks) {
+    const int64_t hubs = counts[0];
+    const int64_t items = counts[2];
+    for (int64_t item = block; item < items; item += hub_blocks) {
+      int64_t lo = 0;
+      int64_t hi = hubs - 1;
+      while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (chunk_off[mid] <= item) lo = mid;
+        else hi = mid - 1;
       }
-    } else {
-      const float* qrow = query + row * F;
-      for (int64_t base = cs + static_cast<int64_t>(wave) * 2; base < ce; base += static_cast<int64_t>(waves) * 2) {
-        dot_edges_scalar(col, qrow, key, out, F, base, 2, ce, g, j);
+      const int64_t row = uniform_i64(order[lo]);
+      const int64_t rs = uniform_i64(crow[row]);
+      const int64_t re = uniform_i64(crow[row + 1]);
+      const int64_t cs = rs + (item - uniform_i64(chunk_off[lo])) * kChunkEdges;
+      const int64_t ce = cs + kChunkEdges < re ? cs + kChunkEdges : re;
+      if constexpr (VEC) {
+        float qv[MF][32 / G];
+        load_query<G, MF>(query + row * F, j, qv);
+        for (int64_t base = cs + static_cast<int64_t>(wave) * NG; base < ce; base += static_cast<int64_t>(waves) * NG)
+          dot_edges_vec<G, MF, 1>(col, key, out, F, qv, base, NG, ce, g, j);
+      } else {
+        const float* qrow = query + row * F;
+        for (int64_t base = cs + static_cast<int64_t>(wave) * 2; base < ce; base += static_cast<int64_t>(waves) * 2)
+          dot_edges_scalar(col, qrow, key, out, F, base, 2, ce, g, j);
       }
     }
+    return;
   }
+  const int64_t row = (block - hub_blocks) * waves + wave;
+  if (row >= n) return;
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
+  if (re - rs >= hub_threshold || re == rs) return;
+  sddmm_row<G, MF, VEC>(col, query, key, out, F, row, rs, re);
 }
 
 struct SddmmArgs {
@@ -259,17 +258,17 @@ int launch_sddmm_rows(const SddmmArgs& a, int64_t hub_threshold, hipStream_t str
 #define AS_ROWS(K) \
   hipLaunchKernelGGL(K, grid, dim3(kBlock), 0, stream, a.crow, a.col, a.q, a.k, a.out, a.n, a.f, hub_threshold, base)
     if (!vec) {
-      AS_ROWS(sddmm_rows_scalar_kernel);
+      AS_ROWS((sddmm_rows_kernel<32, 1, false>));
     } else {
       switch (mf) {
-        case 1: AS_ROWS((sddmm_rows_vec_kernel<8, 1>)); break;
-        case 2: AS_ROWS((sddmm_rows_vec_kernel<8, 2>)); break;
-        case 3: AS_ROWS((sddmm_rows_vec_kernel<8, 3>)); break;
-        case 4: AS_ROWS((sddmm_rows_vec_kernel<8, 4>)); break;
-        case 5: AS_ROWS((sddmm_rows_vec_kernel<8, 5>)); break;
-        case 6: AS_ROWS((sddmm_rows_vec_kernel<8, 6>)); break;
-        case 7: AS_ROWS((sddmm_rows_vec_kernel<8, 7>)); break;
-        default: AS_ROWS((sddmm_rows_vec_kernel<8, 8>)); break;
+        case 1: AS_ROWS((sddmm_rows_kernel<8, 1, true>)); break;
+        case 2: AS_ROWS((sddmm_rows_kernel<8, 2, true>)); break;
+        case 3: AS_ROWS((sddmm_rows_kernel<8, 3, true>)); break;
+        case 4: AS_ROWS((sddmm_rows_kernel<8, 4, true>)); break;
+        case 5: AS_ROWS((sddmm_rows_kernel<8, 5, true>)); break;
+        case 6: AS_ROWS((sddmm_rows_kernel<8, 6, true>)); break;
+        case 7: AS_ROWS((sddmm_rows_kernel<8, 7, true>)); break;
+        default: AS_ROWS((sddmm_rows_kernel<8, 8, true>)); break;
       }
     }
 #undef AS_ROWS
@@ -277,29 +276,37 @@ int launch_sddmm_rows(const SddmmArgs& a, int64_t hub_threshold, hipStream_t str
   return AS_OK;
 }
 
-int launch_sddmm_hubs(const SddmmArgs& a, int waves, int64_t item_upper, const int32_t* order,
-                      const int32_t* counts, const int32_t* chunk_off, hipStream_t stream) {
-  int64_t blocks = item_upper < 4096 ? item_upper : 4096;
-  if (blocks <= 0) return AS_OK;
-  const dim3 grid(static_cast<unsigned>(blocks));
+// Persistent hub workgroups of the scheduled kernel: enough to spread the
+// hub chunks over the chip without holding it (one per CU).
+constexpr int64_t kHubBlocks = 256;
+
+int launch_sddmm_scheduled(const SddmmArgs& a, int waves, int64_t hub_threshold, int64_t item_upper,
+                           const int32_t* order, const int32_t* counts, const int32_t* chunk_off, hipStream_t stream) {
+  const int64_t hub_blocks = item_upper < kHubBlocks ? item_upper : kHubBlocks;
+  const int64_t blocks = hub_blocks + (a.n + waves - 1) / waves;
   const dim3 block(static_cast<unsigned>(waves * kWave));
-#define AS_HUB(K) \
-  hipLaunchKernelGGL(K, grid, block, 0, stream, a.crow, a.col, a.q, a.k, a.out, a.f, order, counts, chunk_off)
-  if (!vec_ok(a)) {
-    AS_HUB((sddmm_hub_chunks_kernel<32, 1, false>));
-  } else {
-    switch (static_cast<int>(a.f / 32)) {
-      case 1: AS_HUB((sddmm_hub_chunks_kernel<8, 1, true>)); break;
-      case 2: AS_HUB((sddmm_hub_chunks_kernel<8, 2, true>)); break;
-      case 3: AS_HUB((sddmm_hub_chunks_kernel<8, 3, true>)); break;
-      case 4: AS_HUB((sddmm_hub_chunks_kernel<8, 4, true>)); break;
-      case 5: AS_HUB((sddmm_hub_chunks_kernel<8, 5, true>)); break;
-      case 6: AS_HUB((sddmm_hub_chunks_kernel<8, 6, true>)); break;
-      case 7: AS_HUB((sddmm_hub_chunks_kernel<8, 7, true>)); break;
-      default: AS_HUB((sddmm_hub_chunks_kernel<8, 8, true>)); break;
+  for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
+    const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
+    const dim3 grid(static_cast<unsigned>(nb));
+#define AS_SCHED(K)                                                                                             \
+  hipLaunchKernelGGL(K, grid, block, 0, stream, a.crow, a.col, a.q, a.k, a.out, a.n, a.f, hub_threshold, order, \
+                     counts, chunk_off, hub_blocks, b0)
+    if (!vec_ok(a)) {
+      AS_SCHED((sddmm_scheduled_kernel<32, 1, false>));
+    } else {
+      switch (static_cast<int>(a.f / 32)) {
+        case 1: AS_SCHED((sddmm_scheduled_kernel<8, 1, true>)); break;
+        case 2: AS_SCHED((sddmm_scheduled_kernel<8, 2, true>)); break;
+        case 3: AS_SCHED((sddmm_scheduled_kernel<8, 3, true>)); break;
+        case 4: AS_SCHED((sddmm_scheduled_kernel<8, 4, true>)); break;
+        case 5: AS_SCHED((sddmm_scheduled_kernel<8, 5, true>)); break;
+        case 6: AS_SCHED((sddmm_scheduled_kernel<8, 6, true>)); break;
+        case 7: AS_SCHED((sddmm_scheduled_kernel<8, 7, true>)); break;
+        default: AS_SCHED((sddmm_scheduled_kernel<8, 8, true>)); break;
+      }
     }
+#undef AS_SCHED
   }
-#undef AS_HUB
   return AS_OK;
 }
 
@@ -362,18 +369,20 @@ int as_sddmm_csr_split_f32(const int64_t* crow, const int64_t* col, const float*
   void* bin_ws = ws + order_bytes + 256;
   int32_t* chunk_off = reinterpret_cast<int32_t*>(ws + as::spmm_split_workspace_bytes(n));
 
-  st = as::launch_sddmm_rows(a, hub_threshold, s);
-  if (st != AS_OK) return st;
   int64_t heavy_upper = nnz / hub_threshold;
   if (heavy_upper > n) heavy_upper = n;
-  if (heavy_upper > 0) {
-    st = as::launch_bin_rows(crow, n, hub_threshold, 1, 1, order, counts, bin_ws, s);
+  if (heavy_upper == 0) {
+    // no row can reach the threshold: the row kernel covers everything
+    st = as::launch_sddmm_rows(a, hub_threshold, s);
     if (st != AS_OK) return st;
-    hipLaunchKernelGGL(as::hub_chunk_scan_kernel, dim3(1), dim3(1024), 0, s, crow, order, counts, chunk_off);
-    const int64_t item_upper = nnz / as::kChunkEdges + heavy_upper;
-    st = as::launch_sddmm_hubs(a, waves_per_block, item_upper, order, counts, chunk_off, s);
-    if (st != AS_OK) return st;
+    return as::check_launch("sddmm_csr_split");
   }
+  st = as::launch_bin_rows(crow, n, hub_threshold, 1, 1, order, counts, bin_ws, s);
+  if (st != AS_OK) return st;
+  hipLaunchKernelGGL(as::hub_chunk_scan_kernel, dim3(1), dim3(1024), 0, s, crow, order, counts, chunk_off);
+  const int64_t item_upper = nnz / as::kChunkEdges + heavy_upper;
+  st = as::launch_sddmm_scheduled(a, waves_per_block, hub_threshold, item_upper, order, counts, chunk_off, s);
+  if (st != AS_OK) return st;
   return as::check_launch("sddmm_csr_split");
 }
 

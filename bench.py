@@ -92,16 +92,26 @@ def time_steps(fn, steps: int, warmup: int) -> tuple[float, list[float]]:
     return total / steps, samples
 
 
+def calibrate(variants: dict, calib: dict) -> str:
+    """Times every variant (5 calls after 1 warmup) and returns the fastest;
+    variants within 0.5 % of the fastest count as tied and the first of them
+    in ``variants`` order (the scheduler's ranking) wins, so the choice is
+    stable from run to run."""
+    for name, fn in variants.items():
+        ms, _ = time_steps(fn, 5, 1)
+        calib[name] = round(ms, 4)
+    best = min(calib.values())
+    return next(name for name in variants if calib[name] <= best * 1.005)
+
+
 def cpu_baseline_spmm(crow: np.ndarray, col: np.ndarray, val, x: np.ndarray, target_nnz: int) -> dict:
     """The reference CPU path (torch.sparse.mm on a CSR tensor, restated in
     oracle/) on the leading rows of the graph holding about ``target_nnz``
     nonzeros, timed on this host's cores."""
     import oracle
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(threads)
-    rows = int(np.searchsorted(crow, min(target_nnz, int(crow[-1])), side="left"))
-    rows = max(1, min(rows, crow.size - 1))
+    threads = _host_threads()
+    rows = _leading_rows(crow, target_nnz)
     s_crow = torch.from_numpy(crow[: rows + 1].copy())
     nnz = int(s_crow[-1])
     s_col = torch.from_numpy(col[:nnz].copy())
@@ -127,6 +137,76 @@ def cpu_baseline_spmm(crow: np.ndarray, col: np.ndarray, val, x: np.ndarray, tar
         "sample": f"torch.sparse.mm CPU CSR SpMM (reference ops.py:124-143 path) on rows [0,{rows}) = "
         f"{nnz} nnz of the same graph, F={f}, median of {reps} after 1 warmup, {t * 1e3:.1f} ms/call",
     }
+
+
+def _host_threads() -> int:
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _leading_rows(crow: np.ndarray, target_nnz: int) -> int:
+    rows = int(np.searchsorted(crow, min(target_nnz, int(crow[-1])), side="left"))
+    return max(1, min(rows, crow.size - 1))
+
+
+def cpu_baseline_sddmm(w, f: int, target_nnz: int = 4_000_000) -> dict:
+    """The reference CPU SDDMM path (gather-dot, autosage/_auto.py:79-92,
+    restated in oracle/) on the leading rows holding about ``target_nnz``
+    nonzeros."""
+    import oracle
+
+    threads = _host_threads()
+    rows = _leading_rows(w.crow, target_nnz)
+    s_crow = torch.from_numpy(w.crow[: rows + 1].copy())
+    nnz = int(s_crow[-1])
+    s_col = torch.from_numpy(w.col[:nnz].copy())
+    q = torch.from_numpy(w.dense["q"])
+    k = torch.from_numpy(w.dense["k"])
+    oracle.torch_gather_dot(s_crow, s_col, q, k)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.torch_gather_dot(s_crow, s_col, q, k)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": 2.0 * nnz * f / t / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"torch gather-dot SDDMM (reference _auto.py:79-92 baseline) on rows [0,{rows}) = {nnz} nnz "
+                      f"of the same graph, F={f}, median of 3 after 1 warmup, {t * 1e3:.1f} ms/call"}
+
+
+def cpu_baseline_attention(w, target_nnz: int = 4_000_000) -> dict:
+    """The reference CPU attention composition (gather-dot SDDMM, torch row
+    softmax, torch.sparse.mm; autosage/_auto.py:762-780 on CPU tensors,
+    restated in oracle/) on the leading rows holding about ``target_nnz``
+    nonzeros."""
+    import oracle
+
+    threads = _host_threads()
+    rows = _leading_rows(w.crow, target_nnz)
+    s_crow = torch.from_numpy(w.crow[: rows + 1].copy())
+    nnz = int(s_crow[-1])
+    s_col = torch.from_numpy(w.col[:nnz].copy())
+    q = torch.from_numpy(w.dense["q"][:rows].copy())
+    k = torch.from_numpy(w.dense["k"])
+    v = torch.from_numpy(w.dense["v"])
+
+    def run():
+        scores = oracle.torch_gather_dot(s_crow, s_col, q, k) * 0.125
+        p = oracle.torch_row_softmax(s_crow, scores)
+        matrix = torch.sparse_csr_tensor(s_crow, s_col, p, size=(rows, v.size(0)))
+        return torch.sparse.mm(matrix, v)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": 2.0 * nnz * (64 + 128) / t / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"reference CPU attention composition on rows [0,{rows}) = {nnz} nnz of the same graph, "
+                      f"median of 3 after 1 warmup, {t * 1e3:.1f} ms/call"}
 
 
 def main() -> int:
@@ -190,10 +270,7 @@ def main() -> int:
                 lambda c=cand: torch.ops.autosage.spmm_csr_split(crow, col, val, x, *c))
         calib = {}
         if args.variant == "calibrated":
-            for name, fn in variants.items():
-                ms, _ = time_steps(fn, 3, 1)
-                calib[name] = round(ms, 4)
-            chosen = min(calib, key=calib.get)
+            chosen = calibrate(variants, calib)
         else:
             chosen = args.variant
             if chosen not in variants:
@@ -271,21 +348,20 @@ def bench_other(args, device) -> dict:
         col = torch.from_numpy(w.col).to(device)
         q = torch.from_numpy(w.dense["q"]).to(device)
         k = torch.from_numpy(w.dense["k"]).to(device)
-        calib = {"whole": time_steps(lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k), 3, 1)[0]}
-        for waves in (2, 4, 8):
-            for thr in (256, 1024, 4096):
-                calib[f"{waves},{thr}"] = time_steps(
-                    lambda a=waves, b=thr: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b), 3, 1)[0]
-        chosen = min(calib, key=calib.get)
-        if chosen == "whole":
-            step = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)  # noqa: E731
-        else:
-            a, b = map(int, chosen.split(","))
-            step = lambda: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b)  # noqa: E731
+        variants = {}
+        for waves in (8, 4, 2):
+            for thr in (1024, 4096, 256):
+                variants[f"{waves},{thr}"] = (
+                    lambda a=waves, b=thr: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b))
+        variants["whole"] = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)
+        calib = {}
+        chosen = calibrate(variants, calib) if args.variant == "calibrated" else args.variant
+        step = variants[chosen]
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * w.nnz * f
         algo = sddmm_bytes(w.rows, w.nnz, f)
         name = f"cfg4 SDDMM fp32 F={f}"
+        cpu = None if args.no_cpu_baseline else cpu_baseline_sddmm(w, f)
     else:
         w = synth.config5(seed=args.seed)
         log(f"generated cfg5: {w.degree_stats()} in {time.time() - t0:.1f}s")
@@ -301,6 +377,8 @@ def bench_other(args, device) -> dict:
         flops = 2.0 * w.nnz * (64 + 128)
         algo = attention_bytes(w.rows, w.nnz, 64, 128)
         name = "cfg5 fused CSR attention fp32 Fqk=64 Fv=128 scale=1/8"
+        cpu = None if args.no_cpu_baseline else cpu_baseline_attention(w)
+    traffic = profiled_traffic(name, chosen)
     return {
         "metric": METRIC,
         "value": round(flops / (ms * 1e-3) / 1e9, 2),
@@ -322,12 +400,15 @@ def bench_other(args, device) -> dict:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": None if traffic is None else traffic["bytes"],
             "algorithmic_bytes": algo,
+            "traffic_source": None if traffic is None else traffic["source"],
+            "traffic_gbps_at_this_step_time": None if traffic is None
+            else round(traffic["bytes"] / (ms * 1e-3) / 1e9, 1),
         },
         "per_call_ms": [round(s, 4) for s in samples],
         "calibration_ms": {k_: round(v_, 4) for k_, v_ in calib.items()},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
 
 
