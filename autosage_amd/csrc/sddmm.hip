@@ -276,13 +276,16 @@ int launch_sddmm_rows(const SddmmArgs& a, int64_t hub_threshold, hipStream_t str
   return AS_OK;
 }
 
-// Persistent hub workgroups of the scheduled kernel: enough to spread the
-// hub chunks over the chip without holding it (one per CU).
-constexpr int64_t kHubBlocks = 256;
+// Waves given to the hub chunks of the scheduled kernel: about half of what
+// the chip holds at once (256 CUs x 32 waves), whatever the workgroup size,
+// so the hub rows finish alongside the light rows (with a fixed 256
+// workgroups, 2-wave workgroups left the hub pass as a 2x tail).
+constexpr int64_t kHubWaves = 4096;
 
 int launch_sddmm_scheduled(const SddmmArgs& a, int waves, int64_t hub_threshold, int64_t item_upper,
                            const int32_t* order, const int32_t* counts, const int32_t* chunk_off, hipStream_t stream) {
-  const int64_t hub_blocks = item_upper < kHubBlocks ? item_upper : kHubBlocks;
+  const int64_t hub_cap = kHubWaves / waves;
+  const int64_t hub_blocks = item_upper < hub_cap ? item_upper : hub_cap;
   const int64_t blocks = hub_blocks + (a.n + waves - 1) / waves;
   const dim3 block(static_cast<unsigned>(waves * kWave));
   for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {

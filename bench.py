@@ -55,14 +55,20 @@ def profiled_traffic(workload: str, variant: str):
     WRITE_SIZE runs for this exact workload and variant, read from the
     ``<!-- traffic: {...} -->`` record of a summary under profiles/; None when
     no record matches."""
+    same_workload = None
     for path in sorted((ROOT / "profiles").glob("*.md")):
         for line in path.read_text(encoding="utf-8").splitlines():
             line = line.strip()
             if line.startswith("<!-- traffic:") and line.endswith("-->"):
                 record = json.loads(line[len("<!-- traffic:"):-3])
-                if record.get("workload") == workload and record.get("variant") == variant:
+                if record.get("workload") != workload:
+                    continue
+                if record.get("variant") == variant:
                     return record
-    return None
+                same_workload = same_workload or record
+    # Calibration can pick another variant of near-equal time than the one the
+    # counters were taken on; the record then says which variant it measured.
+    return same_workload
 
 
 def time_steps(fn, steps: int, warmup: int) -> tuple[float, list[float]]:
@@ -314,6 +320,7 @@ def main() -> int:
                 "traffic": None if traffic is None else traffic["bytes"],
                 "algorithmic_bytes": algo,
                 "traffic_source": None if traffic is None else traffic["source"],
+                "traffic_variant": None if traffic is None else traffic["variant"],
                 "traffic_gbps_at_this_step_time": None if traffic is None
                 else round(traffic["bytes"] / (ms * 1e-3) / 1e9, 1),
             },
@@ -403,6 +410,7 @@ def bench_other(args, device) -> dict:
             "traffic": None if traffic is None else traffic["bytes"],
             "algorithmic_bytes": algo,
             "traffic_source": None if traffic is None else traffic["source"],
+            "traffic_variant": None if traffic is None else traffic["variant"],
             "traffic_gbps_at_this_step_time": None if traffic is None
             else round(traffic["bytes"] / (ms * 1e-3) / 1e9, 1),
         },
