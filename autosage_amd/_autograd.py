@@ -1,0 +1,103 @@
+"""Backward formulas for the ``autosage::*`` SpMM and SDDMM operators.
+
+The reference registers no autograd for its operators, so ``AutoSAGEConv``
+trains only through the PyTorch baseline there.  Here the four operators get
+backward formulas built from the same native kernels:
+
+* ``Y = A·X`` (A: CSR, weights ``val`` or ones):
+  ``dX = Aᵀ·dY`` — a native SpMM over the transposed CSR — and
+  ``dval[e] = <dY[row(e)], X[col(e)]>`` — a native SDDMM.
+* ``s[e] = <Q[row(e)], K[col(e)]>``:
+  ``dQ = A_ds·K`` (SpMM with weights ``ds``) and ``dK = A_dsᵀ·Q``.
+
+The transposed CSR (rows of Aᵀ list the source rows in ascending order, a
+stable sort of the edges by column) is built with torch ops and memoised per
+live (crow, col) tensor pair, like the schedule keys.  Every product is
+deterministic: the same inputs give the same bits.
+"""
+
+from __future__ import annotations
+
+import collections
+import threading
+import weakref
+from typing import Optional
+
+import torch
+
+_LOCK = threading.Lock()
+_TRANSPOSE_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+_MEMO_SIZE = 16
+
+
+def csr_transpose(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(crow_t, col_t, perm) of Aᵀ for a square CSR A; ``perm[k]`` is the
+    edge of A that becomes edge k of Aᵀ, so ``val_t = val[perm]``."""
+    key = (id(crow), crow._version, id(col), col._version)
+    with _LOCK:
+        hit = _TRANSPOSE_MEMO.get(key)
+        if hit is not None and hit[0]() is crow and hit[1]() is col:
+            _TRANSPOSE_MEMO.move_to_end(key)
+            return hit[2]
+    n = crow.numel() - 1
+    counts = (crow[1:] - crow[:-1]).to(torch.long)
+    rows = torch.repeat_interleave(torch.arange(n, device=crow.device, dtype=torch.long), counts)
+    perm = col.argsort(stable=True)
+    crow_t = torch.zeros(n + 1, dtype=torch.long, device=crow.device)
+    crow_t[1:] = torch.bincount(col, minlength=n).cumsum(0)
+    result = (crow_t, rows.index_select(0, perm).contiguous(), perm)
+    with _LOCK:
+        _TRANSPOSE_MEMO[key] = (weakref.ref(crow), weakref.ref(col), result)
+        while len(_TRANSPOSE_MEMO) > _MEMO_SIZE:
+            _TRANSPOSE_MEMO.popitem(last=False)
+    return result
+
+
+def _spmm_setup(ctx, inputs, output) -> None:
+    crow, col, val, x = inputs[:4]
+    ctx.save_for_backward(crow, col, val, x)
+    ctx.has_val = val is not None
+
+
+def _spmm_backward(ctx, grad_y: torch.Tensor):
+    crow, col, val, x = ctx.saved_tensors
+    if not ctx.has_val:
+        val = None
+    grad_x: Optional[torch.Tensor] = None
+    grad_val: Optional[torch.Tensor] = None
+    grad_y = grad_y.contiguous()
+    if ctx.needs_input_grad[3]:
+        crow_t, col_t, perm = csr_transpose(crow, col)
+        val_t = None if val is None else val.index_select(0, perm).contiguous()
+        grad_x = torch.ops.autosage.spmm_csr(crow_t, col_t, val_t, grad_y)
+    if val is not None and ctx.needs_input_grad[2]:
+        grad_val = torch.ops.autosage.sddmm_csr(crow, col, grad_y, x)
+    # one gradient per schema argument (the split op has three int arguments more)
+    extra = (None,) * (len(ctx.needs_input_grad) - 4)
+    return (None, None, grad_val, grad_x, *extra)
+
+
+def _sddmm_setup(ctx, inputs, output) -> None:
+    crow, col, query, key = inputs[:4]
+    ctx.save_for_backward(crow, col, query, key)
+
+
+def _sddmm_backward(ctx, grad_s: torch.Tensor):
+    crow, col, query, key = ctx.saved_tensors
+    grad_s = grad_s.contiguous()
+    grad_q = grad_k = None
+    if ctx.needs_input_grad[2]:
+        grad_q = torch.ops.autosage.spmm_csr(crow, col, grad_s, key)
+    if ctx.needs_input_grad[3]:
+        crow_t, col_t, perm = csr_transpose(crow, col)
+        grad_k = torch.ops.autosage.spmm_csr(crow_t, col_t, grad_s.index_select(0, perm).contiguous(), query)
+    extra = (None,) * (len(ctx.needs_input_grad) - 4)
+    return (None, None, grad_q, grad_k, *extra)
+
+
+def register() -> None:
+    """Attaches the backward formulas to the registered operators."""
+    for name in ("spmm_csr", "spmm_csr_split"):
+        torch.library.register_autograd(f"autosage::{name}", _spmm_backward, setup_context=_spmm_setup)
+    for name in ("sddmm_csr", "sddmm_csr_split"):
+        torch.library.register_autograd(f"autosage::{name}", _sddmm_backward, setup_context=_sddmm_setup)

@@ -344,6 +344,9 @@ def _register_operators() -> None:
         lib.define(schema)
         lib.impl(name, impl, "CUDA")
     _OPS_LIBRARY = lib
+    from . import _autograd
+
+    _autograd.register()
 
 
 def load(path: os.PathLike[str] | str) -> None:
