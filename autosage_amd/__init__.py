@@ -6,7 +6,7 @@ Public names are those of the reference package (``autosage/__init__.py:1-17``).
 from ._auto import calibrate_full, csr_attention_forward, sddmm_csr_auto, spmm_csr_auto
 from ._version import __version__
 from .conv import AutoSAGEConv
-from .ops import load_native, native_available, spmm_csr
+from .ops import load_native, native_available, spmm_csr, validate_csr
 
 __all__ = [
     "AutoSAGEConv",
@@ -18,4 +18,5 @@ __all__ = [
     "sddmm_csr_auto",
     "spmm_csr",
     "spmm_csr_auto",
+    "validate_csr",
 ]

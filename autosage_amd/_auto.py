@@ -29,7 +29,7 @@ import torch
 
 from ._cache import ScheduleCache, device_signature, graph_signature_memo, log_probe
 from .config import SchedulerConfig
-from .ops import _normalize_csr, load_native, native_op, spmm_csr
+from .ops import _normalize_csr, load_native, native_op, spmm_csr, validate_if_requested
 
 AUTOTUNE_SCHEMA_VERSION = 3
 
@@ -484,6 +484,7 @@ def _normalize_sddmm(crow, col, query, key):
         raise ValueError("crow must contain N + 1 entries")
     if not (crow.device == col.device == query.device == key.device):
         raise ValueError("all SDDMM inputs must be on the same device")
+    validate_if_requested(crow, col)
     return crow, col, query, key
 
 

@@ -53,6 +53,7 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_ptr, _c_size, _c_ptr],
     ),
     "as_csr_row_softmax_f32": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr]),
+    "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "as_csr_attention_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "as_csr_attention_f32": (
         _c_int,
@@ -175,6 +176,7 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
 def spmm_csr_impl(crow, col, val, x):
     check_spmm_inputs(crow, col, val, x)
+    _maybe_validate(crow, col)
     y = torch.empty_like(x)
     n, f = x.shape
     if n == 0 or f == 0:
@@ -189,6 +191,7 @@ def spmm_csr_impl(crow, col, val, x):
 
 def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_threshold):
     check_spmm_inputs(crow, col, val, x)
+    _maybe_validate(crow, col)
     _check(feature_tile in (64, 128), "feature_tile must be 64 or 128")
     _check(warps_per_block in (2, 4, 8), "warps_per_block must be 2, 4, or 8")
     _check(hub_threshold > 0, "hub_threshold must be positive")
@@ -210,6 +213,7 @@ def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_th
 
 def sddmm_csr_impl(crow, col, query, key):
     check_sddmm_inputs(crow, col, query, key)
+    _maybe_validate(crow, col)
     nnz = col.numel()
     n, f = query.shape
     if f == 0:
@@ -227,6 +231,7 @@ def sddmm_csr_impl(crow, col, query, key):
 
 def sddmm_csr_split_impl(crow, col, query, key, warps_per_block, hub_threshold):
     check_sddmm_inputs(crow, col, query, key)
+    _maybe_validate(crow, col)
     _check(warps_per_block in (2, 4, 8), "warps_per_block must be 2, 4, or 8")
     _check(0 < hub_threshold <= 2**31 - 1, "hub_threshold must be a positive 32-bit integer")
     nnz = col.numel()
@@ -267,6 +272,7 @@ def csr_row_softmax_impl(crow, scores):
 
 def csr_attention_impl(crow, col, query, key, value, scale=1.0):
     check_sddmm_inputs(crow, col, query, key)
+    _maybe_validate(crow, col)
     _check(value.is_cuda and value.device == query.device, "value must be on the same CUDA device as query")
     _check(value.dtype == torch.float32 and value.dim() == 2 and value.is_contiguous(),
            "value must be contiguous float32 with shape [N, F_v]")
@@ -290,6 +296,40 @@ def csr_attention_impl(crow, col, query, key, value, scale=1.0):
         )
     _raise(status, "autosage::csr_attention")
     return out
+
+
+_VALIDATION_RULES = (
+    (1, "crow[0] must be 0"),
+    (2, "crow must be non-decreasing"),
+    (4, "crow[-1] must equal the number of nonzeros"),
+    (8, "column indices must lie in [0, N)"),
+)
+
+
+def validate_csr(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = None) -> None:
+    """Checks a device CSR graph on the GPU (one pass, one host sync) and
+    raises ``ValueError`` naming every violated rule."""
+    _check(crow.is_cuda and col.is_cuda, "crow and col must be CUDA tensors")
+    _check(crow.dtype == torch.long and col.dtype == torch.long, "crow and col must use torch.long indices")
+    crow = crow.contiguous()
+    col = col.contiguous()
+    n = crow.numel() - 1
+    if n < 0:
+        raise ValueError("crow must contain N + 1 entries")
+    flags = torch.zeros(1, dtype=torch.int32, device=crow.device)
+    with torch.cuda.device(crow.device):
+        status = library().as_csr_validate(_ptr(crow), _ptr(col), n, col.numel(), n if n_cols is None else n_cols,
+                                           _ptr(flags), _stream(crow.device))
+    _raise(status, "csr_validate")
+    bad = int(flags.item())
+    problems = [text for bit, text in _VALIDATION_RULES if bad & bit]
+    if problems:
+        raise ValueError("invalid CSR graph: " + "; ".join(problems))
+
+
+def _maybe_validate(crow: torch.Tensor, col: torch.Tensor) -> None:
+    if os.getenv("AUTOSAGE_VALIDATE") == "1":
+        validate_csr(crow, col)
 
 
 def bin_rows_by_degree(crow: torch.Tensor, threshold: int) -> tuple[torch.Tensor, torch.Tensor]:

@@ -112,7 +112,15 @@ def _normalize_csr(crow, col, val, x):
     if val is not None:
         val = val.to(dtype=x.dtype).contiguous()
     _validate_csr(crow, col, val, x)
+    validate_if_requested(crow, col)
     return crow, col, val, x
+
+
+def validate_if_requested(crow, col) -> None:
+    """Runs ``validate_csr`` on CUDA graphs when ``AUTOSAGE_VALIDATE=1``,
+    before any baseline or native gather touches them."""
+    if os.getenv("AUTOSAGE_VALIDATE") == "1" and crow.is_cuda:
+        validate_csr(crow, col)
 
 
 def _cpu_spmm(crow, col, val, x) -> torch.Tensor:
@@ -139,6 +147,24 @@ def spmm_csr(crow, col, val, x) -> torch.Tensor:
     return op(crow, col, val, x)
 
 
+def validate_csr(crow, col, n_cols: Optional[int] = None) -> None:
+    """Checks a CUDA CSR graph with one native pass: ``crow[0] == 0``,
+    ``crow`` non-decreasing, ``crow[-1] == col.numel()`` and every column in
+    ``[0, n_cols)`` (``n_cols`` defaults to N, the square graphs of the
+    operators).  Raises ``ValueError`` naming each violated rule.  The
+    operators themselves run it first when ``AUTOSAGE_VALIDATE=1``."""
+    if crow.dtype not in (torch.int32, torch.int64) or col.dtype not in (torch.int32, torch.int64):
+        raise TypeError("crow and col must use integer indices")
+    if crow.ndim != 1 or col.ndim != 1:
+        raise ValueError("crow and col must be one-dimensional")
+    if not (crow.is_cuda and col.is_cuda):
+        raise ValueError("validate_csr checks CUDA tensors")
+    if not load_native():
+        detail = f": {_LOAD_ERROR}" if _LOAD_ERROR else ""
+        raise RuntimeError(f"AutoSAGE CUDA extension is unavailable{detail}")
+    _native.validate_csr(crow.to(torch.long), col.to(torch.long), n_cols)
+
+
 def spmm_csr_auto(*args, **kwargs):
     from ._auto import spmm_csr_auto as implementation
 
@@ -152,4 +178,5 @@ __all__ = [
     "native_op",
     "spmm_csr",
     "spmm_csr_auto",
+    "validate_csr",
 ]

@@ -139,6 +139,14 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Structure check of a CSR graph (no reference counterpart: the reference
+ * kernels trust their inputs).  ORs into *flags (device int32, zeroed by the
+ * caller): 1 = crow[0] != 0, 2 = crow decreases somewhere, 4 = crow[n] != nnz,
+ * 8 = a column outside [0, n_cols).  Reads nothing out of bounds. */
+int as_csr_validate(const int64_t* crow, const int64_t* col, int64_t n,
+                    int64_t nnz, int64_t n_cols, int32_t* flags,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,6 +62,10 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert status == 1 and lib.as_last_error() == b"hub_threshold must be positive"
     status = lib.as_sddmm_csr_split_f32(None, None, None, None, None, 4, 0, 8, 4, 0, None, 0, None)
     assert lib.as_last_error() == b"hub_threshold must be a positive 32-bit integer"
+    assert lib.as_csr_validate(None, None, -1, 0, 0, None, None) == 1
+    assert lib.as_last_error() == b"sizes must be non-negative"
+    assert lib.as_csr_validate(None, None, 4, 0, 4, None, None) == 1
+    assert lib.as_last_error() == b"null pointer argument"
     # n == 0 is a no-op success
     assert lib.as_spmm_csr_f32(None, None, None, None, None, 0, 0, 8, 1, None) == 0
 
