@@ -1,7 +1,7 @@
 """Backward formulas for the ``autosage::*`` SpMM and SDDMM operators.
 
 The reference registers no autograd for its operators, so ``AutoSAGEConv``
-trains only through the PyTorch baseline there.  Here the four operators get
+trains only through the PyTorch baseline there.  Here the SpMM and SDDMM operators get
 backward formulas built from the same native kernels:
 
 * ``Y = A·X`` (A: CSR, weights ``val`` or ones):
@@ -97,7 +97,7 @@ def _sddmm_backward(ctx, grad_s: torch.Tensor):
 
 def register() -> None:
     """Attaches the backward formulas to the registered operators."""
-    for name in ("spmm_csr", "spmm_csr_split"):
+    for name in ("spmm_csr", "spmm_csr_split", "spmm_csr_colslice"):
         torch.library.register_autograd(f"autosage::{name}", _spmm_backward, setup_context=_spmm_setup)
     for name in ("sddmm_csr", "sddmm_csr_split"):
         torch.library.register_autograd(f"autosage::{name}", _sddmm_backward, setup_context=_sddmm_setup)

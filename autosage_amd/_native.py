@@ -17,8 +17,11 @@ as ``TORCH_CHECK`` does.
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import os
+import threading
+import weakref
 from pathlib import Path
 from typing import Optional
 
@@ -53,6 +56,10 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_ptr, _c_size, _c_ptr],
     ),
     "as_csr_row_softmax_f32": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr]),
+    "as_spmm_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
+    "as_spmm_csr_colslice_f32": (
+        _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr]
+    ),
     "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "as_csr_attention_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "as_csr_attention_f32": (
@@ -211,6 +218,38 @@ def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_th
     return y
 
 
+COLSLICE_ROW_BYTES = 64  # fp64 partials of the 8 column slices, per feature
+
+
+def _colslice_workspace_cap() -> int:
+    return int(float(os.getenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", "2048")) * 2**20)
+
+
+def spmm_csr_colslice_impl(crow, col, val, x):
+    """Column-sliced SpMM (fp64 accumulation, one column slice per XCD).
+    Needs columns ascending within every row; checked once per graph."""
+    check_spmm_inputs(crow, col, val, x)
+    _maybe_validate(crow, col)
+    if not columns_ascending(crow, col):
+        raise ValueError("spmm_csr_colslice requires column indices ascending within every row")
+    y = torch.empty_like(x)
+    n, f = x.shape
+    if n == 0 or f == 0:
+        return y
+    lib = library()
+    full = lib.as_spmm_colslice_workspace_bytes(n, f)
+    per_row = COLSLICE_ROW_BYTES * f
+    minimum = full - (n - 1) * per_row
+    ws = _workspace(max(minimum, min(full, _colslice_workspace_cap())), x.device)
+    with torch.cuda.device(x.device):
+        status = lib.as_spmm_csr_colslice_f32(
+            _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, _ptr(ws), ws.numel(),
+            _stream(x.device),
+        )
+    _raise(status, "autosage::spmm_csr_colslice")
+    return y
+
+
 def sddmm_csr_impl(crow, col, query, key):
     check_sddmm_inputs(crow, col, query, key)
     _maybe_validate(crow, col)
@@ -306,9 +345,14 @@ _VALIDATION_RULES = (
 )
 
 
-def validate_csr(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = None) -> None:
-    """Checks a device CSR graph on the GPU (one pass, one host sync) and
-    raises ``ValueError`` naming every violated rule."""
+_UNSORTED_FLAG = 16
+_SORTED_LOCK = threading.Lock()
+_SORTED_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+_SORTED_MEMO_SIZE = 64
+
+
+def csr_flags(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = None) -> int:
+    """Bit mask of ``as_csr_validate`` (one device pass, one host sync)."""
     _check(crow.is_cuda and col.is_cuda, "crow and col must be CUDA tensors")
     _check(crow.dtype == torch.long and col.dtype == torch.long, "crow and col must use torch.long indices")
     crow = crow.contiguous()
@@ -321,10 +365,43 @@ def validate_csr(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = 
         status = library().as_csr_validate(_ptr(crow), _ptr(col), n, col.numel(), n if n_cols is None else n_cols,
                                            _ptr(flags), _stream(crow.device))
     _raise(status, "csr_validate")
-    bad = int(flags.item())
+    return int(flags.item())
+
+
+def _raise_for_flags(bad: int) -> None:
     problems = [text for bit, text in _VALIDATION_RULES if bad & bit]
     if problems:
         raise ValueError("invalid CSR graph: " + "; ".join(problems))
+
+
+def validate_csr(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = None) -> None:
+    """Checks a device CSR graph on the GPU (one pass, one host sync) and
+    raises ``ValueError`` naming every violated rule."""
+    _raise_for_flags(csr_flags(crow, col, n_cols))
+
+
+def columns_ascending(crow: torch.Tensor, col: torch.Tensor) -> bool:
+    """Whether the columns of every row are in non-decreasing order (the
+    precondition of the column-sliced SpMM).  Memoised per live, unmodified
+    (crow, col) tensor pair; raises ``ValueError`` for a malformed graph."""
+    key = (id(crow), crow._version, id(col), col._version)
+    with _SORTED_LOCK:
+        hit = _SORTED_MEMO.get(key)
+        if hit is not None and hit[0]() is crow and hit[1]() is col:
+            _SORTED_MEMO.move_to_end(key)
+            return hit[2]
+    bad = csr_flags(crow, col)
+    _raise_for_flags(bad)
+    result = not bad & _UNSORTED_FLAG
+    try:
+        refs = (weakref.ref(crow), weakref.ref(col))
+    except TypeError:
+        return result
+    with _SORTED_LOCK:
+        _SORTED_MEMO[key] = (*refs, result)
+        while len(_SORTED_MEMO) > _SORTED_MEMO_SIZE:
+            _SORTED_MEMO.popitem(last=False)
+    return result
 
 
 def _maybe_validate(crow: torch.Tensor, col: torch.Tensor) -> None:
@@ -358,6 +435,10 @@ _SCHEMAS = {
         "spmm_csr_split(Tensor crow, Tensor col, Tensor? val, Tensor x, int feature_tile, int warps_per_block, "
         "int hub_threshold) -> Tensor",
         spmm_csr_split_impl,
+    ),
+    "spmm_csr_colslice": (
+        "spmm_csr_colslice(Tensor crow, Tensor col, Tensor? val, Tensor x) -> Tensor",
+        spmm_csr_colslice_impl,
     ),
     "sddmm_csr": ("sddmm_csr(Tensor crow, Tensor col, Tensor query, Tensor key) -> Tensor", sddmm_csr_impl),
     "sddmm_csr_split": (

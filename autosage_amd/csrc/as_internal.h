@@ -26,6 +26,20 @@ int check_launch(const char* what);
 void clear_error();
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Argument checks shared by the SpMM entry points (n, F < 2^31: kernels use
+// 32-bit row and feature indices).
+inline int validate_spmm(const int64_t* crow, const int64_t* col, const float* x, float* y, int64_t n,
+                         int64_t nnz, int64_t f) {
+  if (n < 0 || n > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
+  if (f < 0 || f > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "F exceeds kernel index range");
+  if (nnz < 0) return fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
+  if (n > 0 && f > 0 && (crow == nullptr || x == nullptr || y == nullptr))
+    return fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (nnz > 0 && col == nullptr) return fail(AS_ERR_INVALID_ARGUMENT, "null col pointer");
+  return AS_OK;
+}
 
 // Degree binning (binning.hip).
 constexpr int kBinRowsPerThread = 4;

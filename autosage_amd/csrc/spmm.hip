@@ -367,8 +367,6 @@ struct SpmmArgs {
   int64_t f;
 };
 
-bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
-
 int rows_per_wave(int layout) { return layout == kSub16 ? 4 : layout == kSub32 ? 2 : 1; }
 
 // Mean degree below which float4 sub-wave rows are used for short rows
@@ -464,17 +462,6 @@ void launch_sched_v(int hv, int layout, const SpmmArgs& a, const SchedLaunch& l,
     case 2: launch_sched_l<2, HAS_VAL, SPLIT64>(layout, a, l, s); break;
     default: launch_sched_l<1, HAS_VAL, SPLIT64>(layout, a, l, s); break;
   }
-}
-
-int validate_spmm(const int64_t* crow, const int64_t* col, const float* x, float* y, int64_t n, int64_t nnz,
-                  int64_t f) {
-  if (n < 0 || n > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
-  if (f < 0 || f > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "F exceeds kernel index range");
-  if (nnz < 0) return fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
-  if (n > 0 && f > 0 && (crow == nullptr || x == nullptr || y == nullptr))
-    return fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
-  if (nnz > 0 && col == nullptr) return fail(AS_ERR_INVALID_ARGUMENT, "null col pointer");
-  return AS_OK;
 }
 
 }  // namespace

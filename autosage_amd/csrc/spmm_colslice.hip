@@ -1,0 +1,324 @@
+// Column-sliced SpMM Y = A·X for graphs whose columns ascend within every
+// row (fp32 in and out, fp64 accumulation).
+//
+// Why.  An MI355X has 8 XCDs, each with its own 4 MB L2; the X-row gathers
+// that miss it cross the fabric to the 256 MB MALL or HBM.  When one kernel
+// walks whole rows, every XCD gathers from all of X and the eight L2s hold
+// the same hot rows.  Here the column space [0, N) is cut into kSlices = 8
+// equal ranges and workgroup g works only on slice g % 8.  The hardware
+// dispatches the workgroups of a launch round-robin over the XCDs, so each
+// XCD gathers only from its own eighth of X and the eight L2s cache eight
+// times as many distinct rows.  (If the dispatch order were different the
+// results would not change; only the cache benefit would be lost.)
+//
+// Steps.
+//   1. Slice points: off[r·7 + b-1] = index, relative to crow[r], of the first
+//      edge of row r whose column is >= the first column of slice b (a binary
+//      search, valid because columns ascend within the row).
+//   2. Degree order: rows sorted into log2-degree buckets, longest first
+//      (the binning kernel of the split SpMM), so long rows start first.
+//   3. For each chunk of rows of that order: the slice kernel, one wave per
+//      (row, slice), writes the fp64 partial sum of the row's edges in the
+//      slice; the reduction kernel adds the non-empty partials of each row in
+//      slice order in fp64 and rounds once to fp32.
+//
+// Arithmetic.  Products w·x of fp32 values are exact in fp64 and every
+// partial and the final sum are fp64 additions, so each output is within
+// about one fp32 rounding of the exact sum (tighter than a sequential fp32
+// sum), and the result is deterministic.  It is not bit-identical to the
+// sequential CSR product: that order is kept by spmm.hip.
+#include "as_device.h"
+#include "as_internal.h"
+
+namespace as {
+
+namespace {
+
+constexpr int kSlices = 8;                 // one column slice per XCD
+constexpr int kSliceBounds = kSlices - 1;  // inner slice points per row
+constexpr int kColsliceLongRow = 1024;     // slice length from which U = 16
+// Rows per chunk: the slice kernel needs 8·ceil(rows / 4) workgroups.
+constexpr int64_t kMaxChunkRows = kMaxBlocksPerLaunch / kSlices * kWavesPerBlock;
+constexpr int64_t kGridStrideBlocks = 65536;
+
+// First column of slice b for an N-column space.
+__device__ __forceinline__ int64_t slice_start(int64_t n_cols, int b) {
+  return (n_cols * b + kSlices - 1) / kSlices;
+}
+
+__global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __restrict__ crow,
+                                                              const int64_t* __restrict__ col, int64_t n,
+                                                              int32_t* __restrict__ off) {
+  const int64_t total = n * kSliceBounds;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int64_t r = t / kSliceBounds;
+    const int b = static_cast<int>(t - r * kSliceBounds) + 1;
+    const int64_t rs = crow[r];
+    int64_t lo = rs;
+    int64_t hi = crow[r + 1];
+    const int64_t start = slice_start(n, b);
+    while (lo < hi) {
+      const int64_t mid = lo + ((hi - lo) >> 1);
+      if (col[mid] < start) lo = mid + 1;
+      else hi = mid;
+    }
+    off[t] = static_cast<int32_t>(lo - rs);
+  }
+}
+
+// Edge range [a, b) of `slice` in a row of `deg` edges, relative to the row
+// start; clamped to [0, deg] so that no access leaves the row.
+__device__ __forceinline__ void slice_range(const int32_t* __restrict__ off, int64_t row, int slice, int64_t deg,
+                                            int64_t& a, int64_t& b) {
+  a = slice == 0 ? 0 : static_cast<int64_t>(off[row * kSliceBounds + slice - 1]);
+  b = slice == kSlices - 1 ? deg : static_cast<int64_t>(off[row * kSliceBounds + slice]);
+  a = a < 0 ? 0 : (a > deg ? deg : a);
+  b = b < a ? a : (b > deg ? deg : b);
+}
+
+// One wave sums edges [rs, re) of a row into out[0, F) in fp64.  Same lane
+// layout as the exact wave-row kernel: lane owns V consecutive features,
+// 64 column indices per coalesced load (one chunk ahead), broadcast through
+// SGPRs, U gathers in flight.
+template <int V, bool HAS_VAL, int U>
+__device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const float* __restrict__ val,
+                                          const float* __restrict__ x, double* __restrict__ out, int64_t F,
+                                          int64_t rs, int64_t re) {
+  const int lane = lane_id();
+  rs = uniform_i64(rs);
+  re = uniform_i64(re);
+  for (int64_t f0 = 0; f0 < F; f0 += kWave * V) {
+    const int64_t fl = f0 + static_cast<int64_t>(lane) * V;
+    const bool active = fl < F;
+    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : 0) * 4);
+    double acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.0;
+    int next_col = 0;
+    float next_w = 1.f;
+    if (lane < re - rs) {
+      next_col = static_cast<int>(col[rs + lane]);
+      if constexpr (HAS_VAL) next_w = val[rs + lane];
+    }
+    for (int64_t base = rs; base < re; base += kWave) {
+      const int cnt = static_cast<int>((re - base) < kWave ? (re - base) : kWave);
+      const int my_col = next_col;
+      const float my_w = next_w;
+      const int64_t nb = base + kWave;
+      if (nb < re && lane < re - nb) {
+        next_col = static_cast<int>(col[nb + lane]);
+        if constexpr (HAS_VAL) next_w = val[nb + lane];
+      }
+      int j = 0;
+      for (; j + U <= cnt; j += U) {
+        FVec<V> xv[U];
+        float w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = bcast_i32(my_col, j + u);
+          w[u] = HAS_VAL ? bcast_f32(my_w, j + u) : 1.f;
+          xv[u] = load_vec_off<V>(x + row_offset(c, F), lane_bytes);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (HAS_VAL) {
+              acc[v] = __builtin_fma(static_cast<double>(w[u]), static_cast<double>(xv[u].v[v]), acc[v]);
+            } else {
+              acc[v] = acc[v] + static_cast<double>(xv[u].v[v]);
+            }
+          }
+        }
+      }
+      for (; j < cnt; ++j) {
+        const int c = bcast_i32(my_col, j);
+        const FVec<V> xv = load_vec_off<V>(x + row_offset(c, F), lane_bytes);
+        const float w = HAS_VAL ? bcast_f32(my_w, j) : 1.f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (HAS_VAL) {
+            acc[v] = __builtin_fma(static_cast<double>(w), static_cast<double>(xv.v[v]), acc[v]);
+          } else {
+            acc[v] = acc[v] + static_cast<double>(xv.v[v]);
+          }
+        }
+      }
+    }
+    if (active) {
+      // written once, read once by the reduction: keep them out of the way
+      // of the X rows in the caches
+#pragma unroll
+      for (int v = 0; v < V; ++v) __builtin_nontemporal_store(acc[v], out + fl + v);
+    }
+  }
+}
+
+// Wave per (row, slice) for the rows order[item_begin, item_begin + items);
+// workgroup g takes slice g % 8 and waves (g / 8)·4 .. +3 of the chunk.
+// Partial of chunk row `local` in slice s: partial[(s·chunk + local)·F ..].
+template <int V, bool HAS_VAL>
+__global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restrict__ crow,
+                                                          const int64_t* __restrict__ col,
+                                                          const float* __restrict__ val, const float* __restrict__ x,
+                                                          double* __restrict__ partial, int64_t F,
+                                                          const int32_t* __restrict__ order,
+                                                          const int32_t* __restrict__ off, int64_t item_begin,
+                                                          int64_t items, int64_t chunk) {
+  const int slice = static_cast<int>(blockIdx.x % kSlices);
+  const int64_t local = static_cast<int64_t>(blockIdx.x / kSlices) * kWavesPerBlock + wave_in_block();
+  if (local >= items) return;
+  const int64_t row = uniform_i64(order[item_begin + local]);
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t deg = uniform_i64(crow[row + 1]) - rs;
+  int64_t a, b;
+  slice_range(off, row, slice, deg, a, b);
+  a = uniform_i64(a);
+  b = uniform_i64(b);
+  if (a >= b) return;
+  double* out = partial + (slice * chunk + local) * F;
+  if (b - a >= kColsliceLongRow) slice_row<V, HAS_VAL, 16>(col, val, x, out, F, rs + a, rs + b);
+  else slice_row<V, HAS_VAL, 8>(col, val, x, out, F, rs + a, rs + b);
+}
+
+// Y[row, f..f+VR) = sum over the non-empty slices, in slice order, in fp64,
+// rounded once.  Rows without edges get zeros.
+template <int VR>
+__global__ __launch_bounds__(kBlock) void colslice_reduce_kernel(const int64_t* __restrict__ crow,
+                                                                 const int32_t* __restrict__ off,
+                                                                 const double* __restrict__ partial,
+                                                                 const int32_t* __restrict__ order,
+                                                                 float* __restrict__ y, int64_t F,
+                                                                 int64_t item_begin, int64_t items, int64_t chunk) {
+  const int64_t FV = F / VR;
+  const int64_t total = items * FV;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int64_t local = t / FV;
+    const int64_t f = (t - local * FV) * VR;
+    const int64_t row = order[item_begin + local];
+    const int64_t deg = crow[row + 1] - crow[row];
+    double acc[VR];
+#pragma unroll
+    for (int v = 0; v < VR; ++v) acc[v] = 0.0;
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s) {
+      int64_t a, b;
+      slice_range(off, row, s, deg, a, b);
+      if (a < b) {
+        const double* p = partial + (s * chunk + local) * F + f;
+#pragma unroll
+        for (int v = 0; v < VR; ++v) acc[v] += __builtin_nontemporal_load(p + v);
+      }
+    }
+    FVec<VR> out;
+#pragma unroll
+    for (int v = 0; v < VR; ++v) out.v[v] = static_cast<float>(acc[v]);
+    store_vec<VR>(y + row * F + f, out);
+  }
+}
+
+size_t colslice_fixed_bytes(int64_t n) {
+  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
+  return align_up(rows * kSliceBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
+         bin_workspace_bytes(n);
+}
+
+size_t colslice_row_bytes(int64_t f) { return static_cast<size_t>(kSlices) * static_cast<size_t>(f) * sizeof(double); }
+
+template <bool HAS_VAL>
+void launch_colslice(int v, const int64_t* crow, const int64_t* col, const float* val, const float* x,
+                     double* partial, int64_t f, const int32_t* order, const int32_t* off, int64_t item_begin,
+                     int64_t items, int64_t chunk, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock)));
+  switch (v) {
+    case 4:
+      hipLaunchKernelGGL((colslice_kernel<4, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f, order,
+                         off, item_begin, items, chunk);
+      break;
+    case 2:
+      hipLaunchKernelGGL((colslice_kernel<2, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f, order,
+                         off, item_begin, items, chunk);
+      break;
+    default:
+      hipLaunchKernelGGL((colslice_kernel<1, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f, order,
+                         off, item_begin, items, chunk);
+      break;
+  }
+}
+
+}  // namespace
+
+}  // namespace as
+
+extern "C" {
+
+size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f) {
+  if (n < 0) n = 0;
+  if (f < 1) f = 1;
+  return as::colslice_fixed_bytes(n) + static_cast<size_t>(n > 0 ? n : 1) * as::colslice_row_bytes(f);
+}
+
+int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const float* val, const float* x, float* y,
+                             int64_t n, int64_t nnz, int64_t f, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  as::clear_error();
+  int st = as::validate_spmm(crow, col, x, y, n, nnz, f);
+  if (st != AS_OK) return st;
+  if (n == 0 || f == 0) return AS_OK;
+  const size_t fixed = as::colslice_fixed_bytes(n);
+  const size_t row_bytes = as::colslice_row_bytes(f);
+  if (workspace == nullptr || workspace_bytes < fixed + row_bytes)
+    return as::fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu workspace bytes, got %zu",
+                    fixed + row_bytes, workspace_bytes);
+  if (!as::aligned(workspace, 256)) return as::fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed) / row_bytes);
+  if (chunk > n) chunk = n;
+  if (chunk > as::kMaxChunkRows) chunk = as::kMaxChunkRows;
+
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const size_t rows = static_cast<size_t>(n);
+  int32_t* off = reinterpret_cast<int32_t*>(ws);
+  ws += as::align_up(rows * as::kSliceBounds * sizeof(int32_t), 256);
+  int32_t* order = reinterpret_cast<int32_t*>(ws);
+  ws += as::align_up(rows * sizeof(int32_t), 256);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws);
+  ws += 256;
+  void* bin_ws = ws;
+  double* partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed);
+
+  {
+    const int64_t threads = n * as::kSliceBounds;
+    int64_t blocks = (threads + as::kBlock - 1) / as::kBlock;
+    if (blocks > as::kGridStrideBlocks) blocks = as::kGridStrideBlocks;
+    hipLaunchKernelGGL(as::slice_points_kernel, dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s, crow,
+                       col, n, off);
+  }
+  st = as::launch_bin_rows(crow, n, as::kColsliceLongRow, as::kMaxHeavyBuckets, as::kMaxHeavyBuckets, order, counts,
+                           bin_ws, s);
+  if (st != AS_OK) return st;
+
+  int v = 1;
+  if (f % 4 == 0 && f > 128 && as::aligned(x, 16)) v = 4;
+  else if (f % 2 == 0 && f > 64 && as::aligned(x, 8)) v = 2;
+  const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
+  for (int64_t begin = 0; begin < n; begin += chunk) {
+    const int64_t items = n - begin < chunk ? n - begin : chunk;
+    if (val != nullptr) as::launch_colslice<true>(v, crow, col, val, x, partial, f, order, off, begin, items, chunk, s);
+    else as::launch_colslice<false>(v, crow, col, val, x, partial, f, order, off, begin, items, chunk, s);
+    const int64_t threads = items * (f / vr);
+    int64_t blocks = (threads + as::kBlock - 1) / as::kBlock;
+    if (blocks > as::kGridStrideBlocks) blocks = as::kGridStrideBlocks;
+    if (vr == 2)
+      hipLaunchKernelGGL((as::colslice_reduce_kernel<2>), dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s,
+                         crow, off, partial, order, y, f, begin, items, chunk);
+    else
+      hipLaunchKernelGGL((as::colslice_reduce_kernel<1>), dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s,
+                         crow, off, partial, order, y, f, begin, items, chunk);
+  }
+  return as::check_launch("spmm_csr_colslice");
+}
+
+}  // extern "C"

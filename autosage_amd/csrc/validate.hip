@@ -4,7 +4,9 @@
 // out of bounds).  This pass lets a caller reject a malformed graph before
 // any gather runs: crow[0] == 0, crow non-decreasing, crow[n] == nnz and
 // 0 <= col[e] < n_cols.  It writes a bit mask of the violated rules to a
-// caller-provided int32; it never reads col or crow out of bounds.
+// caller-provided int32, plus bit 16 when columns are not ascending within
+// some row (allowed, but the column-sliced SpMM needs ascending columns);
+// it never reads col or crow out of bounds.
 #include "as_device.h"
 #include "as_internal.h"
 
@@ -17,6 +19,7 @@ enum : int32_t {
   kBadOrder = 2,      // crow[r+1] < crow[r] for some r
   kBadLast = 4,       // crow[n] != nnz
   kBadColumn = 8,     // a column index outside [0, n_cols)
+  kUnsorted = 16,     // columns descend somewhere inside a row (not an error)
 };
 
 __global__ __launch_bounds__(kBlock) void csr_validate_kernel(const int64_t* __restrict__ crow,
@@ -40,6 +43,26 @@ __global__ __launch_bounds__(kBlock) void csr_validate_kernel(const int64_t* __r
   if (bad != 0) atomicOr(flags, bad);
 }
 
+// Wave per row: does any edge have a smaller column than its predecessor in
+// the same row?  Row bounds are clamped to [0, nnz] so that a malformed crow
+// (reported by the kernel above) cannot lead this one out of bounds.
+__global__ __launch_bounds__(kBlock) void csr_sorted_kernel(const int64_t* __restrict__ crow,
+                                                            const int64_t* __restrict__ col, int64_t n,
+                                                            int64_t nnz, int32_t* __restrict__ flags) {
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * (blockDim.x >> 6);
+  bool unsorted = false;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block(); r < n; r += waves) {
+    int64_t rs = crow[r];
+    int64_t re = crow[r + 1];
+    rs = rs < 0 ? 0 : (rs > nnz ? nnz : rs);
+    re = re < rs ? rs : (re > nnz ? nnz : re);
+    for (int64_t e = rs + 1 + lane_id(); e < re; e += kWave) {
+      if (col[e] < col[e - 1]) unsorted = true;
+    }
+  }
+  if (unsorted) atomicOr(flags, static_cast<int32_t>(kUnsorted));
+}
+
 }  // namespace
 
 }  // namespace as
@@ -58,6 +81,12 @@ int as_csr_validate(const int64_t* crow, const int64_t* col, int64_t n, int64_t 
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(as::csr_validate_kernel, dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0,
                      static_cast<hipStream_t>(stream), crow, col, n, nnz, n_cols, flags);
+  if (n > 0 && nnz > 0) {
+    int64_t row_blocks = (n + as::kWavesPerBlock - 1) / as::kWavesPerBlock;
+    if (row_blocks > 4096) row_blocks = 4096;
+    hipLaunchKernelGGL(as::csr_sorted_kernel, dim3(static_cast<unsigned>(row_blocks)), dim3(as::kBlock), 0,
+                       static_cast<hipStream_t>(stream), crow, col, n, nnz, flags);
+  }
   return as::check_launch("csr_validate");
 }
 

@@ -95,6 +95,26 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col,
                           int hub_mode, void* workspace, size_t workspace_bytes,
                           void* stream);
 
+/* Bytes of workspace for as_spmm_csr_colslice_f32 to run in one chunk. */
+size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f);
+
+/* Column-sliced SpMM, an alternative schedule for the same product as
+ * as_spmm_csr_f32 (no reference counterpart; it serves the op
+ * `spmm_csr(...)`'s callers through the scheduler, autosage/_auto.py:266-441).
+ * Precondition: columns ascend (non-strictly) within every row.  The column
+ * space is cut into 8 ranges, one per XCD, so that each XCD's L2 caches only
+ * its eighth of X; per-slice partials are accumulated in fp64 and added in
+ * slice order, then rounded once: deterministic, within about one fp32
+ * rounding of the exact sum, not bit-identical to the sequential product.
+ * The workspace (256-byte aligned) holds n·28 B of slice points, the row
+ * order and n·f·64 B of partials; a smaller one (at least the size for one
+ * row) makes the call run in row chunks. */
+int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col,
+                             const float* val, const float* x, float* y,
+                             int64_t n, int64_t nnz, int64_t f,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* out[e] = <query[row(e)], key[col[e]]> for every nonzero, CSR order.
  * Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134), op schema :192.
  * The dot product uses the reference kernel's summation order
@@ -142,7 +162,9 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col,
 /* Structure check of a CSR graph (no reference counterpart: the reference
  * kernels trust their inputs).  ORs into *flags (device int32, zeroed by the
  * caller): 1 = crow[0] != 0, 2 = crow decreases somewhere, 4 = crow[n] != nnz,
- * 8 = a column outside [0, n_cols).  Reads nothing out of bounds. */
+ * 8 = a column outside [0, n_cols); and 16 = columns descend somewhere inside
+ * a row, which is valid CSR but rules out as_spmm_csr_colslice_f32.  Reads
+ * nothing out of bounds. */
 int as_csr_validate(const int64_t* crow, const int64_t* col, int64_t n,
                     int64_t nnz, int64_t n_cols, int32_t* flags,
                     void* stream);

@@ -1,0 +1,140 @@
+"""GPU parity of the column-sliced SpMM (``autosage::spmm_csr_colslice``).
+
+The kernel accumulates each (row, column slice) partial in fp64 and adds the
+partials in fp64 before one rounding, so it is checked against the CPU
+oracle's fp64 product: |gpu - fp64| <= 1e-6·|fp64| + 1e-9 (tighter than the
+1e-5 relative / 1e-6 absolute bar for fp32 results, which is asserted too).
+It is deterministic: repeated and chunked calls give identical bits.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from autosage_amd import _native, synth
+from tests.gpu_common import case_graph, require_gpu, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def _inputs(features, weighted, seed=0, rows=3000, degree=9, hubs=3, hub_degree=2500, empty=0.08):
+    crow, col = case_graph(rows, degree, seed=seed, hubs=hubs, hub_degree=hub_degree, empty=empty)
+    rng = np.random.default_rng(seed + 100)
+    val = rng.standard_normal(col.size).astype(np.float32) if weighted else None
+    x = rng.standard_normal((rows, features)).astype(np.float32)
+    return crow, col, val, x
+
+
+def _assert_fp64_close(got: np.ndarray, exact: np.ndarray) -> None:
+    err = np.abs(got.astype(np.float64) - exact)
+    assert np.all(err <= 1e-6 * np.abs(exact) + 1e-9), float(np.max(err - 1e-6 * np.abs(exact)))
+    assert np.all(err <= 1e-5 * np.abs(exact) + 1e-6)
+
+
+def _colslice(crow, col, val, x):
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    return torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x)
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("features", [1, 3, 33, 64, 96, 128, 200, 256, 300])
+def test_colslice_against_fp64(features, weighted):
+    crow, col, val, x = _inputs(features, weighted, seed=features + 3 * weighted)
+    got = _colslice(crow, col, val, x).cpu().numpy()
+    _assert_fp64_close(got, oracle.spmm_f64(crow, col, val, x))
+
+
+def test_colslice_long_slices_and_empty_rows():
+    # hub rows of 20000 edges: about 2500 per slice, the U = 16 path
+    crow, col, val, x = _inputs(128, True, seed=11, rows=24000, degree=4, hubs=4, hub_degree=20000, empty=0.3)
+    assert np.diff(crow).max() == 20000 and (np.diff(crow) == 0).sum() > 1000
+    got = _colslice(crow, col, val, x).cpu().numpy()
+    _assert_fp64_close(got, oracle.spmm_f64(crow, col, val, x))
+    assert np.all(got[np.diff(crow) == 0] == 0)
+
+
+def test_colslice_edges_in_one_slice_and_tiny_graphs():
+    # all columns of every row fall into the last slice
+    rows = 64
+    crow = np.arange(0, 3 * rows + 1, 3, dtype=np.int64)
+    col = np.tile(np.array([61, 62, 63], dtype=np.int64), rows)
+    x = np.random.default_rng(0).standard_normal((rows, 64)).astype(np.float32)
+    got = _colslice(crow, col, None, x).cpu().numpy()
+    _assert_fp64_close(got, oracle.spmm_f64(crow, col, None, x))
+    # fewer rows than slices; and a graph without edges
+    for n in (1, 2, 7):
+        crow, col = case_graph(n, 2, seed=n)
+        x = np.random.default_rng(n).standard_normal((n, 16)).astype(np.float32)
+        _assert_fp64_close(_colslice(crow, col, None, x).cpu().numpy(), oracle.spmm_f64(crow, col, None, x))
+    crow = np.zeros(11, dtype=np.int64)
+    got = _colslice(crow, np.zeros(0, dtype=np.int64), None, np.ones((10, 8), np.float32))
+    assert torch.count_nonzero(got).item() == 0
+
+
+def test_colslice_deterministic_and_chunked(monkeypatch):
+    crow, col, val, x = _inputs(128, True, seed=5)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    first = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x)
+    again = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x)
+    assert torch.equal(first, again)
+    # a workspace for ~100 rows of partials: the call runs in 30 row chunks
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((100 * 128 * 64 + 200_000) / 2**20))
+    chunked = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x)
+    assert torch.equal(first, chunked)
+
+
+def test_colslice_rejects_unsorted_columns():
+    crow, col, val, x = _inputs(64, False, seed=9)
+    d_crow, d_col, _, d_x = to_dev(crow, col, None, x)
+    assert _native.columns_ascending(d_crow, d_col)
+    row = int(np.argmax(np.diff(crow)))
+    shuffled = col.copy()
+    shuffled[crow[row]:crow[row + 1]] = shuffled[crow[row]:crow[row + 1]][::-1]
+    d_shuffled = torch.from_numpy(shuffled).cuda()
+    assert not _native.columns_ascending(d_crow, d_shuffled)
+    with pytest.raises(ValueError, match="ascending"):
+        torch.ops.autosage.spmm_csr_colslice(d_crow, d_shuffled, None, d_x)
+    # equal neighbouring columns are allowed
+    crow2 = np.array([0, 3], dtype=np.int64)
+    col2 = np.array([0, 0, 0], dtype=np.int64)
+    assert _native.columns_ascending(*to_dev(crow2, col2))
+    # the memo follows in-place changes of col
+    d_col_copy = d_col.clone()
+    assert _native.columns_ascending(d_crow, d_col_copy)
+    d_col_copy[crow[row]:crow[row + 1]] = d_col_copy[crow[row]:crow[row + 1]].flip(0)
+    assert not _native.columns_ascending(d_crow, d_col_copy)
+
+
+def test_colslice_backward_matches_exact_op():
+    crow, col, val, x = _inputs(64, True, seed=21)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    grads = []
+    for op in (torch.ops.autosage.spmm_csr_colslice, torch.ops.autosage.spmm_csr):
+        v = d_val.clone().requires_grad_(True)
+        xx = d_x.clone().requires_grad_(True)
+        y = op(d_crow, d_col, v, xx)
+        (y * torch.arange(64, device="cuda", dtype=torch.float32)).sum().backward()
+        grads.append((v.grad, xx.grad))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+
+
+def test_colslice_skewed_config_rows():
+    """A generated power-law graph (the structure of the benchmark graphs, at
+    a smaller size): sampled rows against fp64 sums on the GPU."""
+    crow, col = synth.random_csr(60000, 40, seed=3, hub_rows=20, hub_degree=30000)
+    x = np.random.default_rng(3).standard_normal((60000, 128)).astype(np.float32)
+    d_crow, d_col, d_x = to_dev(crow, col, x)
+    got = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, None, d_x)
+    rows = np.concatenate([np.argsort(-np.diff(crow))[:20], np.random.default_rng(4).choice(60000, 500, False)])
+    x64 = d_x.double()
+    for r in rows.tolist():
+        exact = x64.index_select(0, d_col[crow[r]:crow[r + 1]]).sum(0).cpu().numpy()
+        _assert_fp64_close(got[r].cpu().numpy(), exact)
