@@ -20,6 +20,7 @@ gfx950 changes:
 
 from __future__ import annotations
 
+import json
 import os
 import statistics
 import time
@@ -184,15 +185,40 @@ def _spmm_candidates(crow: torch.Tensor, feature_width: int, config: SchedulerCo
     return sorted(pool, key=rank)[: max(1, config.candidate_count)]
 
 
+COLSLICE = "colslice"  # candidate value of the column-sliced SpMM
+# Column slicing pays when X is well beyond the 8 x 4 MB of L2 and rows are
+# long enough that the per-(row, slice) fp64 partials (64·F bytes per row)
+# stay small next to the gathers (4·F bytes per edge).
+_COLSLICE_MIN_X_BYTES = 64 << 20
+_COLSLICE_MIN_MEAN_DEGREE = 64
+
+
+def _colslice_eligible(crow, col, x, config: SchedulerConfig) -> bool:
+    """Whether the full-graph check should time the column-sliced SpMM."""
+    if config.column_slices == "off" or not config.full_graph_check or native_op("spmm_csr_colslice") is None:
+        return False
+    n = crow.numel() - 1
+    if n <= 0 or col.numel() == 0:
+        return False
+    if config.column_slices == "auto":
+        if x.numel() * x.element_size() < _COLSLICE_MIN_X_BYTES or col.numel() < _COLSLICE_MIN_MEAN_DEGREE * n:
+            return False
+    from ._native import columns_ascending
+
+    return columns_ascending(crow, col)
+
+
 def _cache_hit_allowed(result: dict[str, Any], config: SchedulerConfig) -> bool:
     if result.get("schema_version") != AUTOTUNE_SCHEMA_VERSION:
         return False
     return True if config.replay_only else result.get("configuration") == config.tuning_signature()
 
 
-def _cached_native_available(operation: str, choice: str, candidate: Optional[list[int]]) -> bool:
+def _cached_native_available(operation: str, choice: str, candidate) -> bool:
     if choice != "autosage":
         return True
+    if candidate == COLSLICE:
+        return native_op(operation + "_colslice") is not None
     return native_op(operation + ("_split" if candidate is not None else "")) is not None
 
 
@@ -208,6 +234,15 @@ def _cpu_info(operation: str) -> dict[str, Any]:
 
 
 def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
+    if choice == "autosage" and candidate == COLSLICE:
+        from ._native import columns_ascending
+
+        # A schedule key hashes only the ends of col, so a cached column-sliced
+        # choice can meet a graph with the same key whose columns are not
+        # ascending; that graph gets the exact whole-graph kernel.
+        if columns_ascending(crow, col):
+            return native_op("spmm_csr_colslice")(crow, col, val, x)
+        return native_op("spmm_csr")(crow, col, val, x)
     if choice == "autosage":
         split, core = native_op("spmm_csr_split"), native_op("spmm_csr")
         if split is not None and candidate is not None:
@@ -397,22 +432,45 @@ def spmm_csr_auto(
         core_call=core_call,
     )
     result = _result_dict("spmm", config, probe, baseline_name, s_crow, s_col, sample_ms)
-    if result["choice"] == "autosage" and config.full_graph_check:
-        full_baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
-        confirm = _full_graph_confirmation(
-            lambda: _run_spmm_choice("autosage", result["candidate"], crow, col, val, x), full_baseline
-        )
-        result["full_graph"] = confirm
-        if confirm["autosage_ms"] > confirm["baseline_ms"]:
-            result["choice"] = "baseline"
-            result["candidate"] = None
-            result["reason"] = "slower than the baseline on the full graph"
+    colslice = _colslice_eligible(crow, col, x, config)
+    if (result["choice"] == "autosage" and config.full_graph_check) or colslice:
+        _confirm_spmm_on_full_graph(result, colslice, crow, col, val, x)
     output = _run_spmm_choice(result["choice"], result["candidate"], crow, col, val, x)
     if config.cache:
         cache.store(device, graph, result)
     log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})
     _verbose("spmm", result, verbose)
     return output, result
+
+
+def _confirm_spmm_on_full_graph(result: dict[str, Any], colslice: bool, crow, col, val, x) -> None:
+    """Times the sampled choice (when native) and, when eligible, the
+    column-sliced SpMM on the full graph against the baseline, and keeps the
+    fastest; a native variant slower than the baseline is dropped."""
+    full_baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
+    sampled = result["candidate"] if result["choice"] == "autosage" else None
+    options: list[Any] = ([sampled] if result["choice"] == "autosage" else []) + ([COLSLICE] if colslice else [])
+    times = {}
+    for option in options:
+        times[json.dumps(option)] = _time_cuda(
+            lambda o=option: _run_spmm_choice("autosage", o, crow, col, val, x), warmup=1, iterations=3
+        )["best_ms"]
+    baseline_ms = _time_cuda(full_baseline, warmup=1, iterations=3)["best_ms"]
+    best = min(options, key=lambda o: times[json.dumps(o)])
+    best_ms = times[json.dumps(best)]
+    confirm: dict[str, Any] = {"autosage_ms": best_ms, "baseline_ms": baseline_ms}
+    if colslice:
+        confirm["colslice_ms"] = times[json.dumps(COLSLICE)]
+        if result["choice"] == "autosage":
+            confirm["sampled_choice_ms"] = times[json.dumps(sampled)]
+    result["full_graph"] = confirm
+    if best_ms > baseline_ms:
+        result["choice"] = "baseline"
+        result["candidate"] = None
+        result["reason"] = "slower than the baseline on the full graph"
+    else:
+        result["choice"] = "autosage"
+        result["candidate"] = best
 
 
 def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dict[str, Any]]:
@@ -443,6 +501,12 @@ def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dic
     elif core is not None:
         best = _time_cuda(lambda: core(crow, col, val, x), warmup=2, iterations=5)["best_ms"]
         timings.append({"candidate": None, "best_ms": best})
+    if _colslice_eligible(crow, col, x, config):
+        colslice_op = native_op("spmm_csr_colslice")
+        t = _time_cuda(lambda: colslice_op(crow, col, val, x), warmup=2, iterations=5)
+        timings.append({"candidate": COLSLICE, "best_ms": t["best_ms"]})
+        if t["best_ms"] < best:
+            best, selected = t["best_ms"], COLSLICE
     choice = "autosage" if best <= guardrail * baseline_timing["best_ms"] else "baseline"
     result = {
         "operation": "spmm",

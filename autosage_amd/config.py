@@ -7,7 +7,12 @@ of cache validity (``_auto.py:219-224``).  One field is added: ``hub_mode``
 gfx950 split kernel, which changes results' rounding and therefore belongs in
 the signature.  ``full_graph_check`` (``AUTOSAGE_FULL_CHECK``) makes a sampled
 "autosage" decision confirm itself once on the full graph against the
-PyTorch-ROCm baseline before it is cached.
+PyTorch-ROCm baseline before it is cached.  ``column_slices``
+(``AUTOSAGE_COLUMN_SLICES`` = ``auto`` | ``on`` | ``off``) controls the
+column-sliced SpMM (one column slice per XCD, fp64 accumulation): ``auto``
+times it on the full graph when the graph is large enough to profit, ``on``
+times it on every graph with ascending columns, ``off`` never uses it, which
+keeps SpMM results bit-identical to the sequential CSR product.
 """
 
 from __future__ import annotations
@@ -53,6 +58,7 @@ class SchedulerConfig:
     hub_threshold: Optional[int] = None
     hub_mode: str = "exact"
     full_graph_check: bool = True
+    column_slices: str = "auto"
 
     def __post_init__(self) -> None:
         if not 0 < self.guardrail <= 1:
@@ -71,6 +77,8 @@ class SchedulerConfig:
             raise ValueError("hub_threshold must be positive")
         if self.hub_mode not in ("exact", "split64"):
             raise ValueError("hub_mode must be 'exact' or 'split64'")
+        if self.column_slices not in ("auto", "on", "off"):
+            raise ValueError("column_slices must be 'auto', 'on' or 'off'")
 
     def tuning_signature(self) -> dict[str, object]:
         return {
@@ -89,6 +97,7 @@ class SchedulerConfig:
             "hub_threshold": self.hub_threshold,
             "hub_mode": self.hub_mode,
             "full_graph_check": self.full_graph_check,
+            "column_slices": self.column_slices,
         }
 
     @classmethod
@@ -112,4 +121,5 @@ class SchedulerConfig:
             hub_threshold=_optional_int("AUTOSAGE_HUB_T"),
             hub_mode=(env("AUTOSAGE_HUB_MODE") or "exact").strip().lower(),
             full_graph_check=_boolean("AUTOSAGE_FULL_CHECK", True),
+            column_slices=(env("AUTOSAGE_COLUMN_SLICES") or "auto").strip().lower(),
         )

@@ -224,7 +224,9 @@ def main() -> int:
     parser.add_argument("--features", type=int, default=None)
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--variant", default="calibrated",
-                        help="calibrated | whole | t,w,h (split candidate)")
+                        help="calibrated | whole | colslice | t,w,h (split candidate)")
+    parser.add_argument("--exact-only", action="store_true",
+                        help="calibrate only variants bit-identical to the sequential CSR product")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gpu-baseline", action="store_true")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -244,6 +246,7 @@ def main() -> int:
     import autosage_amd
     from autosage_amd import synth
     from autosage_amd._auto import _prepare_spmm_baseline, _spmm_candidates
+    from autosage_amd._native import columns_ascending
     from autosage_amd.config import SchedulerConfig
 
     if not autosage_amd.load_native():
@@ -274,11 +277,17 @@ def main() -> int:
         for cand in _spmm_candidates(crow, f, SchedulerConfig(candidate_count=6)):
             variants[",".join(map(str, cand))] = (
                 lambda c=cand: torch.ops.autosage.spmm_csr_split(crow, col, val, x, *c))
+        # the column-sliced SpMM (fp64 accumulation) for graphs with ascending
+        # columns; listed last so that an exact variant wins a tie
+        if not args.exact_only and columns_ascending(crow, col):
+            variants["colslice"] = lambda: torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
         calib = {}
         if args.variant == "calibrated":
             chosen = calibrate(variants, calib)
         else:
             chosen = args.variant
+            if chosen == "colslice" and chosen not in variants:
+                variants[chosen] = lambda: torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
             if chosen not in variants:
                 t_, w_, h_ = map(int, chosen.split(","))
                 variants[chosen] = lambda: torch.ops.autosage.spmm_csr_split(crow, col, val, x, t_, w_, h_)
@@ -308,6 +317,8 @@ def main() -> int:
                 "nnz": nnz,
                 "features": f,
                 "variant": chosen,
+                "accumulation": "fp64 partials per column slice" if chosen == "colslice"
+                else "fp32, CSR edge order (bit-identical to the sequential product)",
                 "graph_fingerprint": w.fingerprint(),
                 "degree_stats": w.degree_stats(),
             },

@@ -138,3 +138,42 @@ def test_colslice_skewed_config_rows():
     for r in rows.tolist():
         exact = x64.index_select(0, d_col[crow[r]:crow[r + 1]]).sum(0).cpu().numpy()
         _assert_fp64_close(got[r].cpu().numpy(), exact)
+
+
+def test_scheduler_times_colslice_on_the_full_graph(monkeypatch, tmp_path):
+    import autosage_amd
+
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "on")
+    crow, col, val, x = _inputs(64, False, seed=31, rows=6000, degree=30)
+    d_crow, d_col, _, d_x = to_dev(crow, col, None, x)
+    out, info = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert "colslice_ms" in info["full_graph"] and info["full_graph"]["colslice_ms"] > 0
+    exact = oracle.spmm_f64(crow, col, None, x)
+    if info["candidate"] == "colslice":
+        _assert_fp64_close(out.cpu().numpy(), exact)
+    elif info["choice"] == "autosage":
+        assert np.array_equal(out.cpu().numpy(), oracle.spmm_seq(crow, col, None, x))
+    again, cached = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert cached["from_cache"] and cached["candidate"] == info["candidate"]
+    assert torch.equal(again, out)
+    # a graph whose columns are not ascending: its schedule key equals the
+    # sorted graph's (the key hashes only the ends of col) ...
+    shuffled = col.copy()
+    r = int(np.argmax(np.diff(crow)))
+    assert 2048 < crow[r] and crow[r + 1] < col.size - 2048
+    shuffled[crow[r]:crow[r + 1]] = shuffled[crow[r]:crow[r + 1]][::-1]
+    d_shuffled = torch.from_numpy(shuffled).cuda()
+    replayed, info_r = autosage_amd.spmm_csr_auto(d_crow, d_shuffled, None, d_x)
+    assert info_r["from_cache"]
+    if info_r["candidate"] == "colslice":
+        # ... so a cached column-sliced choice runs the exact kernel on it
+        assert np.array_equal(replayed.cpu().numpy(), oracle.spmm_seq(crow, shuffled, None, x))
+    # ... and without a cache record it is never timed with column slices
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path / "second"))
+    _, info2 = autosage_amd.spmm_csr_auto(d_crow, d_shuffled, None, d_x)
+    assert "colslice_ms" not in info2.get("full_graph", {}) and info2.get("candidate") != "colslice"
+    # off: never timed
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
+    _, info3 = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert "colslice_ms" not in info3.get("full_graph", {}) and info3.get("candidate") != "colslice"

@@ -53,6 +53,31 @@ def test_hub_mode_is_part_of_the_signature(monkeypatch):
         SchedulerConfig.from_env()
 
 
+def test_column_slices_is_part_of_the_signature(monkeypatch):
+    assert SchedulerConfig.from_env().tuning_signature()["column_slices"] == "auto"
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "OFF")
+    assert SchedulerConfig.from_env().tuning_signature()["column_slices"] == "off"
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "sometimes")
+    with pytest.raises(ValueError, match="column_slices"):
+        SchedulerConfig.from_env()
+
+
+def test_column_slices_never_eligible_without_the_native_op(monkeypatch):
+    from autosage_amd import _auto
+
+    crow = torch.arange(0, 100 * 1000 + 1, 100)
+    col = torch.arange(100 * 1000) % 1000
+    x = torch.zeros(1000, 20000)  # 80 MB
+    monkeypatch.setattr(_auto, "native_op", lambda name: None)
+    assert not _auto._colslice_eligible(crow, col, x, SchedulerConfig(column_slices="on"))
+    monkeypatch.setattr(_auto, "native_op", lambda name: object())
+    assert not _auto._colslice_eligible(crow, col, x, SchedulerConfig(column_slices="off"))
+    assert not _auto._colslice_eligible(crow, col, x, SchedulerConfig(full_graph_check=False))
+    # auto: too little X or too few edges per row
+    assert not _auto._colslice_eligible(crow, col, x[:, :100], SchedulerConfig())
+    assert not _auto._colslice_eligible(crow, col[: 63 * 1000], x, SchedulerConfig())
+
+
 @pytest.mark.parametrize(
     "kwargs, message",
     [
