@@ -77,8 +77,9 @@ __device__ __forceinline__ void slice_range(const int32_t* __restrict__ off, int
   b = b < a ? a : (b > deg ? deg : b);
 }
 
-// One wave sums edges [rs, re) of a row into out[0, F) in fp64.  Same lane
-// layout as the exact wave-row kernel: lane owns V consecutive features,
+// One wave sums edges [rs, re) of a row into out[0, F) in fp64 (F not a
+// multiple of 4, or X not 16-byte aligned).  Same lane layout as the exact
+// wave-row kernel: lane owns V consecutive features,
 // 64 column indices per coalesced load (one chunk ahead), broadcast through
 // SGPRs, U gathers in flight.
 template <int V, bool HAS_VAL, int U>
@@ -155,9 +156,98 @@ __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const
   }
 }
 
+// Wide form of slice_row for F % 4 == 0 and 16-byte aligned X: G lanes per
+// edge, each lane owning 4 consecutive features (a float4 load), so that one
+// gather instruction fetches 64/G = EPI edges.  Gathers that hit L2 run at
+// twice the bytes per instruction of 8-byte lanes (four times of 4-byte
+// lanes).  Lane group k takes edges j + k, j + EPI + k, ... and keeps its own
+// fp64 sums; the groups are added at the end in a fixed butterfly order.
+// Features beyond 4·G are covered by further passes (F > 256).
+template <int G, bool HAS_VAL, int U>
+__device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, const float* __restrict__ val,
+                                               const float* __restrict__ x, double* __restrict__ out, int64_t F,
+                                               int64_t rs, int64_t re) {
+  constexpr int EPI = kWave / G;
+  const int lane = lane_id();
+  const int grp = lane / G;
+  const int gl = lane % G;
+  rs = uniform_i64(rs);
+  re = uniform_i64(re);
+  for (int64_t f0 = 0; f0 < F; f0 += 4 * G) {
+    const int64_t fl = f0 + 4 * static_cast<int64_t>(gl);
+    const bool active = fl < F;
+    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * 4);
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    int next_col = 0;
+    float next_w = 1.f;
+    if (lane < re - rs) {
+      next_col = static_cast<int>(col[rs + lane]);
+      if constexpr (HAS_VAL) next_w = val[rs + lane];
+    }
+    for (int64_t base = rs; base < re; base += kWave) {
+      const int cnt = static_cast<int>((re - base) < kWave ? (re - base) : kWave);
+      const int my_col = next_col;
+      const float my_w = next_w;
+      const int64_t nb = base + kWave;
+      if (nb < re && lane < re - nb) {
+        next_col = static_cast<int>(col[nb + lane]);
+        if constexpr (HAS_VAL) next_w = val[nb + lane];
+      }
+      for (int j = 0; j < cnt; j += U * EPI) {
+        FVec<4> xv[U];
+        float w[U];
+        bool live[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          // this lane group's edge; past the end, a clamped valid edge whose
+          // value is not added
+          live[u] = j + u * EPI + grp < cnt;
+          int c = 0;
+          w[u] = 1.f;
+#pragma unroll
+          for (int k = 0; k < EPI; ++k) {
+            const int e = j + u * EPI + k < cnt ? j + u * EPI + k : cnt - 1;
+            const int ck = bcast_i32(my_col, e);
+            c = grp == k ? ck : c;
+            if constexpr (HAS_VAL) {
+              const float wk = bcast_f32(my_w, e);
+              w[u] = grp == k ? wk : w[u];
+            }
+          }
+          xv[u] = load_vec_off<4>(x + row_offset(c, F), lane_bytes);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (live[u]) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              if constexpr (HAS_VAL) {
+                acc[v] = __builtin_fma(static_cast<double>(w[u]), static_cast<double>(xv[u].v[v]), acc[v]);
+              } else {
+                acc[v] = acc[v] + static_cast<double>(xv[u].v[v]);
+              }
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = G; o < kWave; o <<= 1) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] += __shfl_xor(acc[v], o, kWave);
+    }
+    if (grp == 0 && active) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) __builtin_nontemporal_store(acc[v], out + fl + v);
+    }
+  }
+}
+
 // Wave per (row, slice) for the rows order[item_begin, item_begin + items);
 // workgroup g takes slice g % 8 and waves (g / 8)·4 .. +3 of the chunk.
 // Partial of chunk row `local` in slice s: partial[(s·chunk + local)·F ..].
+// V in {1, 2}: narrow lanes (slice_row); V = 16, 32, 64: wide lanes with
+// G = V lanes per edge (slice_row_wide).
 template <int V, bool HAS_VAL>
 __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restrict__ crow,
                                                           const int64_t* __restrict__ col,
@@ -178,8 +268,12 @@ __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restr
   b = uniform_i64(b);
   if (a >= b) return;
   double* out = partial + (slice * chunk + local) * F;
-  if (b - a >= kColsliceLongRow) slice_row<V, HAS_VAL, 16>(col, val, x, out, F, rs + a, rs + b);
-  else slice_row<V, HAS_VAL, 8>(col, val, x, out, F, rs + a, rs + b);
+  if constexpr (V >= 16) {
+    slice_row_wide<V, HAS_VAL, (V == kWave ? 8 : 4)>(col, val, x, out, F, rs + a, rs + b);
+  } else {
+    if (b - a >= kColsliceLongRow) slice_row<V, HAS_VAL, 16>(col, val, x, out, F, rs + a, rs + b);
+    else slice_row<V, HAS_VAL, 8>(col, val, x, out, F, rs + a, rs + b);
+  }
 }
 
 // Y[row, f..f+VR) = sum over the non-empty slices, in slice order, in fp64,
@@ -233,9 +327,17 @@ void launch_colslice(int v, const int64_t* crow, const int64_t* col, const float
                      int64_t items, int64_t chunk, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock)));
   switch (v) {
-    case 4:
-      hipLaunchKernelGGL((colslice_kernel<4, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f, order,
-                         off, item_begin, items, chunk);
+    case 64:
+      hipLaunchKernelGGL((colslice_kernel<64, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f,
+                         order, off, item_begin, items, chunk);
+      break;
+    case 32:
+      hipLaunchKernelGGL((colslice_kernel<32, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f,
+                         order, off, item_begin, items, chunk);
+      break;
+    case 16:
+      hipLaunchKernelGGL((colslice_kernel<16, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f,
+                         order, off, item_begin, items, chunk);
       break;
     case 2:
       hipLaunchKernelGGL((colslice_kernel<2, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f, order,
@@ -300,8 +402,10 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
                            bin_ws, s);
   if (st != AS_OK) return st;
 
+  // lanes: G = 16/32/64 lanes per edge with float4 loads (F <= 64 / 128 /
+  // more), else 8- or 4-byte lanes with one edge per gather
   int v = 1;
-  if (f % 4 == 0 && f > 128 && as::aligned(x, 16)) v = 4;
+  if (f % 4 == 0 && as::aligned(x, 16)) v = f <= 64 ? 16 : (f <= 128 ? 32 : 64);
   else if (f % 2 == 0 && f > 64 && as::aligned(x, 8)) v = 2;
   const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
   for (int64_t begin = 0; begin < n; begin += chunk) {
