@@ -81,6 +81,21 @@ def test_config3_skewed_spmm(features, monkeypatch):
     assert heavy.sum() >= 8
     assert np.all(np.abs(s64[heavy] - exact[heavy]) <= 1e-6 * np.abs(exact[heavy]) + 1e-9)
     assert np.array_equal(s64[~heavy], ref[~heavy])
+    # column-sliced SpMM (fp64 partials): every sampled row within 1e-6 of
+    # fp64; repeated calls, and a call in row chunks, give the same bits
+    monkeypatch.setenv("AUTOSAGE_HUB_MODE", "exact")
+    sliced = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, None, d_x)
+    got = sliced[d_rows].cpu().numpy()
+    assert np.all(np.abs(got - exact) <= 1e-6 * np.abs(exact) + 1e-9)
+    assert np.all(np.abs(got - exact) <= RTOL * np.abs(exact) + ATOL)
+    assert torch.equal(torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, None, d_x), sliced)
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", "300")
+    assert torch.equal(torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, None, d_x), sliced)
+    # the sequential fp32 order (the reference's) is itself further than
+    # 1e-5 from the fp64 sums on rows that nearly cancel; the sliced sums are not
+    worst_seq = np.max(np.abs(ref - exact) / (RTOL * np.abs(exact) + ATOL))
+    worst_sliced = np.max(np.abs(got - exact) / (RTOL * np.abs(exact) + ATOL))
+    assert worst_sliced < 0.1 and worst_sliced < worst_seq
 
 
 @pytest.mark.parametrize("features", [64, 128])
