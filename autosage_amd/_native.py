@@ -222,7 +222,7 @@ COLSLICE_ROW_BYTES = 64  # fp64 partials of the 8 column slices, per feature
 
 
 def _colslice_workspace_cap() -> int:
-    return int(float(os.getenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", "2048")) * 2**20)
+    return int(float(os.getenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", "4096")) * 2**20)
 
 
 def spmm_csr_colslice_impl(crow, col, val, x):

@@ -162,18 +162,18 @@ __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const
 // twice the bytes per instruction of 8-byte lanes (four times of 4-byte
 // lanes).  Lane group k takes edges j + k, j + EPI + k, ... and keeps its own
 // fp64 sums; the groups are added at the end in a fixed butterfly order.
-// Features beyond 4·G are covered by further passes (F > 256).
+// One call covers the feature tile [f0, f0 + 4·G).
 template <int G, bool HAS_VAL, int U>
 __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, const float* __restrict__ val,
                                                const float* __restrict__ x, double* __restrict__ out, int64_t F,
-                                               int64_t rs, int64_t re) {
+                                               int64_t rs, int64_t re, int64_t f0) {
   constexpr int EPI = kWave / G;
   const int lane = lane_id();
   const int grp = lane / G;
   const int gl = lane % G;
   rs = uniform_i64(rs);
   re = uniform_i64(re);
-  for (int64_t f0 = 0; f0 < F; f0 += 4 * G) {
+  {
     const int64_t fl = f0 + 4 * static_cast<int64_t>(gl);
     const bool active = fl < F;
     const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * 4);
@@ -246,8 +246,12 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
 // Wave per (row, slice) for the rows order[item_begin, item_begin + items);
 // workgroup g takes slice g % 8 and waves (g / 8)·4 .. +3 of the chunk.
 // Partial of chunk row `local` in slice s: partial[(s·chunk + local)·F ..].
-// V in {1, 2}: narrow lanes (slice_row); V = 16, 32, 64: wide lanes with
-// G = V lanes per edge (slice_row_wide).
+// V in {1, 2}: narrow lanes (slice_row, all features); V = 16, 32: wide
+// lanes with G = V lanes per edge (slice_row_wide), one feature tile of 4·G
+// features per wave.  Feature tiles are the outermost grid dimension: every
+// (slice, row) of tile 0 is dispatched before tile 1, so that while a tile
+// runs each XCD gathers only 4·G features of the X rows of its slice (for
+// F > 128 this keeps the per-XCD working set of F = 128).
 template <int V, bool HAS_VAL>
 __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restrict__ crow,
                                                           const int64_t* __restrict__ col,
@@ -256,8 +260,12 @@ __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restr
                                                           const int32_t* __restrict__ order,
                                                           const int32_t* __restrict__ off, int64_t item_begin,
                                                           int64_t items, int64_t chunk) {
-  const int slice = static_cast<int>(blockIdx.x % kSlices);
-  const int64_t local = static_cast<int64_t>(blockIdx.x / kSlices) * kWavesPerBlock + wave_in_block();
+  // blocks per feature tile: 8 slices x ceil(items / 4)
+  const int64_t tile_blocks = kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock);
+  const int64_t tile = blockIdx.x / tile_blocks;
+  const int64_t in_tile = blockIdx.x - tile * tile_blocks;
+  const int slice = static_cast<int>(in_tile % kSlices);
+  const int64_t local = (in_tile / kSlices) * kWavesPerBlock + wave_in_block();
   if (local >= items) return;
   const int64_t row = uniform_i64(order[item_begin + local]);
   const int64_t rs = uniform_i64(crow[row]);
@@ -269,7 +277,7 @@ __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restr
   if (a >= b) return;
   double* out = partial + (slice * chunk + local) * F;
   if constexpr (V >= 16) {
-    slice_row_wide<V, HAS_VAL, (V == kWave ? 8 : 4)>(col, val, x, out, F, rs + a, rs + b);
+    slice_row_wide<V, HAS_VAL, 4>(col, val, x, out, F, rs + a, rs + b, tile * 4 * V);
   } else {
     if (b - a >= kColsliceLongRow) slice_row<V, HAS_VAL, 16>(col, val, x, out, F, rs + a, rs + b);
     else slice_row<V, HAS_VAL, 8>(col, val, x, out, F, rs + a, rs + b);
@@ -325,12 +333,9 @@ template <bool HAS_VAL>
 void launch_colslice(int v, const int64_t* crow, const int64_t* col, const float* val, const float* x,
                      double* partial, int64_t f, const int32_t* order, const int32_t* off, int64_t item_begin,
                      int64_t items, int64_t chunk, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock)));
+  const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
+  const dim3 grid(static_cast<unsigned>(tiles * kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock)));
   switch (v) {
-    case 64:
-      hipLaunchKernelGGL((colslice_kernel<64, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f,
-                         order, off, item_begin, items, chunk);
-      break;
     case 32:
       hipLaunchKernelGGL((colslice_kernel<32, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f,
                          order, off, item_begin, items, chunk);
@@ -402,11 +407,15 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
                            bin_ws, s);
   if (st != AS_OK) return st;
 
-  // lanes: G = 16/32/64 lanes per edge with float4 loads (F <= 64 / 128 /
-  // more), else 8- or 4-byte lanes with one edge per gather
+  // lanes: G = 16 lanes per edge with float4 loads for F <= 64, else G = 32
+  // in tiles of 128 features; 8- or 4-byte lanes with one edge per gather
+  // when F is not a multiple of 4 or X is not 16-byte aligned
   int v = 1;
-  if (f % 4 == 0 && as::aligned(x, 16)) v = f <= 64 ? 16 : (f <= 128 ? 32 : 64);
+  if (f % 4 == 0 && as::aligned(x, 16)) v = f <= 64 ? 16 : 32;
   else if (f % 2 == 0 && f > 64 && as::aligned(x, 8)) v = 2;
+  const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
+  if (chunk > as::kMaxChunkRows / tiles) chunk = as::kMaxChunkRows / tiles;
+  if (chunk < 1) return as::fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
   const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
   for (int64_t begin = 0; begin < n; begin += chunk) {
     const int64_t items = n - begin < chunk ? n - begin : chunk;
