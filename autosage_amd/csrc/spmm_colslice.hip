@@ -15,12 +15,14 @@
 //   1. Slice points: off[r·7 + b-1] = index, relative to crow[r], of the first
 //      edge of row r whose column is >= the first column of slice b (a binary
 //      search, valid because columns ascend within the row).
-//   2. Degree order: rows sorted into log2-degree buckets, longest first
-//      (the binning kernel of the split SpMM), so long rows start first.
+//   2. Degree order: rows of degree >= 128 in log2-degree buckets, longest
+//      first (the binning kernel of the split SpMM), then the shorter rows.
 //   3. For each chunk of rows of that order: the slice kernel, one wave per
 //      (row, slice), writes the fp64 partial sum of the row's edges in the
 //      slice; the reduction kernel adds the non-empty partials of each row in
-//      slice order in fp64 and rounds once to fp32.
+//      slice order in fp64 and rounds once to fp32.  A row shorter than 128
+//      is summed whole by one wave (in fp64, rounded once) that writes Y:
+//      its 8 partials would cost more traffic than slicing saves.
 //
 // Arithmetic.  Products w·x of fp32 values are exact in fp64 and every
 // partial and the final sum are fp64 additions, so each output is within
@@ -37,6 +39,12 @@ namespace {
 constexpr int kSlices = 8;                 // one column slice per XCD
 constexpr int kSliceBounds = kSlices - 1;  // inner slice points per row
 constexpr int kColsliceLongRow = 1024;     // slice length from which U = 16
+// Rows shorter than this are not sliced: 8 fp64 partial rows (128·F bytes
+// written and read) cost more than the cache gain on their few gathers.
+#ifndef AS_COLSLICE_MIN_DEGREE
+#define AS_COLSLICE_MIN_DEGREE 128
+#endif
+constexpr int64_t kColsliceMinDegree = AS_COLSLICE_MIN_DEGREE;
 // Rows per chunk: the slice kernel needs 8·ceil(rows / 4) workgroups.
 constexpr int64_t kMaxChunkRows = kMaxBlocksPerLaunch / kSlices * kWavesPerBlock;
 constexpr int64_t kGridStrideBlocks = 65536;
@@ -77,14 +85,20 @@ __device__ __forceinline__ void slice_range(const int32_t* __restrict__ off, int
   b = b < a ? a : (b > deg ? deg : b);
 }
 
+// fp64 partials are written once and read once by the reduction: keep them
+// out of the way of the X rows in the caches.  Rows that are not sliced are
+// rounded once and written to Y.
+__device__ __forceinline__ void store_out(double* p, double v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void store_out(float* p, double v) { *p = static_cast<float>(v); }
+
 // One wave sums edges [rs, re) of a row into out[0, F) in fp64 (F not a
 // multiple of 4, or X not 16-byte aligned).  Same lane layout as the exact
 // wave-row kernel: lane owns V consecutive features,
 // 64 column indices per coalesced load (one chunk ahead), broadcast through
 // SGPRs, U gathers in flight.
-template <int V, bool HAS_VAL, int U>
+template <int V, bool HAS_VAL, int U, typename OutT>
 __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const float* __restrict__ val,
-                                          const float* __restrict__ x, double* __restrict__ out, int64_t F,
+                                          const float* __restrict__ x, OutT* __restrict__ out, int64_t F,
                                           int64_t rs, int64_t re) {
   const int lane = lane_id();
   rs = uniform_i64(rs);
@@ -148,10 +162,8 @@ __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const
       }
     }
     if (active) {
-      // written once, read once by the reduction: keep them out of the way
-      // of the X rows in the caches
 #pragma unroll
-      for (int v = 0; v < V; ++v) __builtin_nontemporal_store(acc[v], out + fl + v);
+      for (int v = 0; v < V; ++v) store_out(out + fl + v, acc[v]);
     }
   }
 }
@@ -163,9 +175,9 @@ __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const
 // lanes).  Lane group k takes edges j + k, j + EPI + k, ... and keeps its own
 // fp64 sums; the groups are added at the end in a fixed butterfly order.
 // One call covers the feature tile [f0, f0 + 4·G).
-template <int G, bool HAS_VAL, int U>
+template <int G, bool HAS_VAL, int U, typename OutT>
 __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, const float* __restrict__ val,
-                                               const float* __restrict__ x, double* __restrict__ out, int64_t F,
+                                               const float* __restrict__ x, OutT* __restrict__ out, int64_t F,
                                                int64_t rs, int64_t re, int64_t f0) {
   constexpr int EPI = kWave / G;
   const int lane = lane_id();
@@ -238,7 +250,7 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
     }
     if (grp == 0 && active) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) __builtin_nontemporal_store(acc[v], out + fl + v);
+      for (int v = 0; v < 4; ++v) store_out(out + fl + v, acc[v]);
     }
   }
 }
@@ -256,8 +268,9 @@ template <int V, bool HAS_VAL>
 __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restrict__ crow,
                                                           const int64_t* __restrict__ col,
                                                           const float* __restrict__ val, const float* __restrict__ x,
-                                                          double* __restrict__ partial, int64_t F,
-                                                          const int32_t* __restrict__ order,
+                                                          double* __restrict__ partial, float* __restrict__ y,
+                                                          int64_t F, const int32_t* __restrict__ order,
+                                                          const int32_t* __restrict__ counts,
                                                           const int32_t* __restrict__ off, int64_t item_begin,
                                                           int64_t items, int64_t chunk) {
   // blocks per feature tile: 8 slices x ceil(items / 4)
@@ -267,9 +280,21 @@ __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restr
   const int slice = static_cast<int>(in_tile % kSlices);
   const int64_t local = (in_tile / kSlices) * kWavesPerBlock + wave_in_block();
   if (local >= items) return;
-  const int64_t row = uniform_i64(order[item_begin + local]);
+  const int64_t item = item_begin + local;
+  const int64_t row = uniform_i64(order[item]);
   const int64_t rs = uniform_i64(crow[row]);
   const int64_t deg = uniform_i64(crow[row + 1]) - rs;
+  if (item >= counts[0]) {
+    // short row: one wave (of the slice item % 8, to spread them over the
+    // XCDs) sums the whole row and writes Y
+    if (item % kSlices != slice) return;
+    if constexpr (V >= 16) {
+      slice_row_wide<V, HAS_VAL, 4>(col, val, x, y + row * F, F, rs, rs + deg, tile * 4 * V);
+    } else {
+      slice_row<V, HAS_VAL, 8>(col, val, x, y + row * F, F, rs, rs + deg);
+    }
+    return;
+  }
   int64_t a, b;
   slice_range(off, row, slice, deg, a, b);
   a = uniform_i64(a);
@@ -285,16 +310,19 @@ __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restr
 }
 
 // Y[row, f..f+VR) = sum over the non-empty slices, in slice order, in fp64,
-// rounded once.  Rows without edges get zeros.
+// rounded once, for the sliced rows (the short rows wrote Y themselves).
 template <int VR>
 __global__ __launch_bounds__(kBlock) void colslice_reduce_kernel(const int64_t* __restrict__ crow,
                                                                  const int32_t* __restrict__ off,
                                                                  const double* __restrict__ partial,
                                                                  const int32_t* __restrict__ order,
+                                                                 const int32_t* __restrict__ counts,
                                                                  float* __restrict__ y, int64_t F,
                                                                  int64_t item_begin, int64_t items, int64_t chunk) {
   const int64_t FV = F / VR;
-  const int64_t total = items * FV;
+  // only the sliced rows: order[0, counts[0])
+  const int64_t sliced = counts[0] - item_begin;
+  const int64_t total = (sliced < items ? (sliced > 0 ? sliced : 0) : items) * FV;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
     const int64_t local = t / FV;
@@ -331,26 +359,26 @@ size_t colslice_row_bytes(int64_t f) { return static_cast<size_t>(kSlices) * sta
 
 template <bool HAS_VAL>
 void launch_colslice(int v, const int64_t* crow, const int64_t* col, const float* val, const float* x,
-                     double* partial, int64_t f, const int32_t* order, const int32_t* off, int64_t item_begin,
-                     int64_t items, int64_t chunk, hipStream_t s) {
+                     double* partial, float* y, int64_t f, const int32_t* order, const int32_t* counts,
+                     const int32_t* off, int64_t item_begin, int64_t items, int64_t chunk, hipStream_t s) {
   const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
   const dim3 grid(static_cast<unsigned>(tiles * kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock)));
   switch (v) {
     case 32:
-      hipLaunchKernelGGL((colslice_kernel<32, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f,
-                         order, off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_kernel<32, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
+                         order, counts, off, item_begin, items, chunk);
       break;
     case 16:
-      hipLaunchKernelGGL((colslice_kernel<16, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f,
-                         order, off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_kernel<16, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
+                         order, counts, off, item_begin, items, chunk);
       break;
     case 2:
-      hipLaunchKernelGGL((colslice_kernel<2, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f, order,
-                         off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_kernel<2, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
+                         order, counts, off, item_begin, items, chunk);
       break;
     default:
-      hipLaunchKernelGGL((colslice_kernel<1, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, f, order,
-                         off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_kernel<1, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
+                         order, counts, off, item_begin, items, chunk);
       break;
   }
 }
@@ -403,8 +431,9 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
     hipLaunchKernelGGL(as::slice_points_kernel, dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s, crow,
                        col, n, off);
   }
-  st = as::launch_bin_rows(crow, n, as::kColsliceLongRow, as::kMaxHeavyBuckets, as::kMaxHeavyBuckets, order, counts,
-                           bin_ws, s);
+  // order: rows of degree >= kColsliceMinDegree (sliced) in 8 log2-degree
+  // buckets, longest first; then the short rows in row order
+  st = as::launch_bin_rows(crow, n, as::kColsliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
   if (st != AS_OK) return st;
 
   // lanes: G = 16 lanes per edge with float4 loads for F <= 64, else G = 32
@@ -419,17 +448,19 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
   for (int64_t begin = 0; begin < n; begin += chunk) {
     const int64_t items = n - begin < chunk ? n - begin : chunk;
-    if (val != nullptr) as::launch_colslice<true>(v, crow, col, val, x, partial, f, order, off, begin, items, chunk, s);
-    else as::launch_colslice<false>(v, crow, col, val, x, partial, f, order, off, begin, items, chunk, s);
+    if (val != nullptr)
+      as::launch_colslice<true>(v, crow, col, val, x, partial, y, f, order, counts, off, begin, items, chunk, s);
+    else
+      as::launch_colslice<false>(v, crow, col, val, x, partial, y, f, order, counts, off, begin, items, chunk, s);
     const int64_t threads = items * (f / vr);
     int64_t blocks = (threads + as::kBlock - 1) / as::kBlock;
     if (blocks > as::kGridStrideBlocks) blocks = as::kGridStrideBlocks;
     if (vr == 2)
       hipLaunchKernelGGL((as::colslice_reduce_kernel<2>), dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s,
-                         crow, off, partial, order, y, f, begin, items, chunk);
+                         crow, off, partial, order, counts, y, f, begin, items, chunk);
     else
       hipLaunchKernelGGL((as::colslice_reduce_kernel<1>), dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s,
-                         crow, off, partial, order, y, f, begin, items, chunk);
+                         crow, off, partial, order, counts, y, f, begin, items, chunk);
   }
   return as::check_launch("spmm_csr_colslice");
 }

@@ -104,8 +104,9 @@ size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f);
  * Precondition: columns ascend (non-strictly) within every row.  The column
  * space is cut into 8 ranges, one per XCD, so that each XCD's L2 caches only
  * its eighth of X; per-slice partials are accumulated in fp64 and added in
- * slice order, then rounded once: deterministic, within about one fp32
- * rounding of the exact sum, not bit-identical to the sequential product.
+ * slice order, then rounded once (rows shorter than 128 are summed whole in
+ * fp64): deterministic, within about one fp32 rounding of the exact sum, not
+ * bit-identical to the sequential product.
  * The workspace (256-byte aligned) holds n·28 B of slice points, the row
  * order and n·f·64 B of partials; a smaller one (at least the size for one
  * row) makes the call run in row chunks. */
