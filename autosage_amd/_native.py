@@ -218,9 +218,6 @@ def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_th
     return y
 
 
-COLSLICE_ROW_BYTES = 64  # fp64 partials of the 8 column slices, per feature
-
-
 def _colslice_workspace_cap() -> int:
     return int(float(os.getenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", "4096")) * 2**20)
 
@@ -237,10 +234,10 @@ def spmm_csr_colslice_impl(crow, col, val, x):
     if n == 0 or f == 0:
         return y
     lib = library()
+    # the preferred size (two partial buffers of a quarter of the rows); a
+    # smaller cap runs the pipeline in more, smaller chunks
     full = lib.as_spmm_colslice_workspace_bytes(n, f)
-    per_row = COLSLICE_ROW_BYTES * f
-    minimum = full - (n - 1) * per_row
-    ws = _workspace(max(minimum, min(full, _colslice_workspace_cap())), x.device)
+    ws = _workspace(min(full, _colslice_workspace_cap()), x.device)
     with torch.cuda.device(x.device):
         status = lib.as_spmm_csr_colslice_f32(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, _ptr(ws), ws.numel(),

@@ -45,8 +45,9 @@ constexpr int kColsliceLongRow = 1024;     // slice length from which U = 16
 #define AS_COLSLICE_MIN_DEGREE 128
 #endif
 constexpr int64_t kColsliceMinDegree = AS_COLSLICE_MIN_DEGREE;
-// Rows per chunk: the slice kernel needs 8·ceil(rows / 4) workgroups.
-constexpr int64_t kMaxChunkRows = kMaxBlocksPerLaunch / kSlices * kWavesPerBlock;
+#ifndef AS_COLSLICE_OVERLAP
+#define AS_COLSLICE_OVERLAP 1
+#endif
 constexpr int64_t kGridStrideBlocks = 65536;
 
 // First column of slice b for an N-column space.
@@ -255,32 +256,37 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
   }
 }
 
-// Wave per (row, slice) for the rows order[item_begin, item_begin + items);
-// workgroup g takes slice g % 8 and waves (g / 8)·4 .. +3 of the chunk.
-// Partial of chunk row `local` in slice s: partial[(s·chunk + local)·F ..].
+// One chunk of the slice work: rows order[item_begin, item_begin + items),
+// main block mb of 8·ceil(items / 4)·tiles.  Block mb takes slice mb % 8 and
+// waves (mb / 8)·4 .. +3 of the chunk; the wave for (row, slice) writes the
+// partial of chunk row `local` to partial[(slice·chunk_stride + local)·F ..].
 // V in {1, 2}: narrow lanes (slice_row, all features); V = 16, 32: wide
 // lanes with G = V lanes per edge (slice_row_wide), one feature tile of 4·G
-// features per wave.  Feature tiles are the outermost grid dimension: every
-// (slice, row) of tile 0 is dispatched before tile 1, so that while a tile
-// runs each XCD gathers only 4·G features of the X rows of its slice (for
-// F > 128 this keeps the per-XCD working set of F = 128).
+// features per wave.  Feature tiles are the outermost index: every
+// (slice, row) of tile 0 comes before tile 1, so that while a tile runs each
+// XCD gathers only 4·G features of the X rows of its slice (for F > 128 this
+// keeps the per-XCD working set of F = 128).
+struct SliceChunk {
+  int64_t item_begin;
+  int64_t items;
+  double* partial;
+};
+
 template <int V, bool HAS_VAL>
-__global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restrict__ crow,
-                                                          const int64_t* __restrict__ col,
-                                                          const float* __restrict__ val, const float* __restrict__ x,
-                                                          double* __restrict__ partial, float* __restrict__ y,
-                                                          int64_t F, const int32_t* __restrict__ order,
-                                                          const int32_t* __restrict__ counts,
-                                                          const int32_t* __restrict__ off, int64_t item_begin,
-                                                          int64_t items, int64_t chunk) {
-  // blocks per feature tile: 8 slices x ceil(items / 4)
-  const int64_t tile_blocks = kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock);
-  const int64_t tile = blockIdx.x / tile_blocks;
-  const int64_t in_tile = blockIdx.x - tile * tile_blocks;
+__device__ __forceinline__ void colslice_main_block(int64_t mb, const int64_t* __restrict__ crow,
+                                                    const int64_t* __restrict__ col, const float* __restrict__ val,
+                                                    const float* __restrict__ x, float* __restrict__ y, int64_t F,
+                                                    const int32_t* __restrict__ order,
+                                                    const int32_t* __restrict__ counts,
+                                                    const int32_t* __restrict__ off, const SliceChunk& c,
+                                                    int64_t chunk_stride) {
+  const int64_t tile_blocks = kSlices * ((c.items + kWavesPerBlock - 1) / kWavesPerBlock);
+  const int64_t tile = mb / tile_blocks;
+  const int64_t in_tile = mb - tile * tile_blocks;
   const int slice = static_cast<int>(in_tile % kSlices);
   const int64_t local = (in_tile / kSlices) * kWavesPerBlock + wave_in_block();
-  if (local >= items) return;
-  const int64_t item = item_begin + local;
+  if (local >= c.items) return;
+  const int64_t item = c.item_begin + local;
   const int64_t row = uniform_i64(order[item]);
   const int64_t rs = uniform_i64(crow[row]);
   const int64_t deg = uniform_i64(crow[row + 1]) - rs;
@@ -300,7 +306,7 @@ __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restr
   a = uniform_i64(a);
   b = uniform_i64(b);
   if (a >= b) return;
-  double* out = partial + (slice * chunk + local) * F;
+  double* out = c.partial + (slice * chunk_stride + local) * F;
   if constexpr (V >= 16) {
     slice_row_wide<V, HAS_VAL, 4>(col, val, x, out, F, rs + a, rs + b, tile * 4 * V);
   } else {
@@ -309,25 +315,24 @@ __global__ __launch_bounds__(kBlock) void colslice_kernel(const int64_t* __restr
   }
 }
 
-// Y[row, f..f+VR) = sum over the non-empty slices, in slice order, in fp64,
-// rounded once, for the sliced rows (the short rows wrote Y themselves).
+// Reduction of one chunk, block rb of R: Y[row, f..f+VR) = sum over the
+// non-empty slices, in slice order, in fp64, rounded once, for the sliced
+// rows (short rows wrote Y themselves).
 template <int VR>
-__global__ __launch_bounds__(kBlock) void colslice_reduce_kernel(const int64_t* __restrict__ crow,
-                                                                 const int32_t* __restrict__ off,
-                                                                 const double* __restrict__ partial,
-                                                                 const int32_t* __restrict__ order,
-                                                                 const int32_t* __restrict__ counts,
-                                                                 float* __restrict__ y, int64_t F,
-                                                                 int64_t item_begin, int64_t items, int64_t chunk) {
+__device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, const int64_t* __restrict__ crow,
+                                                      const int32_t* __restrict__ off,
+                                                      const int32_t* __restrict__ order,
+                                                      const int32_t* __restrict__ counts, float* __restrict__ y,
+                                                      int64_t F, const SliceChunk& c, int64_t chunk_stride) {
   const int64_t FV = F / VR;
   // only the sliced rows: order[0, counts[0])
-  const int64_t sliced = counts[0] - item_begin;
-  const int64_t total = (sliced < items ? (sliced > 0 ? sliced : 0) : items) * FV;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+  const int64_t sliced = counts[0] - c.item_begin;
+  const int64_t total = (sliced < c.items ? (sliced > 0 ? sliced : 0) : c.items) * FV;
+  const int64_t stride = R * kBlock;
+  for (int64_t t = rb * kBlock + threadIdx.x; t < total; t += stride) {
     const int64_t local = t / FV;
     const int64_t f = (t - local * FV) * VR;
-    const int64_t row = order[item_begin + local];
+    const int64_t row = order[c.item_begin + local];
     const int64_t deg = crow[row + 1] - crow[row];
     double acc[VR];
 #pragma unroll
@@ -337,7 +342,7 @@ __global__ __launch_bounds__(kBlock) void colslice_reduce_kernel(const int64_t* 
       int64_t a, b;
       slice_range(off, row, s, deg, a, b);
       if (a < b) {
-        const double* p = partial + (s * chunk + local) * F + f;
+        const double* p = c.partial + (s * chunk_stride + local) * F + f;
 #pragma unroll
         for (int v = 0; v < VR; ++v) acc[v] += __builtin_nontemporal_load(p + v);
       }
@@ -349,6 +354,35 @@ __global__ __launch_bounds__(kBlock) void colslice_reduce_kernel(const int64_t* 
   }
 }
 
+// One launch of the pipeline: the slice work of chunk `m` and the reduction
+// of the previous chunk `r`, whose partials a previous launch wrote.  The
+// blocks come in groups of 8 (one per XCD); of the TG groups, RG evenly
+// spread ones reduce and the others do slice work, so the HBM-streaming
+// reduction runs beside the latency-bound gathers.  Group g reduces iff
+// floor((g+1)·RG/TG) > floor(g·RG/TG); floor(g·RG/TG) groups before it
+// reduce, so a slice block keeps blockIdx % 8 as its slice.
+template <int V, bool HAS_VAL, int VR>
+__global__ __launch_bounds__(kBlock) void colslice_step_kernel(const int64_t* __restrict__ crow,
+                                                               const int64_t* __restrict__ col,
+                                                               const float* __restrict__ val,
+                                                               const float* __restrict__ x, float* __restrict__ y,
+                                                               int64_t F, const int32_t* __restrict__ order,
+                                                               const int32_t* __restrict__ counts,
+                                                               const int32_t* __restrict__ off, SliceChunk m,
+                                                               SliceChunk r, int64_t chunk_stride, int64_t TG,
+                                                               int64_t RG) {
+  const int64_t g = blockIdx.x / kSlices;
+  const int64_t within = blockIdx.x % kSlices;
+  const int64_t before = g * RG / TG;
+  if ((g + 1) * RG / TG > before) {
+    colslice_reduce_block<VR>(before * kSlices + within, RG * kSlices, crow, off, order, counts, y, F, r,
+                              chunk_stride);
+  } else {
+    colslice_main_block<V, HAS_VAL>((g - before) * kSlices + within, crow, col, val, x, y, F, order, counts, off,
+                                    m, chunk_stride);
+  }
+}
+
 size_t colslice_fixed_bytes(int64_t n) {
   const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
   return align_up(rows * kSliceBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
@@ -357,29 +391,70 @@ size_t colslice_fixed_bytes(int64_t n) {
 
 size_t colslice_row_bytes(int64_t f) { return static_cast<size_t>(kSlices) * static_cast<size_t>(f) * sizeof(double); }
 
-template <bool HAS_VAL>
-void launch_colslice(int v, const int64_t* crow, const int64_t* col, const float* val, const float* x,
-                     double* partial, float* y, int64_t f, const int32_t* order, const int32_t* counts,
-                     const int32_t* off, int64_t item_begin, int64_t items, int64_t chunk, hipStream_t s) {
-  const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
-  const dim3 grid(static_cast<unsigned>(tiles * kSlices * ((items + kWavesPerBlock - 1) / kWavesPerBlock)));
+// Rows per chunk when the workspace allows: the pipeline overlaps the
+// reduction of chunk k with the slice work of chunk k + 1, so all but the
+// last chunk's reduction is hidden.
+#ifndef AS_COLSLICE_CHUNKS
+#define AS_COLSLICE_CHUNKS 4
+#endif
+constexpr int64_t kColsliceChunks = AS_COLSLICE_CHUNKS;
+constexpr int64_t kColsliceMinChunkRows = 4096;
+
+int64_t preferred_chunk_rows(int64_t n) {
+  int64_t c = (n + kColsliceChunks - 1) / kColsliceChunks;
+  if (c < kColsliceMinChunkRows) c = n < kColsliceMinChunkRows ? n : kColsliceMinChunkRows;
+  return c > 0 ? c : 1;
+}
+
+template <bool HAS_VAL, int VR>
+void launch_step_v(int v, dim3 grid, hipStream_t s, const int64_t* crow, const int64_t* col, const float* val,
+                   const float* x, float* y, int64_t f, const int32_t* order, const int32_t* counts,
+                   const int32_t* off, const SliceChunk& m, const SliceChunk& r, int64_t stride, int64_t TG,
+                   int64_t RG) {
   switch (v) {
     case 32:
-      hipLaunchKernelGGL((colslice_kernel<32, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
-                         order, counts, off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_step_kernel<32, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
+                         order, counts, off, m, r, stride, TG, RG);
       break;
     case 16:
-      hipLaunchKernelGGL((colslice_kernel<16, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
-                         order, counts, off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_step_kernel<16, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
+                         order, counts, off, m, r, stride, TG, RG);
       break;
     case 2:
-      hipLaunchKernelGGL((colslice_kernel<2, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
-                         order, counts, off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_step_kernel<2, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
+                         order, counts, off, m, r, stride, TG, RG);
       break;
     default:
-      hipLaunchKernelGGL((colslice_kernel<1, HAS_VAL>), grid, dim3(kBlock), 0, s, crow, col, val, x, partial, y, f,
-                         order, counts, off, item_begin, items, chunk);
+      hipLaunchKernelGGL((colslice_step_kernel<1, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
+                         order, counts, off, m, r, stride, TG, RG);
       break;
+  }
+}
+
+// Launch of slice work `m` (items may be 0) beside the reduction of `r`
+// (items may be 0).
+void launch_step(int v, int vr, bool has_val, int64_t tiles, hipStream_t s, const int64_t* crow, const int64_t* col,
+                 const float* val, const float* x, float* y, int64_t f, const int32_t* order, const int32_t* counts,
+                 const int32_t* off, const SliceChunk& m, const SliceChunk& r, int64_t stride) {
+  const int64_t MG = tiles * ((m.items + kWavesPerBlock - 1) / kWavesPerBlock);  // groups of 8 slice blocks
+  int64_t RG = 0;
+  if (r.items > 0) {
+    // enough reduce blocks for one element per thread, at most a fifth of
+    // the groups when they run beside slice work
+    RG = (r.items * (f / vr) + kSlices * kBlock - 1) / (kSlices * kBlock);
+    const int64_t cap = MG > 0 ? (MG + 3) / 4 : kGridStrideBlocks / kSlices;
+    if (RG > cap) RG = cap;
+    if (RG < 1) RG = 1;
+  }
+  const int64_t TG = MG + RG;
+  if (TG == 0) return;
+  const dim3 grid(static_cast<unsigned>(TG * kSlices));
+  if (has_val) {
+    if (vr == 2) launch_step_v<true, 2>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    else launch_step_v<true, 1>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+  } else {
+    if (vr == 2) launch_step_v<false, 2>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    else launch_step_v<false, 1>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
   }
 }
 
@@ -392,7 +467,7 @@ extern "C" {
 size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f) {
   if (n < 0) n = 0;
   if (f < 1) f = 1;
-  return as::colslice_fixed_bytes(n) + static_cast<size_t>(n > 0 ? n : 1) * as::colslice_row_bytes(f);
+  return as::colslice_fixed_bytes(n) + 2 * static_cast<size_t>(as::preferred_chunk_rows(n)) * as::colslice_row_bytes(f);
 }
 
 int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const float* val, const float* x, float* y,
@@ -404,13 +479,28 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   if (n == 0 || f == 0) return AS_OK;
   const size_t fixed = as::colslice_fixed_bytes(n);
   const size_t row_bytes = as::colslice_row_bytes(f);
-  if (workspace == nullptr || workspace_bytes < fixed + row_bytes)
+  if (workspace == nullptr || workspace_bytes < fixed + 2 * row_bytes)
     return as::fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu workspace bytes, got %zu",
-                    fixed + row_bytes, workspace_bytes);
+                    fixed + 2 * row_bytes, workspace_bytes);
   if (!as::aligned(workspace, 256)) return as::fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed) / row_bytes);
-  if (chunk > n) chunk = n;
-  if (chunk > as::kMaxChunkRows) chunk = as::kMaxChunkRows;
+
+  // lanes: G = 16 lanes per edge with float4 loads for F <= 64, else G = 32
+  // in tiles of 128 features; 8- or 4-byte lanes with one edge per gather
+  // when F is not a multiple of 4 or X is not 16-byte aligned
+  int v = 1;
+  if (f % 4 == 0 && as::aligned(x, 16)) v = f <= 64 ? 16 : 32;
+  else if (f % 2 == 0 && f > 64 && as::aligned(x, 8)) v = 2;
+  const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
+  const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
+
+  // two partial buffers of `chunk` rows each (chunk k writes buffer k % 2)
+  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed) / (2 * row_bytes));
+  const int64_t preferred = as::preferred_chunk_rows(n);
+  if (chunk > preferred) chunk = preferred;
+  // a launch holds at most 5/4 of the slice groups of a chunk
+  const int64_t max_rows = as::kMaxBlocksPerLaunch * 4 / 5 / as::kSlices * as::kWavesPerBlock / tiles;
+  if (chunk > max_rows) chunk = max_rows;
+  if (chunk < 1) return as::fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
@@ -422,7 +512,8 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   int32_t* counts = reinterpret_cast<int32_t*>(ws);
   ws += 256;
   void* bin_ws = ws;
-  double* partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed);
+  double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
+                        reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + chunk * row_bytes)};
 
   {
     const int64_t threads = n * as::kSliceBounds;
@@ -436,31 +527,22 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   st = as::launch_bin_rows(crow, n, as::kColsliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
   if (st != AS_OK) return st;
 
-  // lanes: G = 16 lanes per edge with float4 loads for F <= 64, else G = 32
-  // in tiles of 128 features; 8- or 4-byte lanes with one edge per gather
-  // when F is not a multiple of 4 or X is not 16-byte aligned
-  int v = 1;
-  if (f % 4 == 0 && as::aligned(x, 16)) v = f <= 64 ? 16 : 32;
-  else if (f % 2 == 0 && f > 64 && as::aligned(x, 8)) v = 2;
-  const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
-  if (chunk > as::kMaxChunkRows / tiles) chunk = as::kMaxChunkRows / tiles;
-  if (chunk < 1) return as::fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
-  const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
-  for (int64_t begin = 0; begin < n; begin += chunk) {
-    const int64_t items = n - begin < chunk ? n - begin : chunk;
-    if (val != nullptr)
-      as::launch_colslice<true>(v, crow, col, val, x, partial, y, f, order, counts, off, begin, items, chunk, s);
-    else
-      as::launch_colslice<false>(v, crow, col, val, x, partial, y, f, order, counts, off, begin, items, chunk, s);
-    const int64_t threads = items * (f / vr);
-    int64_t blocks = (threads + as::kBlock - 1) / as::kBlock;
-    if (blocks > as::kGridStrideBlocks) blocks = as::kGridStrideBlocks;
-    if (vr == 2)
-      hipLaunchKernelGGL((as::colslice_reduce_kernel<2>), dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s,
-                         crow, off, partial, order, counts, y, f, begin, items, chunk);
-    else
-      hipLaunchKernelGGL((as::colslice_reduce_kernel<1>), dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s,
-                         crow, off, partial, order, counts, y, f, begin, items, chunk);
+  // launch k: slice work of chunk k beside the reduction of chunk k - 1
+  const int64_t chunks = (n + chunk - 1) / chunk;
+  as::SliceChunk previous{0, 0, buffers[1]};
+  for (int64_t k = 0; k <= chunks; ++k) {
+    as::SliceChunk current{k * chunk, 0, buffers[k % 2]};
+    if (k < chunks) current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
+#if AS_COLSLICE_OVERLAP
+    as::launch_step(v, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current, previous,
+                    chunk);
+#else
+    as::launch_step(v, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current,
+                    as::SliceChunk{0, 0, nullptr}, chunk);
+    as::launch_step(v, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off,
+                    as::SliceChunk{0, 0, nullptr}, current, chunk);
+#endif
+    previous = current;
   }
   return as::check_launch("spmm_csr_colslice");
 }

@@ -95,7 +95,8 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col,
                           int hub_mode, void* workspace, size_t workspace_bytes,
                           void* stream);
 
-/* Bytes of workspace for as_spmm_csr_colslice_f32 to run in one chunk. */
+/* Preferred bytes of workspace for as_spmm_csr_colslice_f32: slice points,
+ * row order and two partial buffers of a quarter of the rows each. */
 size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f);
 
 /* Column-sliced SpMM, an alternative schedule for the same product as
@@ -107,9 +108,10 @@ size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f);
  * slice order, then rounded once (rows shorter than 128 are summed whole in
  * fp64): deterministic, within about one fp32 rounding of the exact sum, not
  * bit-identical to the sequential product.
- * The workspace (256-byte aligned) holds n·28 B of slice points, the row
- * order and n·f·64 B of partials; a smaller one (at least the size for one
- * row) makes the call run in row chunks. */
+ * The rows run in chunks, the partial reduction of one chunk beside the
+ * slice work of the next.  The workspace (256-byte aligned) holds n·28 B of
+ * slice points, the row order and two partial buffers of c·f·64 B for
+ * chunks of c rows; any size down to c = 1 works, in more chunks. */
 int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col,
                              const float* val, const float* x, float* y,
                              int64_t n, int64_t nnz, int64_t f,

@@ -85,7 +85,7 @@ def test_colslice_deterministic_and_chunked(monkeypatch):
     first = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x)
     again = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x)
     assert torch.equal(first, again)
-    # a workspace for ~100 rows of partials: the call runs in 30 row chunks
+    # a workspace for ~100 rows of partials (two buffers of ~50): about 55 chunks
     monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((100 * 128 * 64 + 200_000) / 2**20))
     chunked = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x)
     assert torch.equal(first, chunked)
