@@ -315,14 +315,6 @@ def _probe_and_choose(
     }
 
 
-def _full_graph_confirmation(
-    native: Callable[[], torch.Tensor], baseline: Callable[[], torch.Tensor]
-) -> dict[str, float]:
-    native_t = _time_cuda(native, warmup=1, iterations=3)["best_ms"]
-    baseline_t = _time_cuda(baseline, warmup=1, iterations=3)["best_ms"]
-    return {"autosage_ms": native_t, "baseline_ms": baseline_t}
-
-
 def _result_dict(operation, config, probe, baseline_name, sampled_crow, sampled_col, sample_ms) -> dict[str, Any]:
     baseline_best = probe["baseline_timing"]["best_ms"]
     best = probe["best"]
@@ -447,6 +439,7 @@ def _confirm_spmm_on_full_graph(result: dict[str, Any], colslice: bool, crow, co
     """Times the sampled choice (when native) and, when eligible, the
     column-sliced SpMM on the full graph against the baseline, and keeps the
     fastest; a native variant slower than the baseline is dropped."""
+    wall_start = time.perf_counter()
     full_baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
     sampled = result["candidate"] if result["choice"] == "autosage" else None
     options: list[Any] = ([sampled] if result["choice"] == "autosage" else []) + ([COLSLICE] if colslice else [])
@@ -455,14 +448,23 @@ def _confirm_spmm_on_full_graph(result: dict[str, Any], colslice: bool, crow, co
         times[json.dumps(option)] = _time_cuda(
             lambda o=option: _run_spmm_choice("autosage", o, crow, col, val, x), warmup=1, iterations=3
         )["best_ms"]
-    baseline_ms = _time_cuda(full_baseline, warmup=1, iterations=3)["best_ms"]
     best = min(options, key=lambda o: times[json.dumps(o)])
     best_ms = times[json.dumps(best)]
-    confirm: dict[str, Any] = {"autosage_ms": best_ms, "baseline_ms": baseline_ms}
+    # One baseline call decides when it takes more than twice the best native
+    # time; a closer race gets the full warm timing.  The sampled probe has
+    # already run the baseline, so library set-up is not in this call, and on
+    # large graphs one baseline call costs ~30 native ones.
+    baseline_ms = _time_cuda(full_baseline, warmup=0, iterations=1)["best_ms"]
+    baseline_runs = 1
+    if baseline_ms < 2.0 * best_ms:
+        baseline_ms = _time_cuda(full_baseline, warmup=1, iterations=3)["best_ms"]
+        baseline_runs = 5
+    confirm: dict[str, Any] = {"autosage_ms": best_ms, "baseline_ms": baseline_ms, "baseline_runs": baseline_runs}
     if colslice:
         confirm["colslice_ms"] = times[json.dumps(COLSLICE)]
         if result["choice"] == "autosage":
             confirm["sampled_choice_ms"] = times[json.dumps(sampled)]
+    confirm["wall_ms"] = (time.perf_counter() - wall_start) * 1000.0
     result["full_graph"] = confirm
     if best_ms > baseline_ms:
         result["choice"] = "baseline"
