@@ -30,7 +30,7 @@ import torch
 
 from ._cache import ScheduleCache, device_signature, graph_signature_memo, log_probe
 from .config import SchedulerConfig
-from .ops import _normalize_csr, load_native, native_op, spmm_csr, validate_if_requested
+from .ops import _normalize_csr, load_native, native_load_error, native_op, spmm_csr, validate_if_requested
 
 AUTOTUNE_SCHEMA_VERSION = 3
 
@@ -99,7 +99,9 @@ def _prepare_sddmm_baseline(crow, col, query, key) -> tuple[Callable[[], torch.T
 def _induced_sample_csr(crow, col, val, *, fraction: float, minimum_rows: int, seed: int):
     """Induced sub-graph on a seeded row sample (``_auto.py:95-154``): rows
     ``randperm(N)[:S]`` sorted, S = min(max(int(N·fraction), minimum_rows, 1), N);
-    an edge survives when its column is also sampled; columns are renumbered."""
+    an edge survives when its column is also sampled; columns are renumbered.
+    On the GPU the sub-graph comes from the native sampler; on the CPU from
+    the reference's torch composition (same outputs)."""
     rows = crow.numel() - 1
     size = min(max(int(rows * fraction), minimum_rows, 1), rows)
     device = crow.device
@@ -107,6 +109,21 @@ def _induced_sample_csr(crow, col, val, *, fraction: float, minimum_rows: int, s
     generator.manual_seed(seed)
     selected = torch.randperm(rows, generator=generator, device=device)[:size].sort().values
 
+    if crow.is_cuda and native_op("spmm_csr") is not None and (val is None or val.dtype == torch.float32):
+        # the same sub-graph from two native passes (one host sync)
+        from ._native import induced_sample
+
+        new_crow, new_col, new_val = induced_sample(crow, col, val, selected)
+        return new_crow, new_col, new_val, selected
+    return (*_induced_subgraph_torch(crow, col, val, selected), selected)
+
+
+def _induced_subgraph_torch(crow, col, val, selected):
+    """The sub-graph induced by the sorted row sample ``selected``, as the
+    reference's torch composition (``_auto.py:114-154``)."""
+    rows = crow.numel() - 1
+    size = selected.numel()
+    device = crow.device
     remap = torch.full((rows,), -1, dtype=torch.long, device=device)
     remap[selected] = torch.arange(size, device=device)
     starts = crow.index_select(0, selected)
@@ -118,7 +135,6 @@ def _induced_sample_csr(crow, col, val, *, fraction: float, minimum_rows: int, s
             torch.zeros(size + 1, dtype=torch.long, device=device),
             torch.empty(0, dtype=torch.long, device=col.device),
             empty_val,
-            selected,
         )
     owner = torch.repeat_interleave(torch.arange(size, device=device, dtype=torch.long), counts)
     first = torch.repeat_interleave(torch.cumsum(counts, dim=0) - counts, counts)
@@ -129,7 +145,7 @@ def _induced_sample_csr(crow, col, val, *, fraction: float, minimum_rows: int, s
     new_crow = torch.cat((torch.zeros(1, dtype=torch.long, device=device), kept_counts.cumsum(0)))
     new_col = mapped[keep].contiguous()
     new_val = None if val is None else val.index_select(0, positions)[keep].contiguous()
-    return new_crow, new_col, new_val, selected
+    return new_crow, new_col, new_val
 
 
 def _quantile_ints(degrees: torch.Tensor, points: list[float]) -> list[int]:
@@ -206,6 +222,13 @@ def _colslice_eligible(crow, col, x, config: SchedulerConfig) -> bool:
     from ._native import columns_ascending
 
     return columns_ascending(crow, col)
+
+
+def _require_native() -> None:
+    """CUDA inputs run on the HIP library: without it the schedulers raise
+    instead of quietly running the PyTorch baseline."""
+    if not load_native():
+        raise RuntimeError(f"AutoSAGE HIP library is unavailable: {native_load_error()}")
 
 
 def _cache_hit_allowed(result: dict[str, Any], config: SchedulerConfig) -> bool:
@@ -380,7 +403,7 @@ def spmm_csr_auto(
         run, name = _prepare_spmm_baseline(crow, col, val, x)
         return run(), {**_cpu_info("spmm"), "baseline": name, "reason": "AutoSAGE CUDA kernels require float32 features"}
 
-    load_native()
+    _require_native()
     config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=k)
     device = device_signature()
     graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
@@ -424,9 +447,9 @@ def spmm_csr_auto(
         core_call=core_call,
     )
     result = _result_dict("spmm", config, probe, baseline_name, s_crow, s_col, sample_ms)
-    colslice = _colslice_eligible(crow, col, x, config)
-    if (result["choice"] == "autosage" and config.full_graph_check) or colslice:
-        _confirm_spmm_on_full_graph(result, colslice, crow, col, val, x)
+    if config.full_graph_check:
+        colslice = _colslice_eligible(crow, col, x, config)
+        _confirm_spmm_on_full_graph(result, colslice, config, probe, crow, col, val, x)
     output = _run_spmm_choice(result["choice"], result["candidate"], crow, col, val, x)
     if config.cache:
         cache.store(device, graph, result)
@@ -435,44 +458,74 @@ def spmm_csr_auto(
     return output, result
 
 
-def _confirm_spmm_on_full_graph(result: dict[str, Any], colslice: bool, crow, col, val, x) -> None:
-    """Times the sampled choice (when native) and, when eligible, the
-    column-sliced SpMM on the full graph against the baseline, and keeps the
-    fastest; a native variant slower than the baseline is dropped."""
+_SDDMM_MIN_HUB_DEGREE = 1024
+
+
+def _full_graph_candidate(crow: torch.Tensor, feature_width: int, config: SchedulerConfig) -> list[int]:
+    """The shortlist's preferred point with the FULL graph's q95 as the hub
+    threshold: the sample's quantiles are scaled down by the sampling
+    fraction, so its thresholds can send every full-graph row to the hub
+    path."""
+    _, q95, _ = _degree_quantiles(crow)
+    tile = config.feature_tile or (64 if feature_width <= 64 else 128)
+    waves = config.warps_per_block or _preferred_waves(feature_width)
+    return [int(tile), int(waves), int(config.hub_threshold or q95)]
+
+
+def _decide_on_full_graph(result: dict[str, Any], options: list[Any], run_option, baseline) -> None:
+    """Times each native option on the full graph (1 warmup, best of 3) and
+    the baseline, keeps the fastest native option, and falls back to the
+    baseline only when that is faster.  `result` gets a ``full_graph``
+    record; the sampled probe has only shortlisted."""
     wall_start = time.perf_counter()
-    full_baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
-    sampled = result["candidate"] if result["choice"] == "autosage" else None
-    options: list[Any] = ([sampled] if result["choice"] == "autosage" else []) + ([COLSLICE] if colslice else [])
-    times = {}
-    for option in options:
-        times[json.dumps(option)] = _time_cuda(
-            lambda o=option: _run_spmm_choice("autosage", o, crow, col, val, x), warmup=1, iterations=3
-        )["best_ms"]
-    best = min(options, key=lambda o: times[json.dumps(o)])
-    best_ms = times[json.dumps(best)]
+    options = list(dict.fromkeys(json.dumps(o) for o in options))
+    times = {
+        key: _time_cuda(lambda o=json.loads(key): run_option(o), warmup=1, iterations=3)["best_ms"] for key in options
+    }
+    best_key = min(options, key=lambda k: times[k])
+    best_ms = times[best_key]
     # One baseline call decides when it takes more than twice the best native
     # time; a closer race gets the full warm timing.  The sampled probe has
     # already run the baseline, so library set-up is not in this call, and on
-    # large graphs one baseline call costs ~30 native ones.
-    baseline_ms = _time_cuda(full_baseline, warmup=0, iterations=1)["best_ms"]
+    # large graphs one baseline call costs tens of native ones.
+    baseline_ms = _time_cuda(baseline, warmup=0, iterations=1)["best_ms"]
     baseline_runs = 1
     if baseline_ms < 2.0 * best_ms:
-        baseline_ms = _time_cuda(full_baseline, warmup=1, iterations=3)["best_ms"]
+        baseline_ms = _time_cuda(baseline, warmup=1, iterations=3)["best_ms"]
         baseline_runs = 5
-    confirm: dict[str, Any] = {"autosage_ms": best_ms, "baseline_ms": baseline_ms, "baseline_runs": baseline_runs}
-    if colslice:
-        confirm["colslice_ms"] = times[json.dumps(COLSLICE)]
-        if result["choice"] == "autosage":
-            confirm["sampled_choice_ms"] = times[json.dumps(sampled)]
-    confirm["wall_ms"] = (time.perf_counter() - wall_start) * 1000.0
-    result["full_graph"] = confirm
+    result["full_graph"] = {
+        "autosage_ms": best_ms,
+        "baseline_ms": baseline_ms,
+        "baseline_runs": baseline_runs,
+        "candidates": [{"candidate": json.loads(k), "best_ms": times[k]} for k in options],
+        "sampled_choice": result.get("candidate"),
+        "wall_ms": (time.perf_counter() - wall_start) * 1000.0,
+    }
     if best_ms > baseline_ms:
         result["choice"] = "baseline"
         result["candidate"] = None
         result["reason"] = "slower than the baseline on the full graph"
     else:
         result["choice"] = "autosage"
-        result["candidate"] = best
+        result["candidate"] = json.loads(best_key)
+        result.pop("reason", None)
+
+
+def _confirm_spmm_on_full_graph(result: dict[str, Any], colslice: bool, config: SchedulerConfig, probe,
+                                crow, col, val, x) -> None:
+    """SpMM options on the full graph: the sampled probe's best split
+    candidate, the preferred candidate at the full graph's q95, the
+    whole-graph kernel (candidate None) and, when eligible, the
+    column-sliced SpMM."""
+    options: list[Any] = [probe["chosen"]] if probe["chosen"] is not None else []
+    if native_op("spmm_csr_split") is not None and config.hub_split:
+        options.append(_full_graph_candidate(crow, x.size(1), config))
+    options.append(None)
+    if colslice:
+        options.append(COLSLICE)
+    full_baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
+    _decide_on_full_graph(result, options, lambda o: _run_spmm_choice("autosage", o, crow, col, val, x),
+                          full_baseline)
 
 
 def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dict[str, Any]]:
@@ -486,7 +539,7 @@ def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dic
             "baseline": "torch.sparse.mm(csr)",
             "reason": "AutoSAGE CUDA kernels require float32 features",
         }
-    load_native()
+    _require_native()
     config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=6)
     baseline, baseline_name = _prepare_spmm_baseline(crow, col, val, x)
     baseline_timing = _time_cuda(baseline, warmup=2, iterations=5)
@@ -572,7 +625,7 @@ def sddmm_csr_auto(
         run, name = _prepare_sddmm_baseline(crow, col, query, key)
         return run(), {**_cpu_info("sddmm"), "baseline": name, "reason": "AutoSAGE CUDA kernels require float32 features"}
 
-    load_native()
+    _require_native()
     config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=6)
     device = device_signature()
     graph = graph_signature_memo(crow, col, query.size(1), "sddmm", dtype=query.dtype)
@@ -616,6 +669,20 @@ def sddmm_csr_auto(
         core_call=core_call,
     )
     result = _result_dict("sddmm", config, probe, baseline_name, s_crow, s_col, sample_ms)
+    if config.full_graph_check and split is not None:
+        # the sampled best pair and the pair of the full graph's preferred
+        # candidate, on the full graph
+        # (the SDDMM hub path cuts rows into 2048-edge chunks; below ~1024
+        # edges the one-wave-per-row path is faster: on cfg4, where 101k rows
+        # have degree 197-198 = q95, threshold 197 costs 2.45 ms, 256 or
+        # 1024 cost 1.82 ms)
+        _, waves, threshold = _full_graph_candidate(crow, query.size(1), config)
+        if config.hub_threshold is None:
+            threshold = max(threshold, _SDDMM_MIN_HUB_DEGREE)
+        options = ([probe["chosen"]] if probe["chosen"] is not None else []) + [[waves, threshold]]
+        full_baseline, _ = _prepare_sddmm_baseline(crow, col, query, key)
+        _decide_on_full_graph(result, options, lambda o: _run_sddmm_choice("autosage", o, crow, col, query, key),
+                              full_baseline)
     output = _run_sddmm_choice(result["choice"], result["candidate"], crow, col, query, key)
     if config.cache:
         cache.store(device, graph, result)

@@ -61,6 +61,11 @@ _SIGNATURES = {
         _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr]
     ),
     "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
+    "as_induced_sample_workspace_bytes": (_c_size, [_c_i64]),
+    "as_induced_sample_count": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "as_induced_sample_fill": (
+        _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]
+    ),
     "as_csr_attention_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "as_csr_attention_f32": (
         _c_int,
@@ -404,6 +409,34 @@ def columns_ascending(crow: torch.Tensor, col: torch.Tensor) -> bool:
 def _maybe_validate(crow: torch.Tensor, col: torch.Tensor) -> None:
     if os.getenv("AUTOSAGE_VALIDATE") == "1":
         validate_csr(crow, col)
+
+
+def induced_sample(crow: torch.Tensor, col: torch.Tensor, val: Optional[torch.Tensor], selected: torch.Tensor):
+    """(new_crow, new_col, new_val) of the sub-graph induced by the sorted
+    row sample ``selected`` (``autosage/_auto.py:95-154``), on the device in
+    two native passes and one host sync (the size of the kept edge list)."""
+    _check(crow.is_cuda and col.is_cuda and selected.is_cuda, "induced_sample needs CUDA tensors")
+    _check(crow.dtype == torch.long and col.dtype == torch.long and selected.dtype == torch.long,
+           "crow, col and selected must use torch.long indices")
+    _check(val is None or (val.is_cuda and val.dtype == torch.float32), "val must be a float32 CUDA tensor")
+    crow, col, selected = crow.contiguous(), col.contiguous(), selected.contiguous()
+    val = None if val is None else val.contiguous()
+    n = crow.numel() - 1
+    s = selected.numel()
+    lib = library()
+    ws = _workspace(lib.as_induced_sample_workspace_bytes(n), crow.device)
+    new_crow = torch.empty(s + 1, dtype=torch.long, device=crow.device)
+    with torch.cuda.device(crow.device):
+        stream = _stream(crow.device)
+        _raise(lib.as_induced_sample_count(_ptr(crow), _ptr(col), n, _ptr(selected), s, _ptr(new_crow), _ptr(ws),
+                                           ws.numel(), stream), "induced_sample")
+        kept = int(new_crow[s].item())
+        new_col = torch.empty(kept, dtype=torch.long, device=crow.device)
+        new_val = None if val is None else torch.empty(kept, dtype=val.dtype, device=val.device)
+        _raise(lib.as_induced_sample_fill(_ptr(crow), _ptr(col), _ptr(val), n, _ptr(selected), s, _ptr(new_crow),
+                                          _ptr(new_col), _ptr(new_val), _ptr(ws), ws.numel(), stream),
+               "induced_sample")
+    return new_crow, new_col, new_val
 
 
 def bin_rows_by_degree(crow: torch.Tensor, threshold: int) -> tuple[torch.Tensor, torch.Tensor]:

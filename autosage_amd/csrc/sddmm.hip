@@ -178,8 +178,8 @@ __global__ __launch_bounds__(1024) void hub_chunk_scan_kernel(const int64_t* __r
   if (threadIdx.x == 0) counts[2] = total;
 }
 
-// Split SDDMM in one launch.  Workgroups [0, hub_blocks) are persistent and
-// stride over the hub chunk items (2048-edge pieces of hub rows); the rest take
+// Split SDDMM in one launch.  Workgroups [0, hub_blocks) stride over the hub
+// chunk items (2048-edge pieces of hub rows; usually one each); the rest take
 // the light rows in row order, one per wave, skipping hub and empty rows.
 // Hub workgroups have the lowest indices, so they are dispatched first.
 template <int G, int MF, bool VEC>
@@ -276,16 +276,18 @@ int launch_sddmm_rows(const SddmmArgs& a, int64_t hub_threshold, hipStream_t str
   return AS_OK;
 }
 
-// Waves given to the hub chunks of the scheduled kernel: about half of what
-// the chip holds at once (256 CUs x 32 waves), whatever the workgroup size,
-// so the hub rows finish alongside the light rows (with a fixed 256
-// workgroups, 2-wave workgroups left the hub pass as a 2x tail).
-constexpr int64_t kHubWaves = 4096;
+// Workgroups given to the hub chunks of the scheduled kernel: one per chunk
+// up to this cap (the host knows only an upper bound on the chunk count;
+// workgroups past the real count exit at once).  A small fixed pool was a
+// bottleneck when a low threshold makes tens of thousands of rows hub rows
+// (cfg4, threshold 197: 2.96 ms with 4,096 pool waves against 1.82 ms at
+// threshold 256), and a pool much smaller than the chunk count leaves the
+// hub pass as a tail behind the light rows.
+constexpr int64_t kHubBlocksMax = 65536;
 
 int launch_sddmm_scheduled(const SddmmArgs& a, int waves, int64_t hub_threshold, int64_t item_upper,
                            const int32_t* order, const int32_t* counts, const int32_t* chunk_off, hipStream_t stream) {
-  const int64_t hub_cap = kHubWaves / waves;
-  const int64_t hub_blocks = item_upper < hub_cap ? item_upper : hub_cap;
+  const int64_t hub_blocks = item_upper < kHubBlocksMax ? item_upper : kHubBlocksMax;
   const int64_t blocks = hub_blocks + (a.n + waves - 1) / waves;
   const dim3 block(static_cast<unsigned>(waves * kWave));
   for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {

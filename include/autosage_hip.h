@@ -162,6 +162,28 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Bytes of workspace for the induced-sample entry points (n int32). */
+size_t as_induced_sample_workspace_bytes(int64_t n);
+
+/* Induced sub-graph of a row sample, on the device.  Replaces the torch
+ * composition _induced_sample_csr (autosage/_auto.py:95-154) given its
+ * sorted sample `selected` (s distinct rows).  Two calls with the same
+ * workspace: _count writes new_crow[0..s] (kept edges: those whose column is
+ * sampled); the caller reads new_crow[s] to size new_col/new_val; _fill
+ * writes the kept edges in CSR order with columns renamed to their sample
+ * index, and their values when val is given.  Bit-identical to the
+ * reference's outputs. */
+int as_induced_sample_count(const int64_t* crow, const int64_t* col, int64_t n,
+                            const int64_t* selected, int64_t s,
+                            int64_t* new_crow, void* workspace,
+                            size_t workspace_bytes, void* stream);
+int as_induced_sample_fill(const int64_t* crow, const int64_t* col,
+                           const float* val, int64_t n,
+                           const int64_t* selected, int64_t s,
+                           const int64_t* new_crow, int64_t* new_col,
+                           float* new_val, const void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* Structure check of a CSR graph (no reference counterpart: the reference
  * kernels trust their inputs).  ORs into *flags (device int32, zeroed by the
  * caller): 1 = crow[0] != 0, 2 = crow decreases somewhere, 4 = crow[n] != nnz,

@@ -66,6 +66,9 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_last_error() == b"sizes must be non-negative"
     assert lib.as_csr_validate(None, None, 4, 0, 4, None, None) == 1
     assert lib.as_last_error() == b"null pointer argument"
+    assert lib.as_induced_sample_count(None, None, 10, None, 11, None, None, 0, None) == 1
+    assert lib.as_last_error() == b"sample size must lie in [0, N]"
+    assert lib.as_induced_sample_workspace_bytes(1000) >= 4000
     # n == 0 is a no-op success
     assert lib.as_spmm_csr_f32(None, None, None, None, None, 0, 0, 8, 1, None) == 0
 

@@ -140,6 +140,10 @@ def test_colslice_skewed_config_rows():
         _assert_fp64_close(got[r].cpu().numpy(), exact)
 
 
+def _timed(info) -> list:
+    return [c["candidate"] for c in info.get("full_graph", {}).get("candidates", [])]
+
+
 def test_scheduler_times_colslice_on_the_full_graph(monkeypatch, tmp_path):
     import autosage_amd
 
@@ -148,7 +152,8 @@ def test_scheduler_times_colslice_on_the_full_graph(monkeypatch, tmp_path):
     crow, col, val, x = _inputs(64, False, seed=31, rows=6000, degree=30)
     d_crow, d_col, _, d_x = to_dev(crow, col, None, x)
     out, info = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
-    assert "colslice_ms" in info["full_graph"] and info["full_graph"]["colslice_ms"] > 0
+    assert "colslice" in _timed(info) and None in _timed(info)
+    assert all(c["best_ms"] > 0 for c in info["full_graph"]["candidates"])
     exact = oracle.spmm_f64(crow, col, None, x)
     if info["candidate"] == "colslice":
         _assert_fp64_close(out.cpu().numpy(), exact)
@@ -172,8 +177,8 @@ def test_scheduler_times_colslice_on_the_full_graph(monkeypatch, tmp_path):
     # ... and without a cache record it is never timed with column slices
     monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path / "second"))
     _, info2 = autosage_amd.spmm_csr_auto(d_crow, d_shuffled, None, d_x)
-    assert "colslice_ms" not in info2.get("full_graph", {}) and info2.get("candidate") != "colslice"
+    assert "colslice" not in _timed(info2) and info2.get("candidate") != "colslice"
     # off: never timed
     monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
     _, info3 = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
-    assert "colslice_ms" not in info3.get("full_graph", {}) and info3.get("candidate") != "colslice"
+    assert "colslice" not in _timed(info3) and info3.get("candidate") != "colslice"

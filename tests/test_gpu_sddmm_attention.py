@@ -164,3 +164,34 @@ def test_conv_layer_on_gpu():
     out, info = layer(x, edge_index, edge_weight, return_info=True)
     assert torch.equal(out.cpu(), torch.tensor([[90.0], [20.0], [0.0]]))
     assert info["choice"] == "native"
+
+
+def test_schedulers_decide_on_the_full_graph(monkeypatch, tmp_path):
+    """The sampled probe only shortlists: the full graph times the sampled
+    best, the full-graph-quantile candidate (and, for SpMM, the whole-graph
+    kernel) against one baseline call, so a graph whose small sample favours
+    the baseline still runs the faster native kernel."""
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    crow, col = case_graph(60000, 10, seed=21, hubs=20, hub_degree=20000)
+    q, kk = _qk(60000, 64, seed=5)
+    d_crow, d_col, d_q, d_k = to_dev(crow, col, q, kk)
+    scores, sinfo = sddmm_csr_auto(d_crow, d_col, d_q, d_k)
+    timed = [c["candidate"] for c in sinfo["full_graph"]["candidates"]]
+    assert len(timed) >= 1 and all(isinstance(c, list) for c in timed)
+    fg = sinfo["full_graph"]
+    assert sinfo["choice"] == ("autosage" if fg["autosage_ms"] <= fg["baseline_ms"] else "baseline")
+    if sinfo["choice"] == "autosage":
+        assert sinfo["candidate"] in timed
+        assert bitwise_equal(scores, oracle.sddmm_ref(crow, col, q, kk))
+    x = np.random.default_rng(2).standard_normal((60000, 64)).astype(np.float32)
+    d_x = torch.from_numpy(x).cuda()
+    out, info = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    timed = [c["candidate"] for c in info["full_graph"]["candidates"]]
+    assert None in timed
+    if info["choice"] == "autosage":
+        assert info["candidate"] in timed
+        assert bitwise_equal(out, oracle.spmm_seq(crow, col, None, x))
+    # AUTOSAGE_FULL_CHECK=0: the reference's sampled decision alone
+    monkeypatch.setenv("AUTOSAGE_FULL_CHECK", "0")
+    _, info0 = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert "full_graph" not in info0
