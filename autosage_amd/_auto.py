@@ -202,10 +202,10 @@ def _spmm_candidates(crow: torch.Tensor, feature_width: int, config: SchedulerCo
 
 
 COLSLICE = "colslice"  # candidate value of the column-sliced SpMM
-# Column slicing pays when X is well beyond the 8 x 4 MB of L2 and rows are
-# long enough that the per-(row, slice) fp64 partials (64·F bytes per row)
-# stay small next to the gathers (4·F bytes per edge).
-_COLSLICE_MIN_X_BYTES = 64 << 20
+# Column slicing pays when X is beyond the 8 x 4 MB of L2 and rows are long
+# enough that the per-(row, slice) fp64 partials (128·F bytes per row,
+# written and read) stay small next to the gathers (4·F bytes per edge).
+_COLSLICE_MIN_X_BYTES = 32 << 20
 _COLSLICE_MIN_MEAN_DEGREE = 64
 
 

@@ -67,14 +67,14 @@ def test_column_slices_never_eligible_without_the_native_op(monkeypatch):
 
     crow = torch.arange(0, 100 * 1000 + 1, 100)
     col = torch.arange(100 * 1000) % 1000
-    x = torch.zeros(1000, 20000)  # 80 MB
+    x = torch.zeros(1000, 10000)  # 40 MB
     monkeypatch.setattr(_auto, "native_op", lambda name: None)
     assert not _auto._colslice_eligible(crow, col, x, SchedulerConfig(column_slices="on"))
     monkeypatch.setattr(_auto, "native_op", lambda name: object())
     assert not _auto._colslice_eligible(crow, col, x, SchedulerConfig(column_slices="off"))
     assert not _auto._colslice_eligible(crow, col, x, SchedulerConfig(full_graph_check=False))
     # auto: too little X or too few edges per row
-    assert not _auto._colslice_eligible(crow, col, x[:, :100], SchedulerConfig())
+    assert not _auto._colslice_eligible(crow, col, x[:, :7000], SchedulerConfig())  # 28 MB
     assert not _auto._colslice_eligible(crow, col[: 63 * 1000], x, SchedulerConfig())
 
 
