@@ -52,6 +52,14 @@ def test_colslice_against_fp64(features, weighted):
     _assert_fp64_close(got, oracle.spmm_f64(crow, col, val, x))
 
 
+@pytest.mark.parametrize("features", [512, 1024, 1028])
+def test_colslice_wide_features(features):
+    # 4 / 8 / 9 feature tiles of 128 in one launch (1028: a partial last tile)
+    crow, col, val, x = _inputs(features, True, seed=features, rows=1500, hub_degree=1200)
+    got = _colslice(crow, col, val, x).cpu().numpy()
+    _assert_fp64_close(got, oracle.spmm_f64(crow, col, val, x))
+
+
 def test_colslice_long_slices_and_empty_rows():
     # hub rows of 20000 edges: about 2500 per slice, the U = 16 path
     crow, col, val, x = _inputs(128, True, seed=11, rows=24000, degree=4, hubs=4, hub_degree=20000, empty=0.3)

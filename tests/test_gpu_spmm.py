@@ -35,7 +35,7 @@ def _inputs(features, weighted, seed=0, rows=700, hubs=3, hub_degree=500):
 
 @pytest.mark.parametrize("vec4", ["1", "0"])
 @pytest.mark.parametrize("weighted", [False, True])
-@pytest.mark.parametrize("features", [1, 3, 32, 64, 100, 128, 200, 256, 300])
+@pytest.mark.parametrize("features", [1, 3, 32, 64, 100, 128, 200, 256, 300, 1024])
 def test_spmm_csr_bitwise(features, weighted, vec4, monkeypatch):
     monkeypatch.setenv("AUTOSAGE_VEC4", vec4)
     crow, col, val, x = _inputs(features, weighted, seed=features)
