@@ -529,7 +529,9 @@ def _confirm_spmm_on_full_graph(result: dict[str, Any], colslice: bool, config: 
 
 
 def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dict[str, Any]]:
-    """Full-graph calibration of every shortlisted candidate (``_auto.py:444-522``)."""
+    """Full-graph calibration (``_auto.py:444-522``) of every shortlisted
+    candidate, the whole-graph kernel and, when eligible, the column-sliced
+    SpMM."""
     crow, col, val, x = _normalize_csr(crow, col, val, x)
     if not x.is_cuda:
         return "baseline", _cpu_info("spmm")
@@ -553,9 +555,12 @@ def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dic
             timings.append({"candidate": [tile, waves, threshold], "best_ms": t["best_ms"]})
             if t["best_ms"] < best:
                 best, selected = t["best_ms"], [tile, waves, threshold]
-    elif core is not None:
-        best = _time_cuda(lambda: core(crow, col, val, x), warmup=2, iterations=5)["best_ms"]
-        timings.append({"candidate": None, "best_ms": best})
+    if core is not None:
+        # the whole-graph kernel (candidate None), as in the full-graph decision
+        t = _time_cuda(lambda: core(crow, col, val, x), warmup=2, iterations=5)
+        timings.append({"candidate": None, "best_ms": t["best_ms"]})
+        if t["best_ms"] < best:
+            best, selected = t["best_ms"], None
     if _colslice_eligible(crow, col, x, config):
         colslice_op = native_op("spmm_csr_colslice")
         t = _time_cuda(lambda: colslice_op(crow, col, val, x), warmup=2, iterations=5)

@@ -195,3 +195,24 @@ def test_schedulers_decide_on_the_full_graph(monkeypatch, tmp_path):
     monkeypatch.setenv("AUTOSAGE_FULL_CHECK", "0")
     _, info0 = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
     assert "full_graph" not in info0
+
+
+def test_calibrate_full_times_every_option_and_is_replayed(monkeypatch, tmp_path):
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    crow, col = case_graph(30000, 24, seed=17, hubs=8, hub_degree=8000)
+    x = np.random.default_rng(3).standard_normal((30000, 64)).astype(np.float32)
+    d_crow, d_col, d_x = to_dev(crow, col, x)
+    choice, info = autosage_amd.calibrate_full(d_crow, d_col, None, d_x)
+    timed = [c["candidate"] for c in info["candidates"]]
+    assert None in timed and any(isinstance(c, list) for c in timed)
+    assert info["calibration"] == "full_graph" and choice == info["choice"]
+    if choice == "autosage":
+        assert info["candidate"] in timed
+        assert info["autosage_ms"] == min(c["best_ms"] for c in info["candidates"])
+    out, replay = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert replay["from_cache"] and replay["candidate"] == info["candidate"]
+    ref = oracle.spmm_seq(crow, col, None, x)
+    if choice == "autosage" and info["candidate"] != "colslice":
+        assert bitwise_equal(out, ref)
+    else:
+        assert np.allclose(out.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
