@@ -720,6 +720,55 @@ def _csr_row_softmax(crow: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
     return _torch_row_softmax(crow, scores)
 
 
+def _attention_colslice_eligible(crow, col, query, value, config: SchedulerConfig) -> bool:
+    """Whether the fused path should time the column-sliced attention."""
+    if config.column_slices == "off" or not config.full_graph_check:
+        return False
+    if native_op("csr_attention_colslice") is None or crow.numel() <= 1 or col.numel() == 0:
+        return False
+    from ._native import attention_colslice_supported, columns_ascending
+
+    if not attention_colslice_supported(query, value):
+        return False
+    gathered = (query.size(1) + value.size(1)) * 4 * (crow.numel() - 1)
+    if config.column_slices == "auto" and gathered < _COLSLICE_MIN_X_BYTES:
+        return False
+    return columns_ascending(crow, col)
+
+
+def _attention_variant(crow, col, q, k, v, scale: float) -> tuple[str, dict[str, Any]]:
+    """"fused" (the exact fused kernel) or "colslice" for this graph: the
+    column-sliced attention is timed against the fused kernel once per graph
+    on the full graph when eligible, and the faster one is cached."""
+    config = SchedulerConfig.from_env()
+    if not _attention_colslice_eligible(crow, col, q, v, config):
+        return "fused", {"variant": "fused", "from_cache": False}
+    device = device_signature()
+    graph = graph_signature_memo(crow, col, q.size(1), f"attention:fv={v.size(1)}", dtype=q.dtype)
+    cache = ScheduleCache()
+    if config.cache:
+        record = cache.lookup(device, graph)
+        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
+            result = record["result"]
+            if result.get("variant") in ("fused", "colslice"):
+                return result["variant"], {**result, "from_cache": True}
+    times = {}
+    for name, op in (("fused", native_op("csr_attention")), ("colslice", native_op("csr_attention_colslice"))):
+        times[name] = _time_cuda(lambda o=op: o(crow, col, q, k, v, scale), warmup=1, iterations=3)["best_ms"]
+    variant = min(times, key=times.get)
+    result = {
+        "operation": "attention",
+        "schema_version": AUTOTUNE_SCHEMA_VERSION,
+        "variant": variant,
+        "configuration": config.tuning_signature(),
+        "full_graph": {"fused_ms": times["fused"], "colslice_ms": times["colslice"]},
+        "from_cache": False,
+    }
+    if config.cache:
+        cache.store(device, graph, result)
+    return variant, result
+
+
 def _fused_default() -> bool:
     return os.getenv("AUTOSAGE_FUSED_ATTENTION", "1") == "1"
 
@@ -749,10 +798,14 @@ def csr_attention_forward(
         crow_n, col_n, q, k = _normalize_sddmm(crow, col, query, key)
         if not load_native() or native_op("csr_attention") is None:
             raise RuntimeError("AutoSAGE native csr_attention is unavailable")
-        out = native_op("csr_attention")(crow_n, col_n, q, k, value.contiguous(), float(scale))
+        v = value.contiguous()
+        variant, decision = _attention_variant(crow_n, col_n, q, k, v, float(scale))
+        out = native_op("csr_attention" if variant == "fused" else "csr_attention_colslice")(
+            crow_n, col_n, q, k, v, float(scale))
         info = {"operation": "attention", "schema_version": AUTOTUNE_SCHEMA_VERSION, "choice": "fused",
-                "from_cache": False}
-        return out, {"sddmm": {**info, "operation": "sddmm"}, "spmm": {**info, "operation": "spmm"}, "fused": True}
+                "from_cache": decision.get("from_cache", False)}
+        return out, {"sddmm": {**info, "operation": "sddmm"}, "spmm": {**info, "operation": "spmm"}, "fused": True,
+                     "variant": variant, "attention": decision}
     scores, sddmm_info = sddmm_csr_auto(crow, col, query, key, guardrail=guardrail, seed=seed, verbose=verbose)
     scores = scores.to(query.dtype)
     if scale != 1.0:

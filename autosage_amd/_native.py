@@ -60,6 +60,12 @@ _SIGNATURES = {
     "as_spmm_csr_colslice_f32": (
         _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr]
     ),
+    "as_csr_attention_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "as_csr_attention_colslice_f32": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr,
+         _c_size, _c_ptr],
+    ),
     "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "as_induced_sample_workspace_bytes": (_c_size, [_c_i64]),
     "as_induced_sample_count": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
@@ -339,6 +345,47 @@ def csr_attention_impl(crow, col, query, key, value, scale=1.0):
     return out
 
 
+def attention_colslice_supported(query: torch.Tensor, value: torch.Tensor) -> bool:
+    """Feature widths the column-sliced attention handles (float4 lanes):
+    multiples of 4 in [4, 256], rows 16-byte aligned."""
+    fqk, fv = query.size(1), value.size(1)
+    return (fqk % 4 == 0 and 4 <= fqk <= 256 and fv % 4 == 0 and 4 <= fv <= 256
+            and all(t.data_ptr() % 16 == 0 for t in (query, value)))
+
+
+def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
+    """Column-sliced attention (one column slice per XCD, online softmax per
+    (row, slice)).  Needs columns ascending within every row; checked once
+    per graph."""
+    check_sddmm_inputs(crow, col, query, key)
+    _maybe_validate(crow, col)
+    _check(value.is_cuda and value.device == query.device, "value must be on the same CUDA device as query")
+    _check(value.dtype == torch.float32 and value.dim() == 2 and value.is_contiguous(),
+           "value must be contiguous float32 with shape [N, F_v]")
+    _check(value.size(0) == query.size(0), "value must have one row per node")
+    if not columns_ascending(crow, col):
+        raise ValueError("csr_attention_colslice requires column indices ascending within every row")
+    n, fqk = query.shape
+    fv = value.size(1)
+    nnz = col.numel()
+    if not attention_colslice_supported(query, value) or key.data_ptr() % 16 != 0:
+        raise ValueError("csr_attention_colslice needs F_qk and F_v multiples of 4 in [4, 256] and 16-byte "
+                         "aligned rows")
+    out = torch.empty((n, fv), dtype=value.dtype, device=value.device)
+    if n == 0:
+        return out
+    lib = library()
+    ws = _workspace(min(lib.as_csr_attention_colslice_workspace_bytes(n, nnz, fv), _colslice_workspace_cap()),
+                    query.device)
+    with torch.cuda.device(query.device):
+        status = lib.as_csr_attention_colslice_f32(
+            _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv, float(scale),
+            _ptr(ws), ws.numel(), _stream(query.device),
+        )
+    _raise(status, "autosage::csr_attention_colslice")
+    return out
+
+
 _VALIDATION_RULES = (
     (1, "crow[0] must be 0"),
     (2, "crow must be non-decreasing"),
@@ -480,6 +527,11 @@ _SCHEMAS = {
     "csr_attention": (
         "csr_attention(Tensor crow, Tensor col, Tensor query, Tensor key, Tensor value, float scale=1.0) -> Tensor",
         csr_attention_impl,
+    ),
+    "csr_attention_colslice": (
+        "csr_attention_colslice(Tensor crow, Tensor col, Tensor query, Tensor key, Tensor value, float scale=1.0) "
+        "-> Tensor",
+        csr_attention_colslice_impl,
     ),
 }
 

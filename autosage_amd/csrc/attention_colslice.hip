@@ -1,0 +1,431 @@
+// Column-sliced CSR attention: out[r] = softmax_r(scale · <Q[r], K[c]>) · V,
+// an alternative schedule for the fused attention (attention.hip) on graphs
+// whose columns ascend within every row.
+//
+// Rows of degree >= 128 are cut into the 8 column slices of colslice_common.h;
+// workgroup g works on slice g % 8, so each XCD gathers K and V rows only
+// from its eighth of the columns and its L2 caches eight times as many
+// distinct rows as when every XCD gathers from all of them.  One wave per
+// (row, slice) keeps an online softmax over the slice's edges (running max m,
+// sum l = Σ exp(s - m), acc = Σ exp(s - m)·V[c]) and writes (m, l, acc) as
+// fp32 partials; the reduction merges the 8 partials of a row
+// (m = max m_s, out = Σ e^(m_s - m)·acc_s / Σ e^(m_s - m)·l_s).  Shorter rows
+// run the same online softmax in one wave and write out directly.
+//
+// Gathers use float4 lanes: G lanes per edge for K (G = 16/32/64 for
+// F_qk <= 64/128/256) and for V, 64/G edges per gather instruction.  A batch
+// of 8 edges issues all its K and V gathers first; the scores are reduced
+// inside each K lane group, broadcast through SGPRs and picked up by the V
+// lane group that holds the same edge; each V lane group keeps its own
+// online-softmax state, merged in a fixed butterfly order at the end.
+//
+// Not bit-identical to the fused kernel (that one keeps the reference's
+// stage order); deterministic, and within about 0.2 of the 1e-5 relative /
+// 1e-6 absolute bar against fp64 on the benchmark graph, as is the fused one.
+#include "as_device.h"
+#include "as_internal.h"
+#include "colslice_common.h"
+
+namespace as {
+
+namespace {
+
+constexpr int64_t kAttSliceMinDegree = 128;  // rows below are not sliced
+constexpr int kAttBatch = 8;                 // edges per online-softmax step
+constexpr int64_t kAttChunkRows = 131072;    // sliced rows per partial chunk
+constexpr int64_t kAttSliceBlocks = 4096;    // slice-kernel workgroups per slice
+constexpr int64_t kAttReduceBlocks = 8192;   // reduction workgroups
+
+__device__ __forceinline__ void merge_softmax(float& m, float& l, float (&acc)[4], float mo, float lo,
+                                              const float (&ao)[4]) {
+  const float mn = fmaxf(m, mo);
+  if (mn == -INFINITY) return;  // both sides saw no edge
+  const float c1 = m == -INFINITY ? 0.f : expf(m - mn);
+  const float c2 = mo == -INFINITY ? 0.f : expf(mo - mn);
+  l = l * c1 + lo * c2;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) acc[v] = acc[v] * c1 + ao[v] * c2;
+  m = mn;
+}
+
+// Online softmax of one wave over edges [rs, re) of a row.  On return every
+// lane holds the merged state of the whole range; lane vl of a V group owns
+// features 4·vl .. 4·vl + 3 of acc.
+// FQK / FV > 0: the feature widths as compile-time constants (the row stride
+// of each gather becomes a shift instead of a per-lane 64-bit multiply).
+template <int GK, int GV, int FQK, int FV>
+__device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, const float* __restrict__ key,
+                                             const float* __restrict__ value, int64_t fqk_rt, int64_t fv_rt,
+                                             const FVec<4>& q, float scale, int64_t rs, int64_t re, float& m,
+                                             float& l, float (&acc)[4]) {
+  constexpr int EK = kWave / GK;  // edges per K gather instruction
+  constexpr int EV = kWave / GV;  // edges per V gather instruction
+  constexpr int E = kAttBatch;
+  const int64_t fqk = FQK > 0 ? FQK : fqk_rt;
+  const int64_t fv = FV > 0 ? FV : fv_rt;
+  const int lane = lane_id();
+  const int gk = lane / GK;
+  const int kl = lane % GK;
+  const int gv = lane / GV;
+  const int vl = lane % GV;
+  // lanes past the feature end read feature 0 (their q is 0 / their output
+  // is not stored)
+  const uint32_t kbytes = static_cast<uint32_t>((4 * kl < fqk ? 4 * kl : 0) * 4);
+  const uint32_t vbytes = static_cast<uint32_t>((4 * vl < fv ? 4 * vl : 0) * 4);
+  rs = uniform_i64(rs);
+  re = uniform_i64(re);
+  m = -INFINITY;
+  l = 0.f;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) acc[v] = 0.f;
+  int next_col = 0;
+  if (lane < re - rs) next_col = static_cast<int>(col[rs + lane]);
+  for (int64_t base = rs; base < re; base += kWave) {
+    const int cnt = static_cast<int>((re - base) < kWave ? (re - base) : kWave);
+    const int my_col = next_col;
+    const int64_t nb = base + kWave;
+    if (nb < re && lane < re - nb) next_col = static_cast<int>(col[nb + lane]);
+    for (int j = 0; j < cnt; j += E) {
+      FVec<4> kv[E / EK];
+      FVec<4> vv[E / EV];
+#pragma unroll
+      for (int i = 0; i < E / EK; ++i) {
+        int c = 0;
+#pragma unroll
+        for (int g = 0; g < EK; ++g) {
+          const int e = j + i * EK + g;
+          const int cg = bcast_i32(my_col, e < cnt ? e : cnt - 1);
+          c = gk == g ? cg : c;
+        }
+        kv[i] = load_vec_off<4>(key + row_offset(c, fqk), kbytes);
+      }
+#pragma unroll
+      for (int i = 0; i < E / EV; ++i) {
+        int c = 0;
+#pragma unroll
+        for (int g = 0; g < EV; ++g) {
+          const int e = j + i * EV + g;
+          const int cg = bcast_i32(my_col, e < cnt ? e : cnt - 1);
+          c = gv == g ? cg : c;
+        }
+        vv[i] = load_vec_off<4>(value + row_offset(c, fv), vbytes);
+      }
+      // scores: K instruction i, group g holds edge j + i·EK + g
+      float sk[E / EK];
+#pragma unroll
+      for (int i = 0; i < E / EK; ++i) {
+        float d = q.v[0] * kv[i].v[0];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) d = __builtin_fmaf(q.v[v], kv[i].v[v], d);
+#pragma unroll
+        for (int o = GK / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
+        sk[i] = d * scale;
+      }
+      float s[E / EV];
+      float mb = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < E / EV; ++i) {
+        float si = 0.f;
+#pragma unroll
+        for (int g = 0; g < EV; ++g) {
+          const int e = i * EV + g;  // edge of the batch
+          const float se = bcast_f32(sk[e / EK], GK * (e % EK));
+          si = gv == g ? se : si;
+        }
+        s[i] = j + i * EV + gv < cnt ? si : -INFINITY;
+        mb = fmaxf(mb, s[i]);
+      }
+      const float mn = fmaxf(m, mb);
+      if (mn != -INFINITY) {
+        const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+        l *= corr;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] *= corr;
+#pragma unroll
+        for (int i = 0; i < E / EV; ++i) {
+          const float p = s[i] == -INFINITY ? 0.f : expf(s[i] - mn);
+          l += p;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(p, vv[i].v[v], acc[v]);
+        }
+        m = mn;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = GV; o < kWave; o <<= 1) {
+    const float mo = __shfl_xor(m, o, kWave);
+    const float lo = __shfl_xor(l, o, kWave);
+    float ao[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) ao[v] = __shfl_xor(acc[v], o, kWave);
+    merge_softmax(m, l, acc, mo, lo, ao);
+  }
+}
+
+template <int GK>
+__device__ __forceinline__ FVec<4> load_query_lanes(const float* __restrict__ query, int64_t row, int64_t fqk) {
+  const int kl = lane_id() % GK;
+  FVec<4> q;
+  if (4 * kl < fqk) {
+    q = load_vec<4>(query + row * fqk + 4 * kl);
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) q.v[v] = 0.f;
+  }
+  return q;
+}
+
+struct AttArgs {
+  const int64_t* crow;
+  const int64_t* col;
+  const float* q;
+  const float* k;
+  const float* v;
+  float* out;
+  int64_t n;
+  int64_t fqk;
+  int64_t fv;
+  float scale;
+  const int32_t* order;
+  const int32_t* counts;
+  const int32_t* off;
+};
+
+// Short rows order[H, n), H = counts[0]: one wave per row writes out.  The
+// grid is sized for all n rows; waves stride over the short ones.
+template <int GK, int GV, int FQK, int FV>
+__global__ __launch_bounds__(kBlock) void att_rows_kernel(AttArgs a) {
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const int64_t first = a.counts[0];
+  for (int64_t item = first + static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block(); item < a.n;
+       item += waves) {
+    const int64_t row = uniform_i64(a.order[item]);
+    const FVec<4> q = load_query_lanes<GK>(a.q, row, a.fqk);
+    float m, l, acc[4];
+    attend_edges<GK, GV, FQK, FV>(a.col, a.k, a.v, a.fqk, a.fv, q, a.scale, a.crow[row], a.crow[row + 1], m, l,
+                                  acc);
+    const int lane = lane_id();
+    if (lane < GV && 4 * lane < a.fv) {
+      FVec<4> o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o.v[v] = l > 0.f ? acc[v] / l : 0.f;
+      store_vec<4>(a.out + row * a.fv + 4 * lane, o);
+    }
+  }
+}
+
+// Sliced rows order[begin, begin + items) (those below H): wave per
+// (row, slice) writes the partial state at index slice·stride + local.  The
+// host knows only an upper bound on H, so a chunk may be empty: the grid is
+// capped and the waves of a slice stride over the chunk, which keeps the
+// launch of an empty chunk short.
+template <int GK, int GV, int FQK, int FV>
+__global__ __launch_bounds__(kBlock) void att_slice_kernel(AttArgs a, int64_t begin, int64_t items, int64_t stride,
+                                                           float* __restrict__ pm, float* __restrict__ pl,
+                                                           float* __restrict__ pacc) {
+  const int slice = static_cast<int>(blockIdx.x % kSlices);
+  const int64_t waves = static_cast<int64_t>(gridDim.x / kSlices) * kWavesPerBlock;
+  int64_t end = a.counts[0] - begin;
+  end = end < items ? end : items;
+  const int lane = lane_id();
+  for (int64_t local = static_cast<int64_t>(blockIdx.x / kSlices) * kWavesPerBlock + wave_in_block(); local < end;
+       local += waves) {
+    const int64_t row = uniform_i64(a.order[begin + local]);
+    const int64_t rs = uniform_i64(a.crow[row]);
+    const int64_t deg = uniform_i64(a.crow[row + 1]) - rs;
+    int64_t lo, hi;
+    slice_range(a.off, row, slice, deg, lo, hi);
+    lo = uniform_i64(lo);
+    hi = uniform_i64(hi);
+    const FVec<4> q = load_query_lanes<GK>(a.q, row, a.fqk);
+    float m, l, acc[4];
+    attend_edges<GK, GV, FQK, FV>(a.col, a.k, a.v, a.fqk, a.fv, q, a.scale, rs + lo, rs + hi, m, l, acc);
+    const int64_t at = slice * stride + local;
+    if (lane < GV && 4 * lane < a.fv) {
+      FVec<4> o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o.v[v] = acc[v];
+      store_vec<4>(pacc + at * a.fv + 4 * lane, o);
+    }
+    if (lane == 0) {
+      pm[at] = m;
+      pl[at] = l;
+    }
+  }
+}
+
+// Merge of the 8 partial states of each sliced row of the chunk; thread per
+// (row, 4 features).
+__global__ __launch_bounds__(kBlock) void att_reduce_kernel(AttArgs a, int64_t begin, int64_t items, int64_t stride,
+                                                            const float* __restrict__ pm,
+                                                            const float* __restrict__ pl,
+                                                            const float* __restrict__ pacc) {
+  const int64_t F4 = a.fv / 4;
+  const int64_t total = items * F4;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += step) {
+    const int64_t local = t / F4;
+    const int64_t f = (t - local * F4) * 4;
+    if (begin + local >= a.counts[0]) continue;
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s) m = fmaxf(m, pm[s * stride + local]);
+    float l = 0.f;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (m != -INFINITY) {
+#pragma unroll
+      for (int s = 0; s < kSlices; ++s) {
+        const float ms = pm[s * stride + local];
+        if (ms == -INFINITY) continue;
+        const float c = expf(ms - m);
+        l = __builtin_fmaf(c, pl[s * stride + local], l);
+        const FVec<4> p = load_vec<4>(pacc + (s * stride + local) * a.fv + f);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(c, p.v[v], acc[v]);
+      }
+    }
+    const int64_t row = a.order[begin + local];
+    FVec<4> o;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) o.v[v] = l > 0.f ? acc[v] / l : 0.f;
+    store_vec<4>(a.out + row * a.fv + f, o);
+  }
+}
+
+int lane_group(int64_t f) { return f <= 64 ? 16 : (f <= 128 ? 32 : 64); }
+
+template <int GK, int GV, int FQK = 0, int FV = 0>
+void launch_attention_t(const AttArgs& a, int64_t upper, int64_t chunk, float* pm, float* pl, float* pacc,
+                        hipStream_t s) {
+  // short rows: a grid-stride over order[H, n) (H is known on the device only)
+  int64_t row_blocks = (a.n + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (row_blocks > kMaxBlocksPerLaunch) row_blocks = kMaxBlocksPerLaunch;
+  hipLaunchKernelGGL((att_rows_kernel<GK, GV, FQK, FV>), dim3(static_cast<unsigned>(row_blocks)), dim3(kBlock), 0, s,
+                     a);
+  for (int64_t begin = 0; begin < upper; begin += chunk) {
+    const int64_t items = upper - begin < chunk ? upper - begin : chunk;
+    int64_t per_slice = (items + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (per_slice > kAttSliceBlocks) per_slice = kAttSliceBlocks;
+    hipLaunchKernelGGL((att_slice_kernel<GK, GV, FQK, FV>), dim3(static_cast<unsigned>(kSlices * per_slice)),
+                       dim3(kBlock), 0, s, a, begin, items, chunk, pm, pl, pacc);
+    int64_t blocks = (items * (a.fv / 4) + kBlock - 1) / kBlock;
+    if (blocks > kAttReduceBlocks) blocks = kAttReduceBlocks;
+    hipLaunchKernelGGL(att_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, a, begin, items,
+                       chunk, pm, pl, pacc);
+  }
+}
+
+template <int GK>
+void launch_attention_k(int gv, const AttArgs& a, int64_t upper, int64_t chunk, float* pm, float* pl, float* pacc,
+                        hipStream_t s) {
+  switch (gv) {
+    case 16: launch_attention_t<GK, 16>(a, upper, chunk, pm, pl, pacc, s); break;
+    case 32: launch_attention_t<GK, 32>(a, upper, chunk, pm, pl, pacc, s); break;
+    default: launch_attention_t<GK, 64>(a, upper, chunk, pm, pl, pacc, s); break;
+  }
+}
+
+size_t att_fixed_bytes(int64_t n) {
+  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
+  return align_up(rows * kSliceBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
+         bin_workspace_bytes(n);
+}
+
+// Per sliced row of a chunk: 8 x (m, l, F_v accumulators), fp32.
+size_t att_row_bytes(int64_t fv) { return static_cast<size_t>(kSlices) * (static_cast<size_t>(fv) + 2) * sizeof(float); }
+
+// Upper bound on the sliced rows: degree >= kAttSliceMinDegree.
+int64_t att_sliced_upper(int64_t n, int64_t nnz) {
+  const int64_t u = nnz / kAttSliceMinDegree;
+  return u < n ? u : n;
+}
+
+}  // namespace
+
+}  // namespace as
+
+extern "C" {
+
+size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz, int64_t f_v) {
+  if (n < 0) n = 0;
+  if (nnz < 0) nnz = 0;
+  if (f_v < 4) f_v = 4;
+  int64_t rows = as::att_sliced_upper(n, nnz);
+  if (rows > as::kAttChunkRows) rows = as::kAttChunkRows;
+  if (rows < 1) rows = 1;
+  // + 256 bytes per partial array for alignment
+  return as::att_fixed_bytes(n) + static_cast<size_t>(rows) * as::att_row_bytes(f_v) + 3 * 256;
+}
+
+int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col, const float* query, const float* key,
+                                  const float* value, float* out, int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v,
+                                  float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  as::clear_error();
+  if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
+  if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
+  if (f_qk < 4 || f_qk > 256 || f_qk % 4 != 0 || f_v < 4 || f_v > 256 || f_v % 4 != 0)
+    return as::fail(AS_ERR_UNSUPPORTED, "column-sliced attention needs F_qk and F_v in [4, 256], multiples of 4");
+  if (n == 0) return AS_OK;
+  if (crow == nullptr || query == nullptr || key == nullptr || value == nullptr || out == nullptr ||
+      (nnz > 0 && col == nullptr))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!as::aligned(query, 16) || !as::aligned(key, 16) || !as::aligned(value, 16) || !as::aligned(out, 16))
+    return as::fail(AS_ERR_UNSUPPORTED, "column-sliced attention needs 16-byte aligned Q, K, V and out");
+  const size_t fixed = as::att_fixed_bytes(n);
+  const size_t row_bytes = as::att_row_bytes(f_v);
+  if (workspace == nullptr || workspace_bytes < fixed + row_bytes + 3 * 256)
+    return as::fail(AS_ERR_WORKSPACE, "column-sliced attention needs at least %zu workspace bytes, got %zu",
+                    fixed + row_bytes + 3 * 256, workspace_bytes);
+  if (!as::aligned(workspace, 256)) return as::fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  const int64_t upper = as::att_sliced_upper(n, nnz);
+  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed - 3 * 256) / row_bytes);
+  if (chunk > as::kAttChunkRows) chunk = as::kAttChunkRows;
+  if (chunk > upper) chunk = upper;
+  if (chunk < 1) chunk = 1;
+
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const size_t rows = static_cast<size_t>(n);
+  int32_t* off = reinterpret_cast<int32_t*>(ws);
+  ws += as::align_up(rows * as::kSliceBounds * sizeof(int32_t), 256);
+  int32_t* order = reinterpret_cast<int32_t*>(ws);
+  ws += as::align_up(rows * sizeof(int32_t), 256);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws);
+  ws += 256;
+  void* bin_ws = ws;
+  ws = static_cast<char*>(workspace) + fixed;
+  const size_t states = static_cast<size_t>(as::kSlices) * static_cast<size_t>(chunk);
+  float* pm = reinterpret_cast<float*>(ws);
+  ws += as::align_up(states * sizeof(float), 256);
+  float* pl = reinterpret_cast<float*>(ws);
+  ws += as::align_up(states * sizeof(float), 256);
+  float* pacc = reinterpret_cast<float*>(ws);
+
+  as::launch_slice_points(crow, col, n, as::kAttSliceMinDegree, off, s);
+  // order: rows of degree >= 128 (sliced) longest first, then the others
+  int st = as::launch_bin_rows(crow, n, as::kAttSliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
+  if (st != AS_OK) return st;
+  const as::AttArgs a{crow, col, query, key, value, out, n, f_qk, f_v, scale, order, counts, off};
+  // common widths with compile-time strides
+  if (f_qk == 64 && f_v == 128) {
+    as::launch_attention_t<16, 32, 64, 128>(a, upper, chunk, pm, pl, pacc, s);
+    return as::check_launch("csr_attention_colslice");
+  }
+  if (f_qk == 64 && f_v == 64) {
+    as::launch_attention_t<16, 16, 64, 64>(a, upper, chunk, pm, pl, pacc, s);
+    return as::check_launch("csr_attention_colslice");
+  }
+  if (f_qk == 128 && f_v == 128) {
+    as::launch_attention_t<32, 32, 128, 128>(a, upper, chunk, pm, pl, pacc, s);
+    return as::check_launch("csr_attention_colslice");
+  }
+  switch (as::lane_group(f_qk)) {
+    case 16: as::launch_attention_k<16>(as::lane_group(f_v), a, upper, chunk, pm, pl, pacc, s); break;
+    case 32: as::launch_attention_k<32>(as::lane_group(f_v), a, upper, chunk, pm, pl, pacc, s); break;
+    default: as::launch_attention_k<64>(as::lane_group(f_v), a, upper, chunk, pm, pl, pacc, s); break;
+  }
+  return as::check_launch("csr_attention_colslice");
+}
+
+}  // extern "C"

@@ -31,13 +31,12 @@
 // sequential CSR product: that order is kept by spmm.hip.
 #include "as_device.h"
 #include "as_internal.h"
+#include "colslice_common.h"
 
 namespace as {
 
 namespace {
 
-constexpr int kSlices = 8;                 // one column slice per XCD
-constexpr int kSliceBounds = kSlices - 1;  // inner slice points per row
 constexpr int kColsliceLongRow = 1024;     // slice length from which U = 16
 // Rows shorter than this are not sliced: 8 fp64 partial rows (128·F bytes
 // written and read) cost more than the cache gain on their few gathers.
@@ -48,43 +47,6 @@ constexpr int64_t kColsliceMinDegree = AS_COLSLICE_MIN_DEGREE;
 #ifndef AS_COLSLICE_OVERLAP
 #define AS_COLSLICE_OVERLAP 1
 #endif
-constexpr int64_t kGridStrideBlocks = 65536;
-
-// First column of slice b for an N-column space.
-__device__ __forceinline__ int64_t slice_start(int64_t n_cols, int b) {
-  return (n_cols * b + kSlices - 1) / kSlices;
-}
-
-__global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __restrict__ crow,
-                                                              const int64_t* __restrict__ col, int64_t n,
-                                                              int32_t* __restrict__ off) {
-  const int64_t total = n * kSliceBounds;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
-    const int64_t r = t / kSliceBounds;
-    const int b = static_cast<int>(t - r * kSliceBounds) + 1;
-    const int64_t rs = crow[r];
-    int64_t lo = rs;
-    int64_t hi = crow[r + 1];
-    const int64_t start = slice_start(n, b);
-    while (lo < hi) {
-      const int64_t mid = lo + ((hi - lo) >> 1);
-      if (col[mid] < start) lo = mid + 1;
-      else hi = mid;
-    }
-    off[t] = static_cast<int32_t>(lo - rs);
-  }
-}
-
-// Edge range [a, b) of `slice` in a row of `deg` edges, relative to the row
-// start; clamped to [0, deg] so that no access leaves the row.
-__device__ __forceinline__ void slice_range(const int32_t* __restrict__ off, int64_t row, int slice, int64_t deg,
-                                            int64_t& a, int64_t& b) {
-  a = slice == 0 ? 0 : static_cast<int64_t>(off[row * kSliceBounds + slice - 1]);
-  b = slice == kSlices - 1 ? deg : static_cast<int64_t>(off[row * kSliceBounds + slice]);
-  a = a < 0 ? 0 : (a > deg ? deg : a);
-  b = b < a ? a : (b > deg ? deg : b);
-}
 
 // fp64 partials are written once and read once by the reduction: keep them
 // out of the way of the X rows in the caches.  Rows that are not sliced are
@@ -515,13 +477,7 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
                         reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + chunk * row_bytes)};
 
-  {
-    const int64_t threads = n * as::kSliceBounds;
-    int64_t blocks = (threads + as::kBlock - 1) / as::kBlock;
-    if (blocks > as::kGridStrideBlocks) blocks = as::kGridStrideBlocks;
-    hipLaunchKernelGGL(as::slice_points_kernel, dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s, crow,
-                       col, n, off);
-  }
+  as::launch_slice_points(crow, col, n, as::kColsliceMinDegree, off, s);
   // order: rows of degree >= kColsliceMinDegree (sliced) in 8 log2-degree
   // buckets, longest first; then the short rows in row order
   st = as::launch_bin_rows(crow, n, as::kColsliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);

@@ -458,13 +458,23 @@ def bench_other(args, device) -> dict:
         q = torch.from_numpy(w.dense["q"]).to(device)
         k = torch.from_numpy(w.dense["k"]).to(device)
         v = torch.from_numpy(w.dense["v"]).to(device)
-        step = lambda: torch.ops.autosage.csr_attention(crow, col, q, k, v, 0.125)  # noqa: E731
+        from autosage_amd._native import columns_ascending
+
+        variants = {"fused": lambda: torch.ops.autosage.csr_attention(crow, col, q, k, v, 0.125)}
+        # the column-sliced attention (online softmax per column slice) when
+        # the columns ascend; listed last so that the exact kernel wins a tie
+        if not args.exact_only and columns_ascending(crow, col):
+            variants["colslice"] = lambda: torch.ops.autosage.csr_attention_colslice(crow, col, q, k, v, 0.125)
         calib = {}
-        chosen = "fused"
+        chosen = calibrate(variants, calib) if args.variant == "calibrated" else args.variant
+        if chosen not in variants:
+            raise SystemExit(f"unknown cfg5 variant {chosen!r}: one of {sorted(variants)}")
+        log(f"calibration (ms): {calib}; chosen {chosen}")
+        step = variants[chosen]
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * w.nnz * (64 + 128)
         algo = attention_bytes(w.rows, w.nnz, 64, 128)
-        name = "cfg5 fused CSR attention fp32 Fqk=64 Fv=128 scale=1/8"
+        name = "cfg5 CSR attention fp32 Fqk=64 Fv=128 scale=1/8"
         cpu = None if args.no_cpu_baseline else cpu_baseline_attention(w)
     traffic = profiled_traffic(name, chosen)
     return {

@@ -162,6 +162,28 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Preferred bytes of workspace for as_csr_attention_colslice_f32. */
+size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz,
+                                                 int64_t f_v);
+
+/* Column-sliced attention, an alternative schedule for as_csr_attention_f32
+ * (no reference counterpart; chosen by csr_attention_forward,
+ * autosage/_auto.py:762-780, after a full-graph timing).  Precondition:
+ * columns ascend within every row; f_qk and f_v multiples of 4 in [4, 256];
+ * Q, K, V, out 16-byte aligned.  Rows of degree >= 128 are cut into the 8
+ * column slices (one per XCD) with an online softmax per (row, slice) and
+ * fp32 partial states merged per row; shorter rows run the online softmax in
+ * one wave.  Deterministic; not bit-identical to as_csr_attention_f32.
+ * A workspace smaller than the preferred size (256-byte aligned, at least
+ * the slice points, row order and one row of partial states) runs the sliced
+ * rows in more chunks. */
+int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col,
+                                  const float* query, const float* key,
+                                  const float* value, float* out, int64_t n,
+                                  int64_t nnz, int64_t f_qk, int64_t f_v,
+                                  float scale, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace for the induced-sample entry points (n int32). */
 size_t as_induced_sample_workspace_bytes(int64_t n);
 
