@@ -129,3 +129,11 @@ def test_config5_attention():
     p_ref = oracle.row_softmax(s_crow, oracle.sddmm_ref(s_crow, s_col, q[rows], k) * np.float32(0.125))
     p_got = probs[torch.from_numpy(edges).cuda()].cpu().numpy()
     assert np.all(np.abs(p_got - p_ref) <= ATOL + RTOL * np.abs(p_ref))
+    # the column-sliced attention on the same graph: within the bar of the
+    # fp64 attention on the sampled rows (hubs included), and repeatable
+    del probs, unfused
+    sliced = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, d_q, d_k, d_v, 0.125)
+    assert torch.equal(sliced, torch.ops.autosage.csr_attention_colslice(d_crow, d_col, d_q, d_k, d_v, 0.125))
+    exact = oracle.attention_f64(s_crow, s_col, q[rows], k, v, scale=0.125)
+    got_s = sliced[torch.from_numpy(rows).cuda()].cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got_s - exact) <= ATOL + RTOL * np.abs(exact)), float(np.max(np.abs(got_s - exact)))
