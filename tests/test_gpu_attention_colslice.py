@@ -48,6 +48,9 @@ def test_colslice_attention_against_fp64(fqk, fv):
     d = to_dev(crow, col, q, k, v)
     got = torch.ops.autosage.csr_attention_colslice(*d, 0.125).cpu().numpy()
     _check(got, oracle.attention_f64(crow, col, q, k, v, scale=0.125))
+    # the fp32 reference composition, at the north star's bar too
+    ref = oracle.attention_ref(crow, col, q, k, v, scale=0.125)
+    assert np.all(np.abs(got - ref) <= ATOL + RTOL * np.abs(ref))
     assert np.all(got[np.diff(crow) == 0] == 0)
 
 

@@ -50,6 +50,10 @@ def test_colslice_against_fp64(features, weighted):
     crow, col, val, x = _inputs(features, weighted, seed=features + 3 * weighted)
     got = _colslice(crow, col, val, x).cpu().numpy()
     _assert_fp64_close(got, oracle.spmm_f64(crow, col, val, x))
+    # and against the reference's CPU result (torch.sparse.mm, restated
+    # bit-exactly by the sequential oracle) at the reference's own GPU test
+    # bar (tests/test_cuda.py:40 of the reference: rtol 1e-4, atol 3e-3)
+    assert np.allclose(got, oracle.spmm_seq(crow, col, val, x), rtol=1e-4, atol=3e-3)
 
 
 @pytest.mark.parametrize("features", [512, 1024, 1028])
