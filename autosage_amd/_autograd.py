@@ -6,7 +6,8 @@ backward formulas built from the same native kernels:
 
 * ``Y = A·X`` (A: CSR, weights ``val`` or ones):
   ``dX = Aᵀ·dY`` — a native SpMM over the transposed CSR — and
-  ``dval[e] = <dY[row(e)], X[col(e)]>`` — a native SDDMM.
+  ``dval[e] = <dY[row(e)], X[col(e)]>`` — a native SDDMM;
+  both on the degree-split schedules (same bits as the whole-graph kernels).
 * ``s[e] = <Q[row(e)], K[col(e)]>``:
   ``dQ = A_ds·K`` (SpMM with weights ``ds``) and ``dK = A_dsᵀ·Q``.
 
@@ -53,6 +54,22 @@ def csr_transpose(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, 
     return result
 
 
+# The backward products run on the degree-split schedules: bit-identical to
+# the whole-graph kernels (the SpMM keeps CSR order per output, the SDDMM the
+# reference's dot order), but hub rows are split across waves, which matters
+# on skewed graphs (one wave per 200k-edge row is several times slower).
+_HUB_THRESHOLD = 1024
+
+
+def _spmm(crow, col, val, x):
+    tile = 64 if x.size(1) <= 64 else 128
+    return torch.ops.autosage.spmm_csr_split(crow, col, val, x, tile, 2, _HUB_THRESHOLD)
+
+
+def _sddmm(crow, col, query, key):
+    return torch.ops.autosage.sddmm_csr_split(crow, col, query, key, 4, _HUB_THRESHOLD)
+
+
 def _spmm_setup(ctx, inputs, output) -> None:
     crow, col, val, x = inputs[:4]
     ctx.save_for_backward(crow, col, val, x)
@@ -69,9 +86,9 @@ def _spmm_backward(ctx, grad_y: torch.Tensor):
     if ctx.needs_input_grad[3]:
         crow_t, col_t, perm = csr_transpose(crow, col)
         val_t = None if val is None else val.index_select(0, perm).contiguous()
-        grad_x = torch.ops.autosage.spmm_csr(crow_t, col_t, val_t, grad_y)
+        grad_x = _spmm(crow_t, col_t, val_t, grad_y)
     if val is not None and ctx.needs_input_grad[2]:
-        grad_val = torch.ops.autosage.sddmm_csr(crow, col, grad_y, x)
+        grad_val = _sddmm(crow, col, grad_y, x)
     # one gradient per schema argument (the split op has three int arguments more)
     extra = (None,) * (len(ctx.needs_input_grad) - 4)
     return (None, None, grad_val, grad_x, *extra)
@@ -87,10 +104,10 @@ def _sddmm_backward(ctx, grad_s: torch.Tensor):
     grad_s = grad_s.contiguous()
     grad_q = grad_k = None
     if ctx.needs_input_grad[2]:
-        grad_q = torch.ops.autosage.spmm_csr(crow, col, grad_s, key)
+        grad_q = _spmm(crow, col, grad_s, key)
     if ctx.needs_input_grad[3]:
         crow_t, col_t, perm = csr_transpose(crow, col)
-        grad_k = torch.ops.autosage.spmm_csr(crow_t, col_t, grad_s.index_select(0, perm).contiguous(), query)
+        grad_k = _spmm(crow_t, col_t, grad_s.index_select(0, perm).contiguous(), query)
     extra = (None,) * (len(ctx.needs_input_grad) - 4)
     return (None, None, grad_q, grad_k, *extra)
 
