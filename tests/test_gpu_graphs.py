@@ -1,0 +1,70 @@
+"""The native operators under HIP graph capture (torch.cuda.CUDAGraph).
+
+The kernels take their workspaces from the caller, record no memset and no
+host synchronisation, so a captured call replays the same launches.  The
+per-graph checks (ascending columns) are memoised by an eager call before
+capture.  Every replay is checked against eager results, with eager work and
+synchronisations between replays, and after the inputs change in place."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_common import case_graph, require_gpu, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def test_native_ops_replay_in_a_hip_graph():
+    crow, col = case_graph(6000, 20, seed=4, hubs=12, hub_degree=4000, empty=0.05)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((6000, 128)).astype(np.float32)
+    q = rng.standard_normal((6000, 64)).astype(np.float32)
+    k = rng.standard_normal((6000, 64)).astype(np.float32)
+    d_crow, d_col, d_x, d_q, d_k = to_dev(crow, col, x, q, k)
+    ops = torch.ops.autosage
+    calls = [
+        lambda: ops.spmm_csr(d_crow, d_col, None, d_x),
+        lambda: ops.spmm_csr_split(d_crow, d_col, None, d_x, 128, 2, 1024),
+        lambda: ops.spmm_csr_colslice(d_crow, d_col, None, d_x),
+        lambda: ops.sddmm_csr_split(d_crow, d_col, d_q, d_k, 4, 1024),
+        lambda: ops.csr_attention(d_crow, d_col, d_q, d_k, d_x, 0.125),
+        lambda: ops.csr_attention_colslice(d_crow, d_col, d_q, d_k, d_x, 0.125),
+    ]
+    # eager results, and warm-up on a side stream (default priority) as
+    # graph capture wants
+    eager = [c() for c in calls]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = [c() for c in calls]
+    for replay in range(3):
+        # unrelated eager work and a sync between replays
+        scratch = torch.randn(1 << 20, device="cuda")
+        scratch.mul_(2.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (got, want) in enumerate(zip(captured, eager)):
+            assert torch.equal(got, want), (replay, i)
+    # inputs changed in place: the replay sees them
+    d_x.mul_(2.0)
+    d_q.mul_(0.5)
+    fresh = [c() for c in calls]
+    graph.replay()
+    torch.cuda.synchronize()
+    for i, (got, want) in enumerate(zip(captured, fresh)):
+        assert torch.equal(got, want), i
