@@ -343,6 +343,12 @@ def main() -> int:
             "per_call_ms": [round(s, 4) for s in samples],
             "calibration_ms": calib,
         }
+        exact = {k_: v_ for k_, v_ in calib.items() if k_ != "colslice"}
+        if chosen == "colslice" and exact:
+            # the fastest schedule bit-identical to the reference's CPU result
+            best_exact = min(exact, key=exact.get)
+            result["bit_exact_best"] = {"variant": best_exact, "calibration_ms": exact[best_exact],
+                                        "value": round(flops / (exact[best_exact] * 1e-3) / 1e9, 2)}
         if not args.no_gpu_baseline:
             base, name = _prepare_spmm_baseline(crow, col, val, x)
             bms, _ = time_steps(base, 3, 1)
