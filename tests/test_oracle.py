@@ -223,6 +223,51 @@ def test_attention_composition_against_fp64():
     assert np.allclose(got, exact, rtol=1e-4, atol=1e-5)
 
 
+def test_attention_f64_matches_dense_brute_force():
+    """The fp64 attention the column-sliced kernels are held to, against a
+    dense restatement: an N x N score matrix with -inf off the graph, a
+    row-wise softmax (rows without edges give zeros) and a dense product."""
+    crow, col = _graph(90, 7, seed=8, hubs=2, hub_degree=60, empty=0.1)
+    rng = np.random.default_rng(9)
+    # fp32 inputs (what the kernels take), widened exactly for the dense form
+    q, k, v = (rng.standard_normal(shape).astype(np.float32).astype(np.float64)
+               for shape in ((90, 16), (90, 16), (90, 12)))
+    scores = np.full((90, 90), -np.inf)
+    for r in range(90):
+        for e in range(crow[r], crow[r + 1]):
+            scores[r, col[e]] = 0.5 * (q[r] @ k[col[e]])
+    has = np.isfinite(scores).any(axis=1)
+    p = np.zeros_like(scores)
+    p[has] = np.exp(scores[has] - scores[has].max(axis=1, keepdims=True))
+    p[has] /= p[has].sum(axis=1, keepdims=True)
+    got = oracle.attention_f64(crow, col, q, k, v, scale=0.5)
+    assert np.allclose(got, p @ v, rtol=1e-12, atol=1e-13)
+    assert np.all(got[~has] == 0)
+
+
+def test_attention_f64_closed_forms():
+    # zero scores: every row's output is the mean of its neighbours' V rows
+    crow, col = _graph(60, 5, seed=3, empty=0.2)
+    v = np.random.default_rng(1).standard_normal((60, 8)).astype(np.float32).astype(np.float64)
+    zeros = np.zeros((60, 4))
+    got = oracle.attention_f64(crow, col, zeros, zeros, v)
+    for r in range(60):
+        s, e = crow[r], crow[r + 1]
+        want = v[col[s:e]].mean(axis=0) if e > s else np.zeros(8)
+        assert np.allclose(got[r], want, rtol=1e-13, atol=1e-14)
+    # two edges with scores 1 and 0: weights e/(1+e) and 1/(1+e); a row of
+    # one edge gives that neighbour's V row; an empty row gives zeros
+    crow2 = np.array([0, 2, 3, 3], dtype=np.int64)
+    col2 = np.array([0, 1, 1], dtype=np.int64)
+    q2 = np.array([[1.0], [1.0], [1.0]])
+    k2 = np.array([[1.0], [0.0], [5.0]])
+    v2 = np.array([[4.0], [8.0], [0.0]])
+    got2 = oracle.attention_f64(crow2, col2, q2, k2, v2)
+    e = np.e
+    assert np.isclose(got2[0, 0], (4.0 * e + 8.0) / (1.0 + e), rtol=1e-15)
+    assert got2[1, 0] == 8.0 and got2[2, 0] == 0.0
+
+
 def test_edge_index_to_csr_restatement_matches_package():
     from autosage_amd.utils.csr import edge_index_to_csr
 
