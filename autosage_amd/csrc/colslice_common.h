@@ -1,10 +1,11 @@
 // Column slices shared by the column-sliced SpMM and attention.
 //
-// The column space [0, N) of a square graph is cut into kSlices = 8 equal
-// ranges, one per XCD of an MI355X.  With columns ascending inside every row,
-// the edges of row r in slice s form the contiguous range
-// [crow[r] + off[r·7 + s-1], crow[r] + off[r·7 + s]) (off of slice 0 = 0, of
-// slice 8 = the degree), found once per call by a binary search per
+// The column space [0, N) of a square graph is cut into S equal ranges (S a
+// multiple of kSlices = 8, the XCD count of an MI355X; slice s runs on XCD
+// s % 8).  With columns ascending inside every row, the edges of row r in
+// slice s form the contiguous range
+// [crow[r] + off[r·(S-1) + s-1], crow[r] + off[r·(S-1) + s]) (off of slice 0
+// = 0, of slice S = the degree), found once per call by a binary search per
 // (row, boundary).
 #pragma once
 
@@ -14,29 +15,32 @@
 namespace as {
 namespace {
 
-constexpr int kSlices = 8;                 // one column slice per XCD
-constexpr int kSliceBounds = kSlices - 1;  // inner slice points per row
+constexpr int kSlices = 8;                 // XCDs, and the slices of the attention
+constexpr int kSliceBounds = kSlices - 1;  // inner slice points per row at 8 slices
 constexpr int64_t kGridStrideBlocks = 65536;
 
-// First column of slice b for an N-column space.
+// First column of slice b of S for an N-column space.
+template <int S>
 __device__ __forceinline__ int64_t slice_start(int64_t n_cols, int b) {
-  return (n_cols * b + kSlices - 1) / kSlices;
+  return (n_cols * b + S - 1) / S;
 }
 
 // Rows shorter than `min_degree` are never sliced and keep no slice points.
+template <int S>
 __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __restrict__ crow,
                                                               const int64_t* __restrict__ col, int64_t n,
                                                               int64_t min_degree, int32_t* __restrict__ off) {
-  const int64_t total = n * kSliceBounds;
+  constexpr int kBounds = S - 1;
+  const int64_t total = n * kBounds;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
-    const int64_t r = t / kSliceBounds;
-    const int b = static_cast<int>(t - r * kSliceBounds) + 1;
+    const int64_t r = t / kBounds;
+    const int b = static_cast<int>(t - r * kBounds) + 1;
     const int64_t rs = crow[r];
     int64_t lo = rs;
     int64_t hi = crow[r + 1];
     if (hi - lo < min_degree) continue;
-    const int64_t start = slice_start(n, b);
+    const int64_t start = slice_start<S>(n, b);
     while (lo < hi) {
       const int64_t mid = lo + ((hi - lo) >> 1);
       if (col[mid] < start) lo = mid + 1;
@@ -46,21 +50,23 @@ __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __r
   }
 }
 
+template <int S = kSlices>
 inline void launch_slice_points(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree,
                                 int32_t* off, hipStream_t s) {
-  int64_t blocks = (n * kSliceBounds + kBlock - 1) / kBlock;
+  int64_t blocks = (n * (S - 1) + kBlock - 1) / kBlock;
   if (blocks > kGridStrideBlocks) blocks = kGridStrideBlocks;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(slice_points_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, crow, col, n,
+  hipLaunchKernelGGL(slice_points_kernel<S>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, crow, col, n,
                      min_degree, off);
 }
 
-// Edge range [a, b) of `slice` in a row of `deg` edges, relative to the row
-// start; clamped to [0, deg] so that no access leaves the row.
+// Edge range [a, b) of `slice` (of S) in a row of `deg` edges, relative to
+// the row start; clamped to [0, deg] so that no access leaves the row.
+template <int S = kSlices>
 __device__ __forceinline__ void slice_range(const int32_t* __restrict__ off, int64_t row, int slice, int64_t deg,
                                             int64_t& a, int64_t& b) {
-  a = slice == 0 ? 0 : static_cast<int64_t>(off[row * kSliceBounds + slice - 1]);
-  b = slice == kSlices - 1 ? deg : static_cast<int64_t>(off[row * kSliceBounds + slice]);
+  a = slice == 0 ? 0 : static_cast<int64_t>(off[row * (S - 1) + slice - 1]);
+  b = slice == S - 1 ? deg : static_cast<int64_t>(off[row * (S - 1) + slice]);
   a = a < 0 ? 0 : (a > deg ? deg : a);
   b = b < a ? a : (b > deg ? deg : b);
 }

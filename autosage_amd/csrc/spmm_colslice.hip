@@ -47,6 +47,15 @@ constexpr int64_t kColsliceMinDegree = AS_COLSLICE_MIN_DEGREE;
 #ifndef AS_COLSLICE_OVERLAP
 #define AS_COLSLICE_OVERLAP 1
 #endif
+// Column slices per XCD, worked one after the other: 8·P slices in all, XCD x
+// taking slices x, x + 8, ... in that order, so that at any time an XCD
+// gathers from 1/(8·P) of X.
+#ifndef AS_COLSLICE_PHASES
+#define AS_COLSLICE_PHASES 1
+#endif
+constexpr int kPhases = AS_COLSLICE_PHASES;
+constexpr int kSpmmSlices = kSlices * kPhases;
+constexpr int kSpmmBounds = kSpmmSlices - 1;
 
 // fp64 partials are written once and read once by the reduction: keep them
 // out of the way of the X rows in the caches.  Rows that are not sliced are
@@ -218,10 +227,129 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
   }
 }
 
+// slice_row_wide for 16-lane groups (F <= 64, 4 edges per gather), with
+// less issue work per gather and the same sums in the same order:
+//   * the lane group's column index comes from one ds_bpermute of the 64
+//     indices of the block (instead of 4 readlanes and selects);
+//   * with OFF32 (X smaller than 4 GiB and fewer than 2^24 rows) the X byte
+//     offset is one 24-bit multiply-add and the gather uses the SGPR base
+//     with a 32-bit VGPR offset;
+//   * full batches carry no per-edge liveness test; only the last batch of a
+//     block has one.  A lane group past the end reads the index register of
+//     a lane with no edge in this block, which holds an earlier valid column
+//     (or 0), and does not add what it gathers.
+// On the 115M-edge skewed benchmark graph at F = 64 this takes the call from
+// 2.18 to 2.00 ms; with 32-lane groups (2 edges per gather) the same changes
+// cost about 1 %, so those keep slice_row_wide.
+template <int G, bool HAS_VAL, int U, bool OFF32, typename OutT>
+__device__ __forceinline__ void slice_row_wide_bpermute(const int64_t* __restrict__ col,
+                                                        const float* __restrict__ val, const float* __restrict__ x,
+                                                        OutT* __restrict__ out, int64_t F, int64_t rs, int64_t re,
+                                                        int64_t f0) {
+  constexpr int EPI = kWave / G;
+  constexpr int B = U * EPI;
+  static_assert(kWave % B == 0, "a batch must not straddle a block of 64 column indices");
+  const int lane = lane_id();
+  const int grp = lane / G;
+  const int gl = lane % G;
+  rs = uniform_i64(rs);
+  re = uniform_i64(re);
+  const int64_t fl = f0 + 4 * static_cast<int64_t>(gl);
+  const bool active = fl < F;
+  const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * 4);
+  const uint32_t row_bytes = static_cast<uint32_t>(F * 4);
+  const char* __restrict__ xb = reinterpret_cast<const char*>(x);
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  int next_col = 0;
+  float next_w = 1.f;
+  if (lane < re - rs) {
+    next_col = static_cast<int>(col[rs + lane]);
+    if constexpr (HAS_VAL) next_w = val[rs + lane];
+  }
+  // edges e0 .. e0 + EPI - 1 of the block (e0 uniform), lane group grp
+  // gathers edge e0 + grp
+  auto gather = [&](int my_col, float my_w, int e0, float& w) -> FVec<4> {
+    const int addr = (e0 + grp) * 4;
+    const int c = __builtin_amdgcn_ds_bpermute(addr, my_col);
+    if constexpr (HAS_VAL) w = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(my_w)));
+    if constexpr (OFF32) {
+      const uint32_t off = __umul24(static_cast<uint32_t>(c), row_bytes) + lane_bytes;
+      return *reinterpret_cast<const FVec<4>*>(xb + off);
+    } else {
+      return load_vec_off<4>(x + row_offset(c, F), lane_bytes);
+    }
+  };
+  auto add = [&](const FVec<4>& xv, float w) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if constexpr (HAS_VAL) {
+        acc[v] = __builtin_fma(static_cast<double>(w), static_cast<double>(xv.v[v]), acc[v]);
+      } else {
+        acc[v] = acc[v] + static_cast<double>(xv.v[v]);
+      }
+    }
+  };
+  for (int64_t base = rs; base < re; base += kWave) {
+    const int cnt = static_cast<int>((re - base) < kWave ? (re - base) : kWave);
+    const int my_col = next_col;
+    const float my_w = next_w;
+    const int64_t nb = base + kWave;
+    if (nb < re && lane < re - nb) {
+      next_col = static_cast<int>(col[nb + lane]);
+      if constexpr (HAS_VAL) next_w = val[nb + lane];
+    }
+    int j = 0;
+    for (; j + B <= cnt; j += B) {
+      FVec<4> xv[U];
+      float w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) xv[u] = gather(my_col, my_w, j + u * EPI, w[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) add(xv[u], w[u]);
+    }
+    if (j < cnt) {
+      FVec<4> xv[U];
+      float w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) xv[u] = gather(my_col, my_w, j + u * EPI, w[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u * EPI + grp < cnt) add(xv[u], w[u]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = G; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] += __shfl_xor(acc[v], o, kWave);
+  }
+  if (grp == 0 && active) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) store_out(out + fl + v, acc[v]);
+  }
+}
+
+#ifndef AS_COLSLICE_WIDE_U
+#define AS_COLSLICE_WIDE_U 4
+#endif
+
+template <int G, bool HAS_VAL, bool OFF32, typename OutT>
+__device__ __forceinline__ void slice_wide(const int64_t* __restrict__ col, const float* __restrict__ val,
+                                           const float* __restrict__ x, OutT* __restrict__ out, int64_t F,
+                                           int64_t rs, int64_t re, int64_t f0) {
+  if constexpr (G <= 16) {
+    slice_row_wide_bpermute<G, HAS_VAL, AS_COLSLICE_WIDE_U, OFF32>(col, val, x, out, F, rs, re, f0);
+  } else {
+    slice_row_wide<G, HAS_VAL, AS_COLSLICE_WIDE_U>(col, val, x, out, F, rs, re, f0);
+  }
+}
+
 // One chunk of the slice work: rows order[item_begin, item_begin + items),
-// main block mb of 8·ceil(items / 4)·tiles.  Block mb takes slice mb % 8 and
-// waves (mb / 8)·4 .. +3 of the chunk; the wave for (row, slice) writes the
-// partial of chunk row `local` to partial[(slice·chunk_stride + local)·F ..].
+// main block mb of 8·P·ceil(items / 4)·tiles (P = kPhases).  Within a tile,
+// the blocks of phase p come before those of phase p + 1; a block takes slice
+// 8·p + mb % 8 (so its XCD is mb % 8) and 4 waves of the chunk; the wave for
+// (row, slice) writes the partial of chunk row `local` to
+// partial[(slice·chunk_stride + local)·F ..].
 // V in {1, 2}: narrow lanes (slice_row, all features); V = 16, 32: wide
 // lanes with G = V lanes per edge (slice_row_wide), one feature tile of 4·G
 // features per wave.  Feature tiles are the outermost index: every
@@ -234,7 +362,7 @@ struct SliceChunk {
   double* partial;
 };
 
-template <int V, bool HAS_VAL>
+template <int V, bool HAS_VAL, bool OFF32>
 __device__ __forceinline__ void colslice_main_block(int64_t mb, const int64_t* __restrict__ crow,
                                                     const int64_t* __restrict__ col, const float* __restrict__ val,
                                                     const float* __restrict__ x, float* __restrict__ y, int64_t F,
@@ -242,11 +370,14 @@ __device__ __forceinline__ void colslice_main_block(int64_t mb, const int64_t* _
                                                     const int32_t* __restrict__ counts,
                                                     const int32_t* __restrict__ off, const SliceChunk& c,
                                                     int64_t chunk_stride) {
-  const int64_t tile_blocks = kSlices * ((c.items + kWavesPerBlock - 1) / kWavesPerBlock);
+  const int64_t phase_blocks = kSlices * ((c.items + kWavesPerBlock - 1) / kWavesPerBlock);
+  const int64_t tile_blocks = kPhases * phase_blocks;
   const int64_t tile = mb / tile_blocks;
   const int64_t in_tile = mb - tile * tile_blocks;
-  const int slice = static_cast<int>(in_tile % kSlices);
-  const int64_t local = (in_tile / kSlices) * kWavesPerBlock + wave_in_block();
+  const int64_t phase = in_tile / phase_blocks;
+  const int64_t in_phase = in_tile - phase * phase_blocks;
+  const int slice = static_cast<int>(phase * kSlices + in_phase % kSlices);
+  const int64_t local = (in_phase / kSlices) * kWavesPerBlock + wave_in_block();
   if (local >= c.items) return;
   const int64_t item = c.item_begin + local;
   const int64_t row = uniform_i64(order[item]);
@@ -255,22 +386,22 @@ __device__ __forceinline__ void colslice_main_block(int64_t mb, const int64_t* _
   if (item >= counts[0]) {
     // short row: one wave (of the slice item % 8, to spread them over the
     // XCDs) sums the whole row and writes Y
-    if (item % kSlices != slice) return;
+    if (item % kSpmmSlices != slice) return;
     if constexpr (V >= 16) {
-      slice_row_wide<V, HAS_VAL, 4>(col, val, x, y + row * F, F, rs, rs + deg, tile * 4 * V);
+      slice_wide<V, HAS_VAL, OFF32>(col, val, x, y + row * F, F, rs, rs + deg, tile * 4 * V);
     } else {
       slice_row<V, HAS_VAL, 8>(col, val, x, y + row * F, F, rs, rs + deg);
     }
     return;
   }
   int64_t a, b;
-  slice_range(off, row, slice, deg, a, b);
+  slice_range<kSpmmSlices>(off, row, slice, deg, a, b);
   a = uniform_i64(a);
   b = uniform_i64(b);
   if (a >= b) return;
   double* out = c.partial + (slice * chunk_stride + local) * F;
   if constexpr (V >= 16) {
-    slice_row_wide<V, HAS_VAL, 4>(col, val, x, out, F, rs + a, rs + b, tile * 4 * V);
+    slice_wide<V, HAS_VAL, OFF32>(col, val, x, out, F, rs + a, rs + b, tile * 4 * V);
   } else {
     if (b - a >= kColsliceLongRow) slice_row<V, HAS_VAL, 16>(col, val, x, out, F, rs + a, rs + b);
     else slice_row<V, HAS_VAL, 8>(col, val, x, out, F, rs + a, rs + b);
@@ -300,9 +431,9 @@ __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, con
 #pragma unroll
     for (int v = 0; v < VR; ++v) acc[v] = 0.0;
 #pragma unroll
-    for (int s = 0; s < kSlices; ++s) {
+    for (int s = 0; s < kSpmmSlices; ++s) {
       int64_t a, b;
-      slice_range(off, row, s, deg, a, b);
+      slice_range<kSpmmSlices>(off, row, s, deg, a, b);
       if (a < b) {
         const double* p = c.partial + (s * chunk_stride + local) * F + f;
 #pragma unroll
@@ -323,7 +454,7 @@ __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, con
 // reduction runs beside the latency-bound gathers.  Group g reduces iff
 // floor((g+1)·RG/TG) > floor(g·RG/TG); floor(g·RG/TG) groups before it
 // reduce, so a slice block keeps blockIdx % 8 as its slice.
-template <int V, bool HAS_VAL, int VR>
+template <int V, bool HAS_VAL, int VR, bool OFF32>
 __global__ __launch_bounds__(kBlock) void colslice_step_kernel(const int64_t* __restrict__ crow,
                                                                const int64_t* __restrict__ col,
                                                                const float* __restrict__ val,
@@ -340,18 +471,20 @@ __global__ __launch_bounds__(kBlock) void colslice_step_kernel(const int64_t* __
     colslice_reduce_block<VR>(before * kSlices + within, RG * kSlices, crow, off, order, counts, y, F, r,
                               chunk_stride);
   } else {
-    colslice_main_block<V, HAS_VAL>((g - before) * kSlices + within, crow, col, val, x, y, F, order, counts, off,
+    colslice_main_block<V, HAS_VAL, OFF32>((g - before) * kSlices + within, crow, col, val, x, y, F, order, counts, off,
                                     m, chunk_stride);
   }
 }
 
 size_t colslice_fixed_bytes(int64_t n) {
   const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
-  return align_up(rows * kSliceBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
+  return align_up(rows * kSpmmBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
          bin_workspace_bytes(n);
 }
 
-size_t colslice_row_bytes(int64_t f) { return static_cast<size_t>(kSlices) * static_cast<size_t>(f) * sizeof(double); }
+size_t colslice_row_bytes(int64_t f) {
+  return static_cast<size_t>(kSpmmSlices) * static_cast<size_t>(f) * sizeof(double);
+}
 
 // Rows per chunk when the workspace allows: the pipeline overlaps the
 // reduction of chunk k with the slice work of chunk k + 1, so all but the
@@ -368,37 +501,44 @@ int64_t preferred_chunk_rows(int64_t n) {
   return c > 0 ? c : 1;
 }
 
+template <int V, bool HAS_VAL, int VR, bool OFF32>
+void launch_one(dim3 grid, hipStream_t s, const int64_t* crow, const int64_t* col, const float* val, const float* x,
+                float* y, int64_t f, const int32_t* order, const int32_t* counts, const int32_t* off,
+                const SliceChunk& m, const SliceChunk& r, int64_t stride, int64_t TG, int64_t RG) {
+  hipLaunchKernelGGL((colslice_step_kernel<V, HAS_VAL, VR, OFF32>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
+                     order, counts, off, m, r, stride, TG, RG);
+}
+
+// OFF32 only matters for the wide lanes (V = 16, 32).
 template <bool HAS_VAL, int VR>
-void launch_step_v(int v, dim3 grid, hipStream_t s, const int64_t* crow, const int64_t* col, const float* val,
-                   const float* x, float* y, int64_t f, const int32_t* order, const int32_t* counts,
+void launch_step_v(int v, bool off32, dim3 grid, hipStream_t s, const int64_t* crow, const int64_t* col,
+                   const float* val, const float* x, float* y, int64_t f, const int32_t* order, const int32_t* counts,
                    const int32_t* off, const SliceChunk& m, const SliceChunk& r, int64_t stride, int64_t TG,
                    int64_t RG) {
   switch (v) {
     case 32:
-      hipLaunchKernelGGL((colslice_step_kernel<32, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
-                         order, counts, off, m, r, stride, TG, RG);
+      if (off32) launch_one<32, HAS_VAL, VR, true>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+      else launch_one<32, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
       break;
     case 16:
-      hipLaunchKernelGGL((colslice_step_kernel<16, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
-                         order, counts, off, m, r, stride, TG, RG);
+      if (off32) launch_one<16, HAS_VAL, VR, true>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+      else launch_one<16, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
       break;
     case 2:
-      hipLaunchKernelGGL((colslice_step_kernel<2, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
-                         order, counts, off, m, r, stride, TG, RG);
+      launch_one<2, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
       break;
     default:
-      hipLaunchKernelGGL((colslice_step_kernel<1, HAS_VAL, VR>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
-                         order, counts, off, m, r, stride, TG, RG);
+      launch_one<1, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
       break;
   }
 }
 
 // Launch of slice work `m` (items may be 0) beside the reduction of `r`
 // (items may be 0).
-void launch_step(int v, int vr, bool has_val, int64_t tiles, hipStream_t s, const int64_t* crow, const int64_t* col,
+void launch_step(int v, bool off32, int vr, bool has_val, int64_t tiles, hipStream_t s, const int64_t* crow, const int64_t* col,
                  const float* val, const float* x, float* y, int64_t f, const int32_t* order, const int32_t* counts,
                  const int32_t* off, const SliceChunk& m, const SliceChunk& r, int64_t stride) {
-  const int64_t MG = tiles * ((m.items + kWavesPerBlock - 1) / kWavesPerBlock);  // groups of 8 slice blocks
+  const int64_t MG = tiles * kPhases * ((m.items + kWavesPerBlock - 1) / kWavesPerBlock);  // groups of 8 slice blocks
   int64_t RG = 0;
   if (r.items > 0) {
     // enough reduce blocks for one element per thread, at most a fifth of
@@ -412,11 +552,11 @@ void launch_step(int v, int vr, bool has_val, int64_t tiles, hipStream_t s, cons
   if (TG == 0) return;
   const dim3 grid(static_cast<unsigned>(TG * kSlices));
   if (has_val) {
-    if (vr == 2) launch_step_v<true, 2>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
-    else launch_step_v<true, 1>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    if (vr == 2) launch_step_v<true, 2>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    else launch_step_v<true, 1>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
   } else {
-    if (vr == 2) launch_step_v<false, 2>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
-    else launch_step_v<false, 1>(v, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    if (vr == 2) launch_step_v<false, 2>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    else launch_step_v<false, 1>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
   }
 }
 
@@ -453,6 +593,8 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   if (f % 4 == 0 && as::aligned(x, 16)) v = f <= 64 ? 16 : 32;
   else if (f % 2 == 0 && f > 64 && as::aligned(x, 8)) v = 2;
   const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
+  // every X byte offset fits 32 bits, row index and row bytes fit 24 bits
+  const bool off32 = n <= (int64_t(1) << 24) && f * 4 < (int64_t(1) << 24) && n * f * 4 <= (int64_t(1) << 32);
   const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
 
   // two partial buffers of `chunk` rows each (chunk k writes buffer k % 2)
@@ -460,7 +602,7 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   const int64_t preferred = as::preferred_chunk_rows(n);
   if (chunk > preferred) chunk = preferred;
   // a launch holds at most 5/4 of the slice groups of a chunk
-  const int64_t max_rows = as::kMaxBlocksPerLaunch * 4 / 5 / as::kSlices * as::kWavesPerBlock / tiles;
+  const int64_t max_rows = as::kMaxBlocksPerLaunch * 4 / 5 / as::kSpmmSlices * as::kWavesPerBlock / tiles;
   if (chunk > max_rows) chunk = max_rows;
   if (chunk < 1) return as::fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
 
@@ -468,7 +610,7 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   char* ws = static_cast<char*>(workspace);
   const size_t rows = static_cast<size_t>(n);
   int32_t* off = reinterpret_cast<int32_t*>(ws);
-  ws += as::align_up(rows * as::kSliceBounds * sizeof(int32_t), 256);
+  ws += as::align_up(rows * as::kSpmmBounds * sizeof(int32_t), 256);
   int32_t* order = reinterpret_cast<int32_t*>(ws);
   ws += as::align_up(rows * sizeof(int32_t), 256);
   int32_t* counts = reinterpret_cast<int32_t*>(ws);
@@ -477,7 +619,7 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
   double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
                         reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + chunk * row_bytes)};
 
-  as::launch_slice_points(crow, col, n, as::kColsliceMinDegree, off, s);
+  as::launch_slice_points<as::kSpmmSlices>(crow, col, n, as::kColsliceMinDegree, off, s);
   // order: rows of degree >= kColsliceMinDegree (sliced) in 8 log2-degree
   // buckets, longest first; then the short rows in row order
   st = as::launch_bin_rows(crow, n, as::kColsliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
@@ -490,12 +632,12 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
     as::SliceChunk current{k * chunk, 0, buffers[k % 2]};
     if (k < chunks) current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
 #if AS_COLSLICE_OVERLAP
-    as::launch_step(v, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current, previous,
+    as::launch_step(v, off32, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current, previous,
                     chunk);
 #else
-    as::launch_step(v, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current,
+    as::launch_step(v, off32, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current,
                     as::SliceChunk{0, 0, nullptr}, chunk);
-    as::launch_step(v, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off,
+    as::launch_step(v, off32, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off,
                     as::SliceChunk{0, 0, nullptr}, current, chunk);
 #endif
     previous = current;
