@@ -202,6 +202,9 @@ def _spmm_candidates(crow: torch.Tensor, feature_width: int, config: SchedulerCo
 
 
 COLSLICE = "colslice"  # candidate value of the column-sliced SpMM
+ROUNDED16 = "rounded16"  # candidate value of the bf16 / fp16 SpMM (column slices when the columns ascend)
+ROUNDED16_EDGES = "rounded16:edges"  # the same product with edge slices
+_DTYPES_16 = (torch.bfloat16, torch.float16)
 # Column slicing pays when X is beyond the 8 x 4 MB of L2 and rows are long
 # enough that the per-(row, slice) fp64 partials (128·F bytes per row,
 # written and read) stay small next to the gathers (4·F bytes per edge).
@@ -240,6 +243,8 @@ def _cache_hit_allowed(result: dict[str, Any], config: SchedulerConfig) -> bool:
 def _cached_native_available(operation: str, choice: str, candidate) -> bool:
     if choice != "autosage":
         return True
+    if candidate in (ROUNDED16, ROUNDED16_EDGES):
+        return native_op(operation) is not None
     if candidate == COLSLICE:
         return native_op(operation + "_colslice") is not None
     return native_op(operation + ("_split" if candidate is not None else "")) is not None
@@ -257,6 +262,12 @@ def _cpu_info(operation: str) -> dict[str, Any]:
 
 
 def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
+    if choice == "autosage" and candidate == ROUNDED16:
+        return native_op("spmm_csr")(crow, col, val, x)
+    if choice == "autosage" and candidate == ROUNDED16_EDGES:
+        from ._native import spmm_rounded_16_impl
+
+        return spmm_rounded_16_impl(crow, col, val, x, column_slices=False)
     if choice == "autosage" and candidate == COLSLICE:
         from ._native import columns_ascending
 
@@ -380,7 +391,7 @@ def _verbose(tag: str, result: dict[str, Any], verbose: bool) -> None:
     if verbose or os.getenv("AUTOSAGE_VERBOSE") == "1":
         print(
             f"[autosage:{tag}] rows={result['probe_rows']} nnz={result['probe_nonzeros']} "
-            f"baseline={result['baseline_probe_ms']:.4f} ms auto={result['autosage_probe_ms']} "
+            f"baseline={result['baseline_probe_ms']} ms auto={result['autosage_probe_ms']} "
             f"choice={result['choice']}"
         )
 
@@ -399,6 +410,10 @@ def spmm_csr_auto(
     crow, col, val, x = _normalize_csr(crow, col, val, x)
     if not x.is_cuda:
         return spmm_csr(crow, col, val, x), _cpu_info("spmm")
+    if x.dtype in _DTYPES_16:
+        _require_native()
+        return _spmm_auto_16(crow, col, val, x, SchedulerConfig.from_env(guardrail=guardrail, candidate_count=k),
+                             verbose)
     if x.dtype != torch.float32:
         run, name = _prepare_spmm_baseline(crow, col, val, x)
         return run(), {**_cpu_info("spmm"), "baseline": name, "reason": "AutoSAGE CUDA kernels require float32 features"}
@@ -451,6 +466,71 @@ def spmm_csr_auto(
         colslice = _colslice_eligible(crow, col, x, config)
         _confirm_spmm_on_full_graph(result, colslice, config, probe, crow, col, val, x)
     output = _run_spmm_choice(result["choice"], result["candidate"], crow, col, val, x)
+    if config.cache:
+        cache.store(device, graph, result)
+    log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})
+    _verbose("spmm", result, verbose)
+    return output, result
+
+
+# torch.sparse.mm on a bf16 CSR tensor aborts the process on PyTorch-ROCm
+# 2.10 (inside the sparse library, uncatchable from Python); fp16 is not
+# called for the same reason.  The 16-bit scheduler therefore never runs it.
+_BASELINE_16_NOTE = "torch.sparse.mm on bf16/fp16 CSR is not run: it aborts the process on PyTorch-ROCm"
+
+
+def _spmm_auto_16(crow, col, val, x, config: SchedulerConfig, verbose: bool) -> tuple[torch.Tensor, dict[str, Any]]:
+    """bf16 / fp16 features (the reference runs torch.sparse.mm for them,
+    ``_auto.py:281-287``).  Every output is the exactly rounded sum whatever
+    the schedule, so there is no shortlist to probe and no accuracy trade:
+    the two slicings of the native SpMM (column slices, when the columns
+    ascend, and edge slices) are timed once on the full graph and the faster
+    is cached under the usual key, which includes the dtype.  The PyTorch
+    baseline cannot be run for these types here (see _BASELINE_16_NOTE)."""
+    device = device_signature()
+    graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
+    cache = ScheduleCache()
+    if config.cache:
+        record = cache.lookup(device, graph)
+        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
+            result = record["result"]
+            if result.get("candidate") in (ROUNDED16, ROUNDED16_EDGES):
+                return (_run_spmm_choice("autosage", result["candidate"], crow, col, val, x),
+                        {**result, "from_cache": True})
+    if config.replay_only:
+        info = _replay_miss("spmm", "torch.sparse.mm(csr)")
+        info.update(choice="autosage", candidate=ROUNDED16, reason="cache miss; " + _BASELINE_16_NOTE)
+        return _run_spmm_choice("autosage", ROUNDED16, crow, col, val, x), info
+    from ._native import columns_ascending
+
+    wall_start = time.perf_counter()
+    options = [ROUNDED16_EDGES] + ([ROUNDED16] if columns_ascending(crow, col) else [])
+    times = {
+        o: _time_cuda(lambda o=o: _run_spmm_choice("autosage", o, crow, col, val, x), warmup=1, iterations=3)[
+            "best_ms"]
+        for o in options
+    }
+    best = min(options, key=lambda o: times[o])
+    result: dict[str, Any] = {
+        "operation": "spmm",
+        "schema_version": AUTOTUNE_SCHEMA_VERSION,
+        "choice": "autosage",
+        "candidate": best,
+        "baseline": "torch.sparse.mm(csr)",
+        "guardrail": config.guardrail,
+        "configuration": config.tuning_signature(),
+        "probe_rows": int(crow.numel() - 1),
+        "probe_nonzeros": int(col.numel()),
+        "sampling_ms": 0.0,
+        "probe_ms": (time.perf_counter() - wall_start) * 1000.0,
+        "baseline_probe_ms": None,
+        "autosage_probe_ms": times[best],
+        "sampled_speedup": None,
+        "candidates": [{"candidate": o, "best_ms": times[o]} for o in options],
+        "from_cache": False,
+        "reason": _BASELINE_16_NOTE,
+    }
+    output = _run_spmm_choice("autosage", best, crow, col, val, x)
     if config.cache:
         cache.store(device, graph, result)
     log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})

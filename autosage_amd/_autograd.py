@@ -8,6 +8,8 @@ backward formulas built from the same native kernels:
   ``dX = Aᵀ·dY`` — a native SpMM over the transposed CSR — and
   ``dval[e] = <dY[row(e)], X[col(e)]>`` — a native SDDMM;
   both on the degree-split schedules (same bits as the whole-graph kernels).
+  With bf16 / fp16 features ``dX`` comes from the rounded 16-bit SpMM; the
+  weight gradient would need a 16-bit SDDMM and raises.
 * ``s[e] = <Q[row(e)], K[col(e)]>``:
   ``dQ = A_ds·K`` (SpMM with weights ``ds``) and ``dK = A_dsᵀ·Q``.
 
@@ -62,6 +64,9 @@ _HUB_THRESHOLD = 1024
 
 
 def _spmm(crow, col, val, x):
+    if x.dtype != torch.float32:
+        # bf16 / fp16: the rounded SpMM, the same bits on any schedule
+        return torch.ops.autosage.spmm_csr(crow, col, val, x)
     tile = 64 if x.size(1) <= 64 else 128
     return torch.ops.autosage.spmm_csr_split(crow, col, val, x, tile, 2, _HUB_THRESHOLD)
 
@@ -88,6 +93,8 @@ def _spmm_backward(ctx, grad_y: torch.Tensor):
         val_t = None if val is None else val.index_select(0, perm).contiguous()
         grad_x = _spmm(crow_t, col_t, val_t, grad_y)
     if val is not None and ctx.needs_input_grad[2]:
+        if x.dtype != torch.float32:
+            raise NotImplementedError("the weight gradient of a bf16/fp16 SpMM is not implemented")
         grad_val = _sddmm(crow, col, grad_y, x)
     # one gradient per schema argument (the split op has three int arguments more)
     extra = (None,) * (len(ctx.needs_input_grad) - 4)

@@ -28,9 +28,11 @@ from typing import Optional
 import torch
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
+# 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
+DTYPES_16 = {torch.bfloat16: 1, torch.float16: 2}
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -58,7 +60,13 @@ _SIGNATURES = {
     "as_csr_row_softmax_f32": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr]),
     "as_spmm_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "as_spmm_csr_colslice_f32": (
-        _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr]
+        _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_i64, _c_ptr]
+    ),
+    "as_spmm_colslice_min_degree": (_c_i64, [_c_int]),
+    "as_spmm_csr_rounded_16": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_i64,
+         _c_ptr],
     ),
     "as_csr_attention_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_csr_attention_colslice_f32": (
@@ -152,7 +160,7 @@ def _check(cond: bool, message: str) -> None:
         raise RuntimeError(message)
 
 
-def check_spmm_inputs(crow, col, val, x) -> None:
+def check_spmm_inputs(crow, col, val, x, allow_16: bool = False) -> None:
     _check(crow.is_cuda and col.is_cuda and x.is_cuda, "crow, col, and x must be CUDA tensors")
     _check(crow.dtype == torch.long and col.dtype == torch.long, "crow and col must use torch.long indices")
     _check(crow.dim() == 1 and col.dim() == 1, "crow and col must be one-dimensional")
@@ -160,10 +168,13 @@ def check_spmm_inputs(crow, col, val, x) -> None:
     _check(crow.is_contiguous() and col.is_contiguous(), "crow and col must be contiguous")
     _check(crow.device == x.device and col.device == x.device, "crow, col, and x must be on the same CUDA device")
     _check(crow.numel() == x.size(0) + 1, "crow must contain N + 1 entries")
-    _check(x.dtype == torch.float32, "x must be float32")
+    if allow_16:
+        _check(x.dtype == torch.float32 or x.dtype in DTYPES_16, "x must be float32, bfloat16 or float16")
+    else:
+        _check(x.dtype == torch.float32, "x must be float32")
     if val is not None:
         _check(val.is_cuda and val.device == x.device, "val must be on the same CUDA device as x")
-        _check(val.dtype == torch.float32 and val.is_contiguous(), "val must be contiguous float32")
+        _check(val.dtype == x.dtype and val.is_contiguous(), "val must be contiguous and of x's dtype")
         _check(val.numel() == col.numel(), "val must contain one weight per nonzero")
 
 
@@ -193,8 +204,10 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
 
 def spmm_csr_impl(crow, col, val, x):
-    check_spmm_inputs(crow, col, val, x)
+    check_spmm_inputs(crow, col, val, x, allow_16=True)
     _maybe_validate(crow, col)
+    if x.dtype in DTYPES_16:
+        return spmm_rounded_16_impl(crow, col, val, x, column_slices=columns_ascending(crow, col))
     y = torch.empty_like(x)
     n, f = x.shape
     if n == 0 or f == 0:
@@ -236,10 +249,12 @@ def _colslice_workspace_cap() -> int:
 def spmm_csr_colslice_impl(crow, col, val, x):
     """Column-sliced SpMM (fp64 accumulation, one column slice per XCD).
     Needs columns ascending within every row; checked once per graph."""
-    check_spmm_inputs(crow, col, val, x)
+    check_spmm_inputs(crow, col, val, x, allow_16=True)
     _maybe_validate(crow, col)
     if not columns_ascending(crow, col):
         raise ValueError("spmm_csr_colslice requires column indices ascending within every row")
+    if x.dtype in DTYPES_16:
+        return spmm_rounded_16_impl(crow, col, val, x, column_slices=True)
     y = torch.empty_like(x)
     n, f = x.shape
     if n == 0 or f == 0:
@@ -252,9 +267,31 @@ def spmm_csr_colslice_impl(crow, col, val, x):
     with torch.cuda.device(x.device):
         status = lib.as_spmm_csr_colslice_f32(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, _ptr(ws), ws.numel(),
-            _stream(x.device),
+            sliced_rows(crow, True), _stream(x.device),
         )
     _raise(status, "autosage::spmm_csr_colslice")
+    return y
+
+
+def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
+    """SpMM on bf16/fp16 features (weights of the same type): every output is
+    the fp64 sum of the exact products rounded to fp32 and then to x's dtype,
+    the same bits whatever the schedule.  ``column_slices``: one column slice
+    per XCD (columns must ascend within rows); otherwise rows of degree >= 1024
+    are cut into 8 equal runs of edges."""
+    y = torch.empty_like(x)
+    n, f = x.shape
+    if n == 0 or f == 0:
+        return y
+    lib = library()
+    full = lib.as_spmm_colslice_workspace_bytes(n, f)
+    ws = _workspace(min(full, _colslice_workspace_cap()), x.device)
+    with torch.cuda.device(x.device):
+        status = lib.as_spmm_csr_rounded_16(
+            _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, DTYPES_16[x.dtype],
+            int(bool(column_slices)), _ptr(ws), ws.numel(), sliced_rows(crow, column_slices), _stream(x.device),
+        )
+    _raise(status, "autosage::spmm_csr (16-bit)")
     return y
 
 
@@ -451,6 +488,32 @@ def columns_ascending(crow: torch.Tensor, col: torch.Tensor) -> bool:
         while len(_SORTED_MEMO) > _SORTED_MEMO_SIZE:
             _SORTED_MEMO.popitem(last=False)
     return result
+
+
+_SLICED_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+
+
+def sliced_rows(crow: torch.Tensor, column_slices: bool) -> int:
+    """Rows the column-sliced SpMM slices (degree >= its threshold): a
+    per-graph constant that sizes its launches, computed once per live,
+    unmodified ``crow`` (one host sync) and memoised."""
+    threshold = int(library().as_spmm_colslice_min_degree(int(bool(column_slices))))
+    key = (id(crow), crow._version, threshold)
+    with _SORTED_LOCK:
+        hit = _SLICED_MEMO.get(key)
+        if hit is not None and hit[0]() is crow:
+            _SLICED_MEMO.move_to_end(key)
+            return hit[1]
+    count = int(((crow[1:] - crow[:-1]) >= threshold).sum().item())
+    try:
+        ref = weakref.ref(crow)
+    except TypeError:
+        return count
+    with _SORTED_LOCK:
+        _SLICED_MEMO[key] = (ref, count)
+        while len(_SLICED_MEMO) > _SORTED_MEMO_SIZE:
+            _SLICED_MEMO.popitem(last=False)
+    return count
 
 
 def _maybe_validate(crow: torch.Tensor, col: torch.Tensor) -> None:

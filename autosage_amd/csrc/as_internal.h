@@ -30,7 +30,7 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 
 // Argument checks shared by the SpMM entry points (n, F < 2^31: kernels use
 // 32-bit row and feature indices).
-inline int validate_spmm(const int64_t* crow, const int64_t* col, const float* x, float* y, int64_t n,
+inline int validate_spmm(const int64_t* crow, const int64_t* col, const void* x, const void* y, int64_t n,
                          int64_t nnz, int64_t f) {
   if (n < 0 || n > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
   if (f < 0 || f > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "F exceeds kernel index range");

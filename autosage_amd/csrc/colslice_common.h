@@ -26,10 +26,13 @@ __device__ __forceinline__ int64_t slice_start(int64_t n_cols, int b) {
 }
 
 // Rows shorter than `min_degree` are never sliced and keep no slice points.
+// by_edges: slice b of a row of d edges starts at edge floor(d·b / S) (equal
+// runs of edges, for graphs whose columns do not ascend).
 template <int S>
 __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __restrict__ crow,
                                                               const int64_t* __restrict__ col, int64_t n,
-                                                              int64_t min_degree, int32_t* __restrict__ off) {
+                                                              int64_t min_degree, int32_t* __restrict__ off,
+                                                              bool by_edges) {
   constexpr int kBounds = S - 1;
   const int64_t total = n * kBounds;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -40,6 +43,10 @@ __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __r
     int64_t lo = rs;
     int64_t hi = crow[r + 1];
     if (hi - lo < min_degree) continue;
+    if (by_edges) {
+      off[t] = static_cast<int32_t>((hi - lo) * b / S);
+      continue;
+    }
     const int64_t start = slice_start<S>(n, b);
     while (lo < hi) {
       const int64_t mid = lo + ((hi - lo) >> 1);
@@ -52,12 +59,12 @@ __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __r
 
 template <int S = kSlices>
 inline void launch_slice_points(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree,
-                                int32_t* off, hipStream_t s) {
+                                int32_t* off, hipStream_t s, bool by_edges = false) {
   int64_t blocks = (n * (S - 1) + kBlock - 1) / kBlock;
   if (blocks > kGridStrideBlocks) blocks = kGridStrideBlocks;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(slice_points_kernel<S>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, crow, col, n,
-                     min_degree, off);
+                     min_degree, off, by_edges);
 }
 
 // Edge range [a, b) of `slice` (of S) in a row of `deg` edges, relative to

@@ -1,5 +1,5 @@
-// Column-sliced SpMM Y = A·X for graphs whose columns ascend within every
-// row (fp32 in and out, fp64 accumulation).
+// Column-sliced SpMM Y = A·X (fp32, bf16 or fp16 in and out, fp64
+// accumulation).
 //
 // Why.  An MI355X has 8 XCDs, each with its own 4 MB L2; the X-row gathers
 // that miss it cross the fabric to the 256 MB MALL or HBM.  When one kernel
@@ -14,21 +14,32 @@
 // Steps.
 //   1. Slice points: off[r·7 + b-1] = index, relative to crow[r], of the first
 //      edge of row r whose column is >= the first column of slice b (a binary
-//      search, valid because columns ascend within the row).
-//   2. Degree order: rows of degree >= 128 in log2-degree buckets, longest
-//      first (the binning kernel of the split SpMM), then the shorter rows.
+//      search, valid because columns ascend within the row).  For 16-bit
+//      features on graphs whose columns do not ascend, the slices are instead
+//      8 equal runs of edges (no cache benefit, but long rows still spread
+//      over 8 waves).
+//   2. Degree order: rows of degree >= the slicing threshold in log2-degree
+//      buckets, longest first (the binning kernel of the split SpMM), then
+//      the shorter rows.
 //   3. For each chunk of rows of that order: the slice kernel, one wave per
 //      (row, slice), writes the fp64 partial sum of the row's edges in the
 //      slice; the reduction kernel adds the non-empty partials of each row in
-//      slice order in fp64 and rounds once to fp32.  A row shorter than 128
-//      is summed whole by one wave (in fp64, rounded once) that writes Y:
-//      its 8 partials would cost more traffic than slicing saves.
+//      slice order in fp64 and rounds once.  A shorter row is summed whole by
+//      one wave (in fp64, rounded once) that writes Y: its 8 partials would
+//      cost more traffic than slicing saves.
 //
 // Arithmetic.  Products w·x of fp32 values are exact in fp64 and every
 // partial and the final sum are fp64 additions, so each output is within
 // about one fp32 rounding of the exact sum (tighter than a sequential fp32
 // sum), and the result is deterministic.  It is not bit-identical to the
-// sequential CSR product: that order is kept by spmm.hip.
+// sequential CSR product: that order is kept by spmm.hip.  With bf16 or fp16
+// elements (weights rounded to the same type) the products are exact and the
+// fp64 sums carry ~2^-53 relative error, so the result rounded to fp32 and
+// then to the element type (round to nearest even both times) is the same
+// whatever the order of the additions: every schedule here gives the same
+// bits, those of an fp64 sum in CSR order rounded the same way.
+#include <type_traits>
+
 #include "as_device.h"
 #include "as_internal.h"
 #include "colslice_common.h"
@@ -44,6 +55,9 @@ constexpr int kColsliceLongRow = 1024;     // slice length from which U = 16
 #define AS_COLSLICE_MIN_DEGREE 128
 #endif
 constexpr int64_t kColsliceMinDegree = AS_COLSLICE_MIN_DEGREE;
+// With slices by edge count there is no cache gain, only the spread of long
+// rows over 8 waves.
+constexpr int64_t kEdgeSliceMinDegree = 1024;
 #ifndef AS_COLSLICE_OVERLAP
 #define AS_COLSLICE_OVERLAP 1
 #endif
@@ -57,28 +71,138 @@ constexpr int kPhases = AS_COLSLICE_PHASES;
 constexpr int kSpmmSlices = kSlices * kPhases;
 constexpr int kSpmmBounds = kSpmmSlices - 1;
 
+// ---- element types ---------------------------------------------------------
+// X, the weights and Y share one element type.  bf16 and fp16 values are held
+// as raw 16-bit words; every element converts exactly to fp32 and fp64.
+struct Bf16 {
+  uint16_t bits;
+};
+struct Fp16 {
+  uint16_t bits;
+};
+
+// fp32 -> bf16, round to nearest even; NaN -> the quiet NaN 0x7fc0.
+__device__ __forceinline__ uint16_t bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// fp32 -> fp16, round to nearest even, from the IEEE formats: 16 bits of
+// integer work on the fp32 bits.  Written out because the compiler merges a
+// float -> half conversion that follows a double -> float one into a single
+// double -> half rounding, which decides ties differently.
+__device__ __forceinline__ uint16_t f16_bits(float f) {
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return static_cast<uint16_t>(sign | 0x7e00u);  // NaN
+  if (ax >= 0x477ff000u) return static_cast<uint16_t>(sign | 0x7c00u);  // >= 65520 rounds to inf
+  if (ax < 0x38800000u) {
+    // below 2^-14: a multiple of 2^-24; the scaling by 2^24 is exact and
+    // rintf rounds half to even (1024 encodes 2^-14, the smallest normal)
+    const float units = __uint_as_float(ax) * 16777216.0f;
+    return static_cast<uint16_t>(sign | static_cast<uint32_t>(__builtin_rintf(units)));
+  }
+  uint32_t r = ax - (112u << 23);    // exponent bias 127 -> 15
+  r += 0x0fffu + ((r >> 13) & 1u);   // round the 13 dropped bits half to even
+  return static_cast<uint16_t>(sign | (r >> 13));
+}
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  // element p of consecutive raw little-endian 32-bit words
+  __device__ static float get(const uint32_t* w, int p) { return __uint_as_float(w[p]); }
+  __device__ static float at(const float* p, int64_t i) { return p[i]; }
+  __device__ static void put(float* p, double v) { *p = static_cast<float>(v); }
+};
+template <>
+struct Elem<Bf16> {
+  __device__ static float get(const uint32_t* w, int p) {
+    const uint32_t x = w[p >> 1];
+    return __uint_as_float((p & 1) ? (x & 0xffff0000u) : (x << 16));
+  }
+  __device__ static float at(const Bf16* p, int64_t i) { return __uint_as_float(uint32_t(p[i].bits) << 16); }
+  __device__ static uint16_t bits(double v) { return bf16_bits(static_cast<float>(v)); }
+  __device__ static void put(Bf16* p, double v) { p->bits = bits(v); }
+};
+template <>
+struct Elem<Fp16> {
+  __device__ static float get(const uint32_t* w, int p) {
+    const uint32_t x = w[p >> 1];
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((p & 1) ? (x >> 16) : x)));
+  }
+  __device__ static float at(const Fp16* p, int64_t i) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, p[i].bits));
+  }
+  __device__ static uint16_t bits(double v) { return f16_bits(static_cast<float>(v)); }
+  __device__ static void put(Fp16* p, double v) { p->bits = bits(v); }
+};
+
+// BYTES consecutive bytes (2, 4, 8 or 16, naturally aligned) as 32-bit words;
+// a 2-byte load fills the low half of w[0].
+template <int BYTES>
+struct RawVec {
+  uint32_t w[BYTES >= 4 ? BYTES / 4 : 1];
+};
+template <int BYTES>
+__device__ __forceinline__ RawVec<BYTES> load_raw(const char* p) {
+  RawVec<BYTES> r;
+  if constexpr (BYTES == 2) {
+    r.w[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else {
+    const FVec<BYTES / 4> v = *reinterpret_cast<const FVec<BYTES / 4>*>(p);
+#pragma unroll
+    for (int i = 0; i < BYTES / 4; ++i) r.w[i] = __float_as_uint(v.v[i]);
+  }
+  return r;
+}
+
 // fp64 partials are written once and read once by the reduction: keep them
 // out of the way of the X rows in the caches.  Rows that are not sliced are
 // rounded once and written to Y.
 __device__ __forceinline__ void store_out(double* p, double v) { __builtin_nontemporal_store(v, p); }
-__device__ __forceinline__ void store_out(float* p, double v) { *p = static_cast<float>(v); }
+template <typename T>
+__device__ __forceinline__ void store_out(T* p, double v) {
+  Elem<T>::put(p, v);
+}
+
+// VR consecutive outputs of Y, rounded once.
+template <typename T, int VR>
+__device__ __forceinline__ void store_elems(T* p, const double (&v)[VR]) {
+  if constexpr (std::is_same<T, float>::value) {
+    FVec<VR> o;
+#pragma unroll
+    for (int i = 0; i < VR; ++i) o.v[i] = static_cast<float>(v[i]);
+    store_vec<VR>(p, o);
+  } else if constexpr (VR == 2) {
+    *reinterpret_cast<uint32_t*>(p) = uint32_t(Elem<T>::bits(v[0])) | (uint32_t(Elem<T>::bits(v[1])) << 16);
+  } else {
+    p->bits = Elem<T>::bits(v[0]);
+  }
+}
 
 // One wave sums edges [rs, re) of a row into out[0, F) in fp64 (F not a
-// multiple of 4, or X not 16-byte aligned).  Same lane layout as the exact
-// wave-row kernel: lane owns V consecutive features,
+// multiple of the wide-lane width, or X not 16-byte aligned).  Same lane
+// layout as the exact wave-row kernel: lane owns V consecutive features,
 // 64 column indices per coalesced load (one chunk ahead), broadcast through
 // SGPRs, U gathers in flight.
-template <int V, bool HAS_VAL, int U, typename OutT>
-__device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const float* __restrict__ val,
-                                          const float* __restrict__ x, OutT* __restrict__ out, int64_t F,
-                                          int64_t rs, int64_t re) {
+template <typename T, int V, bool HAS_VAL, int U, typename OutT>
+__device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const T* __restrict__ val,
+                                          const T* __restrict__ x, OutT* __restrict__ out, int64_t F, int64_t rs,
+                                          int64_t re) {
+  constexpr int kBytes = V * static_cast<int>(sizeof(T));
   const int lane = lane_id();
+  const char* __restrict__ xb = reinterpret_cast<const char*>(x);
   rs = uniform_i64(rs);
   re = uniform_i64(re);
   for (int64_t f0 = 0; f0 < F; f0 += kWave * V) {
     const int64_t fl = f0 + static_cast<int64_t>(lane) * V;
     const bool active = fl < F;
-    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : 0) * 4);
+    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : 0) * sizeof(T));
     double acc[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.0;
@@ -86,8 +210,19 @@ __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const
     float next_w = 1.f;
     if (lane < re - rs) {
       next_col = static_cast<int>(col[rs + lane]);
-      if constexpr (HAS_VAL) next_w = val[rs + lane];
+      if constexpr (HAS_VAL) next_w = Elem<T>::at(val, rs + lane);
     }
+    auto add = [&](const RawVec<kBytes>& xv, float w) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const double xe = static_cast<double>(Elem<T>::get(xv.w, v));
+        if constexpr (HAS_VAL) {
+          acc[v] = __builtin_fma(static_cast<double>(w), xe, acc[v]);
+        } else {
+          acc[v] = acc[v] + xe;
+        }
+      }
+    };
     for (int64_t base = rs; base < re; base += kWave) {
       const int cnt = static_cast<int>((re - base) < kWave ? (re - base) : kWave);
       const int my_col = next_col;
@@ -95,42 +230,25 @@ __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const
       const int64_t nb = base + kWave;
       if (nb < re && lane < re - nb) {
         next_col = static_cast<int>(col[nb + lane]);
-        if constexpr (HAS_VAL) next_w = val[nb + lane];
+        if constexpr (HAS_VAL) next_w = Elem<T>::at(val, nb + lane);
       }
       int j = 0;
       for (; j + U <= cnt; j += U) {
-        FVec<V> xv[U];
+        RawVec<kBytes> xv[U];
         float w[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int c = bcast_i32(my_col, j + u);
           w[u] = HAS_VAL ? bcast_f32(my_w, j + u) : 1.f;
-          xv[u] = load_vec_off<V>(x + row_offset(c, F), lane_bytes);
+          xv[u] = load_raw<kBytes>(xb + row_offset(c, F) * sizeof(T) + lane_bytes);
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            if constexpr (HAS_VAL) {
-              acc[v] = __builtin_fma(static_cast<double>(w[u]), static_cast<double>(xv[u].v[v]), acc[v]);
-            } else {
-              acc[v] = acc[v] + static_cast<double>(xv[u].v[v]);
-            }
-          }
-        }
+        for (int u = 0; u < U; ++u) add(xv[u], w[u]);
       }
       for (; j < cnt; ++j) {
         const int c = bcast_i32(my_col, j);
-        const FVec<V> xv = load_vec_off<V>(x + row_offset(c, F), lane_bytes);
-        const float w = HAS_VAL ? bcast_f32(my_w, j) : 1.f;
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          if constexpr (HAS_VAL) {
-            acc[v] = __builtin_fma(static_cast<double>(w), static_cast<double>(xv.v[v]), acc[v]);
-          } else {
-            acc[v] = acc[v] + static_cast<double>(xv.v[v]);
-          }
-        }
+        const RawVec<kBytes> xv = load_raw<kBytes>(xb + row_offset(c, F) * sizeof(T) + lane_bytes);
+        add(xv, HAS_VAL ? bcast_f32(my_w, j) : 1.f);
       }
     }
     if (active) {
@@ -140,33 +258,38 @@ __device__ __forceinline__ void slice_row(const int64_t* __restrict__ col, const
   }
 }
 
-// Wide form of slice_row for F % 4 == 0 and 16-byte aligned X: G lanes per
-// edge, each lane owning 4 consecutive features (a float4 load), so that one
-// gather instruction fetches 64/G = EPI edges.  Gathers that hit L2 run at
-// twice the bytes per instruction of 8-byte lanes (four times of 4-byte
-// lanes).  Lane group k takes edges j + k, j + EPI + k, ... and keeps its own
-// fp64 sums; the groups are added at the end in a fixed butterfly order.
-// One call covers the feature tile [f0, f0 + 4·G).
-template <int G, bool HAS_VAL, int U, typename OutT>
-__device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, const float* __restrict__ val,
-                                               const float* __restrict__ x, OutT* __restrict__ out, int64_t F,
+// Wide form of slice_row for F a multiple of P and 16-byte aligned X: G lanes
+// per edge, each lane owning P = 16 / sizeof(T) consecutive features (one
+// 16-byte load: 4 fp32 or 8 bf16 / fp16), so that one gather instruction
+// fetches 64/G = EPI edges.  Gathers that hit L2 run at twice the bytes per
+// instruction of 8-byte lanes (four times of 4-byte lanes).  Lane group k
+// takes edges j + k, j + EPI + k, ... and keeps its own fp64 sums; the groups
+// are added at the end in a fixed butterfly order.  One call covers the
+// feature tile [f0, f0 + P·G).
+template <typename T, int G, bool HAS_VAL, int U, typename OutT>
+__device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, const T* __restrict__ val,
+                                               const T* __restrict__ x, OutT* __restrict__ out, int64_t F,
                                                int64_t rs, int64_t re, int64_t f0) {
+  constexpr int P = 16 / static_cast<int>(sizeof(T));
   constexpr int EPI = kWave / G;
   const int lane = lane_id();
   const int grp = lane / G;
   const int gl = lane % G;
+  const char* __restrict__ xb = reinterpret_cast<const char*>(x);
   rs = uniform_i64(rs);
   re = uniform_i64(re);
   {
-    const int64_t fl = f0 + 4 * static_cast<int64_t>(gl);
+    const int64_t fl = f0 + P * static_cast<int64_t>(gl);
     const bool active = fl < F;
-    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * 4);
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * sizeof(T));
+    double acc[P];
+#pragma unroll
+    for (int v = 0; v < P; ++v) acc[v] = 0.0;
     int next_col = 0;
     float next_w = 1.f;
     if (lane < re - rs) {
       next_col = static_cast<int>(col[rs + lane]);
-      if constexpr (HAS_VAL) next_w = val[rs + lane];
+      if constexpr (HAS_VAL) next_w = Elem<T>::at(val, rs + lane);
     }
     for (int64_t base = rs; base < re; base += kWave) {
       const int cnt = static_cast<int>((re - base) < kWave ? (re - base) : kWave);
@@ -175,10 +298,10 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
       const int64_t nb = base + kWave;
       if (nb < re && lane < re - nb) {
         next_col = static_cast<int>(col[nb + lane]);
-        if constexpr (HAS_VAL) next_w = val[nb + lane];
+        if constexpr (HAS_VAL) next_w = Elem<T>::at(val, nb + lane);
       }
       for (int j = 0; j < cnt; j += U * EPI) {
-        FVec<4> xv[U];
+        RawVec<16> xv[U];
         float w[U];
         bool live[U];
 #pragma unroll
@@ -198,17 +321,18 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
               w[u] = grp == k ? wk : w[u];
             }
           }
-          xv[u] = load_vec_off<4>(x + row_offset(c, F), lane_bytes);
+          xv[u] = load_raw<16>(xb + row_offset(c, F) * sizeof(T) + lane_bytes);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           if (live[u]) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
+            for (int v = 0; v < P; ++v) {
+              const double xe = static_cast<double>(Elem<T>::get(xv[u].w, v));
               if constexpr (HAS_VAL) {
-                acc[v] = __builtin_fma(static_cast<double>(w[u]), static_cast<double>(xv[u].v[v]), acc[v]);
+                acc[v] = __builtin_fma(static_cast<double>(w[u]), xe, acc[v]);
               } else {
-                acc[v] = acc[v] + static_cast<double>(xv[u].v[v]);
+                acc[v] = acc[v] + xe;
               }
             }
           }
@@ -218,19 +342,19 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
 #pragma unroll
     for (int o = G; o < kWave; o <<= 1) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] += __shfl_xor(acc[v], o, kWave);
+      for (int v = 0; v < P; ++v) acc[v] += __shfl_xor(acc[v], o, kWave);
     }
     if (grp == 0 && active) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) store_out(out + fl + v, acc[v]);
+      for (int v = 0; v < P; ++v) store_out(out + fl + v, acc[v]);
     }
   }
 }
 
-// slice_row_wide for 16-lane groups (F <= 64, 4 edges per gather), with
+// slice_row_wide for 4 or more edges per gather (16- or 8-lane groups), with
 // less issue work per gather and the same sums in the same order:
 //   * the lane group's column index comes from one ds_bpermute of the 64
-//     indices of the block (instead of 4 readlanes and selects);
+//     indices of the block (instead of EPI readlanes and selects);
 //   * with OFF32 (X smaller than 4 GiB and fewer than 2^24 rows) the X byte
 //     offset is one 24-bit multiply-add and the gather uses the SGPR base
 //     with a 32-bit VGPR offset;
@@ -238,14 +362,15 @@ __device__ __forceinline__ void slice_row_wide(const int64_t* __restrict__ col, 
 //     block has one.  A lane group past the end reads the index register of
 //     a lane with no edge in this block, which holds an earlier valid column
 //     (or 0), and does not add what it gathers.
-// On the 115M-edge skewed benchmark graph at F = 64 this takes the call from
-// 2.18 to 2.00 ms; with 32-lane groups (2 edges per gather) the same changes
-// cost about 1 %, so those keep slice_row_wide.
-template <int G, bool HAS_VAL, int U, bool OFF32, typename OutT>
+// On the 115M-edge skewed benchmark graph at F = 64 fp32 this takes the call
+// from 2.18 to 2.00 ms; with 32-lane groups (2 edges per gather) the same
+// changes cost about 1 %, so those keep slice_row_wide.
+template <typename T, int G, bool HAS_VAL, int U, bool OFF32, typename OutT>
 __device__ __forceinline__ void slice_row_wide_bpermute(const int64_t* __restrict__ col,
-                                                        const float* __restrict__ val, const float* __restrict__ x,
+                                                        const T* __restrict__ val, const T* __restrict__ x,
                                                         OutT* __restrict__ out, int64_t F, int64_t rs, int64_t re,
                                                         int64_t f0) {
+  constexpr int P = 16 / static_cast<int>(sizeof(T));
   constexpr int EPI = kWave / G;
   constexpr int B = U * EPI;
   static_assert(kWave % B == 0, "a batch must not straddle a block of 64 column indices");
@@ -254,38 +379,40 @@ __device__ __forceinline__ void slice_row_wide_bpermute(const int64_t* __restric
   const int gl = lane % G;
   rs = uniform_i64(rs);
   re = uniform_i64(re);
-  const int64_t fl = f0 + 4 * static_cast<int64_t>(gl);
+  const int64_t fl = f0 + P * static_cast<int64_t>(gl);
   const bool active = fl < F;
-  const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * 4);
-  const uint32_t row_bytes = static_cast<uint32_t>(F * 4);
+  const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * sizeof(T));
+  const uint32_t row_bytes = static_cast<uint32_t>(F * sizeof(T));
   const char* __restrict__ xb = reinterpret_cast<const char*>(x);
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  double acc[P];
+#pragma unroll
+  for (int v = 0; v < P; ++v) acc[v] = 0.0;
   int next_col = 0;
   float next_w = 1.f;
   if (lane < re - rs) {
     next_col = static_cast<int>(col[rs + lane]);
-    if constexpr (HAS_VAL) next_w = val[rs + lane];
+    if constexpr (HAS_VAL) next_w = Elem<T>::at(val, rs + lane);
   }
   // edges e0 .. e0 + EPI - 1 of the block (e0 uniform), lane group grp
   // gathers edge e0 + grp
-  auto gather = [&](int my_col, float my_w, int e0, float& w) -> FVec<4> {
+  auto gather = [&](int my_col, float my_w, int e0, float& w) -> RawVec<16> {
     const int addr = (e0 + grp) * 4;
     const int c = __builtin_amdgcn_ds_bpermute(addr, my_col);
     if constexpr (HAS_VAL) w = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(my_w)));
     if constexpr (OFF32) {
-      const uint32_t off = __umul24(static_cast<uint32_t>(c), row_bytes) + lane_bytes;
-      return *reinterpret_cast<const FVec<4>*>(xb + off);
+      return load_raw<16>(xb + (__umul24(static_cast<uint32_t>(c), row_bytes) + lane_bytes));
     } else {
-      return load_vec_off<4>(x + row_offset(c, F), lane_bytes);
+      return load_raw<16>(xb + row_offset(c, F) * sizeof(T) + lane_bytes);
     }
   };
-  auto add = [&](const FVec<4>& xv, float w) {
+  auto add = [&](const RawVec<16>& xv, float w) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < P; ++v) {
+      const double xe = static_cast<double>(Elem<T>::get(xv.w, v));
       if constexpr (HAS_VAL) {
-        acc[v] = __builtin_fma(static_cast<double>(w), static_cast<double>(xv.v[v]), acc[v]);
+        acc[v] = __builtin_fma(static_cast<double>(w), xe, acc[v]);
       } else {
-        acc[v] = acc[v] + static_cast<double>(xv.v[v]);
+        acc[v] = acc[v] + xe;
       }
     }
   };
@@ -296,11 +423,11 @@ __device__ __forceinline__ void slice_row_wide_bpermute(const int64_t* __restric
     const int64_t nb = base + kWave;
     if (nb < re && lane < re - nb) {
       next_col = static_cast<int>(col[nb + lane]);
-      if constexpr (HAS_VAL) next_w = val[nb + lane];
+      if constexpr (HAS_VAL) next_w = Elem<T>::at(val, nb + lane);
     }
     int j = 0;
     for (; j + B <= cnt; j += B) {
-      FVec<4> xv[U];
+      RawVec<16> xv[U];
       float w[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) xv[u] = gather(my_col, my_w, j + u * EPI, w[u]);
@@ -308,7 +435,7 @@ __device__ __forceinline__ void slice_row_wide_bpermute(const int64_t* __restric
       for (int u = 0; u < U; ++u) add(xv[u], w[u]);
     }
     if (j < cnt) {
-      FVec<4> xv[U];
+      RawVec<16> xv[U];
       float w[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) xv[u] = gather(my_col, my_w, j + u * EPI, w[u]);
@@ -321,101 +448,171 @@ __device__ __forceinline__ void slice_row_wide_bpermute(const int64_t* __restric
 #pragma unroll
   for (int o = G; o < kWave; o <<= 1) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] += __shfl_xor(acc[v], o, kWave);
+    for (int v = 0; v < P; ++v) acc[v] += __shfl_xor(acc[v], o, kWave);
   }
   if (grp == 0 && active) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) store_out(out + fl + v, acc[v]);
+    for (int v = 0; v < P; ++v) store_out(out + fl + v, acc[v]);
   }
 }
 
 #ifndef AS_COLSLICE_WIDE_U
 #define AS_COLSLICE_WIDE_U 4
 #endif
+#ifndef AS_COLSLICE_WIDE_U_16
+#define AS_COLSLICE_WIDE_U_16 2
+#endif
 
-template <int G, bool HAS_VAL, bool OFF32, typename OutT>
-__device__ __forceinline__ void slice_wide(const int64_t* __restrict__ col, const float* __restrict__ val,
-                                           const float* __restrict__ x, OutT* __restrict__ out, int64_t F,
-                                           int64_t rs, int64_t re, int64_t f0) {
+template <typename T, int G, bool HAS_VAL, bool OFF32, typename OutT>
+__device__ __forceinline__ void slice_wide(const int64_t* __restrict__ col, const T* __restrict__ val,
+                                           const T* __restrict__ x, OutT* __restrict__ out, int64_t F, int64_t rs,
+                                           int64_t re, int64_t f0) {
   if constexpr (G <= 16) {
-    slice_row_wide_bpermute<G, HAS_VAL, AS_COLSLICE_WIDE_U, OFF32>(col, val, x, out, F, rs, re, f0);
+    // 16-bit lanes carry 8 fp64 sums: 2 gathers per batch keep the wave
+    // within 64 VGPRs (8 waves per SIMD)
+    constexpr int U = sizeof(T) == 2 ? AS_COLSLICE_WIDE_U_16 : AS_COLSLICE_WIDE_U;
+    slice_row_wide_bpermute<T, G, HAS_VAL, U, OFF32>(col, val, x, out, F, rs, re, f0);
   } else {
-    slice_row_wide<G, HAS_VAL, AS_COLSLICE_WIDE_U>(col, val, x, out, F, rs, re, f0);
+    slice_row_wide<T, G, HAS_VAL, AS_COLSLICE_WIDE_U>(col, val, x, out, F, rs, re, f0);
   }
 }
 
-// One chunk of the slice work: rows order[item_begin, item_begin + items),
-// main block mb of 8·P·ceil(items / 4)·tiles (P = kPhases).  Within a tile,
-// the blocks of phase p come before those of phase p + 1; a block takes slice
-// 8·p + mb % 8 (so its XCD is mb % 8) and 4 waves of the chunk; the wave for
-// (row, slice) writes the partial of chunk row `local` to
-// partial[(slice·chunk_stride + local)·F ..].
-// V in {1, 2}: narrow lanes (slice_row, all features); V = 16, 32: wide
-// lanes with G = V lanes per edge (slice_row_wide), one feature tile of 4·G
-// features per wave.  Feature tiles are the outermost index: every
-// (slice, row) of tile 0 comes before tile 1, so that while a tile runs each
-// XCD gathers only 4·G features of the X rows of its slice (for F > 128 this
-// keeps the per-XCD working set of F = 128).
+// One chunk of the work: rows order[item_begin, item_begin + items); the
+// first counts[0] rows of the order are sliced, the rest are short.  A launch
+// is made of groups of 8 workgroups (one per XCD, by blockIdx % 8):
+//   * slice groups, Gs per (feature tile, phase): block mb takes slice
+//     8·p + mb % 8 and its 4 waves stride over the chunk's sliced rows; the
+//     wave for (row, slice) writes the partial of chunk row `local` to
+//     partial[(slice·chunk_stride + local)·F ..];
+//   * short groups, Gh per feature tile: every wave sums whole short rows,
+//     striding over them, and writes Y;
+//   * reduce groups (colslice_reduce_block).
+// Gs and Gh are capped, so a chunk of short rows does not launch 8 waves per
+// row; the row counts come from counts[0] on the device, so the host needs no
+// copy of it.  V in {1, 2}: narrow lanes (slice_row, all features); V = 8,
+// 16, 32: wide lanes with G = V lanes per edge (slice_row_wide), one feature
+// tile of 16·G / sizeof(T) features per wave.  Feature tiles are the
+// outermost index: every (slice, row) of tile 0 comes before tile 1, so that
+// while a tile runs each XCD gathers only 16·G bytes of the X rows of its
+// slice (for wider rows this keeps the per-XCD working set of 512-byte rows).
 struct SliceChunk {
   int64_t item_begin;
   int64_t items;
   double* partial;
+  int64_t slice_groups;  // Gs: slice groups per (tile, phase)
+  int64_t short_groups;  // Gh: short groups per tile
+  int64_t sliced;        // the caller's count of sliced rows in the chunk, < 0 if unknown
 };
 
-template <int V, bool HAS_VAL, bool OFF32>
-__device__ __forceinline__ void colslice_main_block(int64_t mb, const int64_t* __restrict__ crow,
-                                                    const int64_t* __restrict__ col, const float* __restrict__ val,
-                                                    const float* __restrict__ x, float* __restrict__ y, int64_t F,
-                                                    const int32_t* __restrict__ order,
-                                                    const int32_t* __restrict__ counts,
-                                                    const int32_t* __restrict__ off, const SliceChunk& c,
-                                                    int64_t chunk_stride) {
-  const int64_t phase_blocks = kSlices * ((c.items + kWavesPerBlock - 1) / kWavesPerBlock);
+#ifndef AS_COLSLICE_SLICE_GROUPS
+#define AS_COLSLICE_SLICE_GROUPS 4096
+#endif
+#ifndef AS_COLSLICE_SHORT_GROUPS
+#define AS_COLSLICE_SHORT_GROUPS 8192
+#endif
+constexpr int64_t kSliceGroupsMax = AS_COLSLICE_SLICE_GROUPS;  // without a hint
+constexpr int64_t kShortGroupsMax = AS_COLSLICE_SHORT_GROUPS;
+constexpr int64_t kMaxSliceGroupsHinted = 65536;
+
+// Group counts of a chunk of `items` rows of which `sliced` are expected to
+// be sliced (the caller's hint; < 0 if unknown).  Any counts >= 1 cover all
+// rows, since the waves stride; the hint only avoids looping waves (too few
+// groups) and idle ones (too many).
+inline void chunk_groups(SliceChunk& c, int64_t sliced) {
+  int64_t gs, gh;
+  if (sliced < 0) {
+    gs = (c.items + kWavesPerBlock - 1) / kWavesPerBlock;
+    gh = (c.items + kSlices * kWavesPerBlock - 1) / (kSlices * kWavesPerBlock);
+    if (gs > kSliceGroupsMax) gs = kSliceGroupsMax;
+  } else {
+    if (sliced > c.items) sliced = c.items;
+    gs = (sliced + kWavesPerBlock - 1) / kWavesPerBlock;
+    gh = (c.items - sliced + kSlices * kWavesPerBlock - 1) / (kSlices * kWavesPerBlock);
+    if (gs > kMaxSliceGroupsHinted) gs = kMaxSliceGroupsHinted;
+  }
+  if (gh > kShortGroupsMax) gh = kShortGroupsMax;
+  c.slice_groups = gs > 0 ? gs : 1;
+  c.short_groups = gh > 0 ? gh : 1;
+  c.sliced = sliced;
+}
+
+// Sliced rows of the chunk: [item_begin, fs), fs = counts[0] clamped.
+__device__ __forceinline__ int64_t first_short(const int32_t* __restrict__ counts, const SliceChunk& c) {
+  const int64_t h = counts[0];
+  const int64_t end = c.item_begin + c.items;
+  return h < c.item_begin ? c.item_begin : (h > end ? end : h);
+}
+
+template <typename T, int V, bool HAS_VAL, bool OFF32>
+__device__ __forceinline__ void colslice_slice_block(int64_t mb, const int64_t* __restrict__ crow,
+                                                     const int64_t* __restrict__ col, const T* __restrict__ val,
+                                                     const T* __restrict__ x, int64_t F,
+                                                     const int32_t* __restrict__ order,
+                                                     const int32_t* __restrict__ counts,
+                                                     const int32_t* __restrict__ off, const SliceChunk& c,
+                                                     int64_t chunk_stride) {
+  constexpr int64_t kTile = 16 * V / static_cast<int64_t>(sizeof(T));  // features of a wide tile
+  const int64_t gs = c.slice_groups;
+  const int64_t phase_blocks = kSlices * gs;
   const int64_t tile_blocks = kPhases * phase_blocks;
   const int64_t tile = mb / tile_blocks;
   const int64_t in_tile = mb - tile * tile_blocks;
   const int64_t phase = in_tile / phase_blocks;
   const int64_t in_phase = in_tile - phase * phase_blocks;
   const int slice = static_cast<int>(phase * kSlices + in_phase % kSlices);
-  const int64_t local = (in_phase / kSlices) * kWavesPerBlock + wave_in_block();
-  if (local >= c.items) return;
-  const int64_t item = c.item_begin + local;
-  const int64_t row = uniform_i64(order[item]);
-  const int64_t rs = uniform_i64(crow[row]);
-  const int64_t deg = uniform_i64(crow[row + 1]) - rs;
-  if (item >= counts[0]) {
-    // short row: one wave (of the slice item % 8, to spread them over the
-    // XCDs) sums the whole row and writes Y
-    if (item % kSpmmSlices != slice) return;
-    if constexpr (V >= 16) {
-      slice_wide<V, HAS_VAL, OFF32>(col, val, x, y + row * F, F, rs, rs + deg, tile * 4 * V);
+  const int64_t sliced = first_short(counts, c) - c.item_begin;
+  for (int64_t local = (in_phase / kSlices) * kWavesPerBlock + wave_in_block(); local < sliced;
+       local += gs * kWavesPerBlock) {
+    const int64_t row = uniform_i64(order[c.item_begin + local]);
+    const int64_t rs = uniform_i64(crow[row]);
+    const int64_t deg = uniform_i64(crow[row + 1]) - rs;
+    int64_t a, b;
+    slice_range<kSpmmSlices>(off, row, slice, deg, a, b);
+    a = uniform_i64(a);
+    b = uniform_i64(b);
+    if (a >= b) continue;
+    double* out = c.partial + (slice * chunk_stride + local) * F;
+    if constexpr (V >= 8) {
+      slice_wide<T, V, HAS_VAL, OFF32>(col, val, x, out, F, rs + a, rs + b, tile * kTile);
     } else {
-      slice_row<V, HAS_VAL, 8>(col, val, x, y + row * F, F, rs, rs + deg);
+      if (b - a >= kColsliceLongRow) slice_row<T, V, HAS_VAL, 16>(col, val, x, out, F, rs + a, rs + b);
+      else slice_row<T, V, HAS_VAL, 8>(col, val, x, out, F, rs + a, rs + b);
     }
-    return;
   }
-  int64_t a, b;
-  slice_range<kSpmmSlices>(off, row, slice, deg, a, b);
-  a = uniform_i64(a);
-  b = uniform_i64(b);
-  if (a >= b) return;
-  double* out = c.partial + (slice * chunk_stride + local) * F;
-  if constexpr (V >= 16) {
-    slice_wide<V, HAS_VAL, OFF32>(col, val, x, out, F, rs + a, rs + b, tile * 4 * V);
-  } else {
-    if (b - a >= kColsliceLongRow) slice_row<V, HAS_VAL, 16>(col, val, x, out, F, rs + a, rs + b);
-    else slice_row<V, HAS_VAL, 8>(col, val, x, out, F, rs + a, rs + b);
+}
+
+template <typename T, int V, bool HAS_VAL, bool OFF32>
+__device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* __restrict__ crow,
+                                                     const int64_t* __restrict__ col, const T* __restrict__ val,
+                                                     const T* __restrict__ x, T* __restrict__ y, int64_t F,
+                                                     const int32_t* __restrict__ order,
+                                                     const int32_t* __restrict__ counts, const SliceChunk& c) {
+  constexpr int64_t kTile = 16 * V / static_cast<int64_t>(sizeof(T));
+  const int64_t tile_blocks = kSlices * c.short_groups;
+  const int64_t tile = hb / tile_blocks;
+  const int64_t k = hb - tile * tile_blocks;
+  const int64_t end = c.item_begin + c.items;
+  for (int64_t item = first_short(counts, c) + k * kWavesPerBlock + wave_in_block(); item < end;
+       item += tile_blocks * kWavesPerBlock) {
+    const int64_t row = uniform_i64(order[item]);
+    const int64_t rs = uniform_i64(crow[row]);
+    const int64_t deg = uniform_i64(crow[row + 1]) - rs;
+    if constexpr (V >= 8) {
+      slice_wide<T, V, HAS_VAL, OFF32>(col, val, x, y + row * F, F, rs, rs + deg, tile * kTile);
+    } else {
+      slice_row<T, V, HAS_VAL, 8>(col, val, x, y + row * F, F, rs, rs + deg);
+    }
   }
 }
 
 // Reduction of one chunk, block rb of R: Y[row, f..f+VR) = sum over the
 // non-empty slices, in slice order, in fp64, rounded once, for the sliced
 // rows (short rows wrote Y themselves).
-template <int VR>
+template <typename T, int VR>
 __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, const int64_t* __restrict__ crow,
                                                       const int32_t* __restrict__ off,
                                                       const int32_t* __restrict__ order,
-                                                      const int32_t* __restrict__ counts, float* __restrict__ y,
+                                                      const int32_t* __restrict__ counts, T* __restrict__ y,
                                                       int64_t F, const SliceChunk& c, int64_t chunk_stride) {
   const int64_t FV = F / VR;
   // only the sliced rows: order[0, counts[0])
@@ -440,39 +637,42 @@ __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, con
         for (int v = 0; v < VR; ++v) acc[v] += __builtin_nontemporal_load(p + v);
       }
     }
-    FVec<VR> out;
-#pragma unroll
-    for (int v = 0; v < VR; ++v) out.v[v] = static_cast<float>(acc[v]);
-    store_vec<VR>(y + row * F + f, out);
+    store_elems<T, VR>(y + row * F + f, acc);
   }
 }
 
-// One launch of the pipeline: the slice work of chunk `m` and the reduction
-// of the previous chunk `r`, whose partials a previous launch wrote.  The
-// blocks come in groups of 8 (one per XCD); of the TG groups, RG evenly
-// spread ones reduce and the others do slice work, so the HBM-streaming
-// reduction runs beside the latency-bound gathers.  Group g reduces iff
-// floor((g+1)·RG/TG) > floor(g·RG/TG); floor(g·RG/TG) groups before it
-// reduce, so a slice block keeps blockIdx % 8 as its slice.
-template <int V, bool HAS_VAL, int VR, bool OFF32>
+// One launch of the pipeline: the slice and short work of chunk `m` and the
+// reduction of the previous chunk `r`, whose partials a previous launch
+// wrote.  Of the TG groups of 8 blocks, RG evenly spread ones reduce, so the
+// HBM-streaming reduction runs beside the latency-bound gathers; the others,
+// in order, are the MG slice groups and then the short groups.  Group g
+// reduces iff floor((g+1)·RG/TG) > floor(g·RG/TG); floor(g·RG/TG) groups
+// before it reduce, so every block keeps blockIdx % 8 as its XCD.
+template <typename T, int V, bool HAS_VAL, int VR, bool OFF32>
 __global__ __launch_bounds__(kBlock) void colslice_step_kernel(const int64_t* __restrict__ crow,
                                                                const int64_t* __restrict__ col,
-                                                               const float* __restrict__ val,
-                                                               const float* __restrict__ x, float* __restrict__ y,
-                                                               int64_t F, const int32_t* __restrict__ order,
+                                                               const T* __restrict__ val, const T* __restrict__ x,
+                                                               T* __restrict__ y, int64_t F,
+                                                               const int32_t* __restrict__ order,
                                                                const int32_t* __restrict__ counts,
                                                                const int32_t* __restrict__ off, SliceChunk m,
                                                                SliceChunk r, int64_t chunk_stride, int64_t TG,
-                                                               int64_t RG) {
+                                                               int64_t RG, int64_t MG) {
   const int64_t g = blockIdx.x / kSlices;
   const int64_t within = blockIdx.x % kSlices;
   const int64_t before = g * RG / TG;
   if ((g + 1) * RG / TG > before) {
-    colslice_reduce_block<VR>(before * kSlices + within, RG * kSlices, crow, off, order, counts, y, F, r,
-                              chunk_stride);
+    colslice_reduce_block<T, VR>(before * kSlices + within, RG * kSlices, crow, off, order, counts, y, F, r,
+                                 chunk_stride);
+    return;
+  }
+  const int64_t work = g - before;
+  if (work < MG) {
+    colslice_slice_block<T, V, HAS_VAL, OFF32>(work * kSlices + within, crow, col, val, x, F, order, counts, off, m,
+                                               chunk_stride);
   } else {
-    colslice_main_block<V, HAS_VAL, OFF32>((g - before) * kSlices + within, crow, col, val, x, y, F, order, counts, off,
-                                    m, chunk_stride);
+    colslice_short_block<T, V, HAS_VAL, OFF32>((work - MG) * kSlices + within, crow, col, val, x, y, F, order,
+                                               counts, m);
   }
 }
 
@@ -501,63 +701,173 @@ int64_t preferred_chunk_rows(int64_t n) {
   return c > 0 ? c : 1;
 }
 
-template <int V, bool HAS_VAL, int VR, bool OFF32>
-void launch_one(dim3 grid, hipStream_t s, const int64_t* crow, const int64_t* col, const float* val, const float* x,
-                float* y, int64_t f, const int32_t* order, const int32_t* counts, const int32_t* off,
-                const SliceChunk& m, const SliceChunk& r, int64_t stride, int64_t TG, int64_t RG) {
-  hipLaunchKernelGGL((colslice_step_kernel<V, HAS_VAL, VR, OFF32>), grid, dim3(kBlock), 0, s, crow, col, val, x, y, f,
-                     order, counts, off, m, r, stride, TG, RG);
+struct StepArgs {
+  const int64_t* crow;
+  const int64_t* col;
+  const void* val;
+  const void* x;
+  void* y;
+  int64_t f;
+  const int32_t* order;
+  const int32_t* counts;
+  const int32_t* off;
+};
+
+struct GroupCounts {
+  int64_t TG, RG, MG;
+};
+
+template <typename T, int V, bool HAS_VAL, int VR, bool OFF32>
+void launch_one(dim3 grid, hipStream_t s, const StepArgs& a, const SliceChunk& m, const SliceChunk& r,
+                int64_t stride, const GroupCounts& n) {
+  hipLaunchKernelGGL((colslice_step_kernel<T, V, HAS_VAL, VR, OFF32>), grid, dim3(kBlock), 0, s, a.crow, a.col,
+                     static_cast<const T*>(a.val), static_cast<const T*>(a.x), static_cast<T*>(a.y), a.f, a.order,
+                     a.counts, a.off, m, r, stride, n.TG, n.RG, n.MG);
 }
 
-// OFF32 only matters for the wide lanes (V = 16, 32).
-template <bool HAS_VAL, int VR>
-void launch_step_v(int v, bool off32, dim3 grid, hipStream_t s, const int64_t* crow, const int64_t* col,
-                   const float* val, const float* x, float* y, int64_t f, const int32_t* order, const int32_t* counts,
-                   const int32_t* off, const SliceChunk& m, const SliceChunk& r, int64_t stride, int64_t TG,
-                   int64_t RG) {
+// OFF32 only matters for the ds_bpermute form of the wide lanes (V <= 16);
+// V = 8 exists for 16-bit elements and V = 2 for fp32 only.
+template <typename T, bool HAS_VAL, int VR>
+void launch_step_v(int v, bool off32, dim3 grid, hipStream_t s, const StepArgs& a, const SliceChunk& m,
+                   const SliceChunk& r, int64_t stride, const GroupCounts& n) {
+  constexpr bool kHalf = sizeof(T) == 2;
   switch (v) {
     case 32:
-      if (off32) launch_one<32, HAS_VAL, VR, true>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
-      else launch_one<32, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+      launch_one<T, 32, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
       break;
     case 16:
-      if (off32) launch_one<16, HAS_VAL, VR, true>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
-      else launch_one<16, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+      if (off32) launch_one<T, 16, HAS_VAL, VR, true>(grid, s, a, m, r, stride, n);
+      else launch_one<T, 16, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
+      break;
+    case 8:
+      if constexpr (kHalf) {
+        if (off32) launch_one<T, 8, HAS_VAL, VR, true>(grid, s, a, m, r, stride, n);
+        else launch_one<T, 8, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
+      }
       break;
     case 2:
-      launch_one<2, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+      if constexpr (!kHalf) launch_one<T, 2, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
       break;
     default:
-      launch_one<1, HAS_VAL, VR, false>(grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+      launch_one<T, 1, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
       break;
   }
 }
 
 // Launch of slice work `m` (items may be 0) beside the reduction of `r`
 // (items may be 0).
-void launch_step(int v, bool off32, int vr, bool has_val, int64_t tiles, hipStream_t s, const int64_t* crow, const int64_t* col,
-                 const float* val, const float* x, float* y, int64_t f, const int32_t* order, const int32_t* counts,
-                 const int32_t* off, const SliceChunk& m, const SliceChunk& r, int64_t stride) {
-  const int64_t MG = tiles * kPhases * ((m.items + kWavesPerBlock - 1) / kWavesPerBlock);  // groups of 8 slice blocks
+template <typename T>
+void launch_step(int v, bool off32, int vr, bool has_val, int64_t tiles, hipStream_t s, const StepArgs& a,
+                 const SliceChunk& m, const SliceChunk& r, int64_t stride) {
+  // groups of 8 blocks: slice groups per (tile, phase), short groups per tile
+  const int64_t MG = m.items > 0 ? tiles * kPhases * m.slice_groups : 0;
+  const int64_t SG = m.items > 0 ? tiles * m.short_groups : 0;
   int64_t RG = 0;
   if (r.items > 0) {
-    // enough reduce blocks for one element per thread, at most a fifth of
-    // the groups when they run beside slice work
-    RG = (r.items * (f / vr) + kSlices * kBlock - 1) / (kSlices * kBlock);
-    const int64_t cap = MG > 0 ? (MG + 3) / 4 : kGridStrideBlocks / kSlices;
+    // enough reduce blocks for one element per thread of the (expected)
+    // sliced rows, at most a fifth of the groups when they run beside other
+    // work; the blocks stride, so any count >= 1 covers them
+    const int64_t rows = r.sliced >= 0 && r.sliced < r.items ? r.sliced : r.items;
+    RG = (rows * (a.f / vr) + kSlices * kBlock - 1) / (kSlices * kBlock);
+    const int64_t cap = MG + SG > 0 ? (MG + SG + 3) / 4 : kGridStrideBlocks / kSlices;
     if (RG > cap) RG = cap;
     if (RG < 1) RG = 1;
   }
-  const int64_t TG = MG + RG;
-  if (TG == 0) return;
-  const dim3 grid(static_cast<unsigned>(TG * kSlices));
+  const GroupCounts n{MG + SG + RG, RG, MG};
+  if (n.TG == 0) return;
+  const dim3 grid(static_cast<unsigned>(n.TG * kSlices));
   if (has_val) {
-    if (vr == 2) launch_step_v<true, 2>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
-    else launch_step_v<true, 1>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    if (vr == 2) launch_step_v<T, true, 2>(v, off32, grid, s, a, m, r, stride, n);
+    else launch_step_v<T, true, 1>(v, off32, grid, s, a, m, r, stride, n);
   } else {
-    if (vr == 2) launch_step_v<false, 2>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
-    else launch_step_v<false, 1>(v, off32, grid, s, crow, col, val, x, y, f, order, counts, off, m, r, stride, TG, RG);
+    if (vr == 2) launch_step_v<T, false, 2>(v, off32, grid, s, a, m, r, stride, n);
+    else launch_step_v<T, false, 1>(v, off32, grid, s, a, m, r, stride, n);
   }
+}
+
+enum Slicing { kSliceColumns = 0, kSliceEdges = 1 };
+
+template <typename T>
+int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
+                 int64_t nnz, int64_t f, Slicing slicing, void* workspace, size_t workspace_bytes,
+                 int64_t sliced_rows, void* stream) {
+  int st = validate_spmm(crow, col, x, y, n, nnz, f);
+  if (st != AS_OK) return st;
+  if (n == 0 || f == 0) return AS_OK;
+  const size_t fixed = colslice_fixed_bytes(n);
+  const size_t row_bytes = colslice_row_bytes(f);
+  if (workspace == nullptr || workspace_bytes < fixed + 2 * row_bytes)
+    return fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu workspace bytes, got %zu",
+                fixed + 2 * row_bytes, workspace_bytes);
+  if (!aligned(workspace, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  constexpr int64_t E = static_cast<int64_t>(sizeof(T));
+  constexpr int64_t P = 16 / E;  // elements per 16-byte lane
+
+  // lanes: G lanes per edge with 16-byte loads when F is a multiple of P and
+  // X is 16-byte aligned (fp32: G = 16 for F <= 64, else 32 in tiles of 128
+  // features; 16-bit: G = 8 / 16 / 32 for F <= 64 / 128 / more, tiles of
+  // 256); otherwise 8-byte (fp32, F > 64 even) or element-wide lanes with one
+  // edge per gather
+  int v = 1;
+  if (f % P == 0 && aligned(x, 16)) {
+    if (E == 4) v = f <= 64 ? 16 : 32;
+    else v = f <= 64 ? 8 : (f <= 128 ? 16 : 32);
+  } else if (E == 4 && f % 2 == 0 && f > 64 && aligned(x, 8)) {
+    v = 2;
+  }
+  const int64_t tiles = v >= 8 ? (f + P * v - 1) / (P * v) : 1;
+  // every X byte offset fits 32 bits, row index and row bytes fit 24 bits
+  const bool off32 = n <= (int64_t(1) << 24) && f * E < (int64_t(1) << 24) && n * f * E <= (int64_t(1) << 32);
+  const int vr = (f % 2 == 0 && aligned(y, static_cast<size_t>(2 * E))) ? 2 : 1;
+
+  // two partial buffers of `chunk` rows each (chunk k writes buffer k % 2)
+  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed) / (2 * row_bytes));
+  const int64_t preferred = preferred_chunk_rows(n);
+  if (chunk > preferred) chunk = preferred;
+  // blocks of a launch: 8 per group, at most tiles·(P·ceil(c/4) + ceil(c/32))
+  // work groups for c rows, and reduce groups at most a quarter of those
+  const int64_t max_rows = (kMaxBlocksPerLaunch * 4 / 5 / (kSlices * tiles) - 2) * 32 / (8 * kPhases + 1);
+  if (chunk > max_rows) chunk = max_rows;
+  if (chunk < 1) return fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
+
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const size_t rows = static_cast<size_t>(n);
+  int32_t* off = reinterpret_cast<int32_t*>(ws);
+  ws += align_up(rows * kSpmmBounds * sizeof(int32_t), 256);
+  int32_t* order = reinterpret_cast<int32_t*>(ws);
+  ws += align_up(rows * sizeof(int32_t), 256);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws);
+  ws += 256;
+  void* bin_ws = ws;
+  double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
+                        reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + chunk * row_bytes)};
+
+  const int64_t min_degree = slicing == kSliceColumns ? kColsliceMinDegree : kEdgeSliceMinDegree;
+  launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, off, s, slicing == kSliceEdges);
+  // order: rows of degree >= min_degree (sliced) in 8 log2-degree buckets,
+  // longest first; then the short rows in row order
+  st = launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
+  if (st != AS_OK) return st;
+
+  // launch k: slice work of chunk k beside the reduction of chunk k - 1
+  const StepArgs a{crow, col, val, x, y, f, order, counts, off};
+  const int64_t chunks = (n + chunk - 1) / chunk;
+  SliceChunk previous{0, 0, buffers[1], 1, 1, -1};
+  for (int64_t k = 0; k <= chunks; ++k) {
+    SliceChunk current{k * chunk, 0, buffers[k % 2], 1, 1, -1};
+    if (k < chunks) current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
+    // the sliced rows come first in the order
+    chunk_groups(current, sliced_rows < 0 ? -1 : (sliced_rows > current.item_begin ? sliced_rows - current.item_begin : 0));
+#if AS_COLSLICE_OVERLAP
+    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, previous, chunk);
+#else
+    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, SliceChunk{0, 0, nullptr, 1, 1, -1}, chunk);
+    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, SliceChunk{0, 0, nullptr, 1, 1, -1}, current, chunk);
+#endif
+    previous = current;
+  }
+  return AS_OK;
 }
 
 }  // namespace
@@ -572,77 +882,36 @@ size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f) {
   return as::colslice_fixed_bytes(n) + 2 * static_cast<size_t>(as::preferred_chunk_rows(n)) * as::colslice_row_bytes(f);
 }
 
+int64_t as_spmm_colslice_min_degree(int column_slices) {
+  return column_slices ? as::kColsliceMinDegree : as::kEdgeSliceMinDegree;
+}
+
 int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const float* val, const float* x, float* y,
                              int64_t n, int64_t nnz, int64_t f, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+                             int64_t sliced_rows, void* stream) {
   as::clear_error();
-  int st = as::validate_spmm(crow, col, x, y, n, nnz, f);
+  const int st = as::colslice_run<float>(crow, col, val, x, y, n, nnz, f, as::kSliceColumns, workspace,
+                                         workspace_bytes, sliced_rows, stream);
   if (st != AS_OK) return st;
-  if (n == 0 || f == 0) return AS_OK;
-  const size_t fixed = as::colslice_fixed_bytes(n);
-  const size_t row_bytes = as::colslice_row_bytes(f);
-  if (workspace == nullptr || workspace_bytes < fixed + 2 * row_bytes)
-    return as::fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu workspace bytes, got %zu",
-                    fixed + 2 * row_bytes, workspace_bytes);
-  if (!as::aligned(workspace, 256)) return as::fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-
-  // lanes: G = 16 lanes per edge with float4 loads for F <= 64, else G = 32
-  // in tiles of 128 features; 8- or 4-byte lanes with one edge per gather
-  // when F is not a multiple of 4 or X is not 16-byte aligned
-  int v = 1;
-  if (f % 4 == 0 && as::aligned(x, 16)) v = f <= 64 ? 16 : 32;
-  else if (f % 2 == 0 && f > 64 && as::aligned(x, 8)) v = 2;
-  const int64_t tiles = v >= 16 ? (f + 4 * v - 1) / (4 * v) : 1;
-  // every X byte offset fits 32 bits, row index and row bytes fit 24 bits
-  const bool off32 = n <= (int64_t(1) << 24) && f * 4 < (int64_t(1) << 24) && n * f * 4 <= (int64_t(1) << 32);
-  const int vr = (f % 2 == 0 && as::aligned(y, 8)) ? 2 : 1;
-
-  // two partial buffers of `chunk` rows each (chunk k writes buffer k % 2)
-  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed) / (2 * row_bytes));
-  const int64_t preferred = as::preferred_chunk_rows(n);
-  if (chunk > preferred) chunk = preferred;
-  // a launch holds at most 5/4 of the slice groups of a chunk
-  const int64_t max_rows = as::kMaxBlocksPerLaunch * 4 / 5 / as::kSpmmSlices * as::kWavesPerBlock / tiles;
-  if (chunk > max_rows) chunk = max_rows;
-  if (chunk < 1) return as::fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
-
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const size_t rows = static_cast<size_t>(n);
-  int32_t* off = reinterpret_cast<int32_t*>(ws);
-  ws += as::align_up(rows * as::kSpmmBounds * sizeof(int32_t), 256);
-  int32_t* order = reinterpret_cast<int32_t*>(ws);
-  ws += as::align_up(rows * sizeof(int32_t), 256);
-  int32_t* counts = reinterpret_cast<int32_t*>(ws);
-  ws += 256;
-  void* bin_ws = ws;
-  double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
-                        reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + chunk * row_bytes)};
-
-  as::launch_slice_points<as::kSpmmSlices>(crow, col, n, as::kColsliceMinDegree, off, s);
-  // order: rows of degree >= kColsliceMinDegree (sliced) in 8 log2-degree
-  // buckets, longest first; then the short rows in row order
-  st = as::launch_bin_rows(crow, n, as::kColsliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
-  if (st != AS_OK) return st;
-
-  // launch k: slice work of chunk k beside the reduction of chunk k - 1
-  const int64_t chunks = (n + chunk - 1) / chunk;
-  as::SliceChunk previous{0, 0, buffers[1]};
-  for (int64_t k = 0; k <= chunks; ++k) {
-    as::SliceChunk current{k * chunk, 0, buffers[k % 2]};
-    if (k < chunks) current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
-#if AS_COLSLICE_OVERLAP
-    as::launch_step(v, off32, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current, previous,
-                    chunk);
-#else
-    as::launch_step(v, off32, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off, current,
-                    as::SliceChunk{0, 0, nullptr}, chunk);
-    as::launch_step(v, off32, vr, val != nullptr, tiles, s, crow, col, val, x, y, f, order, counts, off,
-                    as::SliceChunk{0, 0, nullptr}, current, chunk);
-#endif
-    previous = current;
-  }
   return as::check_launch("spmm_csr_colslice");
+}
+
+int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
+                           int64_t n, int64_t nnz, int64_t f, int dtype, int column_slices, void* workspace,
+                           size_t workspace_bytes, int64_t sliced_rows, void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (!as::aligned(x, 2) || !as::aligned(y, 2) || (val != nullptr && !as::aligned(val, 2)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "x, y and val must be 2-byte aligned");
+  const as::Slicing slicing = column_slices ? as::kSliceColumns : as::kSliceEdges;
+  const int st = dtype == AS_DTYPE_BF16
+                     ? as::colslice_run<as::Bf16>(crow, col, val, x, y, n, nnz, f, slicing, workspace,
+                                                  workspace_bytes, sliced_rows, stream)
+                     : as::colslice_run<as::Fp16>(crow, col, val, x, y, n, nnz, f, slicing, workspace,
+                                                  workspace_bytes, sliced_rows, stream);
+  if (st != AS_OK) return st;
+  return as::check_launch("spmm_csr_rounded_16");
 }
 
 }  // extern "C"

@@ -136,8 +136,8 @@ def spmm_csr(crow, col, val, x) -> torch.Tensor:
     crow, col, val, x = _normalize_csr(crow, col, val, x)
     if not x.is_cuda:
         return _cpu_spmm(crow, col, val, x)
-    if x.dtype != torch.float32:
-        raise TypeError("AutoSAGE CUDA kernels currently support float32 features only")
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError("AutoSAGE CUDA kernels currently support float32 features only (and bf16/fp16 for SpMM)")
     if not load_native():
         detail = f": {_LOAD_ERROR}" if _LOAD_ERROR else ""
         raise RuntimeError(f"AutoSAGE CUDA extension is unavailable{detail}")

@@ -37,9 +37,10 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def spmm_bytes(n: int, nnz: int, f: int, weighted: bool) -> int:
-    """Algorithmic bytes of one SpMM: X-row gathers, Y write, col, crow, val."""
-    return 4 * f * nnz + 4 * f * n + 8 * nnz + 8 * (n + 1) + (4 * nnz if weighted else 0)
+def spmm_bytes(n: int, nnz: int, f: int, weighted: bool, elem: int = 4) -> int:
+    """Algorithmic bytes of one SpMM: X-row gathers, Y write, col, crow, val
+    (elements of ``elem`` bytes)."""
+    return elem * f * nnz + elem * f * n + 8 * nnz + 8 * (n + 1) + (elem * nnz if weighted else 0)
 
 
 def sddmm_bytes(n: int, nnz: int, f: int) -> int:
@@ -230,6 +231,8 @@ def main() -> int:
     parser.add_argument("--probe-overhead", action="store_true",
                         help="instead of the bench line: the scheduler's cost on this workload (a cold call with an "
                              "empty schedule cache, then cached calls) against one call of the chosen kernel")
+    parser.add_argument("--dtype", default="f32", choices=["f32", "bf16", "fp16"],
+                        help="feature type of the SpMM workloads (cfg1-3); bf16/fp16 run the rounded 16-bit SpMM")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gpu-baseline", action="store_true")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -277,15 +280,29 @@ def main() -> int:
         val = None if w.val is None else torch.from_numpy(w.val).to(device)
         x = torch.from_numpy(w.dense["x"]).to(device)
         weighted = val is not None
+        half = args.dtype != "f32"
+        elem = 2 if half else 4
+        if half:
+            from autosage_amd._native import spmm_rounded_16_impl
 
-        variants = {"whole": lambda: torch.ops.autosage.spmm_csr(crow, col, val, x)}
-        for cand in _spmm_candidates(crow, f, SchedulerConfig(candidate_count=6)):
-            variants[",".join(map(str, cand))] = (
-                lambda c=cand: torch.ops.autosage.spmm_csr_split(crow, col, val, x, *c))
-        # the column-sliced SpMM (fp64 accumulation) for graphs with ascending
-        # columns; listed last so that an exact variant wins a tie
-        if not args.exact_only and columns_ascending(crow, col):
-            variants["colslice"] = lambda: torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
+            dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+            x = x.to(dt)
+            val = None if val is None else val.to(dt)
+            # one rule, the same bits on every schedule: column slices (when
+            # the columns ascend) or edge slices
+            variants = {"rounded16:edges": lambda: spmm_rounded_16_impl(crow, col, val, x, column_slices=False)}
+            if columns_ascending(crow, col):
+                variants["rounded16:columns"] = (
+                    lambda: spmm_rounded_16_impl(crow, col, val, x, column_slices=True))
+        else:
+            variants = {"whole": lambda: torch.ops.autosage.spmm_csr(crow, col, val, x)}
+            for cand in _spmm_candidates(crow, f, SchedulerConfig(candidate_count=6)):
+                variants[",".join(map(str, cand))] = (
+                    lambda c=cand: torch.ops.autosage.spmm_csr_split(crow, col, val, x, *c))
+            # the column-sliced SpMM (fp64 accumulation) for graphs with
+            # ascending columns; listed last so that an exact variant wins a tie
+            if not args.exact_only and columns_ascending(crow, col):
+                variants["colslice"] = lambda: torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
         calib = {}
         if args.variant == "calibrated":
             chosen = calibrate(variants, calib)
@@ -300,8 +317,9 @@ def main() -> int:
         step = variants[chosen]
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * nnz * f
-        algo = spmm_bytes(n, nnz, f, weighted)
-        workload_name = f"{args.workload} SpMM fp32 F={f}" + (" weighted" if weighted else " unweighted")
+        algo = spmm_bytes(n, nnz, f, weighted, elem)
+        type_name = {"f32": "fp32", "bf16": "bf16", "fp16": "fp16"}[args.dtype]
+        workload_name = f"{args.workload} SpMM {type_name} F={f}" + (" weighted" if weighted else " unweighted")
         traffic = profiled_traffic(workload_name, chosen)
         result = {
             "metric": METRIC,
@@ -314,7 +332,7 @@ def main() -> int:
             "higher_is_better": True,
             "scaling": "weak",
             "vs_baseline": None,
-            "dtype": "f32",
+            "dtype": args.dtype,
             "data": "synthetic",
             "config": {
                 "workload": workload_name,
@@ -322,7 +340,8 @@ def main() -> int:
                 "nnz": nnz,
                 "features": f,
                 "variant": chosen,
-                "accumulation": "fp64 partials per column slice" if chosen == "colslice"
+                "accumulation": "fp64 sum of the exact products, rounded to fp32 then to " + type_name if half
+                else "fp64 partials per column slice" if chosen == "colslice"
                 else "fp32, CSR edge order (bit-identical to the sequential product)",
                 "graph_fingerprint": w.fingerprint(),
                 "degree_stats": w.degree_stats(),
@@ -349,13 +368,22 @@ def main() -> int:
             best_exact = min(exact, key=exact.get)
             result["bit_exact_best"] = {"variant": best_exact, "calibration_ms": exact[best_exact],
                                         "value": round(flops / (exact[best_exact] * 1e-3) / 1e9, 2)}
-        if not args.no_gpu_baseline:
+        if half:
+            # torch.sparse.mm on a bf16 CSR tensor aborts the process on
+            # PyTorch-ROCm; fp16 is not run for the same reason
+            result["gpu_baseline"] = {"name": "torch.sparse.mm(csr) (PyTorch-ROCm)", "ms": None,
+                                      "note": "not run: aborts the process for bf16 CSR on PyTorch-ROCm"}
+        elif not args.no_gpu_baseline:
             base, name = _prepare_spmm_baseline(crow, col, val, x)
             bms, _ = time_steps(base, 3, 1)
             result["gpu_baseline"] = {"name": f"{name} (PyTorch-ROCm)", "ms": round(bms, 4),
                                       "speedup": round(bms / ms, 3)}
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = cpu_baseline_spmm(w.crow, w.col, w.val, w.dense["x"], target_nnz=nnz // 8)
+            if half:
+                # torch's CPU CSR product (the reference's CPU path) has no
+                # bf16/fp16 kernel: the fp32 path is the nearest CPU baseline
+                result["cpu_baseline"]["sample"] += "; fp32 (the CPU path has no bf16/fp16 CSR product)"
         else:
             result["cpu_baseline"] = None
     else:

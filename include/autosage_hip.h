@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 1
+#define AS_ABI_VERSION 2
 
 typedef enum as_status {
   AS_OK = 0,
@@ -39,6 +39,12 @@ typedef enum as_status {
   AS_ERR_UNSUPPORTED = 3,
   AS_ERR_WORKSPACE = 4
 } as_status;
+
+/* 16-bit element types of as_spmm_csr_rounded_16. */
+enum {
+  AS_DTYPE_BF16 = 1,
+  AS_DTYPE_F16 = 2
+};
 
 /* Hub-row strategy for as_spmm_csr_split_f32 (no reference counterpart; the
  * reference always reassociates, csrc/spmm_hub.cu:40-47,81-90). */
@@ -111,12 +117,42 @@ size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f);
  * The rows run in chunks, the partial reduction of one chunk beside the
  * slice work of the next.  The workspace (256-byte aligned) holds n·28 B of
  * slice points, the row order and two partial buffers of c·f·64 B for
- * chunks of c rows; any size down to c = 1 works, in more chunks. */
+ * chunks of c rows; any size down to c = 1 works, in more chunks.
+ * sliced_rows: the number of rows of degree >= as_spmm_colslice_min_degree(1),
+ * if the caller knows it (it is fixed per graph), else -1.  It only sizes the
+ * launches (too small: waves loop over several rows; too large: idle
+ * waves); the result is the same for any value. */
 int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col,
                              const float* val, const float* x, float* y,
                              int64_t n, int64_t nnz, int64_t f,
                              void* workspace, size_t workspace_bytes,
-                             void* stream);
+                             int64_t sliced_rows, void* stream);
+
+/* Degree from which rows are sliced: 128 for column slices
+ * (column_slices != 0), 1024 for edge slices. */
+int64_t as_spmm_colslice_min_degree(int column_slices);
+
+/* SpMM with bf16 or fp16 features, weights and output (dtype
+ * AS_DTYPE_BF16 / AS_DTYPE_F16; val may be NULL).  The reference has no
+ * kernel for these types: its op raises for them (autosage/ops.py:156-157)
+ * and its scheduler falls back to torch.sparse.mm with the weights cast to
+ * the feature type (autosage/_auto.py:281-287); the CPU torch path has no
+ * bf16/fp16 CSR product.  Result: every output is the fp64 sum of the exact
+ * products, rounded to fp32 and then to the element type (round to nearest
+ * even both times), which does not depend on the order of the additions.
+ * Same kernels and workspace as as_spmm_csr_colslice_f32 (size from
+ * as_spmm_colslice_workspace_bytes).  column_slices != 0: 8 column slices
+ * (columns must ascend within rows); 0: rows of degree >= 1024 are cut into
+ * 8 equal runs of edges instead (any column order).  x, y and val 2-byte
+ * aligned; F a multiple of 8 with 16-byte aligned x takes 16-byte lanes.
+ * sliced_rows: as for as_spmm_csr_colslice_f32, with the degree
+ * as_spmm_colslice_min_degree(column_slices). */
+int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
+                           const void* val, const void* x, void* y,
+                           int64_t n, int64_t nnz, int64_t f, int dtype,
+                           int column_slices, void* workspace,
+                           size_t workspace_bytes, int64_t sliced_rows,
+                           void* stream);
 
 /* out[e] = <query[row(e)], key[col[e]]> for every nonzero, CSR order.
  * Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134), op schema :192.

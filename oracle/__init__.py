@@ -14,7 +14,9 @@ Contents:
   ``torch_cpu_spmm`` (autosage/ops.py:124-143), ``torch_gather_dot``
   (autosage/_auto.py:79-92), ``torch_row_softmax`` (autosage/_auto.py:744-759),
   ``numpy_edge_index_to_csr`` (autosage/utils/csr.py:6-26);
-* ``attention_ref`` = composition of the above (autosage/_auto.py:762-780).
+* ``attention_ref`` = composition of the above (autosage/_auto.py:762-780);
+* ``spmm_rounded_16``: the bf16 / fp16 SpMM rule (fp64 sum of exact
+  products, rounded to fp32, then to the 16-bit type).
 
 How each function is pinned (independent checks in tests/test_oracle.py):
 * or_spmm_seq_f32: bit-identical to torch.sparse.mm on CPU (MKL) on random
@@ -27,6 +29,9 @@ How each function is pinned (independent checks in tests/test_oracle.py):
   reference order and sequential order give different bits.
 * or_row_softmax_f32: KAT (rows sum to 1, single-entry rows = 1.0), torch
   scatter composition within 1e-6 relative, fp64 bound.
+* spmm_rounded_16: exact rational sums (fractions.Fraction) rounded the same
+  way on random graphs; hand-computed ties (round to even, and the fp32 step
+  that decides a tie the exact sum would not), fp16 overflow to inf.
 """
 
 from __future__ import annotations
@@ -99,6 +104,21 @@ def spmm_f64(crow, col, val, x, rows=None) -> np.ndarray:
     y = np.empty((nrows, f), dtype=np.float64)
     _load().or_spmm_f64(_p(crow), _p(col), _p(val), _p(x), _p(rows_a), nrows, f, _p(y))
     return y
+
+
+def spmm_rounded_16(crow, col, val, x, dtype: torch.dtype, rows=None) -> torch.Tensor:
+    """SpMM on bf16 / fp16 features, the rule of as_spmm_csr_rounded_16 (the
+    reference has no kernel for these types, autosage/ops.py:156-157, and no
+    CPU path: torch's CPU CSR product rejects them): weights cast to ``dtype``
+    (as the reference's torch path does, autosage/_auto.py:68-76), the exact
+    products summed in fp64, the sum rounded to fp32 and then to ``dtype``,
+    round to nearest even both times.  ``x`` / ``val``: tensors of ``dtype``
+    or arrays of values it represents exactly."""
+    xt = torch.as_tensor(x).to(dtype)
+    x32 = xt.float().numpy()
+    v32 = None if val is None else torch.as_tensor(val).to(dtype).float().numpy()
+    y64 = spmm_f64(crow, col, v32, x32, rows=rows)
+    return torch.from_numpy(y64).to(torch.float32).to(dtype)
 
 
 def bin_rows(crow, threshold: int) -> tuple[np.ndarray, np.ndarray]:

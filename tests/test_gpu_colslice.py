@@ -194,3 +194,39 @@ def test_scheduler_times_colslice_on_the_full_graph(monkeypatch, tmp_path):
     monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
     _, info3 = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
     assert "colslice" not in _timed(info3) and info3.get("candidate") != "colslice"
+
+
+def test_sliced_rows_hint_only_sizes_the_launches():
+    """The sliced-row count passed through the C ABI sizes the launches; any
+    value (unknown, zero, too small, exact, too large) gives the same bits."""
+    crow, col, val, x = _inputs(128, True, seed=21, rows=9000, degree=20, hubs=40, hub_degree=3000)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    n, f = x.shape
+    lib = _native.library()
+    exact = _native.sliced_rows(d_crow, True)
+    assert exact == int((np.diff(crow) >= lib.as_spmm_colslice_min_degree(1)).sum()) and exact >= 40
+    ws = torch.empty(lib.as_spmm_colslice_workspace_bytes(n, f), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for hint in (-1, 0, 1, exact // 2, exact, exact * 1000):
+        y = torch.empty_like(d_x)
+        status = lib.as_spmm_csr_colslice_f32(d_crow.data_ptr(), d_col.data_ptr(), d_val.data_ptr(), d_x.data_ptr(),
+                                              y.data_ptr(), n, col.size, f, ws.data_ptr(), ws.numel(), hint, stream)
+        assert status == 0, lib.as_last_error()
+        outs.append(y)
+    torch.cuda.synchronize()
+    for y in outs[1:]:
+        assert torch.equal(y, outs[0])
+    # 16-bit features, edge slices (threshold 1024)
+    xb = d_x.to(torch.bfloat16)
+    exact16 = _native.sliced_rows(d_crow, False)
+    outs = []
+    for hint in (-1, 0, exact16, exact16 + 500):
+        y = torch.empty_like(xb)
+        status = lib.as_spmm_csr_rounded_16(d_crow.data_ptr(), d_col.data_ptr(), 0, xb.data_ptr(), y.data_ptr(), n,
+                                            col.size, f, 1, 0, ws.data_ptr(), ws.numel(), hint, stream)
+        assert status == 0, lib.as_last_error()
+        outs.append(y)
+    torch.cuda.synchronize()
+    for y in outs[1:]:
+        assert torch.equal(y, outs[0])

@@ -276,3 +276,49 @@ def test_edge_index_to_csr_restatement_matches_package():
     crow, col = oracle.numpy_edge_index_to_csr(ei, 50)
     t_crow, t_col = edge_index_to_csr(torch.from_numpy(ei), 50)
     assert np.array_equal(crow, t_crow.numpy()) and np.array_equal(col, t_col.numpy())
+
+
+# --- bf16 / fp16 SpMM -----------------------------------------------------------
+
+
+def _round_16(exact: float, dtype) -> float:
+    """Rounds a correctly rounded double to fp32 and then to dtype."""
+    return torch.tensor([np.float32(exact)], dtype=torch.float32).to(dtype).float().item()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_spmm_rounded_16_matches_exact_rational_sums(dtype, weighted):
+    from fractions import Fraction
+
+    crow, col = _graph(40, 6, seed=3, hubs=1, hub_degree=35, empty=0.1)
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy(rng.standard_normal((40, 5)).astype(np.float32)).to(dtype)
+    val = torch.from_numpy(rng.standard_normal(col.size).astype(np.float32)).to(dtype) if weighted else None
+    got = oracle.spmm_rounded_16(crow, col, val, x, dtype).float().numpy()
+    xf = x.float().numpy().astype(np.float64)
+    vf = None if val is None else val.float().numpy().astype(np.float64)
+    for r in range(40):
+        for f in range(5):
+            exact = Fraction(0)
+            for e in range(crow[r], crow[r + 1]):
+                w = Fraction(1) if vf is None else Fraction(vf[e])
+                exact += w * Fraction(xf[col[e], f])
+            assert got[r, f] == _round_16(float(exact), dtype), (r, f)
+
+
+def test_spmm_rounded_16_ties_and_overflow():
+    crow = np.array([0, 2, 4, 7, 9], dtype=np.int64)
+    col = np.array([0, 1, 0, 2, 0, 1, 3, 4, 4], dtype=np.int64)
+    # x[:, 0]: 1, 2^-8, 3·2^-8, 2^-30, 60000
+    x = np.array([[1.0], [2.0**-8], [3 * 2.0**-8], [2.0**-30], [60000.0]], dtype=np.float32)
+    bf = oracle.spmm_rounded_16(crow, col, None, x, torch.bfloat16).float().numpy()[:, 0]
+    # 1 + 2^-8 is halfway between 1 and 1 + 2^-7: even -> 1
+    assert bf[0] == 1.0
+    # 1 + 3·2^-8 is halfway between 1 + 2^-7 and 1 + 2^-6: even -> 1 + 2^-6
+    assert bf[1] == 1.0 + 2.0**-6
+    # 1 + 2^-8 + 2^-30 is above the tie, but fp32 drops the 2^-30 first: 1
+    assert bf[2] == 1.0
+    h = oracle.spmm_rounded_16(crow, col, None, x, torch.float16).float().numpy()[:, 0]
+    assert h[3] == np.inf  # 120000 overflows fp16
+    assert h[0] == 1.00390625  # fp16 represents 1 + 2^-8 exactly
