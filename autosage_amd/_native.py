@@ -28,7 +28,7 @@ from typing import Optional
 import torch
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
 # 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
@@ -66,8 +66,9 @@ _SIGNATURES = {
     "as_spmm_csr_rounded_16": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_i64,
-         _c_ptr],
+         _c_i64, _c_ptr],
     ),
+    "as_spmm_rounded_16_group_degree": (_c_i64, [_c_i64]),
     "as_csr_attention_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_csr_attention_colslice_f32": (
         _c_int,
@@ -286,10 +287,12 @@ def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
     lib = library()
     full = lib.as_spmm_colslice_workspace_bytes(n, f)
     ws = _workspace(min(full, _colslice_workspace_cap()), x.device)
+    threshold = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices))))
+    sliced, grouped = row_counts(crow, threshold, int(lib.as_spmm_rounded_16_group_degree(f)))
     with torch.cuda.device(x.device):
         status = lib.as_spmm_csr_rounded_16(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, DTYPES_16[x.dtype],
-            int(bool(column_slices)), _ptr(ws), ws.numel(), sliced_rows(crow, column_slices), _stream(x.device),
+            int(bool(column_slices)), _ptr(ws), ws.numel(), sliced, grouped, _stream(x.device),
         )
     _raise(status, "autosage::spmm_csr (16-bit)")
     return y
@@ -490,30 +493,37 @@ def columns_ascending(crow: torch.Tensor, col: torch.Tensor) -> bool:
     return result
 
 
-_SLICED_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+_ROW_COUNT_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
 
 
-def sliced_rows(crow: torch.Tensor, column_slices: bool) -> int:
-    """Rows the column-sliced SpMM slices (degree >= its threshold): a
-    per-graph constant that sizes its launches, computed once per live,
-    unmodified ``crow`` (one host sync) and memoised."""
-    threshold = int(library().as_spmm_colslice_min_degree(int(bool(column_slices))))
-    key = (id(crow), crow._version, threshold)
+def row_counts(crow: torch.Tensor, long_from: int, short_below: int) -> tuple[int, int]:
+    """(rows of degree >= ``long_from``, rows of degree < ``short_below``):
+    per-graph constants that size the column-sliced SpMM's launches,
+    computed once per live, unmodified ``crow`` (one host sync) and
+    memoised."""
+    key = (id(crow), crow._version, long_from, short_below)
     with _SORTED_LOCK:
-        hit = _SLICED_MEMO.get(key)
+        hit = _ROW_COUNT_MEMO.get(key)
         if hit is not None and hit[0]() is crow:
-            _SLICED_MEMO.move_to_end(key)
+            _ROW_COUNT_MEMO.move_to_end(key)
             return hit[1]
-    count = int(((crow[1:] - crow[:-1]) >= threshold).sum().item())
+    deg = crow[1:] - crow[:-1]
+    counts = torch.stack([(deg >= long_from).sum(), (deg < short_below).sum()]).tolist()
+    result = (int(counts[0]), int(counts[1]))
     try:
         ref = weakref.ref(crow)
     except TypeError:
-        return count
+        return result
     with _SORTED_LOCK:
-        _SLICED_MEMO[key] = (ref, count)
-        while len(_SLICED_MEMO) > _SORTED_MEMO_SIZE:
-            _SLICED_MEMO.popitem(last=False)
-    return count
+        _ROW_COUNT_MEMO[key] = (ref, result)
+        while len(_ROW_COUNT_MEMO) > _SORTED_MEMO_SIZE:
+            _ROW_COUNT_MEMO.popitem(last=False)
+    return result
+
+
+def sliced_rows(crow: torch.Tensor, column_slices: bool) -> int:
+    """Rows the column-sliced SpMM slices (degree >= its threshold)."""
+    return row_counts(crow, int(library().as_spmm_colslice_min_degree(int(bool(column_slices)))), 0)[0]
 
 
 def _maybe_validate(crow: torch.Tensor, col: torch.Tensor) -> None:

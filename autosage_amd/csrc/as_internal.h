@@ -56,5 +56,9 @@ size_t bin_workspace_bytes(int64_t n);
 int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold,
                     int buckets, int light_buckets, int32_t* order,
                     int32_t* counts, void* workspace, hipStream_t stream);
+// After launch_bin_rows on `workspace`: device address of the order index at
+// which bucket `bucket` (heavy buckets first, then light ones) starts; null
+// for n = 0.
+const int32_t* bin_bucket_start(const void* workspace, int64_t n, int bucket);
 
 }  // namespace as

@@ -150,6 +150,14 @@ size_t bin_workspace_bytes(int64_t n) {
   return 2 * align_up(static_cast<size_t>(tiles) * (2 * kMaxHeavyBuckets) * sizeof(int32_t), 256);
 }
 
+const int32_t* bin_bucket_start(const void* workspace, int64_t n, int bucket) {
+  const int64_t tiles = bin_tiles(n);
+  if (tiles <= 0) return nullptr;
+  const int32_t* offsets =
+      reinterpret_cast<const int32_t*>(static_cast<const char*>(workspace) + bin_workspace_bytes(n) / 2);
+  return offsets + static_cast<int64_t>(bucket) * tiles;
+}
+
 int launch_bin_rows(const int64_t* crow, int64_t n, int64_t threshold, int buckets, int light_buckets,
                     int32_t* order, int32_t* counts, void* workspace, hipStream_t stream) {
   if (buckets < 1 || buckets > kMaxHeavyBuckets || light_buckets < 1 || light_buckets > kMaxHeavyBuckets)

@@ -477,6 +477,94 @@ __device__ __forceinline__ void slice_wide(const int64_t* __restrict__ col, cons
   }
 }
 
+// Short rows of 16-bit features, one lane group of G lanes per row and
+// 64/G rows per wave: each group walks its own row (one edge per gather
+// instruction per group, no reduction across groups), so a wave keeps 64/G
+// rows' dependent loads (order, crow, columns, gathers) in flight instead of
+// one.  The column indices of a block of G edges are loaded one per lane and
+// handed to the group by ds_bpermute; lanes past their row's end read column
+// 0 (valid) and add nothing.  Only rows of degree below 4·G take this form
+// (a lane group would walk a long row alone); 16-bit results do not depend
+// on the order of the fp64 additions, so both forms give the same bits.
+#ifndef AS_COLSLICE_GROUPED_BLOCKS
+#define AS_COLSLICE_GROUPED_BLOCKS 4
+#endif
+constexpr int kGroupedMaxBlocks = AS_COLSLICE_GROUPED_BLOCKS;  // grouped rows have fewer than 4·G edges (0: none)
+
+template <typename T, int G, bool HAS_VAL, int U, bool OFF32>
+__device__ __forceinline__ void short_rows_grouped(const int64_t* __restrict__ crow, const int64_t* __restrict__ col,
+                                                   const T* __restrict__ val, const T* __restrict__ x,
+                                                   T* __restrict__ y, int64_t F, const int32_t* __restrict__ order,
+                                                   int64_t item0, int64_t end, int64_t f0) {
+  constexpr int P = 16 / static_cast<int>(sizeof(T));
+  const int lane = lane_id();
+  const int grp = lane / G;
+  const int gl = lane % G;
+  const int64_t item = item0 + grp;
+  int64_t row = -1, rs = 0;
+  int deg = 0;  // below the slicing threshold, so it fits an int
+  if (item < end) {
+    row = order[item];
+    rs = crow[row];
+    deg = static_cast<int>(crow[row + 1] - rs);
+  }
+  int maxdeg = deg;
+#pragma unroll
+  for (int o = G; o < kWave; o <<= 1) maxdeg = max(maxdeg, __shfl_xor(maxdeg, o, kWave));
+  maxdeg = uniform_i32(maxdeg);
+  const int64_t fl = f0 + P * static_cast<int64_t>(gl);
+  const bool active = fl < F;
+  const uint32_t lane_bytes = static_cast<uint32_t>((active ? fl : f0) * sizeof(T));
+  const uint32_t row_bytes = static_cast<uint32_t>(F * sizeof(T));
+  const char* __restrict__ xb = reinterpret_cast<const char*>(x);
+  double acc[P];
+#pragma unroll
+  for (int v = 0; v < P; ++v) acc[v] = 0.0;
+  for (int base = 0; base < maxdeg; base += G) {
+    int my_col = 0;
+    float my_w = 1.f;
+    if (base + gl < deg) {
+      my_col = static_cast<int>(col[rs + base + gl]);
+      if constexpr (HAS_VAL) my_w = Elem<T>::at(val, rs + base + gl);
+    }
+    const int lim = maxdeg - base < G ? maxdeg - base : G;
+    for (int j = 0; j < lim; j += U) {
+      RawVec<16> xv[U];
+      float w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int addr = (grp * G + j + u) * 4;
+        const int c = __builtin_amdgcn_ds_bpermute(addr, my_col);
+        w[u] = 1.f;
+        if constexpr (HAS_VAL) w[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(my_w)));
+        if constexpr (OFF32) {
+          xv[u] = load_raw<16>(xb + (__umul24(static_cast<uint32_t>(c), row_bytes) + lane_bytes));
+        } else {
+          xv[u] = load_raw<16>(xb + row_offset(c, F) * sizeof(T) + lane_bytes);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (base + j + u < deg) {
+#pragma unroll
+          for (int v = 0; v < P; ++v) {
+            const double xe = static_cast<double>(Elem<T>::get(xv[u].w, v));
+            if constexpr (HAS_VAL) {
+              acc[v] = __builtin_fma(static_cast<double>(w[u]), xe, acc[v]);
+            } else {
+              acc[v] = acc[v] + xe;
+            }
+          }
+        }
+      }
+    }
+  }
+  if (row >= 0 && active) {
+#pragma unroll
+    for (int v = 0; v < P; ++v) store_out(y + row * F + fl + v, acc[v]);
+  }
+}
+
 // One chunk of the work: rows order[item_begin, item_begin + items); the
 // first counts[0] rows of the order are sliced, the rest are short.  A launch
 // is made of groups of 8 workgroups (one per XCD, by blockIdx % 8):
@@ -504,6 +592,12 @@ struct SliceChunk {
   int64_t sliced;        // the caller's count of sliced rows in the chunk, < 0 if unknown
 };
 
+// Where the grouped short rows (16-bit, degree below 4·G) start in the order:
+// the start of a light degree bucket of the binning, read on the device.
+struct GroupedRows {
+  const int32_t* start;  // null: no grouped rows
+};
+
 #ifndef AS_COLSLICE_SLICE_GROUPS
 #define AS_COLSLICE_SLICE_GROUPS 4096
 #endif
@@ -518,7 +612,7 @@ constexpr int64_t kMaxSliceGroupsHinted = 65536;
 // be sliced (the caller's hint; < 0 if unknown).  Any counts >= 1 cover all
 // rows, since the waves stride; the hint only avoids looping waves (too few
 // groups) and idle ones (too many).
-inline void chunk_groups(SliceChunk& c, int64_t sliced) {
+inline void chunk_groups(SliceChunk& c, int64_t sliced, int64_t grouped, int64_t rows_per_wave) {
   int64_t gs, gh;
   if (sliced < 0) {
     gs = (c.items + kWavesPerBlock - 1) / kWavesPerBlock;
@@ -526,8 +620,12 @@ inline void chunk_groups(SliceChunk& c, int64_t sliced) {
     if (gs > kSliceGroupsMax) gs = kSliceGroupsMax;
   } else {
     if (sliced > c.items) sliced = c.items;
+    // short waves: one per other short row, one per rows_per_wave grouped rows
+    if (grouped < 0) grouped = 0;
+    if (grouped > c.items - sliced) grouped = c.items - sliced;
+    const int64_t waves = c.items - sliced - grouped + (grouped + rows_per_wave - 1) / rows_per_wave;
     gs = (sliced + kWavesPerBlock - 1) / kWavesPerBlock;
-    gh = (c.items - sliced + kSlices * kWavesPerBlock - 1) / (kSlices * kWavesPerBlock);
+    gh = (waves + kSlices * kWavesPerBlock - 1) / (kSlices * kWavesPerBlock);
     if (gs > kMaxSliceGroupsHinted) gs = kMaxSliceGroupsHinted;
   }
   if (gh > kShortGroupsMax) gh = kShortGroupsMax;
@@ -586,14 +684,25 @@ __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* 
                                                      const int64_t* __restrict__ col, const T* __restrict__ val,
                                                      const T* __restrict__ x, T* __restrict__ y, int64_t F,
                                                      const int32_t* __restrict__ order,
-                                                     const int32_t* __restrict__ counts, const SliceChunk& c) {
+                                                     const int32_t* __restrict__ counts, const SliceChunk& c,
+                                                     GroupedRows grouped) {
   constexpr int64_t kTile = 16 * V / static_cast<int64_t>(sizeof(T));
   const int64_t tile_blocks = kSlices * c.short_groups;
   const int64_t tile = hb / tile_blocks;
   const int64_t k = hb - tile * tile_blocks;
+  const int64_t waves = tile_blocks * kWavesPerBlock;  // short waves per tile
+  const int64_t w = k * kWavesPerBlock + wave_in_block();
+  const int64_t fs = first_short(counts, c);
   const int64_t end = c.item_begin + c.items;
-  for (int64_t item = first_short(counts, c) + k * kWavesPerBlock + wave_in_block(); item < end;
-       item += tile_blocks * kWavesPerBlock) {
+  int64_t split = end;  // grouped rows: [split, end)
+  if constexpr (sizeof(T) == 2 && V >= 8) {
+    if (grouped.start != nullptr) {
+      split = *grouped.start;
+      split = split < fs ? fs : (split > end ? end : split);
+    }
+  }
+  // one wave per short row
+  for (int64_t item = fs + w; item < split; item += waves) {
     const int64_t row = uniform_i64(order[item]);
     const int64_t rs = uniform_i64(crow[row]);
     const int64_t deg = uniform_i64(crow[row + 1]) - rs;
@@ -601,6 +710,13 @@ __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* 
       slice_wide<T, V, HAS_VAL, OFF32>(col, val, x, y + row * F, F, rs, rs + deg, tile * kTile);
     } else {
       slice_row<T, V, HAS_VAL, 8>(col, val, x, y + row * F, F, rs, rs + deg);
+    }
+  }
+  // 16-bit wide lanes: 64/V grouped rows per wave
+  if constexpr (sizeof(T) == 2 && V >= 8) {
+    constexpr int64_t kRows = kWave / V;
+    for (int64_t item0 = split + w * kRows; item0 < end; item0 += waves * kRows) {
+      short_rows_grouped<T, V, HAS_VAL, 1, OFF32>(crow, col, val, x, y, F, order, item0, end, tile * kTile);
     }
   }
 }
@@ -648,8 +764,11 @@ __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, con
 // in order, are the MG slice groups and then the short groups.  Group g
 // reduces iff floor((g+1)·RG/TG) > floor(g·RG/TG); floor(g·RG/TG) groups
 // before it reduce, so every block keeps blockIdx % 8 as its XCD.
+// At least 7 waves per SIMD: the 16-bit forms (8 fp64 sums per lane, the
+// grouped short rows) otherwise take more VGPRs than that leaves; the fp32
+// forms are below the limit already.
 template <typename T, int V, bool HAS_VAL, int VR, bool OFF32>
-__global__ __launch_bounds__(kBlock) void colslice_step_kernel(const int64_t* __restrict__ crow,
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(7))) void colslice_step_kernel(const int64_t* __restrict__ crow,
                                                                const int64_t* __restrict__ col,
                                                                const T* __restrict__ val, const T* __restrict__ x,
                                                                T* __restrict__ y, int64_t F,
@@ -657,7 +776,7 @@ __global__ __launch_bounds__(kBlock) void colslice_step_kernel(const int64_t* __
                                                                const int32_t* __restrict__ counts,
                                                                const int32_t* __restrict__ off, SliceChunk m,
                                                                SliceChunk r, int64_t chunk_stride, int64_t TG,
-                                                               int64_t RG, int64_t MG) {
+                                                               int64_t RG, int64_t MG, GroupedRows grouped) {
   const int64_t g = blockIdx.x / kSlices;
   const int64_t within = blockIdx.x % kSlices;
   const int64_t before = g * RG / TG;
@@ -672,7 +791,7 @@ __global__ __launch_bounds__(kBlock) void colslice_step_kernel(const int64_t* __
                                                chunk_stride);
   } else {
     colslice_short_block<T, V, HAS_VAL, OFF32>((work - MG) * kSlices + within, crow, col, val, x, y, F, order,
-                                               counts, m);
+                                               counts, m, grouped);
   }
 }
 
@@ -711,6 +830,7 @@ struct StepArgs {
   const int32_t* order;
   const int32_t* counts;
   const int32_t* off;
+  GroupedRows grouped;
 };
 
 struct GroupCounts {
@@ -722,7 +842,7 @@ void launch_one(dim3 grid, hipStream_t s, const StepArgs& a, const SliceChunk& m
                 int64_t stride, const GroupCounts& n) {
   hipLaunchKernelGGL((colslice_step_kernel<T, V, HAS_VAL, VR, OFF32>), grid, dim3(kBlock), 0, s, a.crow, a.col,
                      static_cast<const T*>(a.val), static_cast<const T*>(a.x), static_cast<T*>(a.y), a.f, a.order,
-                     a.counts, a.off, m, r, stride, n.TG, n.RG, n.MG);
+                     a.counts, a.off, m, r, stride, n.TG, n.RG, n.MG, a.grouped);
 }
 
 // OFF32 only matters for the ds_bpermute form of the wide lanes (V <= 16);
@@ -787,10 +907,18 @@ void launch_step(int v, bool off32, int vr, bool has_val, int64_t tiles, hipStre
 
 enum Slicing { kSliceColumns = 0, kSliceEdges = 1 };
 
+// Degree limit of the grouped short rows (16-bit elements, 16-byte lanes):
+// 4·G for the G lanes per edge that F takes; 0 when rows are not grouped.
+inline int64_t grouped_degree(int64_t f, int64_t elem_bytes) {
+  if (elem_bytes != 2 || f <= 0 || f % 8 != 0) return 0;
+  const int64_t g = f <= 64 ? 8 : (f <= 128 ? 16 : 32);
+  return kGroupedMaxBlocks * g;
+}
+
 template <typename T>
 int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
                  int64_t nnz, int64_t f, Slicing slicing, void* workspace, size_t workspace_bytes,
-                 int64_t sliced_rows, void* stream) {
+                 int64_t sliced_rows, int64_t grouped_rows, void* stream) {
   int st = validate_spmm(crow, col, x, y, n, nnz, f);
   if (st != AS_OK) return st;
   if (n == 0 || f == 0) return AS_OK;
@@ -846,19 +974,41 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   const int64_t min_degree = slicing == kSliceColumns ? kColsliceMinDegree : kEdgeSliceMinDegree;
   launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, off, s, slicing == kSliceEdges);
   // order: rows of degree >= min_degree (sliced) in 8 log2-degree buckets,
-  // longest first; then the short rows in row order
-  st = launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
+  // longest first; then the short rows, for 16-bit elements also in 8
+  // log2-degree buckets (a wave of grouped short rows then holds rows of
+  // similar degree)
+  const int light_buckets = E == 2 ? kMaxHeavyBuckets : 1;
+  st = launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, light_buckets, order, counts, bin_ws, s);
   if (st != AS_OK) return st;
 
+  // grouped short rows: the light buckets from level L on, L the first whose
+  // rows all have degree below the limit (light bucket L holds degrees up to
+  // (min_degree - 1) >> L, and bucket L - 1 none below min_degree >> L; both
+  // are powers of two, so these are exactly the rows below the limit)
+  GroupedRows grouped{nullptr};
+  const int64_t limit = v >= 8 ? grouped_degree(f, E) : 0;
+  if (limit > 0) {
+    int level = 0;
+    while (level < light_buckets && ((min_degree - 1) >> level) >= limit) ++level;
+    if (level < light_buckets) grouped.start = bin_bucket_start(bin_ws, n, kMaxHeavyBuckets + level);
+  }
+  const int64_t rows_per_wave = grouped.start != nullptr ? kWave / v : 1;
+  if (grouped.start == nullptr) grouped_rows = 0;
+
   // launch k: slice work of chunk k beside the reduction of chunk k - 1
-  const StepArgs a{crow, col, val, x, y, f, order, counts, off};
+  const StepArgs a{crow, col, val, x, y, f, order, counts, off, grouped};
   const int64_t chunks = (n + chunk - 1) / chunk;
   SliceChunk previous{0, 0, buffers[1], 1, 1, -1};
   for (int64_t k = 0; k <= chunks; ++k) {
     SliceChunk current{k * chunk, 0, buffers[k % 2], 1, 1, -1};
     if (k < chunks) current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
-    // the sliced rows come first in the order
-    chunk_groups(current, sliced_rows < 0 ? -1 : (sliced_rows > current.item_begin ? sliced_rows - current.item_begin : 0));
+    // the sliced rows come first in the order, the grouped ones last
+    const int64_t chunk_end = current.item_begin + current.items;
+    const int64_t grouped_begin = grouped_rows < 0 || grouped_rows > n ? chunk_end : n - grouped_rows;
+    const int64_t from = grouped_begin > current.item_begin ? grouped_begin : current.item_begin;
+    chunk_groups(current,
+                 sliced_rows < 0 ? -1 : (sliced_rows > current.item_begin ? sliced_rows - current.item_begin : 0),
+                 chunk_end > from ? chunk_end - from : 0, rows_per_wave);
 #if AS_COLSLICE_OVERLAP
     launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, previous, chunk);
 #else
@@ -891,14 +1041,16 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
                              int64_t sliced_rows, void* stream) {
   as::clear_error();
   const int st = as::colslice_run<float>(crow, col, val, x, y, n, nnz, f, as::kSliceColumns, workspace,
-                                         workspace_bytes, sliced_rows, stream);
+                                         workspace_bytes, sliced_rows, 0, stream);
   if (st != AS_OK) return st;
   return as::check_launch("spmm_csr_colslice");
 }
 
+int64_t as_spmm_rounded_16_group_degree(int64_t f) { return as::grouped_degree(f, 2); }
+
 int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
                            int64_t n, int64_t nnz, int64_t f, int dtype, int column_slices, void* workspace,
-                           size_t workspace_bytes, int64_t sliced_rows, void* stream) {
+                           size_t workspace_bytes, int64_t sliced_rows, int64_t grouped_rows, void* stream) {
   as::clear_error();
   if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
     return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
@@ -907,9 +1059,9 @@ int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void* 
   const as::Slicing slicing = column_slices ? as::kSliceColumns : as::kSliceEdges;
   const int st = dtype == AS_DTYPE_BF16
                      ? as::colslice_run<as::Bf16>(crow, col, val, x, y, n, nnz, f, slicing, workspace,
-                                                  workspace_bytes, sliced_rows, stream)
+                                                  workspace_bytes, sliced_rows, grouped_rows, stream)
                      : as::colslice_run<as::Fp16>(crow, col, val, x, y, n, nnz, f, slicing, workspace,
-                                                  workspace_bytes, sliced_rows, stream);
+                                                  workspace_bytes, sliced_rows, grouped_rows, stream);
   if (st != AS_OK) return st;
   return as::check_launch("spmm_csr_rounded_16");
 }

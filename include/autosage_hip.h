@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 2
+#define AS_ABI_VERSION 3
 
 typedef enum as_status {
   AS_OK = 0,
@@ -145,14 +145,24 @@ int64_t as_spmm_colslice_min_degree(int column_slices);
  * (columns must ascend within rows); 0: rows of degree >= 1024 are cut into
  * 8 equal runs of edges instead (any column order).  x, y and val 2-byte
  * aligned; F a multiple of 8 with 16-byte aligned x takes 16-byte lanes.
+ * Short rows of degree below as_spmm_rounded_16_group_degree(f) are
+ * summed several to a wavefront (a lane group each), the other rows one
+ * wavefront each or sliced.
  * sliced_rows: as for as_spmm_csr_colslice_f32, with the degree
- * as_spmm_colslice_min_degree(column_slices). */
+ * as_spmm_colslice_min_degree(column_slices); grouped_rows: the number of
+ * rows of degree below as_spmm_rounded_16_group_degree(f), else -1.  Both
+ * only size the launches; the result is the same for any values. */
 int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
                            const void* val, const void* x, void* y,
                            int64_t n, int64_t nnz, int64_t f, int dtype,
                            int column_slices, void* workspace,
                            size_t workspace_bytes, int64_t sliced_rows,
-                           void* stream);
+                           int64_t grouped_rows, void* stream);
+
+/* Degree below which as_spmm_csr_rounded_16 sums rows several to a
+ * wavefront for F features (32, 64 or 128 for F <= 64, <= 128, more; 0 when
+ * F is not a multiple of 8). */
+int64_t as_spmm_rounded_16_group_degree(int64_t f);
 
 /* out[e] = <query[row(e)], key[col[e]]> for every nonzero, CSR order.
  * Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134), op schema :192.

@@ -70,13 +70,15 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_last_error() == b"sample size must lie in [0, N]"
     assert lib.as_induced_sample_workspace_bytes(1000) >= 4000
     # 16-bit SpMM: unknown dtype code, misaligned pointers, null inputs
-    assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 3, 1, None, 0, -1, None) == 1
+    assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 3, 1, None, 0, -1, -1, None) == 1
     assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"
-    assert lib.as_spmm_csr_rounded_16(None, None, None, 1, None, 4, 0, 8, 1, 1, None, 0, -1, None) == 1
+    assert lib.as_spmm_csr_rounded_16(None, None, None, 1, None, 4, 0, 8, 1, 1, None, 0, -1, -1, None) == 1
     assert lib.as_last_error() == b"x, y and val must be 2-byte aligned"
-    assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 2, 0, None, 0, -1, None) == 1
+    assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 2, 0, None, 0, -1, -1, None) == 1
     assert lib.as_last_error() == b"null pointer argument"
     assert lib.as_spmm_colslice_min_degree(1) == 128 and lib.as_spmm_colslice_min_degree(0) == 1024
+    assert [lib.as_spmm_rounded_16_group_degree(f) for f in (8, 64, 72, 128, 136, 512, 7, 0)] == [
+        32, 32, 64, 64, 128, 128, 0, 0]
     # n == 0 is a no-op success
     assert lib.as_spmm_csr_f32(None, None, None, None, None, 0, 0, 8, 1, None) == 0
 

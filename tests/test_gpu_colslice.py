@@ -217,16 +217,22 @@ def test_sliced_rows_hint_only_sizes_the_launches():
     torch.cuda.synchronize()
     for y in outs[1:]:
         assert torch.equal(y, outs[0])
-    # 16-bit features, edge slices (threshold 1024)
+    # 16-bit features, column and edge slices (thresholds 128 and 1024), with
+    # the count of grouped short rows (degree below 64 for F = 128) too
     xb = d_x.to(torch.bfloat16)
-    exact16 = _native.sliced_rows(d_crow, False)
-    outs = []
-    for hint in (-1, 0, exact16, exact16 + 500):
-        y = torch.empty_like(xb)
-        status = lib.as_spmm_csr_rounded_16(d_crow.data_ptr(), d_col.data_ptr(), 0, xb.data_ptr(), y.data_ptr(), n,
-                                            col.size, f, 1, 0, ws.data_ptr(), ws.numel(), hint, stream)
-        assert status == 0, lib.as_last_error()
-        outs.append(y)
-    torch.cuda.synchronize()
-    for y in outs[1:]:
-        assert torch.equal(y, outs[0])
+    limit = lib.as_spmm_rounded_16_group_degree(f)
+    assert limit == 64
+    for column_slices in (1, 0):
+        sliced, grouped = _native.row_counts(d_crow, lib.as_spmm_colslice_min_degree(column_slices), limit)
+        assert grouped == int((np.diff(crow) < limit).sum()) and 0 < grouped < n
+        outs = []
+        for hints in ((-1, -1), (0, 0), (sliced, grouped), (sliced + 500, n), (sliced, 0), (1, 3 * n), (-1, grouped)):
+            y = torch.empty_like(xb)
+            status = lib.as_spmm_csr_rounded_16(d_crow.data_ptr(), d_col.data_ptr(), 0, xb.data_ptr(), y.data_ptr(),
+                                                n, col.size, f, 1, column_slices, ws.data_ptr(), ws.numel(), *hints,
+                                                stream)
+            assert status == 0, lib.as_last_error()
+            outs.append(y)
+        torch.cuda.synchronize()
+        for y in outs[1:]:
+            assert torch.equal(y, outs[0])
