@@ -277,7 +277,9 @@ def spmm_csr_colslice_impl(crow, col, val, x):
 def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
     """SpMM on bf16/fp16 features (weights of the same type): every output is
     the fp64 sum of the exact products rounded to fp32 and then to x's dtype,
-    the same bits whatever the schedule.  ``column_slices``: one column slice
+    the same bits whatever the schedule when that sum is exact.  Short rows
+    of degree below ``as_spmm_rounded_16_group_degree(F)`` run several to a
+    wavefront.  ``column_slices``: one column slice
     per XCD (columns must ascend within rows); otherwise rows of degree >= 1024
     are cut into 8 equal runs of edges."""
     y = torch.empty_like(x)

@@ -33,11 +33,14 @@
 // about one fp32 rounding of the exact sum (tighter than a sequential fp32
 // sum), and the result is deterministic.  It is not bit-identical to the
 // sequential CSR product: that order is kept by spmm.hip.  With bf16 or fp16
-// elements (weights rounded to the same type) the products are exact and the
-// fp64 sums carry ~2^-53 relative error, so the result rounded to fp32 and
-// then to the element type (round to nearest even both times) is the same
-// whatever the order of the additions: every schedule here gives the same
-// bits, those of an fp64 sum in CSR order rounded the same way.
+// elements (weights rounded to the same type) the products are exact and
+// the result is the fp64 sum rounded to fp32 and then to the element type
+// (round to nearest even both times).  When the fp64 sum is exact (the
+// products' bits span at most 53 places) it does not depend on the order of
+// the additions, and every schedule here gives the bits of an fp64 sum in
+// CSR order rounded the same way; otherwise the sums differ by less than
+// 2^-52 of the largest partial, which changes the rounded result only for a
+// sum that close to a tie.
 #include <type_traits>
 
 #include "as_device.h"
@@ -484,8 +487,8 @@ __device__ __forceinline__ void slice_wide(const int64_t* __restrict__ col, cons
 // one.  The column indices of a block of G edges are loaded one per lane and
 // handed to the group by ds_bpermute; lanes past their row's end read column
 // 0 (valid) and add nothing.  Only rows of degree below 4·G take this form
-// (a lane group would walk a long row alone); 16-bit results do not depend
-// on the order of the fp64 additions, so both forms give the same bits.
+// (a lane group would walk a long row alone); both forms sum the same exact
+// products in fp64.
 #ifndef AS_COLSLICE_GROUPED_BLOCKS
 #define AS_COLSLICE_GROUPED_BLOCKS 4
 #endif

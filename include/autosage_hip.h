@@ -139,7 +139,10 @@ int64_t as_spmm_colslice_min_degree(int column_slices);
  * the feature type (autosage/_auto.py:281-287); the CPU torch path has no
  * bf16/fp16 CSR product.  Result: every output is the fp64 sum of the exact
  * products, rounded to fp32 and then to the element type (round to nearest
- * even both times), which does not depend on the order of the additions.
+ * even both times).  The fp64 sum does not depend on the order of the
+ * additions when it is exact (the products' bits span at most 53 places);
+ * otherwise its error is below 2^-52 of the largest partial sum, and two
+ * schedules can round differently only for a sum that close to a tie.
  * Same kernels and workspace as as_spmm_csr_colslice_f32 (size from
  * as_spmm_colslice_workspace_bytes).  column_slices != 0: 8 column slices
  * (columns must ascend within rows); 0: rows of degree >= 1024 are cut into

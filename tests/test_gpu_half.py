@@ -3,11 +3,14 @@
 
 The reference has no kernel for these types (its op raises, its scheduler
 runs torch.sparse.mm).  The rule here: every output is the fp64 sum of the
-exact products rounded to fp32 and then to the 16-bit type, which does not
-depend on the order of the additions.  So the bar is bit-identity with the
-oracle (``oracle.spmm_rounded_16``) for every schedule: column slices
-(ascending columns), edge slices (shuffled columns), short rows, hub rows,
-empty rows, any F.
+exact products rounded to fp32 and then to the 16-bit type.  An exact fp64
+sum does not depend on the order of the additions; an inexact one differs
+between orders by less than 2^-52 of its largest partial, which changes the
+rounded result only for a sum that close to a tie (random inputs do not
+produce one).  So the bar is bit-identity with the oracle
+(``oracle.spmm_rounded_16``, an fp64 sum in CSR order) for every schedule:
+column slices (ascending columns), edge slices (shuffled columns), grouped
+and one-wave short rows, hub rows, empty rows, any F.
 """
 
 from __future__ import annotations
