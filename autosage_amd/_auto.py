@@ -706,6 +706,9 @@ def sddmm_csr_auto(
     if not query.is_cuda:
         run, name = _prepare_sddmm_baseline(crow, col, query, key)
         return run(), {**_cpu_info("sddmm"), "baseline": name}
+    if query.dtype in _DTYPES_16:
+        _require_native()
+        return _sddmm_auto_16(crow, col, query, key, SchedulerConfig.from_env(guardrail=guardrail), verbose)
     if query.dtype != torch.float32:
         run, name = _prepare_sddmm_baseline(crow, col, query, key)
         return run(), {**_cpu_info("sddmm"), "baseline": name, "reason": "AutoSAGE CUDA kernels require float32 features"}
@@ -769,6 +772,67 @@ def sddmm_csr_auto(
         _decide_on_full_graph(result, options, lambda o: _run_sddmm_choice("autosage", o, crow, col, query, key),
                               full_baseline)
     output = _run_sddmm_choice(result["choice"], result["candidate"], crow, col, query, key)
+    if config.cache:
+        cache.store(device, graph, result)
+    log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})
+    _verbose("sddmm", result, verbose)
+    return output, result
+
+
+# Split points timed for 16-bit SDDMM: (waves per block, hub threshold).
+_SDDMM_16_OPTIONS = ([4, 1024], [8, 4096])
+_SDDMM_16_NOTE = ("bf16/fp16 SDDMM is native (fp64 sums of exact products, rounded); the gather-dot baseline "
+                  "rounds every product to the 16-bit type and is not a candidate")
+
+
+def _sddmm_auto_16(crow, col, query, key, config: SchedulerConfig, verbose: bool) -> tuple[torch.Tensor, dict]:
+    """bf16 / fp16 query and key (the reference runs its gather-dot baseline
+    for them, ``_auto.py:575-581``).  Every output is the rounded fp64 sum
+    whatever the split, so the split points of ``_SDDMM_16_OPTIONS`` are
+    timed once on the full graph and the faster is cached under the usual key
+    (which includes the dtype)."""
+    device = device_signature()
+    graph = graph_signature_memo(crow, col, query.size(1), "sddmm", dtype=query.dtype)
+    cache = ScheduleCache()
+    options = [list(o) for o in _SDDMM_16_OPTIONS]
+    if config.cache:
+        record = cache.lookup(device, graph)
+        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
+            result = record["result"]
+            if result.get("choice") == "autosage" and result.get("candidate") in options:
+                return (_run_sddmm_choice("autosage", result["candidate"], crow, col, query, key),
+                        {**result, "from_cache": True})
+    if config.replay_only:
+        info = _replay_miss("sddmm", "gather-dot")
+        info.update(choice="autosage", candidate=options[0], reason="cache miss; " + _SDDMM_16_NOTE)
+        return _run_sddmm_choice("autosage", options[0], crow, col, query, key), info
+    wall_start = time.perf_counter()
+    times = [
+        _time_cuda(lambda o=o: _run_sddmm_choice("autosage", o, crow, col, query, key), warmup=1, iterations=3)[
+            "best_ms"]
+        for o in options
+    ]
+    best = min(range(len(options)), key=lambda i: times[i])
+    result: dict[str, Any] = {
+        "operation": "sddmm",
+        "schema_version": AUTOTUNE_SCHEMA_VERSION,
+        "choice": "autosage",
+        "candidate": options[best],
+        "baseline": "gather-dot",
+        "guardrail": config.guardrail,
+        "configuration": config.tuning_signature(),
+        "probe_rows": int(crow.numel() - 1),
+        "probe_nonzeros": int(col.numel()),
+        "sampling_ms": 0.0,
+        "probe_ms": (time.perf_counter() - wall_start) * 1000.0,
+        "baseline_probe_ms": None,
+        "autosage_probe_ms": times[best],
+        "sampled_speedup": None,
+        "candidates": [{"candidate": o, "best_ms": t} for o, t in zip(options, times)],
+        "from_cache": False,
+        "reason": _SDDMM_16_NOTE,
+    }
+    output = _run_sddmm_choice("autosage", options[best], crow, col, query, key)
     if config.cache:
         cache.store(device, graph, result)
     log_probe({"timestamp": time.time(), "device": device, "graph": graph, "result": result})

@@ -8,8 +8,9 @@ backward formulas built from the same native kernels:
   ``dX = Aᵀ·dY`` — a native SpMM over the transposed CSR — and
   ``dval[e] = <dY[row(e)], X[col(e)]>`` — a native SDDMM;
   both on the degree-split schedules (same bits as the whole-graph kernels).
-  With bf16 / fp16 features ``dX`` comes from the rounded 16-bit SpMM; the
-  weight gradient would need a 16-bit SDDMM and raises.
+  With bf16 / fp16 features both come from the rounded 16-bit kernels
+  (SpMM and SDDMM: fp64 sums of exact products, rounded to fp32 and then to
+  the 16-bit type).
 * ``s[e] = <Q[row(e)], K[col(e)]>``:
   ``dQ = A_ds·K`` (SpMM with weights ``ds``) and ``dK = A_dsᵀ·Q``.
 
@@ -93,8 +94,6 @@ def _spmm_backward(ctx, grad_y: torch.Tensor):
         val_t = None if val is None else val.index_select(0, perm).contiguous()
         grad_x = _spmm(crow_t, col_t, val_t, grad_y)
     if val is not None and ctx.needs_input_grad[2]:
-        if x.dtype != torch.float32:
-            raise NotImplementedError("the weight gradient of a bf16/fp16 SpMM is not implemented")
         grad_val = _sddmm(crow, col, grad_y, x)
     # one gradient per schema argument (the split op has three int arguments more)
     extra = (None,) * (len(ctx.needs_input_grad) - 4)

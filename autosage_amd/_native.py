@@ -69,6 +69,11 @@ _SIGNATURES = {
          _c_i64, _c_ptr],
     ),
     "as_spmm_rounded_16_group_degree": (_c_i64, [_c_i64]),
+    "as_sddmm_csr_rounded_16": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_ptr, _c_size,
+         _c_ptr],
+    ),
     "as_csr_attention_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_csr_attention_colslice_f32": (
         _c_int,
@@ -179,10 +184,13 @@ def check_spmm_inputs(crow, col, val, x, allow_16: bool = False) -> None:
         _check(val.numel() == col.numel(), "val must contain one weight per nonzero")
 
 
-def check_sddmm_inputs(crow, col, query, key) -> None:
+def check_sddmm_inputs(crow, col, query, key, allow_16: bool = False) -> None:
     _check(crow.is_cuda and col.is_cuda and query.is_cuda and key.is_cuda, "all SDDMM inputs must be CUDA tensors")
     _check(crow.dtype == torch.long and col.dtype == torch.long, "crow and col must use torch.long indices")
-    _check(query.dtype == torch.float32 and key.dtype == torch.float32, "query and key must be float32")
+    if allow_16 and query.dtype in DTYPES_16:
+        _check(key.dtype == query.dtype, "query and key must use the same dtype")
+    else:
+        _check(query.dtype == torch.float32 and key.dtype == torch.float32, "query and key must be float32")
     _check(query.dim() == 2 and query.shape == key.shape, "query and key must have the same [N, F] shape")
     _check(crow.numel() == query.size(0) + 1, "crow must contain N + 1 entries")
     _check(
@@ -300,8 +308,16 @@ def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
     return y
 
 
+# Schedule of sddmm_csr on 16-bit inputs: any schedule gives the same bits,
+# so the whole-graph op takes the split one (hub rows in 2048-edge chunks).
+SDDMM_16_WAVES = 4
+SDDMM_16_HUB_THRESHOLD = 1024
+
+
 def sddmm_csr_impl(crow, col, query, key):
-    check_sddmm_inputs(crow, col, query, key)
+    check_sddmm_inputs(crow, col, query, key, allow_16=True)
+    if query.dtype in DTYPES_16:
+        return sddmm_rounded_16_impl(crow, col, query, key, SDDMM_16_WAVES, SDDMM_16_HUB_THRESHOLD)
     _maybe_validate(crow, col)
     nnz = col.numel()
     n, f = query.shape
@@ -319,7 +335,9 @@ def sddmm_csr_impl(crow, col, query, key):
 
 
 def sddmm_csr_split_impl(crow, col, query, key, warps_per_block, hub_threshold):
-    check_sddmm_inputs(crow, col, query, key)
+    check_sddmm_inputs(crow, col, query, key, allow_16=True)
+    if query.dtype in DTYPES_16:
+        return sddmm_rounded_16_impl(crow, col, query, key, warps_per_block, hub_threshold)
     _maybe_validate(crow, col)
     _check(warps_per_block in (2, 4, 8), "warps_per_block must be 2, 4, or 8")
     _check(0 < hub_threshold <= 2**31 - 1, "hub_threshold must be a positive 32-bit integer")
@@ -338,6 +356,35 @@ def sddmm_csr_split_impl(crow, col, query, key, warps_per_block, hub_threshold):
             int(hub_threshold), _ptr(ws), ws.numel(), _stream(query.device),
         )
     _raise(status, "autosage::sddmm_csr_split")
+    return out
+
+
+def sddmm_rounded_16_impl(crow, col, query, key, warps_per_block: int, hub_threshold: int):
+    """SDDMM on bf16/fp16 query and key: out[e] is the fp64 sum of the exact
+    products rounded to fp32 and then to the input dtype; the same bits for
+    any schedule when that sum is exact.  The split schedule of
+    ``sddmm_csr_split`` (rows of degree >= ``hub_threshold`` in 2048-edge
+    chunks)."""
+    check_sddmm_inputs(crow, col, query, key, allow_16=True)
+    _check(query.dtype in DTYPES_16, "query and key must be bfloat16 or float16")
+    _maybe_validate(crow, col)
+    _check(warps_per_block in (2, 4, 8), "warps_per_block must be 2, 4, or 8")
+    _check(0 < hub_threshold <= 2**31 - 1, "hub_threshold must be a positive 32-bit integer")
+    nnz = col.numel()
+    n, f = query.shape
+    if f == 0:
+        return torch.zeros(nnz, dtype=query.dtype, device=query.device)
+    out = torch.empty(nnz, dtype=query.dtype, device=query.device)
+    if n == 0 or nnz == 0:
+        return out
+    lib = library()
+    ws = _workspace(lib.as_sddmm_split_workspace_bytes(n), query.device)
+    with torch.cuda.device(query.device):
+        status = lib.as_sddmm_csr_rounded_16(
+            _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, DTYPES_16[query.dtype],
+            int(warps_per_block), int(hub_threshold), _ptr(ws), ws.numel(), _stream(query.device),
+        )
+    _raise(status, "autosage::sddmm_csr (16-bit)")
     return out
 
 

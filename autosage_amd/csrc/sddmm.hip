@@ -16,6 +16,7 @@
 // (xor o/S, inside the G-lane group); steps with o < S add slots in-lane.
 #include "as_device.h"
 #include "as_internal.h"
+#include "elem16.h"
 
 namespace as {
 
@@ -315,6 +316,252 @@ int launch_sddmm_scheduled(const SddmmArgs& a, int waves, int64_t hub_threshold,
   return AS_OK;
 }
 
+// ---- bf16 / fp16 SDDMM -------------------------------------------------------
+// out[e] = the fp64 sum of the exact products q[row(e), f]·k[col(e), f],
+// rounded to fp32 and then to the element type (round to nearest even both
+// times).  Products of two 16-bit values are exact in fp64, so an exact fp64
+// sum does not depend on the order of the additions, and every schedule here
+// gives the same bits.  There is no reference kernel for these types (its op
+// takes float32 only, csrc/sddmm_csr_op.cu:94; its scheduler runs the
+// gather-dot baseline, autosage/_auto.py:575-581).
+//
+// Vector lanes (F a multiple of 8 up to 512, 16-byte aligned rows): a lane
+// holds 8 consecutive features, chunk j + G·m of the row for m < MB; G lanes
+// per edge (the power of two covering F/8, at most 32), 64/G edges per
+// gather instruction.  The query row is converted to fp64 once per row and
+// kept in registers.  Other shapes take element lanes: 64 lanes per edge,
+// lane l adding features l, l + 64, ...
+// Edges are taken in blocks of 64: one coalesced load brings the block's
+// column indices (one block ahead), and ds_bpermute hands each lane group its
+// edge's column, so a pass waits for one round of key gathers only; UE
+// gathers per lane are in flight (all 64 edges of a block at once for G <= 8,
+// else 32, 16 or 8 at a time).
+template <typename T, int G, int MB, bool OFF32>
+__device__ __forceinline__ void dots16_vec(const int64_t* __restrict__ col, const T* __restrict__ key,
+                                           uint16_t* __restrict__ out, int64_t F, const double (&qd)[MB][8],
+                                           int64_t first, int64_t end, int64_t step, int g, int j) {
+  constexpr int NG = kWave / G;
+  constexpr int UE = NG >= 8 ? kWave / NG : (MB == 1 ? 8 : 4);  // gathers in flight per lane
+  constexpr int kSub = NG * UE;                                    // edges per sub-pass, <= 64
+  static_assert(kSub <= kWave, "a sub-pass stays inside its block of 64 edges");
+  const int lane = lane_id();
+  const int64_t chunks = F / 8;
+  const char* __restrict__ kb = reinterpret_cast<const char*>(key);
+  const uint32_t row_bytes = static_cast<uint32_t>(F * sizeof(T));
+  uint32_t lane_off[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) lane_off[m] = static_cast<uint32_t>((j + G * m < chunks ? j + G * m : 0) * 16);
+  int next_c = first + lane < end ? static_cast<int>(col[first + lane]) : 0;
+  for (int64_t base = first; base < end; base += step) {
+    const int my_c = next_c;
+    const int64_t nb = base + step;
+    if (nb < end) next_c = nb + lane < end ? static_cast<int>(col[nb + lane]) : 0;
+    const int cnt = end - base < kWave ? static_cast<int>(end - base) : kWave;
+    for (int u0 = 0; u0 < cnt; u0 += kSub) {
+      // edge u0 + u·NG + g; steps u with u0 + u·NG >= cnt hold no edge of
+      // any group and are skipped (wave-uniform)
+      RawVec<16> kv[UE][MB];
+#pragma unroll
+      for (int u = 0; u < UE; ++u) {
+        if (u0 + u * NG < cnt) {
+          const int idx = u0 + u * NG + g;  // < 64
+          const int c = __builtin_amdgcn_ds_bpermute(idx * 4, my_c);
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            if constexpr (OFF32) {
+              kv[u][m] = load_raw<16>(kb + (__umul24(static_cast<uint32_t>(c), row_bytes) + lane_off[m]));
+            } else {
+              kv[u][m] = load_raw<16>(kb + static_cast<int64_t>(c) * row_bytes + lane_off[m]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UE; ++u) {
+        if (u0 + u * NG < cnt) {
+          double acc = 0.0;
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            if (j + G * m < chunks) {
+#pragma unroll
+              for (int p = 0; p < 8; ++p)
+                acc = __builtin_fma(qd[m][p], static_cast<double>(Elem<T>::get(kv[u][m].w, p)), acc);
+            }
+          }
+#pragma unroll
+          for (int o = 1; o < G; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+          const int idx = u0 + u * NG + g;
+          if (j == 0 && idx < cnt) out[base + idx] = Elem<T>::bits(acc);
+        }
+      }
+    }
+  }
+}
+
+template <typename T, int G, int MB>
+__device__ __forceinline__ void load_query16(const T* __restrict__ qrow, int64_t F, int j, double (&qd)[MB][8]) {
+  const int64_t chunks = F / 8;
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    const int64_t chunk = j + G * m;
+    const RawVec<16> v = load_raw<16>(reinterpret_cast<const char*>(qrow + (chunk < chunks ? chunk : 0) * 8));
+#pragma unroll
+    for (int p = 0; p < 8; ++p) qd[m][p] = chunk < chunks ? static_cast<double>(Elem<T>::get(v.w, p)) : 0.0;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void dots16_scalar(const int64_t* __restrict__ col, const T* __restrict__ qrow,
+                                              const T* __restrict__ key, uint16_t* __restrict__ out, int64_t F,
+                                              int64_t first, int64_t end, int64_t step) {
+  const int lane = lane_id();
+  for (int64_t e = first; e < end; e += step) {
+    const int64_t c = uniform_i64(col[e]);
+    const T* __restrict__ kr = key + c * F;
+    double acc = 0.0;
+    for (int64_t f = lane; f < F; f += kWave)
+      acc = __builtin_fma(static_cast<double>(Elem<T>::at(qrow, f)), static_cast<double>(Elem<T>::at(kr, f)), acc);
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+    if (lane == 0) out[e] = Elem<T>::bits(acc);
+  }
+}
+
+// Edges [cs, ce) of `row`, taken by `waves` waves (this one is `wave`).
+template <typename T, int G, int MB, bool VEC, bool OFF32>
+__device__ __forceinline__ void sddmm16_edges(const int64_t* __restrict__ col, const T* __restrict__ query,
+                                              const T* __restrict__ key, uint16_t* __restrict__ out, int64_t F,
+                                              int64_t row, int64_t cs, int64_t ce, int wave, int waves) {
+  if constexpr (VEC) {
+    const int lane = lane_id();
+    const int g = lane / G;
+    const int j = lane % G;
+    double qd[MB][8];
+    load_query16<T, G, MB>(query + row * F, F, j, qd);
+    dots16_vec<T, G, MB, OFF32>(col, key, out, F, qd, cs + static_cast<int64_t>(wave) * kWave, ce,
+                         static_cast<int64_t>(waves) * kWave, g, j);
+  } else {
+    dots16_scalar<T>(col, query + row * F, key, out, F, cs + wave, ce, waves);
+  }
+}
+
+// The split schedule of sddmm_scheduled_kernel for 16-bit elements:
+// workgroups [0, hub_blocks) stride over the 2048-edge chunks of the rows of
+// degree >= hub_threshold, the rest take the other rows one per wave.
+template <typename T, int G, int MB, bool VEC, bool OFF32>
+__global__ __launch_bounds__(512) void sddmm16_scheduled_kernel(
+    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const T* __restrict__ query,
+    const T* __restrict__ key, uint16_t* __restrict__ out, int64_t n, int64_t F, int64_t hub_threshold,
+    const int32_t* __restrict__ order, const int32_t* __restrict__ counts, const int32_t* __restrict__ chunk_off,
+    int64_t hub_blocks, int64_t block_base) {
+  const int wave = wave_in_block();
+  const int waves = static_cast<int>(blockDim.x >> 6);
+  const int64_t block = block_base + blockIdx.x;
+  if (block < hub_blocks) {
+    const int64_t hubs = counts[0];
+    const int64_t items = counts[2];
+    for (int64_t item = block; item < items; item += hub_blocks) {
+      int64_t lo = 0;
+      int64_t hi = hubs - 1;
+      while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (chunk_off[mid] <= item) lo = mid;
+        else hi = mid - 1;
+      }
+      const int64_t row = uniform_i64(order[lo]);
+      const int64_t rs = uniform_i64(crow[row]);
+      const int64_t re = uniform_i64(crow[row + 1]);
+      const int64_t cs = rs + (item - uniform_i64(chunk_off[lo])) * kChunkEdges;
+      const int64_t ce = cs + kChunkEdges < re ? cs + kChunkEdges : re;
+      sddmm16_edges<T, G, MB, VEC, OFF32>(col, query, key, out, F, row, cs, ce, wave, waves);
+    }
+    return;
+  }
+  const int64_t row = (block - hub_blocks) * waves + wave;
+  if (row >= n) return;
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
+  if (re - rs >= hub_threshold || re == rs) return;
+  sddmm16_edges<T, G, MB, VEC, OFF32>(col, query, key, out, F, row, rs, re, 0, 1);
+}
+
+struct Sddmm16Args {
+  const int64_t* crow;
+  const int64_t* col;
+  const void* q;
+  const void* k;
+  void* out;
+  int64_t n;
+  int64_t f;
+};
+
+template <typename T, int G, int MB, bool VEC, bool OFF32>
+void launch_sddmm16_v(const Sddmm16Args& a, dim3 grid, dim3 block, int64_t hub_threshold, const int32_t* order,
+                      const int32_t* counts, const int32_t* chunk_off, int64_t hub_blocks, int64_t b0,
+                      hipStream_t s) {
+  hipLaunchKernelGGL((sddmm16_scheduled_kernel<T, G, MB, VEC, OFF32>), grid, block, 0, s, a.crow, a.col,
+                     static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<uint16_t*>(a.out), a.n,
+                     a.f, hub_threshold, order, counts, chunk_off, hub_blocks, b0);
+}
+
+// Lanes per edge G and chunks per lane MB for F features (vector lanes), or
+// G = 0 for element lanes.
+inline void sddmm16_shape(const Sddmm16Args& a, int& g, int& mb) {
+  g = 0;
+  mb = 1;
+  if (a.f % 8 != 0 || a.f > 512 || !aligned(a.q, 16) || !aligned(a.k, 16)) return;
+  const int64_t chunks = a.f / 8;
+  if (chunks > 32) {
+    g = 32;
+    mb = 2;
+    return;
+  }
+  g = 1;
+  while (g < chunks) g <<= 1;
+}
+
+template <typename T>
+void launch_sddmm16(const Sddmm16Args& a, int waves, int64_t hub_threshold, int64_t item_upper,
+                    const int32_t* order, const int32_t* counts, const int32_t* chunk_off, hipStream_t s) {
+  const int64_t hub_blocks = item_upper < kHubBlocksMax ? item_upper : kHubBlocksMax;
+  const int64_t blocks = hub_blocks + (a.n + waves - 1) / waves;
+  const dim3 block(static_cast<unsigned>(waves * kWave));
+  int g, mb;
+  sddmm16_shape(a, g, mb);
+  for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
+    const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
+    const dim3 grid(static_cast<unsigned>(nb));
+  // every key byte offset fits 32 bits (and the row index 24 bits)
+  const bool off32 = a.n <= (int64_t(1) << 24) && a.n * a.f * 2 <= (int64_t(1) << 32);
+#define AS_S16(G, MB, VEC)                                                                                      \
+  do {                                                                                                         \
+    if (off32)                                                                                                 \
+      launch_sddmm16_v<T, G, MB, VEC, true>(a, grid, block, hub_threshold, order, counts, chunk_off, hub_blocks, \
+                                            b0, s);                                                            \
+    else                                                                                                       \
+      launch_sddmm16_v<T, G, MB, VEC, false>(a, grid, block, hub_threshold, order, counts, chunk_off,          \
+                                             hub_blocks, b0, s);                                               \
+  } while (0)
+    if (mb == 2) {
+      AS_S16(32, 2, true);
+    } else {
+      switch (g) {
+        case 1: AS_S16(1, 1, true); break;
+        case 2: AS_S16(2, 1, true); break;
+        case 4: AS_S16(4, 1, true); break;
+        case 8: AS_S16(8, 1, true); break;
+        case 16: AS_S16(16, 1, true); break;
+        case 32: AS_S16(32, 1, true); break;
+        default:
+          launch_sddmm16_v<T, 64, 1, false, false>(a, grid, block, hub_threshold, order, counts, chunk_off,
+                                                   hub_blocks, b0, s);
+          break;
+      }
+    }
+#undef AS_S16
+  }
+}
+
 int validate_sddmm(const SddmmArgs& a, int64_t nnz) {
   if (a.n < 0 || a.n > INT32_MAX || a.f < 0 || a.f > INT32_MAX)
     return fail(AS_ERR_INVALID_ARGUMENT, "SDDMM dimensions exceed the kernel index range");
@@ -389,6 +636,54 @@ int as_sddmm_csr_split_f32(const int64_t* crow, const int64_t* col, const float*
   st = as::launch_sddmm_scheduled(a, waves_per_block, hub_threshold, item_upper, order, counts, chunk_off, s);
   if (st != AS_OK) return st;
   return as::check_launch("sddmm_csr_split");
+}
+
+int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void* query, const void* key, void* out,
+                            int64_t n, int64_t nnz, int64_t f, int dtype, int waves_per_block, int64_t hub_threshold,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (waves_per_block != 2 && waves_per_block != 4 && waves_per_block != 8)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "warps_per_block must be 2, 4, or 8");
+  if (hub_threshold <= 0 || hub_threshold > INT32_MAX)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "hub_threshold must be a positive 32-bit integer");
+  if (!as::aligned(query, 2) || !as::aligned(key, 2) || !as::aligned(out, 2))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "query, key and out must be 2-byte aligned");
+  // the fp32 argument check covers the shapes and null pointers
+  const as::SddmmArgs shape{crow, col, static_cast<const float*>(query), static_cast<const float*>(key),
+                            static_cast<float*>(out), n, f};
+  int st = as::validate_sddmm(shape, nnz);
+  if (st != AS_OK) return st;
+  if (n == 0 || nnz == 0) return AS_OK;
+  if (f == 0) return as::fail(AS_ERR_UNSUPPORTED, "SDDMM with zero features is handled by the caller");
+  if (workspace == nullptr || workspace_bytes < as::sddmm_split_ws(n))
+    return as::fail(AS_ERR_WORKSPACE, "16-bit SDDMM needs %zu workspace bytes, got %zu", as::sddmm_split_ws(n),
+                    workspace_bytes);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const as::Sddmm16Args a{crow, col, query, key, out, n, f};
+  char* ws = static_cast<char*>(workspace);
+  int32_t* order = reinterpret_cast<int32_t*>(ws);
+  const size_t order_bytes = as::align_up(static_cast<size_t>(n) * sizeof(int32_t), 256);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + order_bytes);
+  void* bin_ws = ws + order_bytes + 256;
+  int32_t* chunk_off = reinterpret_cast<int32_t*>(ws + as::spmm_split_workspace_bytes(n));
+  int64_t heavy_upper = nnz / hub_threshold;
+  if (heavy_upper > n) heavy_upper = n;
+  int64_t item_upper = 0;
+  if (heavy_upper > 0) {
+    st = as::launch_bin_rows(crow, n, hub_threshold, 1, 1, order, counts, bin_ws, s);
+    if (st != AS_OK) return st;
+    hipLaunchKernelGGL(as::hub_chunk_scan_kernel, dim3(1), dim3(1024), 0, s, crow, order, counts, chunk_off);
+    item_upper = nnz / as::kChunkEdges + heavy_upper;
+  }
+  // with item_upper == 0 there are no hub workgroups and no row reaches the
+  // threshold, so the kernel reads neither the order nor the counts
+  if (dtype == AS_DTYPE_BF16)
+    as::launch_sddmm16<as::Bf16>(a, waves_per_block, hub_threshold, item_upper, order, counts, chunk_off, s);
+  else
+    as::launch_sddmm16<as::Fp16>(a, waves_per_block, hub_threshold, item_upper, order, counts, chunk_off, s);
+  return as::check_launch("sddmm_csr_rounded_16");
 }
 
 }  // extern "C"

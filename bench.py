@@ -43,8 +43,8 @@ def spmm_bytes(n: int, nnz: int, f: int, weighted: bool, elem: int = 4) -> int:
     return elem * f * nnz + elem * f * n + 8 * nnz + 8 * (n + 1) + (elem * nnz if weighted else 0)
 
 
-def sddmm_bytes(n: int, nnz: int, f: int) -> int:
-    return 4 * f * nnz + 4 * f * n + 4 * nnz + 8 * nnz + 8 * (n + 1)
+def sddmm_bytes(n: int, nnz: int, f: int, elem: int = 4) -> int:
+    return elem * f * nnz + elem * f * n + elem * nnz + 8 * nnz + 8 * (n + 1)
 
 
 def attention_bytes(n: int, nnz: int, fqk: int, fv: int) -> int:
@@ -232,7 +232,8 @@ def main() -> int:
                         help="instead of the bench line: the scheduler's cost on this workload (a cold call with an "
                              "empty schedule cache, then cached calls) against one call of the chosen kernel")
     parser.add_argument("--dtype", default="f32", choices=["f32", "bf16", "fp16"],
-                        help="feature type of the SpMM workloads (cfg1-3); bf16/fp16 run the rounded 16-bit SpMM")
+                        help="feature type of the SpMM workloads (cfg1-3) and the SDDMM one (cfg4); bf16/fp16 run "
+                             "the rounded 16-bit kernels")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gpu-baseline", action="store_true")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -468,22 +469,30 @@ def bench_other(args, device) -> dict:
         log(f"generated cfg4: {w.degree_stats()} in {time.time() - t0:.1f}s")
         crow = torch.from_numpy(w.crow).to(device)
         col = torch.from_numpy(w.col).to(device)
-        q = torch.from_numpy(w.dense["q"]).to(device)
-        k = torch.from_numpy(w.dense["k"]).to(device)
+        # bf16 / fp16: the rounded 16-bit SDDMM (fp64 sums of exact products);
+        # the split points are the ones its scheduler times
+        dt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+        q = torch.from_numpy(w.dense["q"]).to(device).to(dt)
+        k = torch.from_numpy(w.dense["k"]).to(device).to(dt)
         variants = {}
-        for waves in (8, 4, 2):
-            for thr in (1024, 4096, 256):
-                variants[f"{waves},{thr}"] = (
-                    lambda a=waves, b=thr: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b))
-        variants["whole"] = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)
+        splits = [(w_, t_) for w_ in (8, 4, 2) for t_ in (1024, 4096, 256)] if dt == torch.float32 else [
+            (4, 1024), (8, 4096)]
+        for waves, thr in splits:
+            variants[f"{waves},{thr}"] = (
+                lambda a=waves, b=thr: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b))
+        if dt == torch.float32:
+            variants["whole"] = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)
         calib = {}
         chosen = calibrate(variants, calib) if args.variant == "calibrated" else args.variant
         step = variants[chosen]
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * w.nnz * f
-        algo = sddmm_bytes(w.rows, w.nnz, f)
-        name = f"cfg4 SDDMM fp32 F={f}"
+        algo = sddmm_bytes(w.rows, w.nnz, f, elem=q.element_size())
+        type_name = {"f32": "fp32", "bf16": "bf16", "fp16": "fp16"}[args.dtype]
+        name = f"cfg4 SDDMM {type_name} F={f}"
         cpu = None if args.no_cpu_baseline else cpu_baseline_sddmm(w, f)
+        if cpu is not None and dt != torch.float32:
+            cpu["sample"] += "; fp32 (the reference's CPU path is the fp32 gather-dot)"
     else:
         w = synth.config5(seed=args.seed)
         log(f"generated cfg5: {w.degree_stats()} in {time.time() - t0:.1f}s")
@@ -522,7 +531,7 @@ def bench_other(args, device) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": args.dtype if args.workload == "cfg4" else "f32",
         "data": "synthetic",
         "config": {"workload": name, "rows": w.rows, "nnz": w.nnz, "variant": chosen,
                    "degree_stats": w.degree_stats()},

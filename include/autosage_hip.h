@@ -167,6 +167,25 @@ int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
  * F is not a multiple of 8). */
 int64_t as_spmm_rounded_16_group_degree(int64_t f);
 
+/* SDDMM with bf16 or fp16 query, key and output (dtype AS_DTYPE_BF16 /
+ * AS_DTYPE_F16): out[e] is the fp64 sum of the exact products
+ * query[row(e), f]·key[col[e], f], rounded to fp32 and then to the element
+ * type (round to nearest even both times).  The reference has no kernel for
+ * these types: its op takes float32 only (csrc/sddmm_csr_op.cu:94-95) and its
+ * scheduler runs the gather-dot baseline (autosage/_auto.py:575-581).  The
+ * schedule is that of as_sddmm_csr_split_f32 (rows of degree >=
+ * hub_threshold cut into 2048-edge chunks, waves_per_block 2, 4 or 8, the
+ * workspace from as_sddmm_split_workspace_bytes); an exact fp64 sum does not
+ * depend on the order of the additions, so any schedule gives the same bits.
+ * query, key and out 2-byte aligned; F a multiple of 8 up to 512 with
+ * 16-byte aligned query and key takes 16-byte lanes. */
+int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
+                            const void* query, const void* key, void* out,
+                            int64_t n, int64_t nnz, int64_t f, int dtype,
+                            int waves_per_block, int64_t hub_threshold,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* out[e] = <query[row(e)], key[col[e]]> for every nonzero, CSR order.
  * Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134), op schema :192.
  * The dot product uses the reference kernel's summation order

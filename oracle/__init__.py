@@ -15,8 +15,9 @@ Contents:
   (autosage/_auto.py:79-92), ``torch_row_softmax`` (autosage/_auto.py:744-759),
   ``numpy_edge_index_to_csr`` (autosage/utils/csr.py:6-26);
 * ``attention_ref`` = composition of the above (autosage/_auto.py:762-780);
-* ``spmm_rounded_16``: the bf16 / fp16 SpMM rule (fp64 sum of exact
-  products, rounded to fp32, then to the 16-bit type).
+* ``spmm_rounded_16`` / ``sddmm_rounded_16``: the bf16 / fp16 SpMM and
+  SDDMM rule (fp64 sum of exact products, rounded to fp32, then to the 16-bit
+  type).
 
 How each function is pinned (independent checks in tests/test_oracle.py):
 * or_spmm_seq_f32: bit-identical to torch.sparse.mm on CPU (MKL) on random
@@ -32,6 +33,11 @@ How each function is pinned (independent checks in tests/test_oracle.py):
 * spmm_rounded_16: exact rational sums (fractions.Fraction) rounded the same
   way on random graphs; hand-computed ties (round to even, and the fp32 step
   that decides a tie the exact sum would not), fp16 overflow to inf.
+* sddmm_rounded_16: exact rational dot products (fractions.Fraction) on
+  random graphs; hand-computed cases: a product that rounding to the 16-bit
+  type first would change (1 + 2^-7)(1 + 2^-5) - 1, a tie decided to even,
+  fp16 overflow to inf.  (or_sddmm_f64 itself is pinned by a dense
+  brute-force product.)
 """
 
 from __future__ import annotations
@@ -145,6 +151,19 @@ def sddmm_f64(crow, col, query, key) -> np.ndarray:
     out = np.empty(col.size, dtype=np.float64)
     _load().or_sddmm_f64(_p(crow), _p(col), _p(q), _p(k), crow.size - 1, q.shape[1], _p(out))
     return out
+
+
+def sddmm_rounded_16(crow, col, query, key, dtype: torch.dtype) -> torch.Tensor:
+    """SDDMM on bf16 / fp16 query and key, the rule of as_sddmm_csr_rounded_16
+    (the reference's op takes float32 only, csrc/sddmm_csr_op.cu:94-95, and
+    its scheduler runs the gather-dot baseline for other types,
+    autosage/_auto.py:575-581): the exact products summed in fp64 (in feature
+    order), the sum rounded to fp32 and then to ``dtype``, round to nearest
+    even both times."""
+    q32 = torch.as_tensor(query).to(dtype).float().numpy()
+    k32 = torch.as_tensor(key).to(dtype).float().numpy()
+    out64 = sddmm_f64(crow, col, q32, k32)
+    return torch.from_numpy(out64).to(torch.float32).to(dtype)
 
 
 def row_softmax(crow, scores) -> np.ndarray:

@@ -77,6 +77,17 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 2, 0, None, 0, -1, -1, None) == 1
     assert lib.as_last_error() == b"null pointer argument"
     assert lib.as_spmm_colslice_min_degree(1) == 128 and lib.as_spmm_colslice_min_degree(0) == 1024
+    # 16-bit SDDMM: dtype code, split arguments, alignment, null inputs
+    assert lib.as_sddmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 3, 4, 1024, None, 0, None) == 1
+    assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"
+    assert lib.as_sddmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 1, 3, 1024, None, 0, None) == 1
+    assert lib.as_last_error() == b"warps_per_block must be 2, 4, or 8"
+    assert lib.as_sddmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 1, 4, 0, None, 0, None) == 1
+    assert lib.as_last_error() == b"hub_threshold must be a positive 32-bit integer"
+    assert lib.as_sddmm_csr_rounded_16(None, None, 1, None, None, 4, 0, 8, 2, 4, 1024, None, 0, None) == 1
+    assert lib.as_last_error() == b"query, key and out must be 2-byte aligned"
+    assert lib.as_sddmm_csr_rounded_16(None, None, None, None, None, 4, 5, 8, 2, 4, 1024, None, 0, None) == 1
+    assert lib.as_last_error() == b"null crow pointer"
     assert [lib.as_spmm_rounded_16_group_degree(f) for f in (8, 64, 72, 128, 136, 512, 7, 0)] == [
         32, 32, 64, 64, 128, 128, 0, 0]
     # n == 0 is a no-op success

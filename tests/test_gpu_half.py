@@ -1,5 +1,6 @@
 """GPU parity of the bf16 / fp16 SpMM (``autosage::spmm_csr`` and
-``spmm_csr_colslice`` on 16-bit features).
+``spmm_csr_colslice`` on 16-bit features) and SDDMM (``sddmm_csr``,
+``sddmm_csr_split``), their gradients and their scheduler paths.
 
 The reference has no kernel for these types (its op raises, its scheduler
 runs torch.sparse.mm).  The rule here: every output is the fp64 sum of the
@@ -164,11 +165,11 @@ def test_rounded_spmm_backward_for_x(dtype):
     y.backward(g.cuda())
     t_crow, t_col, _ = csr_transpose(torch.from_numpy(crow), torch.from_numpy(col))
     assert _same_bits(d_x.grad, oracle.spmm_rounded_16(t_crow.numpy(), t_col.numpy(), None, g, dtype))
-    # weight gradients of 16-bit SpMM are not implemented
+    # the weight gradient: the 16-bit SDDMM <dY[row], X[col]>
     d_val = torch.ones(col.size, dtype=dtype, device="cuda", requires_grad=True)
     y = torch.ops.autosage.spmm_csr(d_crow, d_col, d_val, x.cuda())
-    with pytest.raises(NotImplementedError, match="weight gradient"):
-        y.backward(g.cuda())
+    y.backward(g.cuda())
+    assert _same_bits(d_val.grad, oracle.sddmm_rounded_16(crow, col, g, x, dtype))
 
 
 def test_fp16_rounding_at_the_ends_of_the_range():
@@ -202,3 +203,108 @@ def test_fp16_rounding_at_the_ends_of_the_range():
     assert _same_bits(got, want), (got.float().cpu()[:n, 0], want.float()[:n, 0])
     expected = [65504.0, float("inf"), float("-inf"), 0.0, u, 2 * u, 2 * u, 2.0**-14, 2.0**-14 - u, 1.0]
     assert want.float()[:n, 0].tolist() == expected
+
+
+# ---- SDDMM ------------------------------------------------------------------
+
+
+def _sddmm_inputs(features, dtype, seed=0, rows=3000, degree=9, hubs=3, hub_degree=2500, empty=0.08):
+    crow, col = case_graph(rows, degree, seed=seed, hubs=hubs, hub_degree=hub_degree, empty=empty)
+    rng = np.random.default_rng(seed + 17)
+    q = torch.from_numpy(rng.standard_normal((rows, features)).astype(np.float32)).to(dtype)
+    k = torch.from_numpy(rng.standard_normal((rows, features)).astype(np.float32)).to(dtype)
+    return crow, col, q, k
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("features", [1, 7, 8, 16, 24, 33, 64, 72, 128, 136, 256, 264, 512, 520])
+def test_rounded_sddmm_equals_oracle_on_every_split(dtype, features):
+    """16-byte lanes for F a multiple of 8 up to 512 (1 to 32 lanes per edge,
+    two chunks per lane above 256), element lanes otherwise; hub rows of 2,500
+    edges cut into 2048-edge chunks, or into many at threshold 64."""
+    crow, col, q, k = _sddmm_inputs(features, dtype, seed=features)
+    want = oracle.sddmm_rounded_16(crow, col, q, k, dtype)
+    d_crow, d_col = to_dev(crow, col)
+    d_q, d_k = q.cuda(), k.cuda()
+    got = torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, d_k)
+    assert got.dtype == dtype
+    assert _same_bits(got, want), (got.float().cpu() - want.float()).abs().max()
+    for waves, threshold in ((2, 64), (8, 2**31 - 1), (4, 1024)):
+        assert _same_bits(torch.ops.autosage.sddmm_csr_split(d_crow, d_col, d_q, d_k, waves, threshold), want)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rounded_sddmm_edge_cases(dtype):
+    # rows that are not 16-byte aligned take the element lanes
+    crow, col, q, k = _sddmm_inputs(64, dtype, seed=31, rows=800, hub_degree=700)
+    want = oracle.sddmm_rounded_16(crow, col, q, k, dtype)
+    d_crow, d_col = to_dev(crow, col)
+    flat = torch.empty(q.numel() + 1, dtype=dtype, device="cuda")
+    flat[1:] = q.reshape(-1).cuda()
+    d_q = flat[1:].view(q.shape)
+    assert d_q.data_ptr() % 16 != 0 and d_q.is_contiguous()
+    assert _same_bits(torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, k.cuda()), want)
+    # no edges; F = 0
+    crow0 = np.zeros(6, dtype=np.int64)
+    d_crow0, d_col0 = to_dev(crow0, np.zeros(0, dtype=np.int64))
+    q0 = torch.ones(5, 16, dtype=dtype, device="cuda")
+    assert torch.ops.autosage.sddmm_csr(d_crow0, d_col0, q0, q0).numel() == 0
+    out = torch.ops.autosage.sddmm_csr(d_crow, d_col, q[:, :0].contiguous().cuda(), k[:, :0].contiguous().cuda())
+    assert out.shape == (col.size,) and torch.count_nonzero(out).item() == 0
+    # mixed types are rejected
+    with pytest.raises(RuntimeError, match="query and key must use the same dtype"):
+        torch.ops.autosage.sddmm_csr(d_crow, d_col, q.cuda(), k.cuda().to(torch.float16 if dtype == torch.bfloat16
+                                                                            else torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rounded_sddmm_gradients(dtype):
+    from autosage_amd._autograd import csr_transpose
+
+    crow, col, q, k = _sddmm_inputs(64, dtype, seed=41, rows=1500, hub_degree=1200)
+    d_crow, d_col = to_dev(crow, col)
+    d_q = q.cuda().requires_grad_(True)
+    d_k = k.cuda().requires_grad_(True)
+    s = torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, d_k)
+    gs = torch.randn(col.size, generator=torch.Generator().manual_seed(5)).to(dtype)
+    s.backward(gs.cuda())
+    assert _same_bits(d_q.grad, oracle.spmm_rounded_16(crow, col, gs, k, dtype))
+    t_crow, t_col, perm = csr_transpose(torch.from_numpy(crow), torch.from_numpy(col))
+    assert _same_bits(d_k.grad, oracle.spmm_rounded_16(t_crow.numpy(), t_col.numpy(), gs[perm], q, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_sddmm_scheduler_on_16_bit_inputs(dtype, monkeypatch, tmp_path):
+    from autosage_amd._auto import sddmm_csr_auto
+
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    crow, col, q, k = _sddmm_inputs(128, dtype, seed=51, rows=4000)
+    want = oracle.sddmm_rounded_16(crow, col, q, k, dtype)
+    d_crow, d_col = to_dev(crow, col)
+    out, info = sddmm_csr_auto(d_crow, d_col, q.cuda(), k.cuda())
+    assert info["operation"] == "sddmm" and info["choice"] == "autosage" and info["from_cache"] is False
+    assert info["candidate"] in ([4, 1024], [8, 4096]) and len(info["candidates"]) == 2
+    assert info["baseline_probe_ms"] is None and _same_bits(out, want)
+    out2, info2 = sddmm_csr_auto(d_crow, d_col, q.cuda(), k.cuda())
+    assert info2["from_cache"] is True and info2["candidate"] == info["candidate"]
+    assert torch.equal(out2, out)
+
+
+def test_attention_on_bf16_inputs_runs_the_native_stages(monkeypatch, tmp_path):
+    """bf16 attention: native SDDMM, the reference's torch row softmax (in
+    bf16), native SpMM; close to the fp32 result at bf16 precision on rows of
+    ~9 edges (the torch softmax sums a row's exponentials in bf16, which
+    loses ~2 digits on rows of a thousand edges)."""
+    from autosage_amd._auto import csr_attention_forward
+
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    crow, col, q, k = _sddmm_inputs(64, torch.float32, seed=61, rows=2000, hubs=0)
+    v = torch.randn(2000, 32, generator=torch.Generator().manual_seed(6))
+    d_crow, d_col = to_dev(crow, col)
+    q, k = q * 0.125, k * 0.125
+    ref, _ = csr_attention_forward(d_crow, d_col, q.cuda(), k.cuda(), v.cuda(), fused=False)
+    out, info = csr_attention_forward(d_crow, d_col, q.bfloat16().cuda(), k.bfloat16().cuda(),
+                                      v.bfloat16().cuda())
+    assert out.dtype == torch.bfloat16
+    assert info["sddmm"]["choice"] == "autosage" and info["spmm"]["choice"] == "autosage"
+    assert (out.float() - ref).abs().max().item() < 0.05

@@ -307,6 +307,47 @@ def test_spmm_rounded_16_matches_exact_rational_sums(dtype, weighted):
             assert got[r, f] == _round_16(float(exact), dtype), (r, f)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sddmm_rounded_16_matches_exact_rational_dots(dtype):
+    from fractions import Fraction
+
+    crow, col = _graph(30, 5, seed=4, hubs=1, hub_degree=25, empty=0.1)
+    rng = np.random.default_rng(12)
+    q = torch.from_numpy(rng.standard_normal((30, 13)).astype(np.float32)).to(dtype)
+    k = torch.from_numpy(rng.standard_normal((30, 13)).astype(np.float32)).to(dtype)
+    got = oracle.sddmm_rounded_16(crow, col, q, k, dtype).float().numpy()
+    qf = q.float().numpy().astype(np.float64)
+    kf = k.float().numpy().astype(np.float64)
+    for r in range(30):
+        for e in range(crow[r], crow[r + 1]):
+            exact = sum((Fraction(qf[r, f]) * Fraction(kf[col[e], f]) for f in range(13)), Fraction(0))
+            assert got[e] == _round_16(float(exact), dtype), (r, e)
+
+
+def test_sddmm_rounded_16_exact_products_ties_and_overflow():
+    crow = np.array([0, 1, 2, 3, 3], dtype=np.int64)
+    col = np.array([1, 2, 3], dtype=np.int64)
+    q = np.zeros((4, 2), dtype=np.float32)
+    k = np.zeros((4, 2), dtype=np.float32)
+    # row 0 · key 1: (1 + 2^-7)(1 + 2^-5) - 1 = 2^-5 + 2^-7 + 2^-12, i.e.
+    # 2^-5·(1 + 2^-2 + 2^-7): exact in bf16.  Rounding the product to bf16
+    # first would drop the 2^-12 and give 2^-5 + 2^-7.
+    q[0] = [1 + 2.0**-7, -1.0]
+    k[1] = [1 + 2.0**-5, 1.0]
+    # row 1 · key 2: 1 + 2^-8, halfway between bf16 neighbours: even -> 1
+    q[1] = [1.0, 2.0**-8]
+    k[2] = [1.0, 1.0]
+    # row 2 · key 3: 60000 + 60000 overflows fp16
+    q[2] = [60000.0, 60000.0]
+    k[3] = [1.0, 1.0]
+    bf = oracle.sddmm_rounded_16(crow, col, q, k, torch.bfloat16).float().numpy()
+    assert bf[0] == 2.0**-5 + 2.0**-7 + 2.0**-12
+    assert bf[1] == 1.0
+    h = oracle.sddmm_rounded_16(crow, col, q, k, torch.float16).float().numpy()
+    assert h[2] == np.inf
+    assert h[1] == 1.00390625  # fp16 holds 1 + 2^-8
+
+
 def test_spmm_rounded_16_ties_and_overflow():
     crow = np.array([0, 2, 4, 7, 9], dtype=np.int64)
     col = np.array([0, 1, 0, 2, 0, 1, 3, 4, 4], dtype=np.int64)
