@@ -855,9 +855,10 @@ def _torch_row_softmax(crow: torch.Tensor, scores: torch.Tensor) -> torch.Tensor
 
 
 def _csr_row_softmax(crow: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
-    """CSR row softmax: the native kernel on the GPU (float32), the reference
-    torch composition on the CPU."""
-    if scores.is_cuda and scores.dtype == torch.float32:
+    """CSR row softmax: the native kernel on the GPU (float32, and bf16 /
+    fp16 computed in fp32 and rounded once), the reference torch composition
+    on the CPU."""
+    if scores.is_cuda and scores.dtype in (torch.float32, torch.bfloat16, torch.float16):
         if not load_native() or native_op("csr_row_softmax") is None:
             raise RuntimeError("AutoSAGE native csr_row_softmax is unavailable")
         return native_op("csr_row_softmax")(crow.to(torch.long).contiguous(), scores.contiguous())

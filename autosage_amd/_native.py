@@ -69,6 +69,7 @@ _SIGNATURES = {
          _c_i64, _c_ptr],
     ),
     "as_spmm_rounded_16_group_degree": (_c_i64, [_c_i64]),
+    "as_csr_row_softmax_16": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_int, _c_ptr]),
     "as_sddmm_csr_rounded_16": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_ptr, _c_size,
@@ -391,7 +392,8 @@ def sddmm_rounded_16_impl(crow, col, query, key, warps_per_block: int, hub_thres
 def csr_row_softmax_impl(crow, scores):
     _check(crow.is_cuda and scores.is_cuda, "crow and scores must be CUDA tensors")
     _check(crow.dtype == torch.long and crow.dim() == 1 and crow.is_contiguous(), "crow must be contiguous torch.long")
-    _check(scores.dtype == torch.float32 and scores.dim() == 1, "scores must be one-dimensional float32")
+    _check((scores.dtype == torch.float32 or scores.dtype in DTYPES_16) and scores.dim() == 1,
+           "scores must be one-dimensional float32 (or bfloat16 / float16)")
     _check(crow.device == scores.device, "crow and scores must be on the same CUDA device")
     scores = scores.contiguous()
     probs = torch.empty_like(scores)
@@ -399,9 +401,16 @@ def csr_row_softmax_impl(crow, scores):
     if n <= 0 or scores.numel() == 0:
         return probs
     with torch.cuda.device(scores.device):
-        status = library().as_csr_row_softmax_f32(
-            _ptr(crow), _ptr(scores), _ptr(probs), n, scores.numel(), _stream(scores.device)
-        )
+        if scores.dtype in DTYPES_16:
+            # fp32 softmax of the exactly converted scores, rounded once
+            status = library().as_csr_row_softmax_16(
+                _ptr(crow), _ptr(scores), _ptr(probs), n, scores.numel(), DTYPES_16[scores.dtype],
+                _stream(scores.device)
+            )
+        else:
+            status = library().as_csr_row_softmax_f32(
+                _ptr(crow), _ptr(scores), _ptr(probs), n, scores.numel(), _stream(scores.device)
+            )
     _raise(status, "autosage::csr_row_softmax")
     return probs
 

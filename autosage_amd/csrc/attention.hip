@@ -20,6 +20,7 @@
 // workgroup whose waves share the scoring and split the value features.
 #include "as_device.h"
 #include "as_internal.h"
+#include "elem16.h"
 
 namespace as {
 
@@ -42,6 +43,30 @@ __global__ __launch_bounds__(kBlock) void csr_row_softmax_kernel(const int64_t* 
   for (int64_t e = rs + lane; e < re; e += kWave) d += expf(scores[e] - m);
   d = wave_sum_f32(d);
   for (int64_t e = rs + lane; e < re; e += kWave) probs[e] = expf(scores[e] - m) / d;
+}
+
+// The same row softmax on bf16 / fp16 scores: each score converts exactly to
+// fp32, m, d and p_e are computed as above in fp32, and p_e is rounded to
+// the 16-bit type (round to nearest even) once.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void csr_row_softmax16_kernel(const int64_t* __restrict__ crow,
+                                                                   const T* __restrict__ scores,
+                                                                   uint16_t* __restrict__ probs, int64_t n,
+                                                                   int64_t idx_base) {
+  const int lane = lane_id();
+  const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
+  if (row >= n) return;
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
+  if (rs == re) return;
+  float m = -INFINITY;
+  for (int64_t e = rs + lane; e < re; e += kWave) m = fmaxf(m, Elem<T>::at(scores, e));
+  m = wave_max_f32(m);
+  float d = 0.f;
+  for (int64_t e = rs + lane; e < re; e += kWave) d += expf(Elem<T>::at(scores, e) - m);
+  d = wave_sum_f32(d);
+  for (int64_t e = rs + lane; e < re; e += kWave)
+    probs[e] = Elem<T>::bits(static_cast<double>(expf(Elem<T>::at(scores, e) - m) / d));
 }
 
 template <int S>
@@ -345,6 +370,34 @@ int as_csr_row_softmax_f32(const int64_t* crow, const float* scores, float* prob
                        scores, probs, n, b0 * as::kWavesPerBlock);
   }
   return as::check_launch("csr_row_softmax");
+}
+
+int as_csr_row_softmax_16(const int64_t* crow, const void* scores, void* probs, int64_t n, int64_t nnz, int dtype,
+                          void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (n < 0 || n > INT32_MAX || nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "softmax sizes out of range");
+  if (!as::aligned(scores, 2) || !as::aligned(probs, 2))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "scores and probs must be 2-byte aligned");
+  if (n == 0 || nnz == 0) return AS_OK;
+  if (crow == nullptr || scores == nullptr || probs == nullptr)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t blocks = (n + as::kWavesPerBlock - 1) / as::kWavesPerBlock;
+  for (int64_t b0 = 0; b0 < blocks; b0 += as::kMaxBlocksPerLaunch) {
+    const int64_t nb = blocks - b0 < as::kMaxBlocksPerLaunch ? blocks - b0 : as::kMaxBlocksPerLaunch;
+    const dim3 grid(static_cast<unsigned>(nb));
+    if (dtype == AS_DTYPE_BF16)
+      hipLaunchKernelGGL(as::csr_row_softmax16_kernel<as::Bf16>, grid, dim3(as::kBlock), 0, s, crow,
+                         static_cast<const as::Bf16*>(scores), static_cast<uint16_t*>(probs), n,
+                         b0 * as::kWavesPerBlock);
+    else
+      hipLaunchKernelGGL(as::csr_row_softmax16_kernel<as::Fp16>, grid, dim3(as::kBlock), 0, s, crow,
+                         static_cast<const as::Fp16*>(scores), static_cast<uint16_t*>(probs), n,
+                         b0 * as::kWavesPerBlock);
+  }
+  return as::check_launch("csr_row_softmax_16");
 }
 
 size_t as_csr_attention_workspace_bytes(int64_t n, int64_t nnz) {

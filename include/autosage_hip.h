@@ -186,6 +186,15 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
                             void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* Row softmax of bf16 or fp16 scores (dtype AS_DTYPE_BF16 / AS_DTYPE_F16):
+ * the scores convert exactly to fp32, the softmax is that of
+ * as_csr_row_softmax_f32 in fp32, and each probability is rounded once to the
+ * element type.  The reference computes it with torch ops in the scores' own
+ * type (autosage/_auto.py:744-759), summing a row's exponentials in bf16 /
+ * fp16. */
+int as_csr_row_softmax_16(const int64_t* crow, const void* scores, void* probs,
+                          int64_t n, int64_t nnz, int dtype, void* stream);
+
 /* out[e] = <query[row(e)], key[col[e]]> for every nonzero, CSR order.
  * Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134), op schema :192.
  * The dot product uses the reference kernel's summation order

@@ -17,7 +17,9 @@ Contents:
 * ``attention_ref`` = composition of the above (autosage/_auto.py:762-780);
 * ``spmm_rounded_16`` / ``sddmm_rounded_16``: the bf16 / fp16 SpMM and
   SDDMM rule (fp64 sum of exact products, rounded to fp32, then to the 16-bit
-  type).
+  type); ``row_softmax_rounded_16``: the fp32 row softmax of 16-bit scores,
+  rounded once (a composition of or_row_softmax_f32 and torch's rounding,
+  pinned through them).
 
 How each function is pinned (independent checks in tests/test_oracle.py):
 * or_spmm_seq_f32: bit-identical to torch.sparse.mm on CPU (MKL) on random
@@ -171,6 +173,14 @@ def row_softmax(crow, scores) -> np.ndarray:
     out = np.zeros_like(s)
     _load().or_row_softmax_f32(_p(crow), _p(s), crow.size - 1, _p(out))
     return out
+
+
+def row_softmax_rounded_16(crow, scores, dtype: torch.dtype) -> torch.Tensor:
+    """The row softmax of 16-bit scores as as_csr_row_softmax_16 defines it:
+    the fp32 softmax (``row_softmax``) of the exactly converted scores, each
+    probability rounded once to ``dtype``."""
+    s32 = torch.as_tensor(scores).to(dtype).float().numpy()
+    return torch.from_numpy(row_softmax(crow, s32)).to(dtype)
 
 
 def row_softmax_f64(crow, scores) -> np.ndarray:
