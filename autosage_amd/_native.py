@@ -315,10 +315,20 @@ SDDMM_16_WAVES = 4
 SDDMM_16_HUB_THRESHOLD = 1024
 
 
+# fp32 sddmm_csr: every output keeps the reference kernel's dot order on any
+# schedule, so graphs that can hold a row of this many edges take the split
+# schedule (such rows cut into 2048-edge chunks over a workgroup's waves)
+# instead of one wave per row; the bits are the same.
+SDDMM_HUB_THRESHOLD = 1024
+SDDMM_WAVES = 4
+
+
 def sddmm_csr_impl(crow, col, query, key):
     check_sddmm_inputs(crow, col, query, key, allow_16=True)
     if query.dtype in DTYPES_16:
         return sddmm_rounded_16_impl(crow, col, query, key, SDDMM_16_WAVES, SDDMM_16_HUB_THRESHOLD)
+    if col.numel() >= SDDMM_HUB_THRESHOLD:
+        return sddmm_csr_split_impl(crow, col, query, key, SDDMM_WAVES, SDDMM_HUB_THRESHOLD)
     _maybe_validate(crow, col)
     nnz = col.numel()
     n, f = query.shape

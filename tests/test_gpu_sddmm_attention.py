@@ -47,6 +47,26 @@ def test_sddmm_csr_bitwise(features):
     assert bitwise_equal(got, ref), mismatch_report(got, ref)
 
 
+def test_sddmm_c_entry_one_wave_per_row():
+    """as_sddmm_csr_f32 (one wave per row, the reference's launch) gives the
+    reference's bits on a graph with hub rows; the op takes the split
+    schedule there, with the same bits."""
+    from autosage_amd import _native
+
+    crow, col = case_graph(900, 9, seed=3, hubs=4, hub_degree=2500, empty=0.05)
+    q, k = _qk(900, 64, seed=3)
+    ref = oracle.sddmm_ref(crow, col, q, k)
+    d_crow, d_col, d_q, d_k = to_dev(crow, col, q, k)
+    out = torch.empty(col.size, dtype=torch.float32, device="cuda")
+    status = _native.library().as_sddmm_csr_f32(d_crow.data_ptr(), d_col.data_ptr(), d_q.data_ptr(),
+                                                d_k.data_ptr(), out.data_ptr(), 900, col.size, 64,
+                                                torch.cuda.current_stream().cuda_stream)
+    assert status == 0
+    torch.cuda.synchronize()
+    assert bitwise_equal(out, ref)
+    assert torch.equal(torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, d_k), out)
+
+
 @pytest.mark.parametrize("waves", [2, 4, 8])
 @pytest.mark.parametrize("threshold", [1, 16, 600, 10**6])
 @pytest.mark.parametrize("features", [33, 64, 128])
