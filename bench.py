@@ -47,8 +47,8 @@ def sddmm_bytes(n: int, nnz: int, f: int, elem: int = 4) -> int:
     return elem * f * nnz + elem * f * n + elem * nnz + 8 * nnz + 8 * (n + 1)
 
 
-def attention_bytes(n: int, nnz: int, fqk: int, fv: int) -> int:
-    return 4 * fqk * nnz + 4 * fqk * n + 4 * fv * nnz + 4 * fv * n + 8 * nnz + 8 * (n + 1)
+def attention_bytes(n: int, nnz: int, fqk: int, fv: int, elem: int = 4) -> int:
+    return elem * (fqk * nnz + fqk * n + fv * nnz + fv * n) + 8 * nnz + 8 * (n + 1)
 
 
 def profiled_traffic(workload: str, variant: str):
@@ -232,8 +232,8 @@ def main() -> int:
                         help="instead of the bench line: the scheduler's cost on this workload (a cold call with an "
                              "empty schedule cache, then cached calls) against one call of the chosen kernel")
     parser.add_argument("--dtype", default="f32", choices=["f32", "bf16", "fp16"],
-                        help="feature type of the SpMM workloads (cfg1-3) and the SDDMM one (cfg4); bf16/fp16 run "
-                             "the rounded 16-bit kernels")
+                        help="feature type of the SpMM workloads (cfg1-3), the SDDMM one (cfg4) and the attention "
+                             "(cfg5); bf16/fp16 run the rounded 16-bit kernels")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gpu-baseline", action="store_true")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -498,16 +498,27 @@ def bench_other(args, device) -> dict:
         log(f"generated cfg5: {w.degree_stats()} in {time.time() - t0:.1f}s")
         crow = torch.from_numpy(w.crow).to(device)
         col = torch.from_numpy(w.col).to(device)
-        q = torch.from_numpy(w.dense["q"]).to(device)
-        k = torch.from_numpy(w.dense["k"]).to(device)
-        v = torch.from_numpy(w.dense["v"]).to(device)
+        dt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+        q = torch.from_numpy(w.dense["q"]).to(device).to(dt)
+        k = torch.from_numpy(w.dense["k"]).to(device).to(dt)
+        v = torch.from_numpy(w.dense["v"]).to(device).to(dt)
         from autosage_amd._native import columns_ascending
 
-        variants = {"fused": lambda: torch.ops.autosage.csr_attention(crow, col, q, k, v, 0.125)}
-        # the column-sliced attention (online softmax per column slice) when
-        # the columns ascend; listed last so that the exact kernel wins a tie
-        if not args.exact_only and columns_ascending(crow, col):
-            variants["colslice"] = lambda: torch.ops.autosage.csr_attention_colslice(crow, col, q, k, v, 0.125)
+        if dt == torch.float32:
+            variants = {"fused": lambda: torch.ops.autosage.csr_attention(crow, col, q, k, v, 0.125)}
+            # the column-sliced attention (online softmax per column slice)
+            # when the columns ascend; listed last so that the exact kernel
+            # wins a tie
+            if not args.exact_only and columns_ascending(crow, col):
+                variants["colslice"] = lambda: torch.ops.autosage.csr_attention_colslice(crow, col, q, k, v, 0.125)
+        else:
+            # 16-bit: the three native stages (SDDMM, row softmax, SpMM), the
+            # scale 1/8 applied exactly to the 16-bit scores
+            def stages():
+                s = torch.ops.autosage.sddmm_csr(crow, col, q, k).mul_(0.125)
+                return torch.ops.autosage.spmm_csr(crow, col, torch.ops.autosage.csr_row_softmax(crow, s), v)
+
+            variants = {"stages16": stages}
         calib = {}
         chosen = calibrate(variants, calib) if args.variant == "calibrated" else args.variant
         if chosen not in variants:
@@ -516,9 +527,12 @@ def bench_other(args, device) -> dict:
         step = variants[chosen]
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * w.nnz * (64 + 128)
-        algo = attention_bytes(w.rows, w.nnz, 64, 128)
-        name = "cfg5 CSR attention fp32 Fqk=64 Fv=128 scale=1/8"
+        algo = attention_bytes(w.rows, w.nnz, 64, 128, elem=q.element_size())
+        type_name = {"f32": "fp32", "bf16": "bf16", "fp16": "fp16"}[args.dtype]
+        name = f"cfg5 CSR attention {type_name} Fqk=64 Fv=128 scale=1/8"
         cpu = None if args.no_cpu_baseline else cpu_baseline_attention(w)
+        if cpu is not None and dt != torch.float32:
+            cpu["sample"] += "; fp32 (the reference's CPU composition in fp32)"
     traffic = profiled_traffic(name, chosen)
     return {
         "metric": METRIC,
@@ -531,7 +545,7 @@ def bench_other(args, device) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": args.dtype if args.workload == "cfg4" else "f32",
+        "dtype": args.dtype,
         "data": "synthetic",
         "config": {"workload": name, "rows": w.rows, "nnz": w.nnz, "variant": chosen,
                    "degree_stats": w.degree_stats()},
