@@ -69,6 +69,7 @@ _SIGNATURES = {
          _c_i64, _c_ptr],
     ),
     "as_spmm_rounded_16_group_degree": (_c_i64, [_c_i64]),
+    "as_spmm_rounded_16_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_csr_row_softmax_16": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_int, _c_ptr]),
     "as_sddmm_csr_rounded_16": (
         _c_int,
@@ -296,10 +297,12 @@ def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
     if n == 0 or f == 0:
         return y
     lib = library()
-    full = lib.as_spmm_colslice_workspace_bytes(n, f)
-    ws = _workspace(min(full, _colslice_workspace_cap()), x.device)
     threshold = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices))))
     sliced, grouped = row_counts(crow, threshold, int(lib.as_spmm_rounded_16_group_degree(f)))
+    # partial rows for the sliced rows only (a short workspace sums the rest
+    # whole, with the same bits)
+    needed = lib.as_spmm_rounded_16_workspace_bytes(n, f, sliced)
+    ws = _workspace(min(needed, _colslice_workspace_cap()), x.device)
     with torch.cuda.device(x.device):
         status = lib.as_spmm_csr_rounded_16(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, DTYPES_16[x.dtype],

@@ -480,7 +480,9 @@ __device__ __forceinline__ void short_rows_grouped(const int64_t* __restrict__ c
 }
 
 // One chunk of the work: rows order[item_begin, item_begin + items); the
-// first counts[0] rows of the order are sliced, the rest are short.  A launch
+// first counts[0] rows of the order are sliced (at most `capacity` of them in
+// a chunk: with 16-bit elements the rest are summed whole), the rest are
+// short.  A launch
 // is made of groups of 8 workgroups (one per XCD, by blockIdx % 8):
 //   * slice groups, Gs per (feature tile, phase): block mb takes slice
 //     8·p + mb % 8 and its 4 waves stride over the chunk's sliced rows; the
@@ -504,6 +506,9 @@ struct SliceChunk {
   int64_t slice_groups;  // Gs: slice groups per (tile, phase)
   int64_t short_groups;  // Gh: short groups per tile
   int64_t sliced;        // the caller's count of sliced rows in the chunk, < 0 if unknown
+  // partial rows of the buffer: sliced rows past them are summed whole
+  // (16-bit elements only, whose results do not depend on the order)
+  int64_t capacity = INT64_MAX;
 };
 
 // Where the grouped short rows (16-bit, degree below 4·G) start in the order:
@@ -552,7 +557,8 @@ inline void chunk_groups(SliceChunk& c, int64_t sliced, int64_t grouped, int64_t
 __device__ __forceinline__ int64_t first_short(const int32_t* __restrict__ counts, const SliceChunk& c) {
   const int64_t h = counts[0];
   const int64_t end = c.item_begin + c.items;
-  return h < c.item_begin ? c.item_begin : (h > end ? end : h);
+  const int64_t cap_end = c.capacity < c.items ? c.item_begin + c.capacity : end;
+  return h < c.item_begin ? c.item_begin : (h > cap_end ? cap_end : h);
 }
 
 template <typename T, int V, bool HAS_VAL, bool OFF32>
@@ -645,9 +651,8 @@ __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, con
                                                       const int32_t* __restrict__ counts, T* __restrict__ y,
                                                       int64_t F, const SliceChunk& c, int64_t chunk_stride) {
   const int64_t FV = F / VR;
-  // only the sliced rows: order[0, counts[0])
-  const int64_t sliced = counts[0] - c.item_begin;
-  const int64_t total = (sliced < c.items ? (sliced > 0 ? sliced : 0) : c.items) * FV;
+  // only the rows the slice blocks took: order[item_begin, first_short)
+  const int64_t total = (first_short(counts, c) - c.item_begin) * FV;
   const int64_t stride = R * kBlock;
   for (int64_t t = rb * kBlock + threadIdx.x; t < total; t += stride) {
     const int64_t local = t / FV;
@@ -862,15 +867,20 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   const bool off32 = n <= (int64_t(1) << 24) && f * E < (int64_t(1) << 24) && n * f * E <= (int64_t(1) << 32);
   const int vr = (f % 2 == 0 && aligned(y, static_cast<size_t>(2 * E))) ? 2 : 1;
 
-  // two partial buffers of `chunk` rows each (chunk k writes buffer k % 2)
-  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed) / (2 * row_bytes));
-  const int64_t preferred = preferred_chunk_rows(n);
-  if (chunk > preferred) chunk = preferred;
+  // two partial buffers of `capacity` rows each (chunk k writes buffer
+  // k % 2).  fp32: chunks of at most `capacity` rows, so that every sliced
+  // row of a chunk has partial rows.  16-bit: chunks of the preferred size
+  // whatever the workspace; sliced rows past the capacity are summed whole,
+  // with the same bits, so a workspace sized for the sliced rows suffices.
+  const int64_t fits = static_cast<int64_t>((workspace_bytes - fixed) / (2 * row_bytes));
+  int64_t chunk = preferred_chunk_rows(n);
+  if (E == 4 && chunk > fits) chunk = fits;
   // blocks of a launch: 8 per group, at most tiles·(P·ceil(c/4) + ceil(c/32))
   // work groups for c rows, and reduce groups at most a quarter of those
   const int64_t max_rows = (kMaxBlocksPerLaunch * 4 / 5 / (kSlices * tiles) - 2) * 32 / (8 * kPhases + 1);
   if (chunk > max_rows) chunk = max_rows;
   if (chunk < 1) return fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
+  const int64_t capacity = fits < chunk ? fits : chunk;
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
@@ -883,7 +893,7 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   ws += 256;
   void* bin_ws = ws;
   double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
-                        reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + chunk * row_bytes)};
+                        reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + capacity * row_bytes)};
 
   const int64_t min_degree = slicing == kSliceColumns ? kColsliceMinDegree : kEdgeSliceMinDegree;
   launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, off, s, slicing == kSliceEdges);
@@ -914,20 +924,20 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   const int64_t chunks = (n + chunk - 1) / chunk;
   SliceChunk previous{0, 0, buffers[1], 1, 1, -1};
   for (int64_t k = 0; k <= chunks; ++k) {
-    SliceChunk current{k * chunk, 0, buffers[k % 2], 1, 1, -1};
+    SliceChunk current{k * chunk, 0, buffers[k % 2], 1, 1, -1, capacity};
     if (k < chunks) current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
     // the sliced rows come first in the order, the grouped ones last
     const int64_t chunk_end = current.item_begin + current.items;
     const int64_t grouped_begin = grouped_rows < 0 || grouped_rows > n ? chunk_end : n - grouped_rows;
     const int64_t from = grouped_begin > current.item_begin ? grouped_begin : current.item_begin;
-    chunk_groups(current,
-                 sliced_rows < 0 ? -1 : (sliced_rows > current.item_begin ? sliced_rows - current.item_begin : 0),
-                 chunk_end > from ? chunk_end - from : 0, rows_per_wave);
+    int64_t sliced_here = sliced_rows < 0 ? -1 : (sliced_rows > current.item_begin ? sliced_rows - current.item_begin : 0);
+    if (sliced_here > capacity) sliced_here = capacity;
+    chunk_groups(current, sliced_here, chunk_end > from ? chunk_end - from : 0, rows_per_wave);
 #if AS_COLSLICE_OVERLAP
-    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, previous, chunk);
+    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, previous, capacity);
 #else
-    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, SliceChunk{0, 0, nullptr, 1, 1, -1}, chunk);
-    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, SliceChunk{0, 0, nullptr, 1, 1, -1}, current, chunk);
+    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, SliceChunk{0, 0, nullptr, 1, 1, -1}, capacity);
+    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, SliceChunk{0, 0, nullptr, 1, 1, -1}, current, capacity);
 #endif
     previous = current;
   }
@@ -961,6 +971,14 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
 }
 
 int64_t as_spmm_rounded_16_group_degree(int64_t f) { return as::grouped_degree(f, 2); }
+
+size_t as_spmm_rounded_16_workspace_bytes(int64_t n, int64_t f, int64_t sliced_rows) {
+  if (n < 0) n = 0;
+  if (f < 1) f = 1;
+  int64_t rows = as::preferred_chunk_rows(n);
+  if (sliced_rows >= 0 && sliced_rows < rows) rows = sliced_rows > 0 ? sliced_rows : 1;
+  return as::colslice_fixed_bytes(n) + 2 * static_cast<size_t>(rows) * as::colslice_row_bytes(f);
+}
 
 int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
                            int64_t n, int64_t nnz, int64_t f, int dtype, int column_slices, void* workspace,

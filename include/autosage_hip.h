@@ -143,8 +143,9 @@ int64_t as_spmm_colslice_min_degree(int column_slices);
  * additions when it is exact (the products' bits span at most 53 places);
  * otherwise its error is below 2^-52 of the largest partial sum, and two
  * schedules can round differently only for a sum that close to a tie.
- * Same kernels and workspace as as_spmm_csr_colslice_f32 (size from
- * as_spmm_colslice_workspace_bytes).  column_slices != 0: 8 column slices
+ * Same kernels and workspace layout as as_spmm_csr_colslice_f32 (size from
+ * as_spmm_rounded_16_workspace_bytes: it needs partial rows for the sliced
+ * rows only).  column_slices != 0: 8 column slices
  * (columns must ascend within rows); 0: rows of degree >= 1024 are cut into
  * 8 equal runs of edges instead (any column order).  x, y and val 2-byte
  * aligned; F a multiple of 8 with 16-byte aligned x takes 16-byte lanes.
@@ -161,6 +162,13 @@ int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
                            int column_slices, void* workspace,
                            size_t workspace_bytes, int64_t sliced_rows,
                            int64_t grouped_rows, void* stream);
+
+/* Workspace bytes for as_spmm_csr_rounded_16: as
+ * as_spmm_colslice_workspace_bytes, with partial buffers for sliced_rows rows
+ * (all of a chunk's when sliced_rows < 0).  A workspace with fewer partial
+ * rows than a chunk's sliced rows also works: the sliced rows past them are
+ * summed whole, one wavefront each, with the same bits. */
+size_t as_spmm_rounded_16_workspace_bytes(int64_t n, int64_t f, int64_t sliced_rows);
 
 /* Degree below which as_spmm_csr_rounded_16 sums rows several to a
  * wavefront for F features (32, 64 or 128 for F <= 64, <= 128, more; 0 when

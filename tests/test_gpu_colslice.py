@@ -236,3 +236,16 @@ def test_sliced_rows_hint_only_sizes_the_launches():
         torch.cuda.synchronize()
         for y in outs[1:]:
             assert torch.equal(y, outs[0])
+        # partial buffers for 1 row, half the sliced rows and all of them: the
+        # sliced rows past the capacity are summed whole, with the same bits
+        fixed = lib.as_spmm_rounded_16_workspace_bytes(n, f, 0) - 2 * 8 * f * 8
+        for rows in (1, max(sliced // 2, 1), sliced):
+            small = torch.empty(fixed + 2 * rows * 8 * f * 8, dtype=torch.uint8, device="cuda")
+            assert lib.as_spmm_rounded_16_workspace_bytes(n, f, rows) == small.numel()
+            y = torch.empty_like(xb)
+            status = lib.as_spmm_csr_rounded_16(d_crow.data_ptr(), d_col.data_ptr(), 0, xb.data_ptr(), y.data_ptr(),
+                                                n, col.size, f, 1, column_slices, small.data_ptr(), small.numel(),
+                                                sliced, grouped, stream)
+            assert status == 0, lib.as_last_error()
+            torch.cuda.synchronize()
+            assert torch.equal(y, outs[0]), rows
