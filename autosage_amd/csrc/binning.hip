@@ -100,14 +100,18 @@ __global__ __launch_bounds__(kScanThreads) void bin_scan_kernel(const int32_t* _
   const int64_t per = (entries + kScanThreads - 1) / kScanThreads;
   const int64_t begin = static_cast<int64_t>(threadIdx.x) * per;
   const int64_t end = begin + per < entries ? begin + per : entries;
+  // each thread's entries are read once, 8 loads in flight at a time
   int local = 0;
   int local_heavy = 0;
+#pragma unroll 8
   for (int64_t t = begin; t < end; ++t) {
-    local += table[t];
-    if (t < heavy_entries) local_heavy += table[t];
+    const int v = table[t];
+    local += v;
+    if (t < heavy_entries) local_heavy += v;
   }
   int total = 0;
   int running = block_excl_scan(local, lds, &total);
+#pragma unroll 8
   for (int64_t t = begin; t < end; ++t) {
     offsets[t] = running;
     running += table[t];
