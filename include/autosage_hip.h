@@ -198,8 +198,7 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
  * the scores convert exactly to fp32, the softmax is that of
  * as_csr_row_softmax_f32 in fp32, and each probability is rounded once to the
  * element type.  The reference computes it with torch ops in the scores' own
- * type (autosage/_auto.py:744-759), summing a row's exponentials in bf16 /
- * fp16. */
+ * type (autosage/_auto.py:744-759). */
 int as_csr_row_softmax_16(const int64_t* crow, const void* scores, void* probs,
                           int64_t n, int64_t nnz, int dtype, void* stream);
 

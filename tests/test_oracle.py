@@ -348,6 +348,23 @@ def test_sddmm_rounded_16_exact_products_ties_and_overflow():
     assert h[1] == 1.00390625  # fp16 holds 1 + 2^-8
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_row_softmax_rounded_16_closed_forms(dtype):
+    """Rows of 4 equal scores, 1 score, scores (1, 0) and 1,000 equal scores:
+    1/4, 1, e/(1+e) and 1/1000, each rounded once to the 16-bit type (a
+    softmax computed in the 16-bit type itself, e.g. its denominator summed
+    in bf16, stalls at 256 and gives 1/256 for the last row)."""
+    crow = np.array([0, 4, 5, 7, 1007], dtype=np.int64)
+    scores = np.zeros(1007, dtype=np.float32)
+    scores[4] = 3.0
+    scores[5] = 1.0
+    got = oracle.row_softmax_rounded_16(crow, scores, dtype).float().numpy()
+    assert np.all(got[:4] == 0.25) and got[4] == 1.0
+    e = np.exp(1.0)
+    assert got[5] == _round_16(e / (1 + e), dtype) and got[6] == _round_16(1 / (1 + e), dtype)
+    assert np.all(got[7:] == _round_16(1e-3, dtype))
+
+
 def test_spmm_rounded_16_ties_and_overflow():
     crow = np.array([0, 2, 4, 7, 9], dtype=np.int64)
     col = np.array([0, 1, 0, 2, 0, 1, 3, 4, 4], dtype=np.int64)
