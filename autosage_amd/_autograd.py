@@ -13,6 +13,10 @@ backward formulas built from the same native kernels:
   the 16-bit type).
 * ``s[e] = <Q[row(e)], K[col(e)]>``:
   ``dQ = A_ds·K`` (SpMM with weights ``ds``) and ``dK = A_dsᵀ·Q``.
+* ``p = softmax_row(s)``: ``ds = p·(dp − Σ_row dp·p)`` (native kernel).
+* the fused attention ``out = softmax_row(scale·s)·V``: the scores and
+  probabilities are recomputed with the native ops and the three formulas
+  above are chained (``dV = Pᵀ·dOut``).
 
 The transposed CSR (rows of Aᵀ list the source rows in ascending order, a
 stable sort of the edges by column) is built with torch ops and memoised per
@@ -118,9 +122,57 @@ def _sddmm_backward(ctx, grad_s: torch.Tensor):
     return (None, None, grad_q, grad_k, *extra)
 
 
+def _softmax_setup(ctx, inputs, output) -> None:
+    ctx.save_for_backward(inputs[0], output)
+
+
+def _softmax_backward(ctx, grad_p: torch.Tensor):
+    from ._native import csr_row_softmax_backward_impl
+
+    crow, probs = ctx.saved_tensors
+    return None, csr_row_softmax_backward_impl(crow, probs, grad_p.contiguous())
+
+
+def _attention_setup(ctx, inputs, output) -> None:
+    crow, col, query, key, value = inputs[:5]
+    ctx.save_for_backward(crow, col, query, key, value)
+    ctx.scale = float(inputs[5])
+
+
+def _attention_backward(ctx, grad_out: torch.Tensor):
+    """out = P·V with P = softmax_row(scale·SDDMM(Q, K)): the scores and P
+    are recomputed with the native ops, then
+    dV = Pᵀ·dOut, dP[e] = <dOut[row(e)], V[col(e)]>, dS = softmax'(P, dP)·scale,
+    dQ = A_dS·K, dK = A_dSᵀ·Q (native SpMM / SDDMM / softmax backward)."""
+    from ._native import csr_row_softmax_backward_impl
+
+    crow, col, query, key, value = ctx.saved_tensors
+    grad_out = grad_out.contiguous()
+    scores = _sddmm(crow, col, query, key)
+    if ctx.scale != 1.0:
+        scores = scores * ctx.scale
+    probs = torch.ops.autosage.csr_row_softmax(crow, scores)
+    grad_q = grad_k = grad_v = None
+    crow_t, col_t, perm = csr_transpose(crow, col)
+    if ctx.needs_input_grad[4]:
+        grad_v = _spmm(crow_t, col_t, probs.index_select(0, perm).contiguous(), grad_out)
+    if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
+        grad_s = csr_row_softmax_backward_impl(crow, probs, _sddmm(crow, col, grad_out, value))
+        if ctx.scale != 1.0:
+            grad_s = grad_s * ctx.scale
+        if ctx.needs_input_grad[2]:
+            grad_q = _spmm(crow, col, grad_s, key)
+        if ctx.needs_input_grad[3]:
+            grad_k = _spmm(crow_t, col_t, grad_s.index_select(0, perm).contiguous(), query)
+    return None, None, grad_q, grad_k, grad_v, None
+
+
 def register() -> None:
     """Attaches the backward formulas to the registered operators."""
     for name in ("spmm_csr", "spmm_csr_split", "spmm_csr_colslice"):
         torch.library.register_autograd(f"autosage::{name}", _spmm_backward, setup_context=_spmm_setup)
     for name in ("sddmm_csr", "sddmm_csr_split"):
         torch.library.register_autograd(f"autosage::{name}", _sddmm_backward, setup_context=_sddmm_setup)
+    torch.library.register_autograd("autosage::csr_row_softmax", _softmax_backward, setup_context=_softmax_setup)
+    for name in ("csr_attention", "csr_attention_colslice"):
+        torch.library.register_autograd(f"autosage::{name}", _attention_backward, setup_context=_attention_setup)

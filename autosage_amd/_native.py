@@ -71,6 +71,7 @@ _SIGNATURES = {
     "as_spmm_rounded_16_group_degree": (_c_i64, [_c_i64]),
     "as_spmm_rounded_16_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_csr_row_softmax_16": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_int, _c_ptr]),
+    "as_csr_row_softmax_backward": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_int, _c_ptr]),
     "as_sddmm_csr_rounded_16": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_ptr, _c_size,
@@ -426,6 +427,29 @@ def csr_row_softmax_impl(crow, scores):
             )
     _raise(status, "autosage::csr_row_softmax")
     return probs
+
+
+def csr_row_softmax_backward_impl(crow, probs, grad):
+    """dL/dscores of ``csr_row_softmax`` from its output ``probs`` and
+    dL/dprobs (fp32 arithmetic; 16-bit values convert exactly and each result
+    is rounded once)."""
+    _check(crow.is_cuda and probs.is_cuda and grad.is_cuda, "crow, probs and grad must be CUDA tensors")
+    _check(crow.dtype == torch.long and crow.dim() == 1 and crow.is_contiguous(), "crow must be contiguous torch.long")
+    _check(probs.dtype == grad.dtype and probs.shape == grad.shape and probs.dim() == 1,
+           "probs and grad must be one-dimensional, of one dtype and shape")
+    _check(probs.dtype == torch.float32 or probs.dtype in DTYPES_16, "probs must be float32, bfloat16 or float16")
+    probs, grad = probs.contiguous(), grad.contiguous()
+    out = torch.empty_like(probs)
+    n = crow.numel() - 1
+    if n <= 0 or probs.numel() == 0:
+        return out.zero_()
+    dtype = 0 if probs.dtype == torch.float32 else DTYPES_16[probs.dtype]
+    with torch.cuda.device(probs.device):
+        status = library().as_csr_row_softmax_backward(
+            _ptr(crow), _ptr(probs), _ptr(grad), _ptr(out), n, probs.numel(), dtype, _stream(probs.device)
+        )
+    _raise(status, "autosage::csr_row_softmax (backward)")
+    return out
 
 
 def csr_attention_impl(crow, col, query, key, value, scale=1.0):

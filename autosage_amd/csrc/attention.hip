@@ -18,6 +18,8 @@
 // bit-identical to the three unfused stages.  Rows of degree >= 1024 are
 // binned (longest bucket first, as for the split SpMM) and each gets a
 // workgroup whose waves share the scoring and split the value features.
+#include <type_traits>
+
 #include "as_device.h"
 #include "as_internal.h"
 #include "elem16.h"
@@ -67,6 +69,56 @@ __global__ __launch_bounds__(kBlock) void csr_row_softmax16_kernel(const int64_t
   d = wave_sum_f32(d);
   for (int64_t e = rs + lane; e < re; e += kWave)
     probs[e] = Elem<T>::bits(static_cast<double>(expf(Elem<T>::at(scores, e) - m) / d));
+}
+
+// Backward of the row softmax: given p = softmax(s) and dp = dL/dp,
+//   t = sum_e dp_e · p_e   (lane l: e = rs+l, rs+l+64, ... with fmaf, in
+//                           order; then the 32/16/8/4/2/1 butterfly)
+//   ds_e = p_e · (dp_e - t)
+// in fp32 (16-bit inputs convert exactly; each ds_e is rounded once).
+template <typename T>
+__device__ __forceinline__ float sm_load(const T* __restrict__ p, int64_t e) {
+  if constexpr (std::is_same<T, float>::value) return p[e];
+  else return Elem<T>::at(p, e);
+}
+template <typename T>
+__device__ __forceinline__ void sm_store(T* __restrict__ p, int64_t e, float v) {
+  if constexpr (std::is_same<T, float>::value) p[e] = v;
+  else p[e].bits = Elem<T>::bits(static_cast<double>(v));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void csr_row_softmax_backward_kernel(const int64_t* __restrict__ crow,
+                                                                          const T* __restrict__ probs,
+                                                                          const T* __restrict__ grad,
+                                                                          T* __restrict__ grad_scores, int64_t n,
+                                                                          int64_t idx_base) {
+  const int lane = lane_id();
+  const int64_t row = idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block();
+  if (row >= n) return;
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t re = uniform_i64(crow[row + 1]);
+  if (rs == re) return;
+  float t = 0.f;
+  for (int64_t e = rs + lane; e < re; e += kWave) t = __builtin_fmaf(sm_load(grad, e), sm_load(probs, e), t);
+  t = wave_sum_f32(t);
+  for (int64_t e = rs + lane; e < re; e += kWave) {
+    const float p = sm_load(probs, e);
+    sm_store(grad_scores, e, p * (sm_load(grad, e) - t));
+  }
+}
+
+template <typename T>
+int launch_softmax_backward(const int64_t* crow, const void* probs, const void* grad, void* grad_scores, int64_t n,
+                            hipStream_t s) {
+  const int64_t blocks = (n + kWavesPerBlock - 1) / kWavesPerBlock;
+  for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
+    const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
+    hipLaunchKernelGGL(csr_row_softmax_backward_kernel<T>, dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0, s, crow,
+                       static_cast<const T*>(probs), static_cast<const T*>(grad), static_cast<T*>(grad_scores), n,
+                       b0 * kWavesPerBlock);
+  }
+  return check_launch("csr_row_softmax_backward");
 }
 
 template <int S>
@@ -370,6 +422,24 @@ int as_csr_row_softmax_f32(const int64_t* crow, const float* scores, float* prob
                        scores, probs, n, b0 * as::kWavesPerBlock);
   }
   return as::check_launch("csr_row_softmax");
+}
+
+int as_csr_row_softmax_backward(const int64_t* crow, const void* probs, const void* grad, void* grad_scores,
+                                int64_t n, int64_t nnz, int dtype, void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_F32 && dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (n < 0 || n > INT32_MAX || nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "softmax sizes out of range");
+  const size_t align = dtype == AS_DTYPE_F32 ? 4 : 2;
+  if (!as::aligned(probs, align) || !as::aligned(grad, align) || !as::aligned(grad_scores, align))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "probs, grad and grad_scores must be aligned to their element size");
+  if (n == 0 || nnz == 0) return AS_OK;
+  if (crow == nullptr || probs == nullptr || grad == nullptr || grad_scores == nullptr)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == AS_DTYPE_F32) return as::launch_softmax_backward<float>(crow, probs, grad, grad_scores, n, s);
+  if (dtype == AS_DTYPE_BF16) return as::launch_softmax_backward<as::Bf16>(crow, probs, grad, grad_scores, n, s);
+  return as::launch_softmax_backward<as::Fp16>(crow, probs, grad, grad_scores, n, s);
 }
 
 int as_csr_row_softmax_16(const int64_t* crow, const void* scores, void* probs, int64_t n, int64_t nnz, int dtype,

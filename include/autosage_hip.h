@@ -40,8 +40,10 @@ typedef enum as_status {
   AS_ERR_WORKSPACE = 4
 } as_status;
 
-/* 16-bit element types of as_spmm_csr_rounded_16. */
+/* Element types of the entry points that take a dtype (AS_DTYPE_F32 only
+ * where stated). */
 enum {
+  AS_DTYPE_F32 = 0,
   AS_DTYPE_BF16 = 1,
   AS_DTYPE_F16 = 2
 };
@@ -201,6 +203,18 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
  * type (autosage/_auto.py:744-759). */
 int as_csr_row_softmax_16(const int64_t* crow, const void* scores, void* probs,
                           int64_t n, int64_t nnz, int dtype, void* stream);
+
+/* Backward of the row softmax (no reference counterpart: the reference
+ * registers no autograd, and its torch composition, autosage/_auto.py:744-759,
+ * is differentiated by torch there): given probs = softmax(scores) row by row
+ * and grad = dL/dprobs, grad_scores[e] = probs[e]·(grad[e] − t) with
+ * t = Σ grad·probs over the row, in fp32: lane l of a wavefront adds edges
+ * l, l+64, ... of the row with fmaf, in order, then a 32/16/8/4/2/1
+ * butterfly.  dtype AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16 (16-bit
+ * values convert exactly; each result is rounded once). */
+int as_csr_row_softmax_backward(const int64_t* crow, const void* probs, const void* grad,
+                                void* grad_scores, int64_t n, int64_t nnz, int dtype,
+                                void* stream);
 
 /* out[e] = <query[row(e)], key[col[e]]> for every nonzero, CSR order.
  * Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134), op schema :192.

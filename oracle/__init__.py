@@ -30,6 +30,11 @@ How each function is pinned (independent checks in tests/test_oracle.py):
 * or_sddmm_ref_f32: KAT [4, 7, 10] (reference test_cpu.py:45-53), fp64
   bound, torch gather-dot within tolerance, and a tree-order check where the
   reference order and sequential order give different bits.
+* or_row_softmax_backward_f32: a Python restatement of the lane order on
+  values whose products and sums are exact in fp64 (so every fmaf is one
+  rounding), with a row where that order and a sequential sum differ; fp64
+  closed forms (uniform probabilities with constant grad -> 0, one-entry rows
+  -> 0, torch autograd of the fp64 softmax within 1e-6).
 * or_row_softmax_f32: KAT (rows sum to 1, single-entry rows = 1.0), torch
   scatter composition within 1e-6 relative, fp64 bound.
 * spmm_rounded_16: exact rational sums (fractions.Fraction) rounded the same
@@ -74,8 +79,9 @@ def _load() -> ctypes.CDLL:
         lib.or_sddmm_f64.argtypes = [p, p, p, p, i64, i64, p]
         lib.or_row_softmax_f32.argtypes = [p, p, i64, p]
         lib.or_row_softmax_f64.argtypes = [p, p, i64, p]
+        lib.or_row_softmax_backward_f32.argtypes = [p, p, p, i64, p]
         for name in ("or_spmm_seq_f32", "or_spmm_f64", "or_bin_rows", "or_sddmm_ref_f32", "or_sddmm_f64",
-                     "or_row_softmax_f32", "or_row_softmax_f64"):
+                     "or_row_softmax_f32", "or_row_softmax_f64", "or_row_softmax_backward_f32"):
             getattr(lib, name).restype = None
         _lib = lib
     return _lib
@@ -173,6 +179,24 @@ def row_softmax(crow, scores) -> np.ndarray:
     out = np.zeros_like(s)
     _load().or_row_softmax_f32(_p(crow), _p(s), crow.size - 1, _p(out))
     return out
+
+
+def row_softmax_backward(crow, probs, grad) -> np.ndarray:
+    """dL/dscores of the row softmax from its output and dL/dprobs, fp32 in
+    the GPU kernel's order (64 lane partials of grad·p, butterfly)."""
+    crow = _np(crow, np.int64)
+    p, g = _np(probs, np.float32), _np(grad, np.float32)
+    out = np.zeros(p.size, dtype=np.float32)
+    _load().or_row_softmax_backward_f32(_p(crow), _p(p), _p(g), crow.size - 1, _p(out))
+    return out
+
+
+def row_softmax_backward_rounded_16(crow, probs, grad, dtype: torch.dtype) -> torch.Tensor:
+    """The same on 16-bit values: exact conversions to fp32, each result
+    rounded once to ``dtype``."""
+    p32 = torch.as_tensor(probs).to(dtype).float().numpy()
+    g32 = torch.as_tensor(grad).to(dtype).float().numpy()
+    return torch.from_numpy(row_softmax_backward(crow, p32, g32)).to(dtype)
 
 
 def row_softmax_rounded_16(crow, scores, dtype: torch.dtype) -> torch.Tensor:

@@ -128,3 +128,31 @@ void or_row_softmax_f64(const int64_t* crow, const double* scores, int64_t n, do
     for (int64_t e = s0; e < s1; ++e) probs[e] = exp(scores[e] - m) / d;
   }
 }
+
+/* Backward of the row softmax in the order the GPU kernel defines (the
+ * reference registers no autograd; its torch composition,
+ * autosage/_auto.py:744-759, has the same mathematical gradient):
+ *   t = sum_e grad_e * p_e  as 64 lane partials (edge e of the row goes to
+ *       lane (e - row start) mod 64, each lane an fmaf chain in edge order),
+ *       then the butterfly v_l += v_{l xor o} for o = 32, 16, 8, 4, 2, 1;
+ *   out_e = p_e * (grad_e - t). */
+void or_row_softmax_backward_f32(const int64_t* crow, const float* probs, const float* grad, int64_t n,
+                                 float* out) {
+  for (int64_t r = 0; r < n; ++r) {
+    const int64_t s0 = crow[r], s1 = crow[r + 1];
+    if (s0 == s1) continue;
+    float lane[64];
+    for (int l = 0; l < 64; ++l) lane[l] = 0.0f;
+    for (int64_t e = s0; e < s1; ++e) {
+      const int l = (int)((e - s0) % 64);
+      lane[l] = fmaf(grad[e], probs[e], lane[l]);
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      float next[64];
+      for (int l = 0; l < 64; ++l) next[l] = lane[l] + lane[l ^ o];
+      for (int l = 0; l < 64; ++l) lane[l] = next[l];
+    }
+    const float t = lane[0];
+    for (int64_t e = s0; e < s1; ++e) out[e] = probs[e] * (grad[e] - t);
+  }
+}

@@ -365,6 +365,69 @@ def test_row_softmax_rounded_16_closed_forms(dtype):
     assert np.all(got[7:] == _round_16(1e-3, dtype))
 
 
+def _softmax_backward_lane_order(crow, probs, grad):
+    """Independent restatement of the lane order in numpy float32, for values
+    whose products and partial sums are exact in fp64 (so each fmaf is one
+    rounding to fp32)."""
+    out = np.zeros(probs.size, dtype=np.float32)
+    for r in range(crow.size - 1):
+        s0, s1 = crow[r], crow[r + 1]
+        if s0 == s1:
+            continue
+        lanes = [np.float32(0.0)] * 64
+        for e in range(s0, s1):
+            lanes[(e - s0) % 64] = np.float32(np.float64(grad[e]) * np.float64(probs[e]) + np.float64(lanes[(e - s0) % 64]))
+        for o in (32, 16, 8, 4, 2, 1):
+            lanes = [np.float32(lanes[l] + lanes[l ^ o]) for l in range(64)]
+        t = lanes[0]
+        out[s0:s1] = probs[s0:s1] * (grad[s0:s1] - t)
+    return out
+
+
+def test_row_softmax_backward_lane_order():
+    rng = np.random.default_rng(21)
+    deg = np.array([200, 64, 1, 65, 0, 130])
+    crow = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    nnz = int(crow[-1])
+    # probabilities k/2^14, gradients j/2^8 in [0, 8): exact products, sums
+    # that outgrow fp32's 24 bits (so the order of the additions shows)
+    probs = (rng.integers(0, 1 << 14, nnz) / float(1 << 14)).astype(np.float32)
+    grad = (rng.integers(0, 1 << 11, nnz) / 256.0).astype(np.float32)
+    got = oracle.row_softmax_backward(crow, probs, grad)
+    want = _softmax_backward_lane_order(crow, probs, grad)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the order matters here: a sequential fp32 sum gives other bits somewhere
+    seq = np.zeros(nnz, dtype=np.float32)
+    for r in range(deg.size):
+        s0, s1 = crow[r], crow[r + 1]
+        t = np.float32(0.0)
+        for e in range(s0, s1):
+            t = np.float32(np.float64(grad[e]) * np.float64(probs[e]) + np.float64(t))
+        seq[s0:s1] = probs[s0:s1] * (grad[s0:s1] - t)
+    assert not np.array_equal(seq, want)
+
+
+def test_row_softmax_backward_closed_forms_and_fp64():
+    # uniform probabilities with a constant gradient, and a one-entry row: 0
+    crow = np.array([0, 4, 5], dtype=np.int64)
+    probs = np.array([0.25, 0.25, 0.25, 0.25, 1.0], dtype=np.float32)
+    grad = np.array([3.0, 3.0, 3.0, 3.0, -7.5], dtype=np.float32)
+    assert np.all(oracle.row_softmax_backward(crow, probs, grad) == 0.0)
+    # torch autograd of the fp64 softmax
+    crow, col = _graph(60, 12, seed=9, hubs=1, hub_degree=300, empty=0.1)
+    rng = np.random.default_rng(10)
+    scores = torch.from_numpy(rng.standard_normal(col.size) * 3).requires_grad_(True)
+    rows = torch.repeat_interleave(torch.arange(60), torch.from_numpy(np.diff(crow)))
+    m = torch.zeros(60, dtype=torch.float64).scatter_reduce(0, rows, scores.detach(), "amax", include_self=False)
+    ex = (scores - m[rows]).exp()
+    p64 = ex / torch.zeros(60, dtype=torch.float64).index_add(0, rows, ex)[rows]
+    g = torch.from_numpy(rng.standard_normal(col.size))
+    (p64 * g).sum().backward()
+    got = oracle.row_softmax_backward(crow, p64.detach().numpy().astype(np.float32), g.numpy().astype(np.float32))
+    want = scores.grad.numpy()
+    assert np.max(np.abs(got - want)) <= 1e-6 * max(1.0, np.max(np.abs(want)))
+
+
 def test_spmm_rounded_16_ties_and_overflow():
     crow = np.array([0, 2, 4, 7, 9], dtype=np.int64)
     col = np.array([0, 1, 0, 2, 0, 1, 3, 4, 4], dtype=np.int64)
