@@ -204,6 +204,8 @@ def _spmm_candidates(crow: torch.Tensor, feature_width: int, config: SchedulerCo
 COLSLICE = "colslice"  # candidate value of the column-sliced SpMM
 ROUNDED16 = "rounded16"  # candidate value of the bf16 / fp16 SpMM (column slices when the columns ascend)
 ROUNDED16_EDGES = "rounded16:edges"  # the same product with edge slices
+ROUNDED16_ROWS = "rounded16:rows"  # the same product, every row whole (one launch)
+_ROUNDED16_ALL = (ROUNDED16, ROUNDED16_EDGES, ROUNDED16_ROWS)
 _DTYPES_16 = (torch.bfloat16, torch.float16)
 # Column slicing pays when X is beyond the 8 x 4 MB of L2 and rows are long
 # enough that the per-(row, slice) fp64 partials (128·F bytes per row,
@@ -243,7 +245,7 @@ def _cache_hit_allowed(result: dict[str, Any], config: SchedulerConfig) -> bool:
 def _cached_native_available(operation: str, choice: str, candidate) -> bool:
     if choice != "autosage":
         return True
-    if candidate in (ROUNDED16, ROUNDED16_EDGES):
+    if candidate in _ROUNDED16_ALL:
         return native_op(operation) is not None
     if candidate == COLSLICE:
         return native_op(operation + "_colslice") is not None
@@ -262,12 +264,15 @@ def _cpu_info(operation: str) -> dict[str, Any]:
 
 
 def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
-    if choice == "autosage" and candidate == ROUNDED16:
-        return native_op("spmm_csr")(crow, col, val, x)
-    if choice == "autosage" and candidate == ROUNDED16_EDGES:
-        from ._native import spmm_rounded_16_impl
+    if choice == "autosage" and candidate in _ROUNDED16_ALL:
+        from ._native import columns_ascending, spmm_rounded_16_impl, spmm_rows_16_impl
 
-        return spmm_rounded_16_impl(crow, col, val, x, column_slices=False)
+        if candidate == ROUNDED16_ROWS:
+            return spmm_rows_16_impl(crow, col, val, x)
+        # column slices need ascending columns (a cached choice may meet
+        # another graph with the same key); every schedule gives the same bits
+        columns = candidate == ROUNDED16 and columns_ascending(crow, col)
+        return spmm_rounded_16_impl(crow, col, val, x, column_slices=columns)
     if choice == "autosage" and candidate == COLSLICE:
         from ._native import columns_ascending
 
@@ -483,9 +488,10 @@ def _spmm_auto_16(crow, col, val, x, config: SchedulerConfig, verbose: bool) -> 
     """bf16 / fp16 features (the reference runs torch.sparse.mm for them,
     ``_auto.py:281-287``).  Every output is the exactly rounded sum whatever
     the schedule, so there is no shortlist to probe and no accuracy trade:
-    the two slicings of the native SpMM (column slices, when the columns
-    ascend, and edge slices) are timed once on the full graph and the faster
-    is cached under the usual key, which includes the dtype.  The PyTorch
+    the schedules of the native SpMM (column slices, when the columns ascend,
+    edge slices, and rows whole in one launch) are timed once on the full
+    graph and the fastest is cached under the usual key, which includes the
+    dtype.  The PyTorch
     baseline cannot be run for these types here (see _BASELINE_16_NOTE)."""
     device = device_signature()
     graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
@@ -494,7 +500,7 @@ def _spmm_auto_16(crow, col, val, x, config: SchedulerConfig, verbose: bool) -> 
         record = cache.lookup(device, graph)
         if record is not None and _cache_hit_allowed(record.get("result", {}), config):
             result = record["result"]
-            if result.get("candidate") in (ROUNDED16, ROUNDED16_EDGES):
+            if result.get("candidate") in _ROUNDED16_ALL:
                 return (_run_spmm_choice("autosage", result["candidate"], crow, col, val, x),
                         {**result, "from_cache": True})
     if config.replay_only:
@@ -504,7 +510,7 @@ def _spmm_auto_16(crow, col, val, x, config: SchedulerConfig, verbose: bool) -> 
     from ._native import columns_ascending
 
     wall_start = time.perf_counter()
-    options = [ROUNDED16_EDGES] + ([ROUNDED16] if columns_ascending(crow, col) else [])
+    options = [ROUNDED16_EDGES] + ([ROUNDED16] if columns_ascending(crow, col) else []) + [ROUNDED16_ROWS]
     times = {
         o: _time_cuda(lambda o=o: _run_spmm_choice("autosage", o, crow, col, val, x), warmup=1, iterations=3)[
             "best_ms"]

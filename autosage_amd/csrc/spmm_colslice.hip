@@ -826,6 +826,58 @@ void launch_step(int v, bool off32, int vr, bool has_val, int64_t tiles, hipStre
 
 enum Slicing { kSliceColumns = 0, kSliceEdges = 1 };
 
+// 16-bit SpMM without slicing: one launch, no workspace.  Wave w of feature
+// tile t sums rows w, w + W, ... whole (the short-row forms above, rounded
+// once into Y).  For small graphs, where the slice points, the binning and the
+// chunk launches of the sliced schedule cost more than the product.
+template <typename T, int V, bool HAS_VAL, bool OFF32>
+__global__ __launch_bounds__(kBlock) void rows16_kernel(const int64_t* __restrict__ crow,
+                                                        const int64_t* __restrict__ col, const T* __restrict__ val,
+                                                        const T* __restrict__ x, T* __restrict__ y, int64_t n,
+                                                        int64_t F, int64_t tile_blocks) {
+  constexpr int64_t kTile = 16 * V / static_cast<int64_t>(sizeof(T));
+  const int64_t tile = blockIdx.x / tile_blocks;
+  const int64_t waves = tile_blocks * kWavesPerBlock;
+  const int64_t w = (blockIdx.x - tile * tile_blocks) * kWavesPerBlock + wave_in_block();
+  for (int64_t row = w; row < n; row += waves) {
+    const int64_t rs = uniform_i64(crow[row]);
+    const int64_t re = uniform_i64(crow[row + 1]);
+    if constexpr (V >= 8) {
+      slice_wide<T, V, HAS_VAL, OFF32>(col, val, x, y + row * F, F, rs, re, tile * kTile);
+    } else {
+      slice_row<T, V, HAS_VAL, 8>(col, val, x, y + row * F, F, rs, re);
+    }
+  }
+}
+
+template <typename T, bool HAS_VAL>
+int rows16_run(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
+               int64_t f, hipStream_t s) {
+  constexpr int64_t P = 8;  // 16-bit elements per 16-byte lane
+  int v = 1;
+  if (f % P == 0 && aligned(x, 16)) v = f <= 64 ? 8 : (f <= 128 ? 16 : 32);
+  const int64_t tiles = v >= 8 ? (f + P * v - 1) / (P * v) : 1;
+  const bool off32 = n <= (int64_t(1) << 24) && f * 2 < (int64_t(1) << 24) && n * f * 2 <= (int64_t(1) << 32);
+  int64_t tile_blocks = (n + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int64_t cap = kMaxBlocksPerLaunch / tiles;
+  if (tile_blocks > cap) tile_blocks = cap;
+  if (tile_blocks < 1) tile_blocks = 1;
+  const dim3 grid(static_cast<unsigned>(tiles * tile_blocks));
+  const T* vp = static_cast<const T*>(val);
+  const T* xp = static_cast<const T*>(x);
+  T* yp = static_cast<T*>(y);
+#define AS_ROWS16(V_, O_) \
+  hipLaunchKernelGGL((rows16_kernel<T, V_, HAS_VAL, O_>), grid, dim3(kBlock), 0, s, crow, col, vp, xp, yp, n, f, tile_blocks)
+  switch (v) {
+    case 32: if (off32) AS_ROWS16(32, true); else AS_ROWS16(32, false); break;
+    case 16: if (off32) AS_ROWS16(16, true); else AS_ROWS16(16, false); break;
+    case 8: if (off32) AS_ROWS16(8, true); else AS_ROWS16(8, false); break;
+    default: AS_ROWS16(1, false); break;
+  }
+#undef AS_ROWS16
+  return AS_OK;
+}
+
 // Degree limit of the grouped short rows (16-bit elements, 16-byte lanes):
 // 4·G for the G lanes per edge that F takes; 0 when rows are not grouped.
 inline int64_t grouped_degree(int64_t f, int64_t elem_bytes) {
@@ -971,6 +1023,27 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
 }
 
 int64_t as_spmm_rounded_16_group_degree(int64_t f) { return as::grouped_degree(f, 2); }
+
+int as_spmm_csr_rows_16(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
+                        int64_t nnz, int64_t f, int dtype, void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (!as::aligned(x, 2) || !as::aligned(y, 2) || (val != nullptr && !as::aligned(val, 2)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "x, y and val must be 2-byte aligned");
+  int st = as::validate_spmm(crow, col, x, y, n, nnz, f);
+  if (st != AS_OK) return st;
+  if (n == 0 || f == 0) return AS_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == AS_DTYPE_BF16)
+    st = val ? as::rows16_run<as::Bf16, true>(crow, col, val, x, y, n, f, s)
+             : as::rows16_run<as::Bf16, false>(crow, col, val, x, y, n, f, s);
+  else
+    st = val ? as::rows16_run<as::Fp16, true>(crow, col, val, x, y, n, f, s)
+             : as::rows16_run<as::Fp16, false>(crow, col, val, x, y, n, f, s);
+  if (st != AS_OK) return st;
+  return as::check_launch("spmm_csr_rows_16");
+}
 
 size_t as_spmm_rounded_16_workspace_bytes(int64_t n, int64_t f, int64_t sliced_rows) {
   if (n < 0) n = 0;

@@ -290,11 +290,14 @@ def main() -> int:
             x = x.to(dt)
             val = None if val is None else val.to(dt)
             # one rule, the same bits on every schedule: column slices (when
-            # the columns ascend) or edge slices
+            # the columns ascend), edge slices, or rows whole
+            from autosage_amd._native import spmm_rows_16_impl
+
             variants = {"rounded16:edges": lambda: spmm_rounded_16_impl(crow, col, val, x, column_slices=False)}
             if columns_ascending(crow, col):
                 variants["rounded16:columns"] = (
                     lambda: spmm_rounded_16_impl(crow, col, val, x, column_slices=True))
+            variants["rounded16:rows"] = lambda: spmm_rows_16_impl(crow, col, val, x)
         else:
             variants = {"whole": lambda: torch.ops.autosage.spmm_csr(crow, col, val, x)}
             for cand in _spmm_candidates(crow, f, SchedulerConfig(candidate_count=6)):

@@ -172,6 +172,14 @@ int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
  * summed whole, one wavefront each, with the same bits. */
 size_t as_spmm_rounded_16_workspace_bytes(int64_t n, int64_t f, int64_t sliced_rows);
 
+/* The product of as_spmm_csr_rounded_16 (same bits) without slicing: one
+ * launch, no workspace, every row summed whole by one wavefront.  For small
+ * graphs, where the sliced schedule's set-up costs more than the product;
+ * any column order. */
+int as_spmm_csr_rows_16(const int64_t* crow, const int64_t* col, const void* val,
+                        const void* x, void* y, int64_t n, int64_t nnz, int64_t f,
+                        int dtype, void* stream);
+
 /* Degree below which as_spmm_csr_rounded_16 sums rows several to a
  * wavefront for F features (32, 64 or 128 for F <= 64, <= 128, more; 0 when
  * F is not a multiple of 8). */

@@ -77,6 +77,12 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 2, 0, None, 0, -1, -1, None) == 1
     assert lib.as_last_error() == b"null pointer argument"
     assert lib.as_spmm_colslice_min_degree(1) == 128 and lib.as_spmm_colslice_min_degree(0) == 1024
+    # 16-bit SpMM, rows whole
+    assert lib.as_spmm_csr_rows_16(None, None, None, None, None, 4, 0, 8, 3, None) == 1
+    assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"
+    assert lib.as_spmm_csr_rows_16(None, None, None, 1, None, 4, 0, 8, 1, None) == 1
+    assert lib.as_last_error() == b"x, y and val must be 2-byte aligned"
+    assert lib.as_spmm_csr_rows_16(None, None, None, None, None, 0, 0, 8, 2, None) == 0
     # 16-bit row softmax
     assert lib.as_csr_row_softmax_16(None, None, None, 4, 8, 3, None) == 1
     assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"

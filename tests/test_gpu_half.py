@@ -69,12 +69,14 @@ def test_rounded_spmm_equals_oracle_on_every_schedule(dtype, weighted, features)
     d_crow, d_col = to_dev(crow, col)
     d_x = x.cuda()
     d_val = None if val is None else val.cuda()
-    # ascending columns: column slices (spmm_csr picks them; the colslice op
-    # takes them explicitly)
+    # ascending columns: column slices (the colslice op takes them
+    # explicitly), rows whole (spmm_csr on this small graph)
     got = torch.ops.autosage.spmm_csr(d_crow, d_col, d_val, d_x)
     assert got.dtype == dtype
     assert _same_bits(got, want), (got.float().cpu() - want.float()).abs().max()
     assert _same_bits(torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x), want)
+    assert _same_bits(_native.spmm_rounded_16_impl(d_crow, d_col, d_val, d_x, column_slices=True), want)
+    assert _same_bits(_native.spmm_rows_16_impl(d_crow, d_col, d_val, d_x), want)
     # the same rows with shuffled columns: edge slices, same bits (the
     # weights move with their columns)
     idx = _shuffle_within_rows(crow, seed=features)
@@ -82,8 +84,11 @@ def test_rounded_spmm_equals_oracle_on_every_schedule(dtype, weighted, features)
     s_val = None if val is None else val[torch.from_numpy(idx)]
     d_scol, = to_dev(s_col)
     assert not _native.columns_ascending(d_crow, d_scol) or crow[-1] == 0
-    got_s = torch.ops.autosage.spmm_csr(d_crow, d_scol, None if s_val is None else s_val.cuda(), d_x)
+    d_sval = None if s_val is None else s_val.cuda()
+    got_s = torch.ops.autosage.spmm_csr(d_crow, d_scol, d_sval, d_x)
     assert _same_bits(got_s, want)
+    assert _same_bits(_native.spmm_rounded_16_impl(d_crow, d_scol, d_sval, d_x, column_slices=False), want)
+    assert _same_bits(_native.spmm_rows_16_impl(d_crow, d_scol, d_sval, d_x), want)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -99,11 +104,14 @@ def test_rounded_spmm_edge_cases(dtype):
     d_crow, d_col = to_dev(crow, col)
     got = torch.ops.autosage.spmm_csr(d_crow, d_col, val.cuda(), x.cuda())
     assert _same_bits(got, oracle.spmm_rounded_16(crow, col, val, x, dtype))
-    # hubs of 20,000 edges (column slices of ~2,500 edges each)
+    # hubs of 20,000 edges (column slices of ~2,500 edges each), every schedule
     crow, col, val, x = _inputs(128, False, dtype, seed=6, rows=6000, degree=5, hubs=2, hub_degree=20000)
     d_crow, d_col = to_dev(crow, col)
     want = oracle.spmm_rounded_16(crow, col, None, x, dtype)
     assert _same_bits(torch.ops.autosage.spmm_csr(d_crow, d_col, None, x.cuda()), want)
+    for columns in (True, False):
+        assert _same_bits(_native.spmm_rounded_16_impl(d_crow, d_col, None, x.cuda(), column_slices=columns), want)
+    assert _same_bits(_native.spmm_rows_16_impl(d_crow, d_col, None, x.cuda()), want)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -130,7 +138,7 @@ def test_rounded_spmm_rejects_mixed_types():
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_ops_api_and_scheduler_on_16_bit_features(dtype, monkeypatch, tmp_path):
     from autosage_amd import ops
-    from autosage_amd._auto import ROUNDED16, ROUNDED16_EDGES, spmm_csr_auto
+    from autosage_amd._auto import ROUNDED16, ROUNDED16_EDGES, ROUNDED16_ROWS, spmm_csr_auto
 
     monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
     crow, col, val, x = _inputs(64, True, dtype, seed=12, rows=4000)
@@ -143,9 +151,9 @@ def test_ops_api_and_scheduler_on_16_bit_features(dtype, monkeypatch, tmp_path):
     # 16-bit types: it aborts the process on PyTorch-ROCm) and caches it
     out, info = spmm_csr_auto(d_crow, d_col, val.float().cuda(), x.cuda())
     assert info["operation"] == "spmm" and info["from_cache"] is False
-    # both slicings are timed (the columns ascend); either gives the same bits
-    assert info["choice"] == "autosage" and info["candidate"] in (ROUNDED16, ROUNDED16_EDGES)
-    assert {c["candidate"] for c in info["candidates"]} == {ROUNDED16, ROUNDED16_EDGES}
+    # all three schedules are timed (the columns ascend); each gives the same bits
+    assert info["choice"] == "autosage" and info["candidate"] in (ROUNDED16, ROUNDED16_EDGES, ROUNDED16_ROWS)
+    assert {c["candidate"] for c in info["candidates"]} == {ROUNDED16, ROUNDED16_EDGES, ROUNDED16_ROWS}
     assert _same_bits(out, want)
     assert info["autosage_probe_ms"] > 0 and info["baseline_probe_ms"] is None
     out2, info2 = spmm_csr_auto(d_crow, d_col, val.float().cuda(), x.cuda())

@@ -22,7 +22,7 @@ import pytest
 import torch
 
 import oracle
-from autosage_amd import synth
+from autosage_amd import _native, synth
 from tests.gpu_common import require_gpu, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -74,8 +74,13 @@ def test_random_case(seed):
     dtype = torch.bfloat16 if seed % 2 == 0 else torch.float16
     x16, q16 = torch.from_numpy(x).to(dtype), torch.from_numpy(q).to(dtype)
     v16 = None if val is None else torch.from_numpy(val).to(dtype)
-    y16 = torch.ops.autosage.spmm_csr(d_crow, d_col, None if v16 is None else v16.cuda(), x16.cuda()).cpu()
-    assert torch.equal(y16.view(torch.int16), oracle.spmm_rounded_16(crow, col, v16, x16, dtype).view(torch.int16)), tag
+    want16 = oracle.spmm_rounded_16(crow, col, v16, x16, dtype).view(torch.int16)
+    d_v16 = None if v16 is None else v16.cuda()
+    y16 = torch.ops.autosage.spmm_csr(d_crow, d_col, d_v16, x16.cuda()).cpu()
+    assert torch.equal(y16.view(torch.int16), want16), tag
+    for columns in (True, False):
+        y16 = _native.spmm_rounded_16_impl(d_crow, d_col, d_v16, x16.cuda(), column_slices=columns).cpu()
+        assert torch.equal(y16.view(torch.int16), want16), (tag, columns)
     s16 = torch.ops.autosage.sddmm_csr(d_crow, d_col, q16.cuda(), x16.cuda()).cpu()
     assert torch.equal(s16.view(torch.int16), oracle.sddmm_rounded_16(crow, col, q16, x16, dtype).view(torch.int16)), tag
     # row softmax of the fp32 scores
