@@ -48,8 +48,59 @@ __global__ __launch_bounds__(kBlock) void csr_row_softmax_kernel(const int64_t* 
 }
 
 // The same row softmax on bf16 / fp16 scores: each score converts exactly to
-// fp32, m, d and p_e are computed as above in fp32, and p_e is rounded to
-// the 16-bit type (round to nearest even) once.
+// fp32, m, d and p_e are computed in fp32 and p_e is rounded to the 16-bit
+// type (round to nearest even) once.  Rows of at most kSm16GroupDegree edges
+// take a group of 16 lanes (4 rows per wave, csr_row_softmax16_grouped_kernel),
+// longer rows a wave each (csr_row_softmax16_kernel); the two sum d in
+// different orders, which can move a result by one 16-bit unit near a tie.
+constexpr int64_t kSm16GroupDegree = 64;
+constexpr int kSm16Group = 16;
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void csr_row_softmax16_grouped_kernel(const int64_t* __restrict__ crow,
+                                                                           const T* __restrict__ scores,
+                                                                           uint16_t* __restrict__ probs, int64_t n,
+                                                                           int64_t idx_base) {
+  constexpr int kRowsPerWave = kWave / kSm16Group;
+  const int lane = lane_id();
+  const int g = lane / kSm16Group;
+  const int gl = lane % kSm16Group;
+  const int64_t row =
+      (idx_base + static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave_in_block()) * kRowsPerWave + g;
+  int64_t rs = 0, re = 0;
+  if (row < n) {
+    rs = crow[row];
+    re = crow[row + 1];
+    if (re - rs > kSm16GroupDegree) re = rs;  // a whole wave takes it
+  }
+  // a lane holds its <= 4 scores: one read of the row, one exp per score
+  constexpr int kPer = static_cast<int>(kSm16GroupDegree / kSm16Group);
+  float v[kPer];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int64_t e = rs + gl + i * kSm16Group;
+    v[i] = e < re ? Elem<T>::at(scores, e) : -INFINITY;
+    m = fmaxf(m, v[i]);
+  }
+#pragma unroll
+  for (int o = 1; o < kSm16Group; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+  float d = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int64_t e = rs + gl + i * kSm16Group;
+    v[i] = e < re ? expf(v[i] - m) : 0.f;
+    d += v[i];
+  }
+#pragma unroll
+  for (int o = 1; o < kSm16Group; o <<= 1) d += __shfl_xor(d, o, kWave);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int64_t e = rs + gl + i * kSm16Group;
+    if (e < re) probs[e] = Elem<T>::bits(static_cast<double>(v[i] / d));
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void csr_row_softmax16_kernel(const int64_t* __restrict__ crow,
                                                                    const T* __restrict__ scores,
@@ -60,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void csr_row_softmax16_kernel(const int64_t
   if (row >= n) return;
   const int64_t rs = uniform_i64(crow[row]);
   const int64_t re = uniform_i64(crow[row + 1]);
-  if (rs == re) return;
+  if (re - rs <= kSm16GroupDegree) return;  // the grouped kernel takes it
   float m = -INFINITY;
   for (int64_t e = rs + lane; e < re; e += kWave) m = fmaxf(m, Elem<T>::at(scores, e));
   m = wave_max_f32(m);
@@ -454,6 +505,22 @@ int as_csr_row_softmax_16(const int64_t* crow, const void* scores, void* probs, 
   if (crow == nullptr || scores == nullptr || probs == nullptr)
     return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  // short rows: 4 per wave
+  const int64_t group_waves = (n + 3) / 4;
+  const int64_t gblocks = (group_waves + as::kWavesPerBlock - 1) / as::kWavesPerBlock;
+  for (int64_t b0 = 0; b0 < gblocks; b0 += as::kMaxBlocksPerLaunch) {
+    const int64_t nb = gblocks - b0 < as::kMaxBlocksPerLaunch ? gblocks - b0 : as::kMaxBlocksPerLaunch;
+    const dim3 grid(static_cast<unsigned>(nb));
+    if (dtype == AS_DTYPE_BF16)
+      hipLaunchKernelGGL(as::csr_row_softmax16_grouped_kernel<as::Bf16>, grid, dim3(as::kBlock), 0, s, crow,
+                         static_cast<const as::Bf16*>(scores), static_cast<uint16_t*>(probs), n,
+                         b0 * as::kWavesPerBlock);
+    else
+      hipLaunchKernelGGL(as::csr_row_softmax16_grouped_kernel<as::Fp16>, grid, dim3(as::kBlock), 0, s, crow,
+                         static_cast<const as::Fp16*>(scores), static_cast<uint16_t*>(probs), n,
+                         b0 * as::kWavesPerBlock);
+  }
+  // long rows: a wave each
   const int64_t blocks = (n + as::kWavesPerBlock - 1) / as::kWavesPerBlock;
   for (int64_t b0 = 0; b0 < blocks; b0 += as::kMaxBlocksPerLaunch) {
     const int64_t nb = blocks - b0 < as::kMaxBlocksPerLaunch ? blocks - b0 : as::kMaxBlocksPerLaunch;
