@@ -51,8 +51,9 @@ __global__ __launch_bounds__(kBlock) void csr_row_softmax_kernel(const int64_t* 
 // fp32, m, d and p_e are computed in fp32 and p_e is rounded to the 16-bit
 // type (round to nearest even) once.  Rows of at most kSm16GroupDegree edges
 // take a group of 16 lanes (4 rows per wave, csr_row_softmax16_grouped_kernel),
-// longer rows a wave each (csr_row_softmax16_kernel); the two sum d in
-// different orders, which can move a result by one 16-bit unit near a tie.
+// longer rows a wave each with a running max and sum (csr_row_softmax16_kernel);
+// the sums of d differ in order from the fp32 kernel's, which can move a
+// result by one 16-bit unit near a tie.
 constexpr int64_t kSm16GroupDegree = 64;
 constexpr int kSm16Group = 16;
 
@@ -112,14 +113,24 @@ __global__ __launch_bounds__(kBlock) void csr_row_softmax16_kernel(const int64_t
   const int64_t rs = uniform_i64(crow[row]);
   const int64_t re = uniform_i64(crow[row + 1]);
   if (re - rs <= kSm16GroupDegree) return;  // the grouped kernel takes it
+  // one read for m and d: each lane keeps a running max and the sum of
+  // exp(s - max), rescaled when the max grows; the lanes then merge
   float m = -INFINITY;
-  for (int64_t e = rs + lane; e < re; e += kWave) m = fmaxf(m, Elem<T>::at(scores, e));
-  m = wave_max_f32(m);
   float d = 0.f;
-  for (int64_t e = rs + lane; e < re; e += kWave) d += expf(Elem<T>::at(scores, e) - m);
+  for (int64_t e = rs + lane; e < re; e += kWave) {
+    const float v = Elem<T>::at(scores, e);
+    if (v > m) {
+      d = d * expf(m - v) + 1.f;
+      m = v;
+    } else if (v != -INFINITY) {  // -inf adds nothing (and -inf - -inf is NaN)
+      d += expf(v - m);
+    }
+  }
+  const float mw = wave_max_f32(m);
+  d = m == -INFINITY ? 0.f : d * expf(m - mw);
   d = wave_sum_f32(d);
   for (int64_t e = rs + lane; e < re; e += kWave)
-    probs[e] = Elem<T>::bits(static_cast<double>(expf(Elem<T>::at(scores, e) - m) / d));
+    probs[e] = Elem<T>::bits(static_cast<double>(expf(Elem<T>::at(scores, e) - mw) / d));
 }
 
 // Backward of the row softmax: given p = softmax(s) and dp = dL/dp,

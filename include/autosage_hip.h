@@ -206,9 +206,9 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
 
 /* Row softmax of bf16 or fp16 scores (dtype AS_DTYPE_BF16 / AS_DTYPE_F16):
  * the scores convert exactly to fp32, the softmax is computed in fp32 (rows
- * of at most 64 edges by 16-lane groups, longer rows as
- * as_csr_row_softmax_f32 does), and each probability is rounded once to the
- * element type.  The reference computes it with torch ops in the scores' own
+ * of at most 64 edges by 16-lane groups, longer rows by a wavefront with a
+ * running max and sum), and each probability is rounded once to the element
+ * type.  The reference computes it with torch ops in the scores' own
  * type (autosage/_auto.py:744-759). */
 int as_csr_row_softmax_16(const int64_t* crow, const void* scores, void* probs,
                           int64_t n, int64_t nnz, int dtype, void* stream);
