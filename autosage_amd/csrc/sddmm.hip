@@ -449,7 +449,7 @@ __device__ __forceinline__ void sddmm16_edges(const int64_t* __restrict__ col, c
 // workgroups [0, hub_blocks) stride over the 2048-edge chunks of the rows of
 // degree >= hub_threshold, the rest take the other rows one per wave.
 template <typename T, int G, int MB, bool VEC, bool OFF32>
-__global__ __launch_bounds__(512) void sddmm16_scheduled_kernel(
+__device__ __forceinline__ void sddmm16_scheduled_body(
     const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const T* __restrict__ query,
     const T* __restrict__ key, uint16_t* __restrict__ out, int64_t n, int64_t F, int64_t hub_threshold,
     const int32_t* __restrict__ order, const int32_t* __restrict__ counts, const int32_t* __restrict__ chunk_off,
@@ -485,6 +485,28 @@ __global__ __launch_bounds__(512) void sddmm16_scheduled_kernel(
   sddmm16_edges<T, G, MB, VEC, OFF32>(col, query, key, out, F, row, rs, re, 0, 1);
 }
 
+// The kernel, and the same with at most 80 VGPRs (6 waves per SIMD, a few
+// bytes spilled) for 16 lanes per edge: F = 128 in bf16 on cfg4 takes 1.97 ms
+// with it against 2.21 at 89 VGPRs (5 waves), while F = 64 (8 lanes) gains
+// nothing (1.163 against 1.155).
+#define AS_SDDMM16_PARAMS                                                                                    \
+  const int64_t *__restrict__ crow, const int64_t *__restrict__ col, const T *__restrict__ query,          \
+      const T *__restrict__ key, uint16_t *__restrict__ out, int64_t n, int64_t F, int64_t hub_threshold, \
+      const int32_t *__restrict__ order, const int32_t *__restrict__ counts,                              \
+      const int32_t *__restrict__ chunk_off, int64_t hub_blocks, int64_t block_base
+#define AS_SDDMM16_ARGS crow, col, query, key, out, n, F, hub_threshold, order, counts, chunk_off, hub_blocks, block_base
+template <typename T, int G, int MB, bool VEC, bool OFF32>
+__global__ __launch_bounds__(512) void sddmm16_scheduled_kernel(AS_SDDMM16_PARAMS) {
+  sddmm16_scheduled_body<T, G, MB, VEC, OFF32>(AS_SDDMM16_ARGS);
+}
+template <typename T, int G, int MB, bool VEC, bool OFF32>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void sddmm16_scheduled_kernel_w6(
+    AS_SDDMM16_PARAMS) {
+  sddmm16_scheduled_body<T, G, MB, VEC, OFF32>(AS_SDDMM16_ARGS);
+}
+#undef AS_SDDMM16_PARAMS
+#undef AS_SDDMM16_ARGS
+
 struct Sddmm16Args {
   const int64_t* crow;
   const int64_t* col;
@@ -499,9 +521,15 @@ template <typename T, int G, int MB, bool VEC, bool OFF32>
 void launch_sddmm16_v(const Sddmm16Args& a, dim3 grid, dim3 block, int64_t hub_threshold, const int32_t* order,
                       const int32_t* counts, const int32_t* chunk_off, int64_t hub_blocks, int64_t b0,
                       hipStream_t s) {
-  hipLaunchKernelGGL((sddmm16_scheduled_kernel<T, G, MB, VEC, OFF32>), grid, block, 0, s, a.crow, a.col,
-                     static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<uint16_t*>(a.out), a.n,
-                     a.f, hub_threshold, order, counts, chunk_off, hub_blocks, b0);
+  if constexpr (VEC && G == 16) {
+    hipLaunchKernelGGL((sddmm16_scheduled_kernel_w6<T, G, MB, VEC, OFF32>), grid, block, 0, s, a.crow, a.col,
+                       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<uint16_t*>(a.out), a.n,
+                       a.f, hub_threshold, order, counts, chunk_off, hub_blocks, b0);
+  } else {
+    hipLaunchKernelGGL((sddmm16_scheduled_kernel<T, G, MB, VEC, OFF32>), grid, block, 0, s, a.crow, a.col,
+                       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<uint16_t*>(a.out), a.n,
+                       a.f, hub_threshold, order, counts, chunk_off, hub_blocks, b0);
+  }
 }
 
 // Lanes per edge G and chunks per lane MB for F features (vector lanes), or
