@@ -683,11 +683,15 @@ __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, con
 // in order, are the MG slice groups and then the short groups.  Group g
 // reduces iff floor((g+1)·RG/TG) > floor(g·RG/TG); floor(g·RG/TG) groups
 // before it reduce, so every block keeps blockIdx % 8 as its XCD.
-// At least 7 waves per SIMD: the 16-bit forms (8 fp64 sums per lane, the
-// grouped short rows) otherwise take more VGPRs than that leaves; the fp32
-// forms are below the limit already.
+// 8 waves per SIMD (at most 64 VGPRs, no spills in any form): the 16-bit
+// forms (8 fp64 sums per lane, the grouped short rows) otherwise take up to
+// 88 VGPRs; at 8 waves cfg3 in bf16 takes 1.985 ms at F = 128 and 1.10 at
+// F = 64, against 2.02 and 1.13 at 7.  The fp32 forms are unchanged.
+#ifndef AS_COLSLICE_WAVES_PER_EU
+#define AS_COLSLICE_WAVES_PER_EU 8
+#endif
 template <typename T, int V, bool HAS_VAL, int VR, bool OFF32>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(7))) void colslice_step_kernel(const int64_t* __restrict__ crow,
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(AS_COLSLICE_WAVES_PER_EU))) void colslice_step_kernel(const int64_t* __restrict__ crow,
                                                                const int64_t* __restrict__ col,
                                                                const T* __restrict__ val, const T* __restrict__ x,
                                                                T* __restrict__ y, int64_t F,
