@@ -7,7 +7,9 @@ backward formulas built from the same native kernels:
 * ``Y = A·X`` (A: CSR, weights ``val`` or ones):
   ``dX = Aᵀ·dY`` — a native SpMM over the transposed CSR — and
   ``dval[e] = <dY[row(e)], X[col(e)]>`` — a native SDDMM;
-  both on the degree-split schedules (same bits as the whole-graph kernels).
+  both on the degree-split schedules (same bits as the whole-graph kernels);
+  the column-sliced operators take dX on the column-sliced SpMM instead
+  (same fp64-partial contract as their forward).
   With bf16 / fp16 features both come from the rounded 16-bit kernels
   (SpMM and SDDMM: fp64 sums of exact products, rounded to fp32 and then to
   the 16-bit type).
@@ -68,12 +70,23 @@ def csr_transpose(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, 
 _HUB_THRESHOLD = 1024
 
 
-def _spmm(crow, col, val, x):
+def _spmm(crow, col, val, x, sliced: bool = False):
     if x.dtype != torch.float32:
         # bf16 / fp16: the rounded SpMM, the same bits on any schedule
         return torch.ops.autosage.spmm_csr(crow, col, val, x)
+    if sliced and _column_slices_allowed():
+        # the column-sliced operators' gradients keep their forward's contract
+        # (fp64 partials, within 1e-6 of fp64); the transposed CSR and the
+        # forward graphs they are called on list columns in ascending order
+        return torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
     tile = 64 if x.size(1) <= 64 else 128
     return torch.ops.autosage.spmm_csr_split(crow, col, val, x, tile, 2, _HUB_THRESHOLD)
+
+
+def _column_slices_allowed() -> bool:
+    from .config import SchedulerConfig
+
+    return SchedulerConfig.from_env().column_slices != "off"
 
 
 def _sddmm(crow, col, query, key):
@@ -84,6 +97,12 @@ def _spmm_setup(ctx, inputs, output) -> None:
     crow, col, val, x = inputs[:4]
     ctx.save_for_backward(crow, col, val, x)
     ctx.has_val = val is not None
+    ctx.sliced = False
+
+
+def _spmm_sliced_setup(ctx, inputs, output) -> None:
+    _spmm_setup(ctx, inputs, output)
+    ctx.sliced = True
 
 
 def _spmm_backward(ctx, grad_y: torch.Tensor):
@@ -96,7 +115,7 @@ def _spmm_backward(ctx, grad_y: torch.Tensor):
     if ctx.needs_input_grad[3]:
         crow_t, col_t, perm = csr_transpose(crow, col)
         val_t = None if val is None else val.index_select(0, perm).contiguous()
-        grad_x = _spmm(crow_t, col_t, val_t, grad_y)
+        grad_x = _spmm(crow_t, col_t, val_t, grad_y, ctx.sliced)
     if val is not None and ctx.needs_input_grad[2]:
         grad_val = _sddmm(crow, col, grad_y, x)
     # one gradient per schema argument (the split op has three int arguments more)
@@ -137,6 +156,12 @@ def _attention_setup(ctx, inputs, output) -> None:
     crow, col, query, key, value = inputs[:5]
     ctx.save_for_backward(crow, col, query, key, value)
     ctx.scale = float(inputs[5])
+    ctx.sliced = False
+
+
+def _attention_sliced_setup(ctx, inputs, output) -> None:
+    _attention_setup(ctx, inputs, output)
+    ctx.sliced = True
 
 
 def _attention_backward(ctx, grad_out: torch.Tensor):
@@ -155,24 +180,27 @@ def _attention_backward(ctx, grad_out: torch.Tensor):
     grad_q = grad_k = grad_v = None
     crow_t, col_t, perm = csr_transpose(crow, col)
     if ctx.needs_input_grad[4]:
-        grad_v = _spmm(crow_t, col_t, probs.index_select(0, perm).contiguous(), grad_out)
+        grad_v = _spmm(crow_t, col_t, probs.index_select(0, perm).contiguous(), grad_out, ctx.sliced)
     if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
         grad_s = csr_row_softmax_backward_impl(crow, probs, _sddmm(crow, col, grad_out, value))
         if ctx.scale != 1.0:
             grad_s = grad_s * ctx.scale
         if ctx.needs_input_grad[2]:
-            grad_q = _spmm(crow, col, grad_s, key)
+            grad_q = _spmm(crow, col, grad_s, key, ctx.sliced)
         if ctx.needs_input_grad[3]:
-            grad_k = _spmm(crow_t, col_t, grad_s.index_select(0, perm).contiguous(), query)
+            grad_k = _spmm(crow_t, col_t, grad_s.index_select(0, perm).contiguous(), query, ctx.sliced)
     return None, None, grad_q, grad_k, grad_v, None
 
 
 def register() -> None:
     """Attaches the backward formulas to the registered operators."""
-    for name in ("spmm_csr", "spmm_csr_split", "spmm_csr_colslice"):
+    for name in ("spmm_csr", "spmm_csr_split"):
         torch.library.register_autograd(f"autosage::{name}", _spmm_backward, setup_context=_spmm_setup)
+    torch.library.register_autograd("autosage::spmm_csr_colslice", _spmm_backward, setup_context=_spmm_sliced_setup)
     for name in ("sddmm_csr", "sddmm_csr_split"):
         torch.library.register_autograd(f"autosage::{name}", _sddmm_backward, setup_context=_sddmm_setup)
     torch.library.register_autograd("autosage::csr_row_softmax", _softmax_backward, setup_context=_softmax_setup)
-    for name in ("csr_attention", "csr_attention_colslice"):
-        torch.library.register_autograd(f"autosage::{name}", _attention_backward, setup_context=_attention_setup)
+    torch.library.register_autograd("autosage::csr_attention", _attention_backward, setup_context=_attention_setup)
+    torch.library.register_autograd(
+        "autosage::csr_attention_colslice", _attention_backward, setup_context=_attention_sliced_setup
+    )

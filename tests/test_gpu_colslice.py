@@ -125,17 +125,32 @@ def test_colslice_rejects_unsorted_columns():
     assert not _native.columns_ascending(d_crow, d_col_copy)
 
 
-def test_colslice_backward_matches_exact_op():
+def _grads(op, d_crow, d_col, d_val, d_x):
+    v = d_val.clone().requires_grad_(True)
+    xx = d_x.clone().requires_grad_(True)
+    y = op(d_crow, d_col, v, xx)
+    (y * torch.arange(d_x.size(1), device="cuda", dtype=torch.float32)).sum().backward()
+    return v.grad, xx.grad
+
+
+def test_colslice_backward(monkeypatch):
+    """dX = Aᵀ·dY of the column-sliced op runs column-sliced over the
+    transposed CSR (fp64 bound); dval is the bit-exact SDDMM; with column
+    slices off both equal the exact op's gradients bit for bit."""
+    from autosage_amd._autograd import csr_transpose
+
     crow, col, val, x = _inputs(64, True, seed=21)
     d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
-    grads = []
-    for op in (torch.ops.autosage.spmm_csr_colslice, torch.ops.autosage.spmm_csr):
-        v = d_val.clone().requires_grad_(True)
-        xx = d_x.clone().requires_grad_(True)
-        y = op(d_crow, d_col, v, xx)
-        (y * torch.arange(64, device="cuda", dtype=torch.float32)).sum().backward()
-        grads.append((v.grad, xx.grad))
-    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    exact = _grads(torch.ops.autosage.spmm_csr, d_crow, d_col, d_val, d_x)
+    sliced = _grads(torch.ops.autosage.spmm_csr_colslice, d_crow, d_col, d_val, d_x)
+    assert torch.equal(sliced[0], exact[0])
+    g = np.broadcast_to(np.arange(64, dtype=np.float32), x.shape)
+    t_crow, t_col, perm = csr_transpose(torch.from_numpy(crow), torch.from_numpy(col))
+    _assert_fp64_close(sliced[1].cpu().numpy(), oracle.spmm_f64(t_crow, t_col, val[perm.numpy()], g))
+    assert torch.equal(sliced[1], _grads(torch.ops.autosage.spmm_csr_colslice, d_crow, d_col, d_val, d_x)[1])
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
+    off = _grads(torch.ops.autosage.spmm_csr_colslice, d_crow, d_col, d_val, d_x)
+    assert torch.equal(off[0], exact[0]) and torch.equal(off[1], exact[1])
 
 
 def test_colslice_skewed_config_rows():
