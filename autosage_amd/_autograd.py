@@ -63,10 +63,12 @@ def csr_transpose(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, 
     return result
 
 
-# The backward products run on the degree-split schedules: bit-identical to
-# the whole-graph kernels (the SpMM keeps CSR order per output, the SDDMM the
-# reference's dot order), but hub rows are split across waves, which matters
-# on skewed graphs (one wave per 200k-edge row is several times slower).
+# The backward products run on the degree-split schedules when the graph has
+# hub rows: bit-identical to the whole-graph kernels (the SpMM keeps CSR
+# order per output, the SDDMM the reference's dot order), but hub rows are
+# split across waves, which matters on skewed graphs (one wave per 200k-edge
+# row is several times slower).  Without hub rows the whole-graph SpMM runs
+# (memoised per-graph row count, one launch).
 _HUB_THRESHOLD = 1024
 
 
@@ -79,6 +81,11 @@ def _spmm(crow, col, val, x, sliced: bool = False):
         # (fp64 partials, within 1e-6 of fp64); the transposed CSR and the
         # forward graphs they are called on list columns in ascending order
         return torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
+    from ._native import row_counts
+
+    if row_counts(crow, _HUB_THRESHOLD, 0)[0] == 0:
+        # no hub row: the whole-graph kernel, one launch without binning
+        return torch.ops.autosage.spmm_csr(crow, col, val, x)
     tile = 64 if x.size(1) <= 64 else 128
     return torch.ops.autosage.spmm_csr_split(crow, col, val, x, tile, 2, _HUB_THRESHOLD)
 

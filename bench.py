@@ -234,6 +234,8 @@ def main() -> int:
     parser.add_argument("--dtype", default="f32", choices=["f32", "bf16", "fp16"],
                         help="feature type of the SpMM workloads (cfg1-3), the SDDMM one (cfg4) and the attention "
                              "(cfg5); bf16/fp16 run the rounded 16-bit kernels")
+    parser.add_argument("--backward", action="store_true",
+                        help="cfg1-3 fp32: time forward + dX backward (flops and bytes of both products)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gpu-baseline", action="store_true")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -319,11 +321,29 @@ def main() -> int:
                 variants[chosen] = lambda: torch.ops.autosage.spmm_csr_split(crow, col, val, x, t_, w_, h_)
         log(f"calibration (ms): {calib}; chosen {chosen}")
         step = variants[chosen]
+        passes = 1
+        if args.backward:
+            if half:
+                raise SystemExit("--backward times the fp32 operators")
+            # one training step of the aggregation (AutoSAGEConv's SpMM with
+            # fixed edge weights): Y = A·X, then dX = Aᵀ·dY through the op's
+            # backward (memoised transposed CSR, built in the warmup)
+            x = x.detach().requires_grad_(True)
+            grad_y = torch.randn_like(x)
+            forward = variants[chosen]
+
+            def step():
+                x.grad = None
+                forward().backward(grad_y)
+
+            passes = 2
         ms, samples = time_steps(step, args.steps, args.warmup)
-        flops = 2.0 * nnz * f
-        algo = spmm_bytes(n, nnz, f, weighted, elem)
+        flops = 2.0 * nnz * f * passes
+        algo = spmm_bytes(n, nnz, f, weighted, elem) * passes
         type_name = {"f32": "fp32", "bf16": "bf16", "fp16": "fp16"}[args.dtype]
         workload_name = f"{args.workload} SpMM {type_name} F={f}" + (" weighted" if weighted else " unweighted")
+        if args.backward:
+            workload_name += " forward+backward (dX)"
         traffic = profiled_traffic(workload_name, chosen)
         result = {
             "metric": METRIC,
@@ -367,7 +387,7 @@ def main() -> int:
             "calibration_ms": calib,
         }
         exact = {k_: v_ for k_, v_ in calib.items() if k_ != "colslice"}
-        if chosen == "colslice" and exact:
+        if chosen == "colslice" and exact and not args.backward:
             # the fastest schedule bit-identical to the reference's CPU result
             best_exact = min(exact, key=exact.get)
             result["bit_exact_best"] = {"variant": best_exact, "calibration_ms": exact[best_exact],
@@ -377,12 +397,14 @@ def main() -> int:
             # PyTorch-ROCm; fp16 is not run for the same reason
             result["gpu_baseline"] = {"name": "torch.sparse.mm(csr) (PyTorch-ROCm)", "ms": None,
                                       "note": "not run: aborts the process for bf16 CSR on PyTorch-ROCm"}
+        elif args.backward:
+            result["gpu_baseline"] = None
         elif not args.no_gpu_baseline:
             base, name = _prepare_spmm_baseline(crow, col, val, x)
             bms, _ = time_steps(base, 3, 1)
             result["gpu_baseline"] = {"name": f"{name} (PyTorch-ROCm)", "ms": round(bms, 4),
                                       "speedup": round(bms / ms, 3)}
-        if not args.no_cpu_baseline:
+        if not args.no_cpu_baseline and not args.backward:
             result["cpu_baseline"] = cpu_baseline_spmm(w.crow, w.col, w.val, w.dense["x"], target_nnz=nnz // 8)
             if half:
                 # torch's CPU CSR product (the reference's CPU path) has no
