@@ -100,3 +100,28 @@ def test_attention_gradients(variant):
         want = leaf.grad.numpy()
         err = np.max(np.abs(got.grad.cpu().numpy() - want))
         assert err <= 2e-5 * np.max(np.abs(want)), (variant, err, np.max(np.abs(want)))
+
+
+def test_colslice_attention_backward_schedules(monkeypatch):
+    """The backward recomputes from the saved inputs, so the column-sliced
+    op's gradients equal the fused op's bit for bit once column slices are
+    off, and are deterministic with them on."""
+    crow, col = case_graph(1200, 12, seed=10, hubs=2, hub_degree=1100, empty=0.05)
+    rng = np.random.default_rng(11)
+    arrays = [(rng.standard_normal((1200, f)) * 0.25).astype(np.float32) for f in (64, 64, 48)]
+    g = torch.from_numpy(rng.standard_normal((1200, 48)).astype(np.float32)).cuda()
+    d_crow, d_col = to_dev(crow, col)
+
+    def grads(op):
+        leaves = [torch.from_numpy(a).cuda().requires_grad_(True) for a in arrays]
+        op(d_crow, d_col, *leaves, 0.125).backward(g)
+        return [leaf.grad for leaf in leaves]
+
+    sliced = grads(torch.ops.autosage.csr_attention_colslice)
+    assert all(torch.equal(a, b) for a, b in zip(sliced, grads(torch.ops.autosage.csr_attention_colslice)))
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
+    fused = grads(torch.ops.autosage.csr_attention)
+    off = grads(torch.ops.autosage.csr_attention_colslice)
+    assert all(torch.equal(a, b) for a, b in zip(off, fused))
+    for a, b in zip(sliced, fused):
+        assert torch.max(torch.abs(a - b)) <= 2e-5 * torch.max(torch.abs(b))
