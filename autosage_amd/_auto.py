@@ -77,7 +77,18 @@ def _time_cuda(
 
 
 def _prepare_spmm_baseline(crow, col, val, x) -> tuple[Callable[[], torch.Tensor], str]:
-    """PyTorch CSR SpMM (hipSPARSE on ROCm), ``_auto.py:57-76``."""
+    """PyTorch CSR SpMM (hipSPARSE on ROCm), ``_auto.py:57-76``.
+
+    On PyTorch-ROCm, ``torch.sparse.mm`` on a bf16 CSR tensor on the GPU
+    aborts the whole process inside the sparse library (no Python exception
+    can be caught), and fp16 goes through the same library path.  For those
+    feature types this raises ``RuntimeError`` before building the matrix;
+    the schedulers time the native 16-bit kernels instead."""
+    if x.is_cuda and x.dtype in _DTYPES_16:
+        raise RuntimeError(
+            f"torch.sparse.mm has no usable {x.dtype} CSR kernel on PyTorch-ROCm (the call aborts the process); "
+            "use the native 16-bit SpMM (torch.ops.autosage.spmm_csr) instead"
+        )
     weights = torch.ones(col.numel(), device=x.device, dtype=x.dtype) if val is None else val
     matrix = torch.sparse_csr_tensor(
         crow, col, weights.to(dtype=x.dtype), size=(crow.numel() - 1, x.size(0)), device=x.device, dtype=x.dtype
@@ -226,7 +237,10 @@ def _colslice_eligible(crow, col, x, config: SchedulerConfig) -> bool:
             return False
     from ._native import columns_ascending
 
-    return columns_ascending(crow, col)
+    # checks the graph once (a malformed one raises); a graph whose columns
+    # do not ascend is eligible too: the op runs on its row-sorted copy
+    columns_ascending(crow, col)
+    return True
 
 
 def _require_native() -> None:
@@ -274,14 +288,9 @@ def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
         columns = candidate == ROUNDED16 and columns_ascending(crow, col)
         return spmm_rounded_16_impl(crow, col, val, x, column_slices=columns)
     if choice == "autosage" and candidate == COLSLICE:
-        from ._native import columns_ascending
-
-        # A schedule key hashes only the ends of col, so a cached column-sliced
-        # choice can meet a graph with the same key whose columns are not
-        # ascending; that graph gets the exact whole-graph kernel.
-        if columns_ascending(crow, col):
-            return native_op("spmm_csr_colslice")(crow, col, val, x)
-        return native_op("spmm_csr")(crow, col, val, x)
+        # any column order: a graph whose columns do not ascend runs on its
+        # row-sorted copy, made once per graph
+        return native_op("spmm_csr_colslice")(crow, col, val, x)
     if choice == "autosage":
         split, core = native_op("spmm_csr_split"), native_op("spmm_csr")
         if split is not None and candidate is not None:
@@ -884,7 +893,8 @@ def _attention_colslice_eligible(crow, col, query, value, config: SchedulerConfi
     gathered = (query.size(1) + value.size(1)) * 4 * (crow.numel() - 1)
     if config.column_slices == "auto" and gathered < _COLSLICE_MIN_X_BYTES:
         return False
-    return columns_ascending(crow, col)
+    columns_ascending(crow, col)  # a malformed graph raises; any column order is eligible
+    return True
 
 
 def _attention_variant(crow, col, q, k, v, scale: float) -> tuple[str, dict[str, Any]]:

@@ -28,39 +28,31 @@ deterministic: the same inputs give the same bits.
 
 from __future__ import annotations
 
-import collections
-import threading
-import weakref
 from typing import Optional
 
 import torch
 
-_LOCK = threading.Lock()
-_TRANSPOSE_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
-_MEMO_SIZE = 16
+from ._memo import GraphMemo
+
+# The transposed CSR of a cfg3-sized graph holds about 16·nnz bytes (1.8 GB);
+# entries go when their graph's tensors die, and at most 4 GiB stay cached.
+_TRANSPOSE_MEMO = GraphMemo("csr_transpose", max_entries=16, max_bytes=4 << 30)
 
 
 def csr_transpose(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(crow_t, col_t, perm) of Aᵀ for a square CSR A; ``perm[k]`` is the
     edge of A that becomes edge k of Aᵀ, so ``val_t = val[perm]``."""
-    key = (id(crow), crow._version, id(col), col._version)
-    with _LOCK:
-        hit = _TRANSPOSE_MEMO.get(key)
-        if hit is not None and hit[0]() is crow and hit[1]() is col:
-            _TRANSPOSE_MEMO.move_to_end(key)
-            return hit[2]
+    return _TRANSPOSE_MEMO.get((crow, col), None, lambda: _build_transpose(crow, col))
+
+
+def _build_transpose(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     n = crow.numel() - 1
     counts = (crow[1:] - crow[:-1]).to(torch.long)
     rows = torch.repeat_interleave(torch.arange(n, device=crow.device, dtype=torch.long), counts)
     perm = col.argsort(stable=True)
     crow_t = torch.zeros(n + 1, dtype=torch.long, device=crow.device)
     crow_t[1:] = torch.bincount(col, minlength=n).cumsum(0)
-    result = (crow_t, rows.index_select(0, perm).contiguous(), perm)
-    with _LOCK:
-        _TRANSPOSE_MEMO[key] = (weakref.ref(crow), weakref.ref(col), result)
-        while len(_TRANSPOSE_MEMO) > _MEMO_SIZE:
-            _TRANSPOSE_MEMO.popitem(last=False)
-    return result
+    return crow_t, rows.index_select(0, perm).contiguous(), perm
 
 
 # The backward products run on the degree-split schedules when the graph has
@@ -78,8 +70,8 @@ def _spmm(crow, col, val, x, sliced: bool = False):
         return torch.ops.autosage.spmm_csr(crow, col, val, x)
     if sliced and _column_slices_allowed():
         # the column-sliced operators' gradients keep their forward's contract
-        # (fp64 partials, within 1e-6 of fp64); the transposed CSR and the
-        # forward graphs they are called on list columns in ascending order
+        # (fp64 partials, within 1e-6 of fp64); the transposed CSR lists its
+        # columns in ascending order, so it needs no row-sorted copy
         return torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
     from ._native import row_counts
 

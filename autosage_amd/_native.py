@@ -17,15 +17,14 @@ as ``TORCH_CHECK`` does.
 
 from __future__ import annotations
 
-import collections
 import ctypes
 import os
-import threading
-import weakref
 from pathlib import Path
 from typing import Optional
 
 import torch
+
+from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
 ABI_VERSION = 3
@@ -50,6 +49,11 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_int, _c_int,
          _c_ptr, _c_size, _c_ptr],
+    ),
+    "as_spmm_csr_split_f32_static": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_int, _c_int,
+         _c_ptr],
     ),
     "as_sddmm_csr_f32": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr]),
     "as_sddmm_split_workspace_bytes": (_c_size, [_c_i64]),
@@ -267,11 +271,14 @@ def _colslice_workspace_cap() -> int:
 
 def spmm_csr_colslice_impl(crow, col, val, x):
     """Column-sliced SpMM (fp64 accumulation, one column slice per XCD).
-    Needs columns ascending within every row; checked once per graph."""
+    The kernels cut rows along ascending columns: a graph whose columns do
+    not ascend runs on its row-sorted copy (``row_sorted``, built once per
+    graph), which has the same products in every row."""
     check_spmm_inputs(crow, col, val, x, allow_16=True)
     _maybe_validate(crow, col)
-    if not columns_ascending(crow, col):
-        raise ValueError("spmm_csr_colslice requires column indices ascending within every row")
+    sorted_col, perm = row_sorted(crow, col)
+    val = _row_sorted_weights(col, val, perm)
+    col = sorted_col
     if x.dtype in DTYPES_16:
         return spmm_rounded_16_impl(crow, col, val, x, column_slices=True)
     y = torch.empty_like(x)
@@ -520,16 +527,18 @@ def attention_colslice_supported(query: torch.Tensor, value: torch.Tensor) -> bo
 
 def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
     """Column-sliced attention (one column slice per XCD, online softmax per
-    (row, slice)).  Needs columns ascending within every row; checked once
-    per graph."""
+    (row, slice)).  A graph whose columns do not ascend runs on its row-sorted
+    copy (``row_sorted``, built once per graph)."""
     check_sddmm_inputs(crow, col, query, key)
     _maybe_validate(crow, col)
     _check(value.is_cuda and value.device == query.device, "value must be on the same CUDA device as query")
     _check(value.dtype == torch.float32 and value.dim() == 2 and value.is_contiguous(),
            "value must be contiguous float32 with shape [N, F_v]")
     _check(value.size(0) == query.size(0), "value must have one row per node")
-    if not columns_ascending(crow, col):
-        raise ValueError("csr_attention_colslice requires column indices ascending within every row")
+    # the slices are cut along ascending columns: other graphs run on their
+    # row-sorted copy (the same edges per row; the row softmax and the sum
+    # over a row do not depend on the edge order beyond rounding)
+    col = row_sorted(crow, col)[0]
     n, fqk = query.shape
     fv = value.size(1)
     nnz = col.numel()
@@ -560,9 +569,12 @@ _VALIDATION_RULES = (
 
 
 _UNSORTED_FLAG = 16
-_SORTED_LOCK = threading.Lock()
-_SORTED_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
-_SORTED_MEMO_SIZE = 64
+_ASCENDING_MEMO = GraphMemo("columns_ascending", max_entries=64)
+_ROW_COUNT_MEMO = GraphMemo("row_counts", max_entries=64)
+# A row-sorted copy of a cfg3-sized graph holds 16·nnz bytes (1.8 GB); it goes
+# with its graph, and at most 4 GiB stay cached.
+_ROW_SORTED_MEMO = GraphMemo("row_sorted", max_entries=16, max_bytes=4 << 30)
+_SORTED_WEIGHTS_MEMO = GraphMemo("row_sorted_weights", max_entries=16, max_bytes=2 << 30)
 
 
 def csr_flags(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = None) -> int:
@@ -595,30 +607,53 @@ def validate_csr(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = 
 
 
 def columns_ascending(crow: torch.Tensor, col: torch.Tensor) -> bool:
-    """Whether the columns of every row are in non-decreasing order (the
-    precondition of the column-sliced SpMM).  Memoised per live, unmodified
-    (crow, col) tensor pair; raises ``ValueError`` for a malformed graph."""
-    key = (id(crow), crow._version, id(col), col._version)
-    with _SORTED_LOCK:
-        hit = _SORTED_MEMO.get(key)
-        if hit is not None and hit[0]() is crow and hit[1]() is col:
-            _SORTED_MEMO.move_to_end(key)
-            return hit[2]
-    bad = csr_flags(crow, col)
-    _raise_for_flags(bad)
-    result = not bad & _UNSORTED_FLAG
-    try:
-        refs = (weakref.ref(crow), weakref.ref(col))
-    except TypeError:
-        return result
-    with _SORTED_LOCK:
-        _SORTED_MEMO[key] = (*refs, result)
-        while len(_SORTED_MEMO) > _SORTED_MEMO_SIZE:
-            _SORTED_MEMO.popitem(last=False)
-    return result
+    """Whether the columns of every row are in non-decreasing order (what
+    the column slices of the sliced kernels are cut along).  Memoised per
+    live, unmodified (crow, col) tensor pair; raises ``ValueError`` for a
+    malformed graph."""
+
+    def compute() -> bool:
+        bad = csr_flags(crow, col)
+        _raise_for_flags(bad)
+        return not bad & _UNSORTED_FLAG
+
+    return _ASCENDING_MEMO.get((crow, col), None, compute)
 
 
-_ROW_COUNT_MEMO: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+def row_sorted(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """(col', perm) with the columns of every row in ascending order:
+    ``col'[k] = col[perm[k]]`` and ``perm`` permutes edges only inside their
+    row (stable, so equal columns keep their order).  ``perm`` is None and
+    ``col'`` is ``col`` when the columns already ascend.  The row-sorted
+    graph has the same rows and the same multiset of (column, weight) pairs
+    per row, so the column-sliced products over it are products of the
+    original graph.  Built on the device once per live, unmodified graph
+    (one sort of the nnz (row, column) keys) and memoised."""
+    if columns_ascending(crow, col):
+        return col, None
+
+    def compute():
+        n = crow.numel() - 1
+        counts = (crow[1:] - crow[:-1]).to(torch.long)
+        rows = torch.repeat_interleave(torch.arange(n, device=crow.device, dtype=torch.long), counts,
+                                       output_size=col.numel())
+        # rows ascend already, so (row, column) keys sort each row's columns
+        # in place; n < 2^31 keeps row·n + column inside int64
+        keys = rows.mul_(n).add_(col)
+        sorted_keys, perm = torch.sort(keys, stable=True)
+        del keys
+        col_sorted = sorted_keys.remainder_(n) if n > 0 else sorted_keys
+        return col_sorted.contiguous(), perm
+
+    return _ROW_SORTED_MEMO.get((crow, col), None, compute)
+
+
+def _row_sorted_weights(col: torch.Tensor, val: Optional[torch.Tensor], perm: Optional[torch.Tensor]):
+    """``val`` in the order of ``row_sorted``'s permutation, memoised per live,
+    unmodified (col, val) pair (edge weights usually stay fixed per graph)."""
+    if val is None or perm is None:
+        return val
+    return _SORTED_WEIGHTS_MEMO.get((col, val), None, lambda: val.index_select(0, perm))
 
 
 def row_counts(crow: torch.Tensor, long_from: int, short_below: int) -> tuple[int, int]:
@@ -626,24 +661,13 @@ def row_counts(crow: torch.Tensor, long_from: int, short_below: int) -> tuple[in
     per-graph constants that size the column-sliced SpMM's launches,
     computed once per live, unmodified ``crow`` (one host sync) and
     memoised."""
-    key = (id(crow), crow._version, long_from, short_below)
-    with _SORTED_LOCK:
-        hit = _ROW_COUNT_MEMO.get(key)
-        if hit is not None and hit[0]() is crow:
-            _ROW_COUNT_MEMO.move_to_end(key)
-            return hit[1]
-    deg = crow[1:] - crow[:-1]
-    counts = torch.stack([(deg >= long_from).sum(), (deg < short_below).sum()]).tolist()
-    result = (int(counts[0]), int(counts[1]))
-    try:
-        ref = weakref.ref(crow)
-    except TypeError:
-        return result
-    with _SORTED_LOCK:
-        _ROW_COUNT_MEMO[key] = (ref, result)
-        while len(_ROW_COUNT_MEMO) > _SORTED_MEMO_SIZE:
-            _ROW_COUNT_MEMO.popitem(last=False)
-    return result
+
+    def compute() -> tuple[int, int]:
+        deg = crow[1:] - crow[:-1]
+        counts = torch.stack([(deg >= long_from).sum(), (deg < short_below).sum()]).tolist()
+        return int(counts[0]), int(counts[1])
+
+    return _ROW_COUNT_MEMO.get((crow,), (long_from, short_below), compute)
 
 
 def sliced_rows(crow: torch.Tensor, column_slices: bool) -> int:

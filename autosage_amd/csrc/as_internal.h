@@ -28,12 +28,17 @@ void clear_error();
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Argument checks shared by the SpMM entry points (n, F < 2^31: kernels use
-// 32-bit row and feature indices).
+// Feature widths must stay below 2^28: the kernels form a lane's byte offset
+// inside a feature row as a 32-bit value (F · 8 bytes at most < 2^31).
+constexpr int64_t kMaxFeatures = int64_t(1) << 28;
+
+// Argument checks shared by the SpMM entry points (n < 2^31: kernels use
+// 32-bit row indices; F below kMaxFeatures).
 inline int validate_spmm(const int64_t* crow, const int64_t* col, const void* x, const void* y, int64_t n,
                          int64_t nnz, int64_t f) {
   if (n < 0 || n > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
-  if (f < 0 || f > INT32_MAX) return fail(AS_ERR_INVALID_ARGUMENT, "F exceeds kernel index range");
+  if (f < 0) return fail(AS_ERR_INVALID_ARGUMENT, "F must be non-negative");
+  if (f >= kMaxFeatures) return fail(AS_ERR_UNSUPPORTED, "F must be below 2^28 (32-bit lane offsets)");
   if (nnz < 0) return fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
   if (n > 0 && f > 0 && (crow == nullptr || x == nullptr || y == nullptr))
     return fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");

@@ -556,8 +556,10 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col, const float* q
                          const float* value, float* out, int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v,
                          float scale, void* workspace, size_t workspace_bytes, void* stream) {
   as::clear_error();
-  if (n < 0 || n > INT32_MAX || nnz < 0 || f_qk < 0 || f_qk > INT32_MAX || f_v < 0 || f_v > INT32_MAX)
+  if (n < 0 || n > INT32_MAX || nnz < 0 || f_qk < 0 || f_v < 0)
     return as::fail(AS_ERR_INVALID_ARGUMENT, "attention sizes out of range");
+  if (f_qk >= as::kMaxFeatures || f_v >= as::kMaxFeatures)
+    return as::fail(AS_ERR_UNSUPPORTED, "F_qk and F_v must be below 2^28 (32-bit lane offsets)");
   if (n == 0 || f_v == 0) return AS_OK;
   if (crow == nullptr || value == nullptr || out == nullptr || (nnz > 0 && (col == nullptr || query == nullptr ||
                                                                            key == nullptr)))

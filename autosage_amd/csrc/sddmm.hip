@@ -591,8 +591,9 @@ void launch_sddmm16(const Sddmm16Args& a, int waves, int64_t hub_threshold, int6
 }
 
 int validate_sddmm(const SddmmArgs& a, int64_t nnz) {
-  if (a.n < 0 || a.n > INT32_MAX || a.f < 0 || a.f > INT32_MAX)
+  if (a.n < 0 || a.n > INT32_MAX || a.f < 0)
     return fail(AS_ERR_INVALID_ARGUMENT, "SDDMM dimensions exceed the kernel index range");
+  if (a.f >= as::kMaxFeatures) return fail(AS_ERR_UNSUPPORTED, "F must be below 2^28 (32-bit lane offsets)");
   if (nnz < 0) return fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
   if (a.n > 0 && a.crow == nullptr) return fail(AS_ERR_INVALID_ARGUMENT, "null crow pointer");
   if (nnz > 0 && (a.col == nullptr || a.q == nullptr || a.k == nullptr || a.out == nullptr))

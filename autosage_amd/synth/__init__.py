@@ -290,3 +290,45 @@ def random_csr(rows: int, mean_degree: float, seed: int = 0, hub_rows: int = 0, 
         deg[rng.choice(rows, size=hub_rows, replace=False)] = min(hub_degree, cols)
     crow = _crow_from_degrees(deg)
     return crow, fill_columns(crow, cols, seed)
+
+
+def erdos_renyi(rows: int = 200_000, probability: float = 2e-5, seed: int = 0, features: int = 64) -> Workload:
+    """The reference benchmark's ``synth:<rows>:<p>`` graph
+    (``scripts/benchmark.py:97-108``, CSR build ``:64-76``): int(p·rows²)
+    (row, column) pairs drawn uniformly with ``default_rng(seed).integers``,
+    duplicates removed, rows ascending and columns ascending within rows.
+    The same generator calls in the same order give the same graph (the
+    published run, ``artifacts/results/spmm/synth_er.csv``, has 799,994
+    nonzeros for 200,000 rows at p = 2e-5, seed 0).  X [rows, features]
+    ~ N(0, 1) is drawn afterwards from the same generator."""
+    rng = np.random.default_rng(seed)
+    count = max(1, int(probability * rows * rows))
+    src = rng.integers(0, rows, size=count, dtype=np.int64)
+    dst = rng.integers(0, rows, size=count, dtype=np.int64)
+    # unique (row, column) keys come back sorted: rows ascending, columns
+    # ascending inside each row
+    keys = np.unique(src * np.int64(rows) + dst)
+    row, col = keys // np.int64(rows), keys % np.int64(rows)
+    crow = np.zeros(rows + 1, dtype=np.int64)
+    np.cumsum(np.bincount(row, minlength=rows), out=crow[1:])
+    x = rng.standard_normal((rows, features), dtype=np.float32)
+    return Workload("er", crow, col, None, {"x": x}, {"probability": probability})
+
+
+def hub_sweep_graph(rows: int = 20_000, hub_degree: int = 12_000, other_degree: int = 32, seed: int = 0,
+                    device: str = "cuda"):
+    """The reference hub sweep's graph (``scripts/sweep_hubs.py:15-27``):
+    row 0 has ``hub_degree`` edges, every other row ``other_degree``; the
+    columns are uniform draws of ``torch.randint`` from a device generator
+    seeded with ``seed``, in CSR order (not sorted within rows, duplicates
+    allowed).  Returns device tensors (crow, col)."""
+    import torch
+
+    generator = torch.Generator(device=device)
+    generator.manual_seed(seed)
+    degrees = torch.full((rows,), other_degree, device=device, dtype=torch.long)
+    degrees[0] = hub_degree
+    crow = torch.cat((torch.zeros(1, device=device, dtype=torch.long), degrees.cumsum(0)))
+    nnz = hub_degree + (rows - 1) * other_degree
+    col = torch.randint(0, rows, (nnz,), generator=generator, device=device)
+    return crow, col

@@ -5,8 +5,10 @@
  * (passed as `void*`, a hipStream_t; NULL means the default stream).  The
  * library never allocates device memory: outputs and workspaces are owned by
  * the caller (the Python host layer allocates them with torch), and the
- * library keeps no per-call state.  All launches are asynchronous on the given
- * stream; no entry point synchronises the host.
+ * library keeps no per-call state.  The one exception is
+ * as_spmm_csr_split_f32_static, whose workspace is a static device array.
+ * All launches are asynchronous on the given stream; no entry point
+ * synchronises the host.
  *
  * Return value: AS_OK (0) or a positive as_status; as_last_error() then
  * returns a thread-local message describing the failure.
@@ -102,6 +104,26 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col,
                           int waves_per_block, int64_t hub_threshold, int vec4,
                           int hub_mode, void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/* Largest row count of as_spmm_csr_split_f32_static. */
+#define AS_STATIC_MAX_ROWS (1 << 22)
+
+/* The degree-split SpMM of as_spmm_csr_split_f32 (same arguments, kernels
+ * and bits) without a workspace argument and without allocating: the row
+ * order and binning tables live in a static device array of about 18 MiB
+ * that every GPU the library runs on keeps until the process ends.  No
+ * counterpart in the reference; for callers that cannot allocate device
+ * memory (HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  n <= AS_STATIC_MAX_ROWS, else AS_ERR_WORKSPACE.  The stream
+ * must belong to the current device.  All calls on one GPU share that GPU's
+ * array: calls that overlap on one GPU (other streams, other host threads)
+ * race and must be ordered by the caller. */
+int as_spmm_csr_split_f32_static(const int64_t* crow, const int64_t* col,
+                                 const float* val, const float* x, float* y,
+                                 int64_t n, int64_t nnz, int64_t f,
+                                 int feature_tile, int waves_per_block,
+                                 int64_t hub_threshold, int vec4,
+                                 int hub_mode, void* stream);
 
 /* Preferred bytes of workspace for as_spmm_csr_colslice_f32: slice points,
  * row order and two partial buffers of a quarter of the rows each. */

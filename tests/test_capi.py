@@ -106,6 +106,19 @@ def test_argument_errors_are_reported_without_a_launch(lib):
         32, 32, 64, 64, 128, 128, 0, 0]
     # n == 0 is a no-op success
     assert lib.as_spmm_csr_f32(None, None, None, None, None, 0, 0, 8, 1, None) == 0
+    # feature widths from 2^28 on are refused (the kernels' lane offsets in a
+    # feature row are 32-bit), before any pointer is looked at
+    big = 1 << 28
+    assert lib.as_spmm_csr_f32(None, None, None, None, None, 4, 0, big, 1, None) == 3
+    assert lib.as_last_error() == b"F must be below 2^28 (32-bit lane offsets)"
+    assert lib.as_spmm_csr_rows_16(None, None, None, None, None, 4, 0, big, 1, None) == 3
+    assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, big, 1, 1, None, 0, -1, -1, None) == 3
+    assert lib.as_spmm_csr_colslice_f32(None, None, None, None, None, 4, 0, big, None, 0, -1, None) == 3
+    assert lib.as_sddmm_csr_f32(None, None, None, None, None, 4, 0, big, None) == 3
+    assert lib.as_sddmm_csr_rounded_16(None, None, None, None, None, 4, 0, big, 1, 4, 1024, None, 0, None) == 3
+    assert lib.as_csr_attention_f32(None, None, None, None, None, None, 4, 0, 8, big, 1.0, None, 0, None) == 3
+    assert lib.as_last_error() == b"F_qk and F_v must be below 2^28 (32-bit lane offsets)"
+    assert lib.as_spmm_csr_f32(None, None, None, None, None, 4, 0, -1, 1, None) == 1
 
 
 def test_library_targets_gfx950_only():

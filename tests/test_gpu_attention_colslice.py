@@ -3,8 +3,9 @@
 Online softmax per (row, column slice) with fp32 partial states merged per
 row: checked against the oracle's fp64 attention at the 1e-5 relative /
 1e-6 absolute bar for fp32 results; deterministic across calls and across
-partial-state chunks; selected by ``csr_attention_forward`` only after a
-full-graph timing, and never for graphs whose columns are not ascending."""
+partial-state chunks; graphs whose columns do not ascend run on their
+row-sorted copy; selected by ``csr_attention_forward`` only after a
+full-graph timing."""
 
 from __future__ import annotations
 
@@ -65,14 +66,18 @@ def test_colslice_attention_deterministic_and_chunked(monkeypatch):
     _check(first.cpu().numpy(), oracle.attention_f64(crow, col, q, k, v, scale=0.5))
 
 
-def test_colslice_attention_rejects_what_it_cannot_run():
+def test_colslice_attention_unsorted_columns_and_rejections():
     crow, col, q, k, v = _inputs(64, 128, seed=5)
     r = int(np.argmax(np.diff(crow)))
     shuffled = col.copy()
     shuffled[crow[r]:crow[r + 1]] = shuffled[crow[r]:crow[r + 1]][::-1]
+    # a graph whose columns do not ascend runs on its row-sorted copy: the
+    # same result as the sorted graph, and the fp64 bar of the shuffled one
     d_crow, d_col, d_q, d_k, d_v = to_dev(crow, shuffled, q, k, v)
-    with pytest.raises(ValueError, match="ascending"):
-        torch.ops.autosage.csr_attention_colslice(d_crow, d_col, d_q, d_k, d_v, 1.0)
+    got = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, d_q, d_k, d_v, 1.0)
+    d_sorted = torch.from_numpy(col).cuda()
+    assert torch.equal(got, torch.ops.autosage.csr_attention_colslice(d_crow, d_sorted, d_q, d_k, d_v, 1.0))
+    _check(got.cpu().numpy(), oracle.attention_f64(crow, shuffled, q, k, v, scale=1.0))
     d = to_dev(crow, col, q[:, :3].copy(), k[:, :3].copy(), v)
     with pytest.raises(ValueError, match="multiples of 4"):
         torch.ops.autosage.csr_attention_colslice(*d, 1.0)

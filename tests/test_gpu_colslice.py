@@ -103,26 +103,63 @@ def test_colslice_deterministic_and_chunked(monkeypatch):
     assert torch.equal(first, chunked)
 
 
-def test_colslice_rejects_unsorted_columns():
-    crow, col, val, x = _inputs(64, False, seed=9)
-    d_crow, d_col, _, d_x = to_dev(crow, col, None, x)
+@pytest.mark.parametrize("weighted", [False, True])
+def test_colslice_unsorted_columns_run_row_sorted(weighted):
+    """A graph whose columns do not ascend runs on its row-sorted copy: the
+    same result as the op on the sorted graph (bit for bit: the same edges
+    per row, sorted the same way) and the fp64 bar of the shuffled graph."""
+    crow, col, val, x = _inputs(64, weighted, seed=9)
+    rng = np.random.default_rng(90)
+    perm = np.arange(col.size)
+    for r in range(crow.size - 1):
+        rng.shuffle(perm[crow[r]:crow[r + 1]])
+    s_col = col[perm]
+    s_val = None if val is None else val[perm]
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    d_scol = torch.from_numpy(s_col).cuda()
+    d_sval = None if s_val is None else torch.from_numpy(s_val).cuda()
     assert _native.columns_ascending(d_crow, d_col)
-    row = int(np.argmax(np.diff(crow)))
-    shuffled = col.copy()
-    shuffled[crow[row]:crow[row + 1]] = shuffled[crow[row]:crow[row + 1]][::-1]
-    d_shuffled = torch.from_numpy(shuffled).cuda()
-    assert not _native.columns_ascending(d_crow, d_shuffled)
-    with pytest.raises(ValueError, match="ascending"):
-        torch.ops.autosage.spmm_csr_colslice(d_crow, d_shuffled, None, d_x)
-    # equal neighbouring columns are allowed
+    assert not _native.columns_ascending(d_crow, d_scol)
+    # the row-sorted copy restores the sorted graph and its permutation
+    sorted_col, p = _native.row_sorted(d_crow, d_scol)
+    assert torch.equal(sorted_col, d_col)
+    assert np.array_equal(s_col[p.cpu().numpy()], col)
+    assert _native.row_sorted(d_crow, d_col)[1] is None
+    got = torch.ops.autosage.spmm_csr_colslice(d_crow, d_scol, d_sval, d_x)
+    assert torch.equal(got, torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x))
+    _assert_fp64_close(got.cpu().numpy(), oracle.spmm_f64(crow, s_col, s_val, x))
+    # memoised per graph: the second call reuses the sorted copy
+    assert _native.row_sorted(d_crow, d_scol)[0] is sorted_col
+    # new weights on the same graph are permuted afresh
+    if d_sval is not None:
+        d_sval.mul_(-2.0)
+        again = torch.ops.autosage.spmm_csr_colslice(d_crow, d_scol, d_sval, d_x)
+        _assert_fp64_close(again.cpu().numpy(), oracle.spmm_f64(crow, s_col, -2.0 * s_val, x))
+    # equal neighbouring columns count as ascending
     crow2 = np.array([0, 3], dtype=np.int64)
     col2 = np.array([0, 0, 0], dtype=np.int64)
     assert _native.columns_ascending(*to_dev(crow2, col2))
     # the memo follows in-place changes of col
     d_col_copy = d_col.clone()
     assert _native.columns_ascending(d_crow, d_col_copy)
+    row = int(np.argmax(np.diff(crow)))
     d_col_copy[crow[row]:crow[row + 1]] = d_col_copy[crow[row]:crow[row + 1]].flip(0)
     assert not _native.columns_ascending(d_crow, d_col_copy)
+
+
+def test_row_sorted_memo_drops_dead_graphs():
+    """Derived per-graph buffers go when the graph's tensors are collected."""
+    import gc
+
+    crow, col, _, x = _inputs(16, False, seed=4)
+    d_crow = torch.from_numpy(crow).cuda()
+    d_col = torch.from_numpy(np.concatenate([col[crow[r]:crow[r + 1]][::-1] for r in range(crow.size - 1)])).cuda()
+    before = len(_native._ROW_SORTED_MEMO)
+    _native.row_sorted(d_crow, d_col)
+    assert len(_native._ROW_SORTED_MEMO) == before + 1
+    del d_col
+    gc.collect()
+    assert len(_native._ROW_SORTED_MEMO) == before
 
 
 def _grads(op, d_crow, d_col, d_val, d_x):
@@ -199,12 +236,14 @@ def test_scheduler_times_colslice_on_the_full_graph(monkeypatch, tmp_path):
     replayed, info_r = autosage_amd.spmm_csr_auto(d_crow, d_shuffled, None, d_x)
     assert info_r["from_cache"]
     if info_r["candidate"] == "colslice":
-        # ... so a cached column-sliced choice runs the exact kernel on it
-        assert np.array_equal(replayed.cpu().numpy(), oracle.spmm_seq(crow, shuffled, None, x))
-    # ... and without a cache record it is never timed with column slices
+        # ... so a cached column-sliced choice runs on its row-sorted copy
+        _assert_fp64_close(replayed.cpu().numpy(), oracle.spmm_f64(crow, shuffled, None, x))
+    # ... and without a cache record it is timed with column slices too
     monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path / "second"))
-    _, info2 = autosage_amd.spmm_csr_auto(d_crow, d_shuffled, None, d_x)
-    assert "colslice" not in _timed(info2) and info2.get("candidate") != "colslice"
+    out2, info2 = autosage_amd.spmm_csr_auto(d_crow, d_shuffled, None, d_x)
+    assert "colslice" in _timed(info2)
+    if info2["candidate"] == "colslice":
+        _assert_fp64_close(out2.cpu().numpy(), oracle.spmm_f64(crow, shuffled, None, x))
     # off: never timed
     monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
     _, info3 = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)

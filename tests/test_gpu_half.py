@@ -87,6 +87,8 @@ def test_rounded_spmm_equals_oracle_on_every_schedule(dtype, weighted, features)
     d_sval = None if s_val is None else s_val.cuda()
     got_s = torch.ops.autosage.spmm_csr(d_crow, d_scol, d_sval, d_x)
     assert _same_bits(got_s, want)
+    # the colslice op runs column slices on the row-sorted copy: same bits
+    assert _same_bits(torch.ops.autosage.spmm_csr_colslice(d_crow, d_scol, d_sval, d_x), want)
     assert _same_bits(_native.spmm_rounded_16_impl(d_crow, d_scol, d_sval, d_x, column_slices=False), want)
     assert _same_bits(_native.spmm_rows_16_impl(d_crow, d_scol, d_sval, d_x), want)
 
@@ -332,3 +334,32 @@ def test_attention_on_bf16_inputs_runs_the_native_stages(monkeypatch, tmp_path):
     assert out.dtype == torch.bfloat16
     assert info["sddmm"]["choice"] == "autosage" and info["spmm"]["choice"] == "autosage"
     assert (out.float() - ref).abs().max().item() < 0.03
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_torch_baseline_raises_for_16_bit_cuda_features(monkeypatch, dtype):
+    """``_prepare_spmm_baseline`` and the baseline branch of
+    ``_run_spmm_choice`` raise RuntimeError on 16-bit CUDA features instead
+    of calling torch.sparse.mm, which aborts the process for bf16 CSR on
+    PyTorch-ROCm.  The sparse entry points are replaced by functions that
+    fail the test, so the real call is never reached even if the guard were
+    missing."""
+    from autosage_amd import _auto
+
+    def never(*args, **kwargs):
+        raise AssertionError("torch.sparse must not be reached for 16-bit CUDA features")
+
+    monkeypatch.setattr(torch.sparse, "mm", never)
+    monkeypatch.setattr(torch, "sparse_csr_tensor", never)
+    crow, col, val, x = _inputs(16, True, dtype, seed=3, rows=200, hubs=0)
+    d_crow, d_col = to_dev(crow, col)
+    d_val, d_x = val.cuda(), x.cuda()
+    with pytest.raises(RuntimeError, match="torch.sparse.mm"):
+        _auto._prepare_spmm_baseline(d_crow, d_col, d_val, d_x)
+    with pytest.raises(RuntimeError, match="torch.sparse.mm"):
+        _auto._run_spmm_choice("baseline", None, d_crow, d_col, None, d_x)
+    # the drop-in import path reaches the same guard
+    from autosage._auto import _prepare_spmm_baseline
+
+    with pytest.raises(RuntimeError, match="native 16-bit SpMM"):
+        _prepare_spmm_baseline(d_crow, d_col, None, d_x)
