@@ -39,3 +39,52 @@ def mismatch_report(gpu: torch.Tensor, ref: np.ndarray) -> str:
     got = gpu.detach().cpu().numpy()
     bad = np.argwhere(got != ref)
     return f"{len(bad)} mismatches, first {bad[:5].tolist()}: got {got[tuple(bad[0])] if len(bad) else None}"
+
+
+def elementwise_parity(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, *, tight_rel: float,
+                       tight_abs: float, rtol: float = 1e-5, atol: float = 1e-6) -> dict:
+    """Per-element parity of a reassociating kernel with the reference's fp32
+    result ``ref``, against the exact (fp64) result ``exact``.  With
+    bar(v) = rtol·|v| + atol and the kernel's bound δ = tight_rel·|exact| +
+    tight_abs, every element must satisfy one of:
+
+    (a) |got − ref| <= bar(ref): within the bar of the reference;
+    (b) |ref − exact| > bar(exact): the reference itself misses the bar
+        against the exact result, while |got − exact| <= δ and
+        |got − exact| <= |ref − exact|;
+    (c) bar(exact) − δ < |ref − exact| <= bar(exact): the reference is within
+        δ of missing the bar, while |got − exact| <= δ and |got − exact| <=
+        |ref − exact|.  If |got − exact| <= δ and (a) fails, the triangle
+        inequality puts |ref − exact| above roughly bar − δ, so (c) is the
+        boundary band that (a) and (b) leave between them.
+
+    Returns the counts (and the largest |ref − exact| / bar(exact) among the
+    elements of (b) and (c)); raises AssertionError naming them when an
+    element meets none."""
+    got = got.astype(np.float64)
+    ref = ref.astype(np.float64)
+    bar_exact = rtol * np.abs(exact) + atol
+    bound = tight_rel * np.abs(exact) + tight_abs
+    near_ref = np.abs(got - ref) <= rtol * np.abs(ref) + atol
+    ref_err = np.abs(ref - exact)
+    got_err = np.abs(got - exact)
+    kernel_ok = (got_err <= bound) & (got_err <= ref_err)
+    ref_misses = ref_err > bar_exact
+    ref_edge = ~ref_misses & (ref_err > bar_exact - bound)
+    case_b = ~near_ref & ref_misses & kernel_ok
+    case_c = ~near_ref & ref_edge & kernel_ok
+    neither = ~near_ref & ~case_b & ~case_c
+    ratio = ref_err / bar_exact
+    counts = {
+        "elements": int(got.size),
+        "a_within_bar_of_reference": int(near_ref.sum()),
+        "b_reference_off_bar_kernel_within_bound": int(case_b.sum()),
+        "c_reference_at_bar_edge_kernel_within_bound": int(case_c.sum()),
+        "reference_off_bar_total": int(ref_misses.sum()),
+        "worst_reference_error_over_bar": float(ratio.max()) if ratio.size else 0.0,
+        "min_reference_error_over_bar_in_c": float(ratio[case_c].min()) if case_c.any() else None,
+        "neither": int(neither.sum()),
+    }
+    print(f"[parity] {counts}", flush=True)
+    assert counts["neither"] == 0, counts
+    return counts

@@ -17,7 +17,7 @@ import torch
 
 import oracle
 from autosage_amd import synth
-from tests.gpu_common import bitwise_equal, require_gpu
+from tests.gpu_common import bitwise_equal, elementwise_parity, require_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -101,6 +101,45 @@ def test_config3_skewed_spmm(features, monkeypatch):
     # tests/test_cuda.py:40: rtol 1e-4, atol 3e-3)
     assert np.max(np.abs(got - ref)) <= RTOL * np.max(np.abs(ref))
     assert np.allclose(got, ref, rtol=1e-4, atol=3e-3)
+    # element by element against the reference's fp32 result (the sequential
+    # CPU product, torch.sparse.mm): each output is within 1e-5·|ref| + 1e-6
+    # of it, or the reference is itself off that bar against fp64 (or within
+    # 1e-6·|fp64| + 1e-9 of being off it) and the sliced output is within
+    # 1e-6·|fp64| + 1e-9 of fp64 and closer to it than the reference
+    elementwise_parity(got, ref, exact, tight_rel=1e-6, tight_abs=1e-9)
+
+
+def test_config3_shuffled_columns_take_the_sliced_schedule():
+    """cfg3 at F = 128 with the columns of every row in a random order (what
+    ``edge_index_to_csr`` gives for an edge list not sorted by source): the
+    column-sliced schedule runs on the row-sorted copy, ``spmm_csr_auto``
+    still chooses it, and the sampled rows are within 1e-6·|fp64|."""
+    import autosage_amd
+
+    w = synth.config3(seed=0, features=128)
+    d_crow, d_col, d_x = dev(w.crow), dev(w.col), dev(w.dense["x"])
+    n = w.rows
+    edge_rows = torch.repeat_interleave(torch.arange(n, device="cuda"), d_crow[1:] - d_crow[:-1],
+                                        output_size=w.nnz)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    noise = torch.randint(0, 1 << 31, (w.nnz,), generator=gen, device="cuda")
+    shuffled = d_col.index_select(0, torch.argsort(edge_rows * (1 << 31) + noise)).contiguous()
+    del edge_rows, noise, d_col
+    from autosage_amd import _native
+
+    assert not _native.columns_ascending(d_crow, shuffled)
+    out, info = autosage_amd.spmm_csr_auto(d_crow, shuffled, None, d_x)
+    timed = {tuple(c["candidate"]) if isinstance(c["candidate"], list) else c["candidate"]: c["best_ms"]
+             for c in info["full_graph"]["candidates"]}
+    assert info["candidate"] == "colslice", timed
+    rows = sample_rows(w.crow, 1500, seed=3)
+    exact = oracle.spmm_f64(w.crow, shuffled.cpu().numpy(), None, w.dense["x"], rows=rows)
+    got = out[torch.from_numpy(rows).cuda()].cpu().numpy()
+    assert np.all(np.abs(got - exact) <= 1e-6 * np.abs(exact) + 1e-9)
+    # cached: the same choice, the same bits
+    again, cached = autosage_amd.spmm_csr_auto(d_crow, shuffled, None, d_x)
+    assert cached["from_cache"] and torch.equal(again, out)
 
 
 @pytest.mark.parametrize("features", [64, 128])
@@ -142,3 +181,10 @@ def test_config5_attention():
     exact = oracle.attention_f64(s_crow, s_col, q[rows], k, v, scale=0.125)
     got_s = sliced[torch.from_numpy(rows).cuda()].cpu().numpy().astype(np.float64)
     assert np.all(np.abs(got_s - exact) <= ATOL + RTOL * np.abs(exact)), float(np.max(np.abs(got_s - exact)))
+    # element by element against the reference's fp32 composition (SDDMM,
+    # row softmax, sequential SpMM): within 1e-5·|ref| + 1e-6 of it, or the
+    # reference is itself off that bar against fp64 while the sliced output
+    # (fp32 online softmax, fp32 partial states) is within it and closer
+    elementwise_parity(got_s, ref, exact, tight_rel=RTOL, tight_abs=ATOL)
+    # the fused kernel (the reference's stage order) against the same result
+    elementwise_parity(got, ref, exact, tight_rel=RTOL, tight_abs=ATOL)
