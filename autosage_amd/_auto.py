@@ -223,6 +223,11 @@ _DTYPES_16 = (torch.bfloat16, torch.float16)
 # written and read) stay small next to the gathers (4·F bytes per edge).
 _COLSLICE_MIN_X_BYTES = 32 << 20
 _COLSLICE_MIN_MEAN_DEGREE = 64
+# It also pays on any graph with a row this long: the exact schedules walk a
+# row's edges in order on one wave, the sliced one spreads them over 8 (on
+# the reference's hub-sweep graph, one 12,000-edge row among 20,000 rows of
+# 32, 0.18 ms against 0.45 ms for the best exact split at F = 128).
+_COLSLICE_HUB_DEGREE = 2048
 
 
 def _colslice_eligible(crow, col, x, config: SchedulerConfig) -> bool:
@@ -232,10 +237,12 @@ def _colslice_eligible(crow, col, x, config: SchedulerConfig) -> bool:
     n = crow.numel() - 1
     if n <= 0 or col.numel() == 0:
         return False
+    from ._native import columns_ascending, row_counts
+
     if config.column_slices == "auto":
-        if x.numel() * x.element_size() < _COLSLICE_MIN_X_BYTES or col.numel() < _COLSLICE_MIN_MEAN_DEGREE * n:
+        large = x.numel() * x.element_size() >= _COLSLICE_MIN_X_BYTES and col.numel() >= _COLSLICE_MIN_MEAN_DEGREE * n
+        if not large and row_counts(crow, _COLSLICE_HUB_DEGREE, 0)[0] == 0:
             return False
-    from ._native import columns_ascending
 
     # checks the graph once (a malformed one raises); a graph whose columns
     # do not ascend is eligible too: the op runs on its row-sorted copy
@@ -886,12 +893,13 @@ def _attention_colslice_eligible(crow, col, query, value, config: SchedulerConfi
         return False
     if native_op("csr_attention_colslice") is None or crow.numel() <= 1 or col.numel() == 0:
         return False
-    from ._native import attention_colslice_supported, columns_ascending
+    from ._native import attention_colslice_supported, columns_ascending, row_counts
 
     if not attention_colslice_supported(query, value):
         return False
     gathered = (query.size(1) + value.size(1)) * 4 * (crow.numel() - 1)
-    if config.column_slices == "auto" and gathered < _COLSLICE_MIN_X_BYTES:
+    if (config.column_slices == "auto" and gathered < _COLSLICE_MIN_X_BYTES
+            and row_counts(crow, _COLSLICE_HUB_DEGREE, 0)[0] == 0):
         return False
     columns_ascending(crow, col)  # a malformed graph raises; any column order is eligible
     return True
@@ -950,11 +958,27 @@ def csr_attention_forward(
     """softmax_row(scale · SDDMM(query, key)) · value (``_auto.py:762-780``;
     the reference has no scale, i.e. scale = 1).
 
-    On the GPU with float32 inputs and ``fused`` (default: the
-    ``AUTOSAGE_FUSED_ATTENTION`` switch, on) the three stages run as one
-    native kernel; otherwise as the scheduled SDDMM, the row softmax and the
-    scheduled SpMM, as in the reference."""
+    On the GPU with ``fused`` (default: the ``AUTOSAGE_FUSED_ATTENTION``
+    switch, on) the three stages run as one native kernel: for float32 the
+    exact fused kernel or the column-sliced one, whichever a full-graph
+    timing picks; for bf16 / fp16 the column-sliced kernel in fp32 arithmetic
+    with each output rounded once (when its widths fit: multiples of 8 up to
+    512).  Otherwise the stages run as the scheduled SDDMM, the row softmax
+    and the scheduled SpMM, as in the reference."""
     use_fused = _fused_default() if fused is None else bool(fused)
+    if (use_fused and query.is_cuda and query.dtype in _DTYPES_16 and value.dtype == query.dtype
+            and key.dtype == query.dtype):
+        crow_n, col_n, q, k = _normalize_sddmm(crow, col, query, key)
+        from ._native import attention_colslice_supported
+
+        v = value.contiguous()
+        if attention_colslice_supported(q, v) and k.data_ptr() % 16 == 0:
+            _require_native()
+            out = native_op("csr_attention_colslice")(crow_n, col_n, q, k, v, float(scale))
+            info = {"operation": "attention", "schema_version": AUTOTUNE_SCHEMA_VERSION, "choice": "fused",
+                    "from_cache": False}
+            return out, {"sddmm": {**info, "operation": "sddmm"}, "spmm": {**info, "operation": "spmm"},
+                         "fused": True, "variant": "colslice16", "attention": {"variant": "colslice16"}}
     if use_fused and query.is_cuda and query.dtype == torch.float32 and value.dtype == torch.float32:
         crow_n, col_n, q, k = _normalize_sddmm(crow, col, query, key)
         if not load_native() or native_op("csr_attention") is None:

@@ -88,6 +88,11 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr,
          _c_size, _c_ptr],
     ),
+    "as_csr_attention_colslice_16": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_int,
+         _c_ptr, _c_size, _c_ptr],
+    ),
     "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "as_induced_sample_workspace_bytes": (_c_size, [_c_i64]),
     "as_induced_sample_count": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
@@ -518,22 +523,27 @@ def csr_attention_impl(crow, col, query, key, value, scale=1.0):
 
 
 def attention_colslice_supported(query: torch.Tensor, value: torch.Tensor) -> bool:
-    """Feature widths the column-sliced attention handles (float4 lanes):
-    multiples of 4 in [4, 256], rows 16-byte aligned."""
+    """Feature widths the column-sliced attention handles (16-byte lanes):
+    fp32 multiples of 4 in [4, 256], bf16 / fp16 multiples of 8 in [8, 512];
+    rows 16-byte aligned."""
     fqk, fv = query.size(1), value.size(1)
-    return (fqk % 4 == 0 and 4 <= fqk <= 256 and fv % 4 == 0 and 4 <= fv <= 256
-            and all(t.data_ptr() % 16 == 0 for t in (query, value)))
+    if query.dtype in DTYPES_16:
+        widths = fqk % 8 == 0 and 8 <= fqk <= 512 and fv % 8 == 0 and 8 <= fv <= 512
+    else:
+        widths = fqk % 4 == 0 and 4 <= fqk <= 256 and fv % 4 == 0 and 4 <= fv <= 256
+    return widths and all(t.data_ptr() % 16 == 0 for t in (query, value))
 
 
 def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
     """Column-sliced attention (one column slice per XCD, online softmax per
     (row, slice)).  A graph whose columns do not ascend runs on its row-sorted
-    copy (``row_sorted``, built once per graph)."""
-    check_sddmm_inputs(crow, col, query, key)
+    copy (``row_sorted``, built once per graph).  float32 inputs, or bf16 /
+    fp16 (computed in fp32, each output rounded once)."""
+    check_sddmm_inputs(crow, col, query, key, allow_16=True)
     _maybe_validate(crow, col)
     _check(value.is_cuda and value.device == query.device, "value must be on the same CUDA device as query")
-    _check(value.dtype == torch.float32 and value.dim() == 2 and value.is_contiguous(),
-           "value must be contiguous float32 with shape [N, F_v]")
+    _check(value.dtype == query.dtype and value.dim() == 2 and value.is_contiguous(),
+           "value must be contiguous with shape [N, F_v] and query's dtype")
     _check(value.size(0) == query.size(0), "value must have one row per node")
     # the slices are cut along ascending columns: other graphs run on their
     # row-sorted copy (the same edges per row; the row softmax and the sum
@@ -542,9 +552,10 @@ def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
     n, fqk = query.shape
     fv = value.size(1)
     nnz = col.numel()
+    half = query.dtype in DTYPES_16
     if not attention_colslice_supported(query, value) or key.data_ptr() % 16 != 0:
-        raise ValueError("csr_attention_colslice needs F_qk and F_v multiples of 4 in [4, 256] and 16-byte "
-                         "aligned rows")
+        raise ValueError("csr_attention_colslice needs F_qk and F_v multiples of 4 in [4, 256] (float32) or of 8 "
+                         "in [8, 512] (bfloat16 / float16) and 16-byte aligned rows")
     out = torch.empty((n, fv), dtype=value.dtype, device=value.device)
     if n == 0:
         return out
@@ -552,10 +563,16 @@ def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
     ws = _workspace(min(lib.as_csr_attention_colslice_workspace_bytes(n, nnz, fv), _colslice_workspace_cap()),
                     query.device)
     with torch.cuda.device(query.device):
-        status = lib.as_csr_attention_colslice_f32(
-            _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv, float(scale),
-            _ptr(ws), ws.numel(), _stream(query.device),
-        )
+        if half:
+            status = lib.as_csr_attention_colslice_16(
+                _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv,
+                float(scale), DTYPES_16[query.dtype], _ptr(ws), ws.numel(), _stream(query.device),
+            )
+        else:
+            status = lib.as_csr_attention_colslice_f32(
+                _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv,
+                float(scale), _ptr(ws), ws.numel(), _stream(query.device),
+            )
     _raise(status, "autosage::csr_attention_colslice")
     return out
 

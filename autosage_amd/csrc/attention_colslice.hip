@@ -22,9 +22,18 @@
 // Not bit-identical to the fused kernel (that one keeps the reference's
 // stage order); deterministic, and within about 0.2 of the 1e-5 relative /
 // 1e-6 absolute bar against fp64 on the benchmark graph, as is the fused one.
+//
+// bf16 / fp16 inputs run the same kernels: a 16-byte lane holds 8 elements
+// (4 for fp32), converted exactly to fp32; the online softmax and the partial
+// states are fp32 and each output is rounded once to the element type (round
+// to nearest even).  Scores and probabilities never leave registers, so a
+// 16-bit attention is one pass over K and V instead of three stages, and it
+// is more accurate than the stages, which round every score and probability
+// to 16 bits.
 #include "as_device.h"
 #include "as_internal.h"
 #include "colslice_common.h"
+#include "elem16.h"
 
 namespace as {
 
@@ -36,31 +45,47 @@ constexpr int64_t kAttChunkRows = 131072;    // sliced rows per partial chunk
 constexpr int64_t kAttSliceBlocks = 4096;    // slice-kernel workgroups per slice
 constexpr int64_t kAttReduceBlocks = 8192;   // reduction workgroups
 
-__device__ __forceinline__ void merge_softmax(float& m, float& l, float (&acc)[4], float mo, float lo,
-                                              const float (&ao)[4]) {
+// Elements of type T in one 16-byte lane.
+template <typename T>
+constexpr int lane_elems() {
+  return 16 / static_cast<int>(sizeof(T));
+}
+
+template <int P>
+__device__ __forceinline__ void merge_softmax(float& m, float& l, float (&acc)[P], float mo, float lo,
+                                              const float (&ao)[P]) {
   const float mn = fmaxf(m, mo);
   if (mn == -INFINITY) return;  // both sides saw no edge
   const float c1 = m == -INFINITY ? 0.f : expf(m - mn);
   const float c2 = mo == -INFINITY ? 0.f : expf(mo - mn);
   l = l * c1 + lo * c2;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) acc[v] = acc[v] * c1 + ao[v] * c2;
+  for (int v = 0; v < P; ++v) acc[v] = acc[v] * c1 + ao[v] * c2;
   m = mn;
+}
+
+// The P elements of a 16-byte lane as exact fp32 values.
+template <typename T>
+__device__ __forceinline__ void lane_values(const RawVec<16>& r, float (&out)[lane_elems<T>()]) {
+#pragma unroll
+  for (int v = 0; v < lane_elems<T>(); ++v) out[v] = Elem<T>::get(r.w, v);
 }
 
 // Online softmax of one wave over edges [rs, re) of a row.  On return every
 // lane holds the merged state of the whole range; lane vl of a V group owns
-// features 4·vl .. 4·vl + 3 of acc.
+// features P·vl .. P·vl + P-1 of acc.
 // FQK / FV > 0: the feature widths as compile-time constants (the row stride
 // of each gather becomes a shift instead of a per-lane 64-bit multiply).
-template <int GK, int GV, int FQK, int FV>
-__device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, const float* __restrict__ key,
-                                             const float* __restrict__ value, int64_t fqk_rt, int64_t fv_rt,
-                                             const FVec<4>& q, float scale, int64_t rs, int64_t re, float& m,
-                                             float& l, float (&acc)[4]) {
+template <typename T, int GK, int GV, int FQK, int FV>
+__device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, const T* __restrict__ key,
+                                             const T* __restrict__ value, int64_t fqk_rt, int64_t fv_rt,
+                                             const float (&q)[lane_elems<T>()], float scale, int64_t rs,
+                                             int64_t re, float& m, float& l, float (&acc)[lane_elems<T>()]) {
+  constexpr int P = lane_elems<T>();
   constexpr int EK = kWave / GK;  // edges per K gather instruction
   constexpr int EV = kWave / GV;  // edges per V gather instruction
   constexpr int E = kAttBatch;
+  static_assert(E % EK == 0 && E % EV == 0, "a batch holds whole gather instructions");
   const int64_t fqk = FQK > 0 ? FQK : fqk_rt;
   const int64_t fv = FV > 0 ? FV : fv_rt;
   const int lane = lane_id();
@@ -68,16 +93,18 @@ __device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, co
   const int kl = lane % GK;
   const int gv = lane / GV;
   const int vl = lane % GV;
+  const char* __restrict__ kb = reinterpret_cast<const char*>(key);
+  const char* __restrict__ vb = reinterpret_cast<const char*>(value);
   // lanes past the feature end read feature 0 (their q is 0 / their output
   // is not stored)
-  const uint32_t kbytes = static_cast<uint32_t>((4 * kl < fqk ? 4 * kl : 0) * 4);
-  const uint32_t vbytes = static_cast<uint32_t>((4 * vl < fv ? 4 * vl : 0) * 4);
+  const uint32_t kbytes = static_cast<uint32_t>((P * kl < fqk ? P * kl : 0) * sizeof(T));
+  const uint32_t vbytes = static_cast<uint32_t>((P * vl < fv ? P * vl : 0) * sizeof(T));
   rs = uniform_i64(rs);
   re = uniform_i64(re);
   m = -INFINITY;
   l = 0.f;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) acc[v] = 0.f;
+  for (int v = 0; v < P; ++v) acc[v] = 0.f;
   int next_col = 0;
   if (lane < re - rs) next_col = static_cast<int>(col[rs + lane]);
   for (int64_t base = rs; base < re; base += kWave) {
@@ -86,8 +113,8 @@ __device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, co
     const int64_t nb = base + kWave;
     if (nb < re && lane < re - nb) next_col = static_cast<int>(col[nb + lane]);
     for (int j = 0; j < cnt; j += E) {
-      FVec<4> kv[E / EK];
-      FVec<4> vv[E / EV];
+      RawVec<16> kv[E / EK];
+      RawVec<16> vv[E / EV];
 #pragma unroll
       for (int i = 0; i < E / EK; ++i) {
         int c = 0;
@@ -97,7 +124,7 @@ __device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, co
           const int cg = bcast_i32(my_col, e < cnt ? e : cnt - 1);
           c = gk == g ? cg : c;
         }
-        kv[i] = load_vec_off<4>(key + row_offset(c, fqk), kbytes);
+        kv[i] = load_raw<16>(kb + row_offset(c, fqk) * sizeof(T) + kbytes);
       }
 #pragma unroll
       for (int i = 0; i < E / EV; ++i) {
@@ -108,15 +135,17 @@ __device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, co
           const int cg = bcast_i32(my_col, e < cnt ? e : cnt - 1);
           c = gv == g ? cg : c;
         }
-        vv[i] = load_vec_off<4>(value + row_offset(c, fv), vbytes);
+        vv[i] = load_raw<16>(vb + row_offset(c, fv) * sizeof(T) + vbytes);
       }
       // scores: K instruction i, group g holds edge j + i·EK + g
       float sk[E / EK];
 #pragma unroll
       for (int i = 0; i < E / EK; ++i) {
-        float d = q.v[0] * kv[i].v[0];
+        float k[P];
+        lane_values<T>(kv[i], k);
+        float d = q[0] * k[0];
 #pragma unroll
-        for (int v = 1; v < 4; ++v) d = __builtin_fmaf(q.v[v], kv[i].v[v], d);
+        for (int v = 1; v < P; ++v) d = __builtin_fmaf(q[v], k[v], d);
 #pragma unroll
         for (int o = GK / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
         sk[i] = d * scale;
@@ -140,13 +169,15 @@ __device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, co
         const float corr = m == -INFINITY ? 0.f : expf(m - mn);
         l *= corr;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[v] *= corr;
+        for (int v = 0; v < P; ++v) acc[v] *= corr;
 #pragma unroll
         for (int i = 0; i < E / EV; ++i) {
           const float p = s[i] == -INFINITY ? 0.f : expf(s[i] - mn);
           l += p;
+          float x[P];
+          lane_values<T>(vv[i], x);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(p, vv[i].v[v], acc[v]);
+          for (int v = 0; v < P; ++v) acc[v] = __builtin_fmaf(p, x[v], acc[v]);
         }
         m = mn;
       }
@@ -156,33 +187,59 @@ __device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, co
   for (int o = GV; o < kWave; o <<= 1) {
     const float mo = __shfl_xor(m, o, kWave);
     const float lo = __shfl_xor(l, o, kWave);
-    float ao[4];
+    float ao[P];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) ao[v] = __shfl_xor(acc[v], o, kWave);
-    merge_softmax(m, l, acc, mo, lo, ao);
+    for (int v = 0; v < P; ++v) ao[v] = __shfl_xor(acc[v], o, kWave);
+    merge_softmax<P>(m, l, acc, mo, lo, ao);
   }
 }
 
-template <int GK>
-__device__ __forceinline__ FVec<4> load_query_lanes(const float* __restrict__ query, int64_t row, int64_t fqk) {
+template <typename T, int GK>
+__device__ __forceinline__ void load_query_lanes(const T* __restrict__ query, int64_t row, int64_t fqk,
+                                                 float (&q)[lane_elems<T>()]) {
+  constexpr int P = lane_elems<T>();
   const int kl = lane_id() % GK;
-  FVec<4> q;
-  if (4 * kl < fqk) {
-    q = load_vec<4>(query + row * fqk + 4 * kl);
+  if (P * kl < fqk) {
+    lane_values<T>(load_raw<16>(reinterpret_cast<const char*>(query + row * fqk + P * kl)), q);
   } else {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) q.v[v] = 0.f;
+    for (int v = 0; v < P; ++v) q[v] = 0.f;
   }
-  return q;
 }
 
+// N consecutive outputs (N = 4 or 8, 4·N-byte aligned for fp32, 2·N-byte
+// for 16-bit), each rounded once to T.
+template <typename T, int N>
+__device__ __forceinline__ void store_out(T* p, const float (&v)[N]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      FVec<4> o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o.v[k] = v[i + k];
+      store_vec<4>(reinterpret_cast<float*>(p) + i, o);
+    }
+  } else {
+    uint32_t w[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i)
+      w[i] = uint32_t(Elem<T>::bits(v[2 * i])) | (uint32_t(Elem<T>::bits(v[2 * i + 1])) << 16);
+    if constexpr (N == 8) {
+      *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    }
+  }
+}
+
+template <typename T>
 struct AttArgs {
   const int64_t* crow;
   const int64_t* col;
-  const float* q;
-  const float* k;
-  const float* v;
-  float* out;
+  const T* q;
+  const T* k;
+  const T* v;
+  T* out;
   int64_t n;
   int64_t fqk;
   int64_t fv;
@@ -194,23 +251,25 @@ struct AttArgs {
 
 // Short rows order[H, n), H = counts[0]: one wave per row writes out.  The
 // grid is sized for all n rows; waves stride over the short ones.
-template <int GK, int GV, int FQK, int FV>
-__global__ __launch_bounds__(kBlock) void att_rows_kernel(AttArgs a) {
+template <typename T, int GK, int GV, int FQK, int FV>
+__global__ __launch_bounds__(kBlock) void att_rows_kernel(AttArgs<T> a) {
+  constexpr int P = lane_elems<T>();
   const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
   const int64_t first = a.counts[0];
   for (int64_t item = first + static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block(); item < a.n;
        item += waves) {
     const int64_t row = uniform_i64(a.order[item]);
-    const FVec<4> q = load_query_lanes<GK>(a.q, row, a.fqk);
-    float m, l, acc[4];
-    attend_edges<GK, GV, FQK, FV>(a.col, a.k, a.v, a.fqk, a.fv, q, a.scale, a.crow[row], a.crow[row + 1], m, l,
-                                  acc);
+    float q[P];
+    load_query_lanes<T, GK>(a.q, row, a.fqk, q);
+    float m, l, acc[P];
+    attend_edges<T, GK, GV, FQK, FV>(a.col, a.k, a.v, a.fqk, a.fv, q, a.scale, a.crow[row], a.crow[row + 1], m, l,
+                                     acc);
     const int lane = lane_id();
-    if (lane < GV && 4 * lane < a.fv) {
-      FVec<4> o;
+    if (lane < GV && P * lane < a.fv) {
+      float o[P];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) o.v[v] = l > 0.f ? acc[v] / l : 0.f;
-      store_vec<4>(a.out + row * a.fv + 4 * lane, o);
+      for (int v = 0; v < P; ++v) o[v] = l > 0.f ? acc[v] / l : 0.f;
+      store_out<T, P>(a.out + row * a.fv + P * lane, o);
     }
   }
 }
@@ -220,10 +279,11 @@ __global__ __launch_bounds__(kBlock) void att_rows_kernel(AttArgs a) {
 // host knows only an upper bound on H, so a chunk may be empty: the grid is
 // capped and the waves of a slice stride over the chunk, which keeps the
 // launch of an empty chunk short.
-template <int GK, int GV, int FQK, int FV>
-__global__ __launch_bounds__(kBlock) void att_slice_kernel(AttArgs a, int64_t begin, int64_t items, int64_t stride,
-                                                           float* __restrict__ pm, float* __restrict__ pl,
-                                                           float* __restrict__ pacc) {
+template <typename T, int GK, int GV, int FQK, int FV>
+__global__ __launch_bounds__(kBlock) void att_slice_kernel(AttArgs<T> a, int64_t begin, int64_t items,
+                                                           int64_t stride, float* __restrict__ pm,
+                                                           float* __restrict__ pl, float* __restrict__ pacc) {
+  constexpr int P = lane_elems<T>();
   const int slice = static_cast<int>(blockIdx.x % kSlices);
   const int64_t waves = static_cast<int64_t>(gridDim.x / kSlices) * kWavesPerBlock;
   int64_t end = a.counts[0] - begin;
@@ -238,15 +298,19 @@ __global__ __launch_bounds__(kBlock) void att_slice_kernel(AttArgs a, int64_t be
     slice_range(a.off, row, slice, deg, lo, hi);
     lo = uniform_i64(lo);
     hi = uniform_i64(hi);
-    const FVec<4> q = load_query_lanes<GK>(a.q, row, a.fqk);
-    float m, l, acc[4];
-    attend_edges<GK, GV, FQK, FV>(a.col, a.k, a.v, a.fqk, a.fv, q, a.scale, rs + lo, rs + hi, m, l, acc);
+    float q[P];
+    load_query_lanes<T, GK>(a.q, row, a.fqk, q);
+    float m, l, acc[P];
+    attend_edges<T, GK, GV, FQK, FV>(a.col, a.k, a.v, a.fqk, a.fv, q, a.scale, rs + lo, rs + hi, m, l, acc);
     const int64_t at = slice * stride + local;
-    if (lane < GV && 4 * lane < a.fv) {
-      FVec<4> o;
+    if (lane < GV && P * lane < a.fv) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) o.v[v] = acc[v];
-      store_vec<4>(pacc + at * a.fv + 4 * lane, o);
+      for (int i = 0; i < P; i += 4) {
+        FVec<4> o;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o.v[v] = acc[i + v];
+        store_vec<4>(pacc + at * a.fv + P * lane + i, o);
+      }
     }
     if (lane == 0) {
       pm[at] = m;
@@ -257,8 +321,9 @@ __global__ __launch_bounds__(kBlock) void att_slice_kernel(AttArgs a, int64_t be
 
 // Merge of the 8 partial states of each sliced row of the chunk; thread per
 // (row, 4 features).
-__global__ __launch_bounds__(kBlock) void att_reduce_kernel(AttArgs a, int64_t begin, int64_t items, int64_t stride,
-                                                            const float* __restrict__ pm,
+template <typename T>
+__global__ __launch_bounds__(kBlock) void att_reduce_kernel(AttArgs<T> a, int64_t begin, int64_t items,
+                                                            int64_t stride, const float* __restrict__ pm,
                                                             const float* __restrict__ pl,
                                                             const float* __restrict__ pacc) {
   const int64_t F4 = a.fv / 4;
@@ -286,43 +351,55 @@ __global__ __launch_bounds__(kBlock) void att_reduce_kernel(AttArgs a, int64_t b
       }
     }
     const int64_t row = a.order[begin + local];
-    FVec<4> o;
+    float o[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) o.v[v] = l > 0.f ? acc[v] / l : 0.f;
-    store_vec<4>(a.out + row * a.fv + f, o);
+    for (int v = 0; v < 4; ++v) o[v] = l > 0.f ? acc[v] / l : 0.f;
+    store_out<T, 4>(a.out + row * a.fv + f, o);
   }
 }
 
-int lane_group(int64_t f) { return f <= 64 ? 16 : (f <= 128 ? 32 : 64); }
+// Lanes per K (or V) row: one 16-byte lane per P elements, a power of two;
+// fp32 keeps at least 16 lanes (4 edges per gather), 16-bit at least 8.
+template <typename T>
+int lane_group(int64_t f) {
+  if constexpr (sizeof(T) == 4) {
+    return f <= 64 ? 16 : (f <= 128 ? 32 : 64);
+  } else {
+    return f <= 64 ? 8 : (f <= 128 ? 16 : (f <= 256 ? 32 : 64));
+  }
+}
 
-template <int GK, int GV, int FQK = 0, int FV = 0>
-void launch_attention_t(const AttArgs& a, int64_t upper, int64_t chunk, float* pm, float* pl, float* pacc,
+template <typename T, int GK, int GV, int FQK = 0, int FV = 0>
+void launch_attention_t(const AttArgs<T>& a, int64_t upper, int64_t chunk, float* pm, float* pl, float* pacc,
                         hipStream_t s) {
   // short rows: a grid-stride over order[H, n) (H is known on the device only)
   int64_t row_blocks = (a.n + kWavesPerBlock - 1) / kWavesPerBlock;
   if (row_blocks > kMaxBlocksPerLaunch) row_blocks = kMaxBlocksPerLaunch;
-  hipLaunchKernelGGL((att_rows_kernel<GK, GV, FQK, FV>), dim3(static_cast<unsigned>(row_blocks)), dim3(kBlock), 0, s,
-                     a);
+  hipLaunchKernelGGL((att_rows_kernel<T, GK, GV, FQK, FV>), dim3(static_cast<unsigned>(row_blocks)), dim3(kBlock),
+                     0, s, a);
   for (int64_t begin = 0; begin < upper; begin += chunk) {
     const int64_t items = upper - begin < chunk ? upper - begin : chunk;
     int64_t per_slice = (items + kWavesPerBlock - 1) / kWavesPerBlock;
     if (per_slice > kAttSliceBlocks) per_slice = kAttSliceBlocks;
-    hipLaunchKernelGGL((att_slice_kernel<GK, GV, FQK, FV>), dim3(static_cast<unsigned>(kSlices * per_slice)),
+    hipLaunchKernelGGL((att_slice_kernel<T, GK, GV, FQK, FV>), dim3(static_cast<unsigned>(kSlices * per_slice)),
                        dim3(kBlock), 0, s, a, begin, items, chunk, pm, pl, pacc);
     int64_t blocks = (items * (a.fv / 4) + kBlock - 1) / kBlock;
     if (blocks > kAttReduceBlocks) blocks = kAttReduceBlocks;
-    hipLaunchKernelGGL(att_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, a, begin, items,
-                       chunk, pm, pl, pacc);
+    hipLaunchKernelGGL((att_reduce_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, a, begin,
+                       items, chunk, pm, pl, pacc);
   }
 }
 
-template <int GK>
-void launch_attention_k(int gv, const AttArgs& a, int64_t upper, int64_t chunk, float* pm, float* pl, float* pacc,
-                        hipStream_t s) {
+template <typename T, int GK>
+void launch_attention_k(int gv, const AttArgs<T>& a, int64_t upper, int64_t chunk, float* pm, float* pl,
+                        float* pacc, hipStream_t s) {
   switch (gv) {
-    case 16: launch_attention_t<GK, 16>(a, upper, chunk, pm, pl, pacc, s); break;
-    case 32: launch_attention_t<GK, 32>(a, upper, chunk, pm, pl, pacc, s); break;
-    default: launch_attention_t<GK, 64>(a, upper, chunk, pm, pl, pacc, s); break;
+    case 8:
+      if constexpr (sizeof(T) == 2) launch_attention_t<T, GK, 8>(a, upper, chunk, pm, pl, pacc, s);
+      break;
+    case 16: launch_attention_t<T, GK, 16>(a, upper, chunk, pm, pl, pacc, s); break;
+    case 32: launch_attention_t<T, GK, 32>(a, upper, chunk, pm, pl, pacc, s); break;
+    default: launch_attention_t<T, GK, 64>(a, upper, chunk, pm, pl, pacc, s); break;
   }
 }
 
@@ -339,6 +416,74 @@ size_t att_row_bytes(int64_t fv) { return static_cast<size_t>(kSlices) * (static
 int64_t att_sliced_upper(int64_t n, int64_t nnz) {
   const int64_t u = nnz / kAttSliceMinDegree;
   return u < n ? u : n;
+}
+
+// Both entry points after their element-specific checks: carves the
+// workspace, computes the slice points and the row order, launches.
+template <typename T>
+int attention_run(const int64_t* crow, const int64_t* col, const T* query, const T* key, const T* value, T* out,
+                  int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v, float scale, void* workspace,
+                  size_t workspace_bytes, void* stream, const char* what) {
+  if (n == 0) return AS_OK;
+  if (crow == nullptr || query == nullptr || key == nullptr || value == nullptr || out == nullptr ||
+      (nnz > 0 && col == nullptr))
+    return fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!aligned(query, 16) || !aligned(key, 16) || !aligned(value, 16) || !aligned(out, 16))
+    return fail(AS_ERR_UNSUPPORTED, "column-sliced attention needs 16-byte aligned Q, K, V and out");
+  const size_t fixed = att_fixed_bytes(n);
+  const size_t row_bytes = att_row_bytes(f_v);
+  if (workspace == nullptr || workspace_bytes < fixed + row_bytes + 3 * 256)
+    return fail(AS_ERR_WORKSPACE, "column-sliced attention needs at least %zu workspace bytes, got %zu",
+                fixed + row_bytes + 3 * 256, workspace_bytes);
+  if (!aligned(workspace, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  const int64_t upper = att_sliced_upper(n, nnz);
+  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed - 3 * 256) / row_bytes);
+  if (chunk > kAttChunkRows) chunk = kAttChunkRows;
+  if (chunk > upper) chunk = upper;
+  if (chunk < 1) chunk = 1;
+
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const size_t rows = static_cast<size_t>(n);
+  int32_t* off = reinterpret_cast<int32_t*>(ws);
+  ws += align_up(rows * kSliceBounds * sizeof(int32_t), 256);
+  int32_t* order = reinterpret_cast<int32_t*>(ws);
+  ws += align_up(rows * sizeof(int32_t), 256);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws);
+  ws += 256;
+  void* bin_ws = ws;
+  ws = static_cast<char*>(workspace) + fixed;
+  const size_t states = static_cast<size_t>(kSlices) * static_cast<size_t>(chunk);
+  float* pm = reinterpret_cast<float*>(ws);
+  ws += align_up(states * sizeof(float), 256);
+  float* pl = reinterpret_cast<float*>(ws);
+  ws += align_up(states * sizeof(float), 256);
+  float* pacc = reinterpret_cast<float*>(ws);
+
+  launch_slice_points(crow, col, n, kAttSliceMinDegree, off, s);
+  // order: rows of degree >= 128 (sliced) longest first, then the others
+  int st = launch_bin_rows(crow, n, kAttSliceMinDegree, kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
+  if (st != AS_OK) return st;
+  const AttArgs<T> a{crow, col, query, key, value, out, n, f_qk, f_v, scale, order, counts, off};
+  // common widths with compile-time strides
+  constexpr bool kHalf = sizeof(T) == 2;
+  if (f_qk == 64 && f_v == 128) {
+    launch_attention_t<T, kHalf ? 8 : 16, kHalf ? 16 : 32, 64, 128>(a, upper, chunk, pm, pl, pacc, s);
+  } else if (f_qk == 64 && f_v == 64) {
+    launch_attention_t<T, kHalf ? 8 : 16, kHalf ? 8 : 16, 64, 64>(a, upper, chunk, pm, pl, pacc, s);
+  } else if (f_qk == 128 && f_v == 128) {
+    launch_attention_t<T, kHalf ? 16 : 32, kHalf ? 16 : 32, 128, 128>(a, upper, chunk, pm, pl, pacc, s);
+  } else {
+    switch (lane_group<T>(f_qk)) {
+      case 8:
+        if constexpr (kHalf) launch_attention_k<T, 8>(lane_group<T>(f_v), a, upper, chunk, pm, pl, pacc, s);
+        break;
+      case 16: launch_attention_k<T, 16>(lane_group<T>(f_v), a, upper, chunk, pm, pl, pacc, s); break;
+      case 32: launch_attention_k<T, 32>(lane_group<T>(f_v), a, upper, chunk, pm, pl, pacc, s); break;
+      default: launch_attention_k<T, 64>(lane_group<T>(f_v), a, upper, chunk, pm, pl, pacc, s); break;
+    }
+  }
+  return check_launch(what);
 }
 
 }  // namespace
@@ -366,66 +511,28 @@ int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col, const
   if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
   if (f_qk < 4 || f_qk > 256 || f_qk % 4 != 0 || f_v < 4 || f_v > 256 || f_v % 4 != 0)
     return as::fail(AS_ERR_UNSUPPORTED, "column-sliced attention needs F_qk and F_v in [4, 256], multiples of 4");
-  if (n == 0) return AS_OK;
-  if (crow == nullptr || query == nullptr || key == nullptr || value == nullptr || out == nullptr ||
-      (nnz > 0 && col == nullptr))
-    return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
-  if (!as::aligned(query, 16) || !as::aligned(key, 16) || !as::aligned(value, 16) || !as::aligned(out, 16))
-    return as::fail(AS_ERR_UNSUPPORTED, "column-sliced attention needs 16-byte aligned Q, K, V and out");
-  const size_t fixed = as::att_fixed_bytes(n);
-  const size_t row_bytes = as::att_row_bytes(f_v);
-  if (workspace == nullptr || workspace_bytes < fixed + row_bytes + 3 * 256)
-    return as::fail(AS_ERR_WORKSPACE, "column-sliced attention needs at least %zu workspace bytes, got %zu",
-                    fixed + row_bytes + 3 * 256, workspace_bytes);
-  if (!as::aligned(workspace, 256)) return as::fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  const int64_t upper = as::att_sliced_upper(n, nnz);
-  int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed - 3 * 256) / row_bytes);
-  if (chunk > as::kAttChunkRows) chunk = as::kAttChunkRows;
-  if (chunk > upper) chunk = upper;
-  if (chunk < 1) chunk = 1;
+  return as::attention_run<float>(crow, col, query, key, value, out, n, nnz, f_qk, f_v, scale, workspace,
+                                  workspace_bytes, stream, "csr_attention_colslice");
+}
 
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const size_t rows = static_cast<size_t>(n);
-  int32_t* off = reinterpret_cast<int32_t*>(ws);
-  ws += as::align_up(rows * as::kSliceBounds * sizeof(int32_t), 256);
-  int32_t* order = reinterpret_cast<int32_t*>(ws);
-  ws += as::align_up(rows * sizeof(int32_t), 256);
-  int32_t* counts = reinterpret_cast<int32_t*>(ws);
-  ws += 256;
-  void* bin_ws = ws;
-  ws = static_cast<char*>(workspace) + fixed;
-  const size_t states = static_cast<size_t>(as::kSlices) * static_cast<size_t>(chunk);
-  float* pm = reinterpret_cast<float*>(ws);
-  ws += as::align_up(states * sizeof(float), 256);
-  float* pl = reinterpret_cast<float*>(ws);
-  ws += as::align_up(states * sizeof(float), 256);
-  float* pacc = reinterpret_cast<float*>(ws);
-
-  as::launch_slice_points(crow, col, n, as::kAttSliceMinDegree, off, s);
-  // order: rows of degree >= 128 (sliced) longest first, then the others
-  int st = as::launch_bin_rows(crow, n, as::kAttSliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
-  if (st != AS_OK) return st;
-  const as::AttArgs a{crow, col, query, key, value, out, n, f_qk, f_v, scale, order, counts, off};
-  // common widths with compile-time strides
-  if (f_qk == 64 && f_v == 128) {
-    as::launch_attention_t<16, 32, 64, 128>(a, upper, chunk, pm, pl, pacc, s);
-    return as::check_launch("csr_attention_colslice");
-  }
-  if (f_qk == 64 && f_v == 64) {
-    as::launch_attention_t<16, 16, 64, 64>(a, upper, chunk, pm, pl, pacc, s);
-    return as::check_launch("csr_attention_colslice");
-  }
-  if (f_qk == 128 && f_v == 128) {
-    as::launch_attention_t<32, 32, 128, 128>(a, upper, chunk, pm, pl, pacc, s);
-    return as::check_launch("csr_attention_colslice");
-  }
-  switch (as::lane_group(f_qk)) {
-    case 16: as::launch_attention_k<16>(as::lane_group(f_v), a, upper, chunk, pm, pl, pacc, s); break;
-    case 32: as::launch_attention_k<32>(as::lane_group(f_v), a, upper, chunk, pm, pl, pacc, s); break;
-    default: as::launch_attention_k<64>(as::lane_group(f_v), a, upper, chunk, pm, pl, pacc, s); break;
-  }
-  return as::check_launch("csr_attention_colslice");
+int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col, const void* query, const void* key,
+                                 const void* value, void* out, int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v,
+                                 float scale, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
+  if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
+  if (f_qk < 8 || f_qk > 512 || f_qk % 8 != 0 || f_v < 8 || f_v > 512 || f_v % 8 != 0)
+    return as::fail(AS_ERR_UNSUPPORTED, "16-bit attention needs F_qk and F_v in [8, 512], multiples of 8");
+  if (dtype == AS_DTYPE_BF16)
+    return as::attention_run<as::Bf16>(crow, col, static_cast<const as::Bf16*>(query),
+                                       static_cast<const as::Bf16*>(key), static_cast<const as::Bf16*>(value),
+                                       static_cast<as::Bf16*>(out), n, nnz, f_qk, f_v, scale, workspace,
+                                       workspace_bytes, stream, "csr_attention_colslice (bf16)");
+  return as::attention_run<as::Fp16>(crow, col, static_cast<const as::Fp16*>(query), static_cast<const as::Fp16*>(key),
+                                     static_cast<const as::Fp16*>(value), static_cast<as::Fp16*>(out), n, nnz, f_qk,
+                                     f_v, scale, workspace, workspace_bytes, stream, "csr_attention_colslice (fp16)");
 }
 
 }  // extern "C"

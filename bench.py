@@ -714,6 +714,10 @@ def probe_overhead(args, device) -> dict:
     w = gen(seed=args.seed) if args.workload == "cfg5" else gen(seed=args.seed, features=f)
     crow = torch.from_numpy(w.crow).to(device)
     col = torch.from_numpy(w.col).to(device)
+    if args.shuffle_columns:
+        # columns out of order inside rows: the cold call also builds the
+        # row-sorted copy the column-sliced schedule runs on
+        col = _shuffle_within_rows(crow, col, args.seed + 1)
     dense = {k: torch.from_numpy(v).to(device) for k, v in w.dense.items()}
     if args.workload in ("cfg1", "cfg2", "cfg3"):
         val = None if w.val is None else torch.from_numpy(w.val).to(device)
@@ -750,9 +754,21 @@ def probe_overhead(args, device) -> dict:
             "full_graph_ms": round(i.get("full_graph", {}).get("wall_ms", 0.0), 3),
             "full_graph": i.get("full_graph"),
         })
+    sort_ms = None
+    if args.shuffle_columns:
+        # the one-time row sort on its own, for a fresh copy of the graph
+        from autosage_amd._native import row_sorted
+
+        fresh = col.clone()
+        torch.cuda.synchronize()
+        s0 = time.perf_counter()
+        row_sorted(crow, fresh)
+        torch.cuda.synchronize()
+        sort_ms = round((time.perf_counter() - s0) * 1e3, 3)
     return {
         "metric": "scheduler overhead (cold call with an empty schedule cache, then cached calls)",
-        "workload": args.workload, "features": f, "entry": name, "rows": w.rows, "nnz": w.nnz,
+        "workload": args.workload + (" shuffled columns" if args.shuffle_columns else ""), "features": f,
+        "entry": name, "rows": w.rows, "nnz": w.nnz, "row_sort_ms": sort_ms,
         "cold_call_ms": round(cold_ms, 3), "cached_call_ms": round(warm["best_ms"], 4),
         "cold_over_cached": round(cold_ms / warm["best_ms"], 1), "ops": per_op,
     }
@@ -783,8 +799,20 @@ def bench_other(args, device) -> dict:
         if dt == torch.float32:
             variants["whole"] = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)
         calib = {}
-        chosen = calibrate(variants, calib) if args.variant == "calibrated" else args.variant
+        chosen = calibrate(variants, calib) if args.variant in ("calibrated", "auto") else args.variant
         step = variants[chosen]
+        if args.variant == "auto":
+            # the scheduler with a warm cache (its full-graph decision made once)
+            import tempfile
+
+            from autosage_amd import sddmm_csr_auto
+
+            os.environ["AUTOSAGE_CACHE_DIR"] = tempfile.mkdtemp(prefix="autosage-bench-")
+            _, info = sddmm_csr_auto(crow, col, q, k)
+            cand = info.get("candidate")
+            chosen = "baseline" if info.get("choice") != "autosage" else (
+                "whole" if cand is None else ",".join(map(str, cand)))
+            step = lambda: sddmm_csr_auto(crow, col, q, k)[0]  # noqa: E731
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * w.nnz * f
         algo = sddmm_bytes(w.rows, w.nnz, f, elem=q.element_size())
@@ -814,19 +842,32 @@ def bench_other(args, device) -> dict:
             if not args.exact_only and columns_ascending(crow, col):
                 variants["colslice"] = lambda: torch.ops.autosage.csr_attention_colslice(crow, col, q, k, v, 0.125)
         else:
-            # 16-bit: the three native stages (SDDMM, row softmax, SpMM), the
-            # scale 1/8 applied exactly to the 16-bit scores
+            # 16-bit: one kernel (fp32 online softmax, each output rounded
+            # once: csr_attention_forward's default), and the three native
+            # stages (SDDMM, row softmax, SpMM, the scale 1/8 applied exactly
+            # to the 16-bit scores), which round scores and probabilities
             def stages():
                 s = torch.ops.autosage.sddmm_csr(crow, col, q, k).mul_(0.125)
                 return torch.ops.autosage.spmm_csr(crow, col, torch.ops.autosage.csr_row_softmax(crow, s), v)
 
-            variants = {"stages16": stages}
+            variants = {"colslice16": lambda: torch.ops.autosage.csr_attention_colslice(crow, col, q, k, v, 0.125),
+                        "stages16": stages}
         calib = {}
-        chosen = calibrate(variants, calib) if args.variant == "calibrated" else args.variant
+        chosen = calibrate(variants, calib) if args.variant in ("calibrated", "auto") else args.variant
         if chosen not in variants:
             raise SystemExit(f"unknown cfg5 variant {chosen!r}: one of {sorted(variants)}")
-        log(f"calibration (ms): {calib}; chosen {chosen}")
         step = variants[chosen]
+        if args.variant == "auto":
+            # csr_attention_forward's default path with a warm cache
+            import tempfile
+
+            from autosage_amd import csr_attention_forward
+
+            os.environ["AUTOSAGE_CACHE_DIR"] = tempfile.mkdtemp(prefix="autosage-bench-")
+            _, info = csr_attention_forward(crow, col, q, k, v, scale=0.125)
+            chosen = info.get("variant", "stages")
+            step = lambda: csr_attention_forward(crow, col, q, k, v, scale=0.125)[0]  # noqa: E731
+        log(f"calibration (ms): {calib}; chosen {chosen}")
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * w.nnz * (64 + 128)
         algo = attention_bytes(w.rows, w.nnz, 64, 128, elem=q.element_size())

@@ -313,6 +313,25 @@ int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col,
                                   float scale, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
+/* The column-sliced attention on bf16 or fp16 query, key, value and output
+ * (dtype AS_DTYPE_BF16 / AS_DTYPE_F16): the kernels of
+ * as_csr_attention_colslice_f32 with 16-byte lanes of 8 elements, every
+ * input converted exactly to fp32, the online softmax and the partial states
+ * in fp32, and each output rounded once to the element type (round to
+ * nearest even).  Scores and probabilities stay in registers.  The reference
+ * composes its attention for any feature type from torch ops
+ * (csr_attention_forward, autosage/_auto.py:762-780), rounding the scores and
+ * probabilities to the feature type; there is no 16-bit kernel to replace.
+ * f_qk and f_v multiples of 8 in [8, 512]; 16-byte aligned Q, K, V and out;
+ * columns ascending within every row; the workspace of
+ * as_csr_attention_colslice_workspace_bytes. */
+int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col,
+                                 const void* query, const void* key,
+                                 const void* value, void* out, int64_t n,
+                                 int64_t nnz, int64_t f_qk, int64_t f_v,
+                                 float scale, int dtype, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace for the induced-sample entry points (n int32). */
 size_t as_induced_sample_workspace_bytes(int64_t n);
 

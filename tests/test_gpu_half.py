@@ -330,10 +330,18 @@ def test_attention_on_bf16_inputs_runs_the_native_stages(monkeypatch, tmp_path):
     q, k = q * 0.125, k * 0.125
     ref, _ = csr_attention_forward(d_crow, d_col, q.cuda(), k.cuda(), v.cuda(), fused=False)
     out, info = csr_attention_forward(d_crow, d_col, q.bfloat16().cuda(), k.bfloat16().cuda(),
-                                      v.bfloat16().cuda())
+                                      v.bfloat16().cuda(), fused=False)
     assert out.dtype == torch.bfloat16
     assert info["sddmm"]["choice"] == "autosage" and info["spmm"]["choice"] == "autosage"
     assert (out.float() - ref).abs().max().item() < 0.03
+    # the default (fused): one kernel in fp32 arithmetic, each output rounded
+    # once, so within one bf16 rounding of the fp32 result
+    fused, finfo = csr_attention_forward(d_crow, d_col, q.bfloat16().cuda(), k.bfloat16().cuda(),
+                                         v.bfloat16().cuda())
+    assert finfo["fused"] and fused.dtype == torch.bfloat16
+    ref16 = csr_attention_forward(d_crow, d_col, q.bfloat16().float().cuda(), k.bfloat16().float().cuda(),
+                                  v.bfloat16().float().cuda(), fused=False)[0]
+    assert (fused.float() - ref16).abs().max().item() <= 2.0 ** -8 * ref16.abs().max().item() + 1e-5
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

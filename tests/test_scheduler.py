@@ -76,6 +76,17 @@ def test_column_slices_never_eligible_without_the_native_op(monkeypatch):
     # auto: too little X or too few edges per row
     assert not _auto._colslice_eligible(crow, col, x[:, :7000], SchedulerConfig())  # 28 MB
     assert not _auto._colslice_eligible(crow, col[: 63 * 1000], x, SchedulerConfig())
+    # ... unless a row is long enough to be worth spreading over the slices
+    # (the device check of the graph is stubbed out here, on the CPU)
+    from autosage_amd import _native
+
+    monkeypatch.setattr(_native, "columns_ascending", lambda crow_, col_: True)
+    hub = torch.cat([torch.tensor([0, 2048]), torch.arange(1, 999) + 2048])
+    hub_col = torch.arange(hub[-1].item()) % 1000
+    small_x = torch.zeros(1000, 128)  # 0.5 MB
+    assert _auto._colslice_eligible(hub, hub_col, small_x, SchedulerConfig())
+    short = torch.cat([torch.tensor([0, 2047]), torch.arange(1, 999) + 2047])
+    assert not _auto._colslice_eligible(short, hub_col[:-1], small_x, SchedulerConfig())
 
 
 @pytest.mark.parametrize(
