@@ -83,6 +83,42 @@ def test_spmm_backward(split, features):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("features", [64, 128])
+def test_spmm_backward_with_in_degree_hubs(features):
+    """A = Hᵀ for a graph H with hub rows: A's columns have in-degree hubs, so
+    the transposed CSR of the backward (= H) has rows of 3,000 edges.  dX of
+    the exact op then runs the degree-split schedule (rows of >= 1024 edges
+    split over waves) and must still equal the oracle's sequential product
+    over Aᵀ bit for bit; dX of the column-sliced op slices those rows and
+    must be within 1e-6·|fp64| of the fp64 product."""
+    require_gpu()
+    n = 6000
+    h_crow, h_col = case_graph(n, 6, seed=features, hubs=4, hub_degree=3000, empty=0.05)
+    a_crow, a_col, _ = csr_transpose(torch.from_numpy(h_crow), torch.from_numpy(h_col))
+    crow, col = a_crow.numpy(), a_col.numpy()
+    t_crow, t_col, perm = csr_transpose(a_crow, a_col)
+    assert np.diff(t_crow.numpy()).max() >= 3000 and np.diff(crow).max() < 1024
+    rng = np.random.default_rng(features + 1)
+    val = rng.standard_normal(col.size).astype(np.float32)
+    x = rng.standard_normal((n, features)).astype(np.float32)
+    g = rng.standard_normal((n, features)).astype(np.float32)
+    d_crow, d_col = to_dev(crow, col)
+    for sliced in (False, True):
+        d_val = torch.from_numpy(val).cuda().requires_grad_(True)
+        d_x = torch.from_numpy(x).cuda().requires_grad_(True)
+        op = torch.ops.autosage.spmm_csr_colslice if sliced else torch.ops.autosage.spmm_csr
+        op(d_crow, d_col, d_val, d_x).backward(torch.from_numpy(g).cuda())
+        v_t = val[perm.numpy()]
+        if sliced:
+            exact = oracle.spmm_f64(t_crow.numpy(), t_col.numpy(), v_t, g)
+            got = d_x.grad.cpu().numpy()
+            assert np.all(np.abs(got - exact) <= 1e-6 * np.abs(exact) + 1e-9)
+        else:
+            assert bitwise_equal(d_x.grad, oracle.spmm_seq(t_crow, t_col, v_t, g))
+        assert bitwise_equal(d_val.grad, oracle.sddmm_ref(crow, col, g, x))
+
+
+@pytest.mark.gpu
 def test_spmm_backward_unweighted_and_no_grad_inputs():
     require_gpu()
     crow, col = case_graph(500, 8, seed=1)
