@@ -27,7 +27,7 @@ import torch
 from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
 # 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
@@ -66,7 +66,7 @@ _SIGNATURES = {
     "as_spmm_csr_colslice_f32": (
         _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_i64, _c_ptr]
     ),
-    "as_spmm_colslice_min_degree": (_c_i64, [_c_int]),
+    "as_spmm_colslice_min_degree": (_c_i64, [_c_int, _c_i64, _c_int]),
     "as_spmm_csr_rounded_16": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_i64,
@@ -233,7 +233,7 @@ def spmm_csr_impl(crow, col, val, x):
         # graphs without a row to slice (one launch), else edge slices (with
         # 2-byte features the fp64 partials of column slices cost more than
         # their cache gain: 1.99 against 2.36 ms on the skewed graph)
-        if col.numel() <= ROWS_16_MAX_NNZ or sliced_rows(crow, False) == 0:
+        if col.numel() <= ROWS_16_MAX_NNZ or sliced_rows(crow, False, x.size(1), x.dtype) == 0:
             return spmm_rows_16_impl(crow, col, val, x)
         return spmm_rounded_16_impl(crow, col, val, x, column_slices=False)
     y = torch.empty_like(x)
@@ -298,7 +298,7 @@ def spmm_csr_colslice_impl(crow, col, val, x):
     with torch.cuda.device(x.device):
         status = lib.as_spmm_csr_colslice_f32(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, _ptr(ws), ws.numel(),
-            sliced_rows(crow, True), _stream(x.device),
+            sliced_rows(crow, True, f, x.dtype), _stream(x.device),
         )
     _raise(status, "autosage::spmm_csr_colslice")
     return y
@@ -340,7 +340,7 @@ def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
     if n == 0 or f == 0:
         return y
     lib = library()
-    threshold = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices))))
+    threshold = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices)), f, DTYPES_16[x.dtype]))
     sliced, grouped = row_counts(crow, threshold, int(lib.as_spmm_rounded_16_group_degree(f)))
     # partial rows for the sliced rows only (a short workspace sums the rest
     # whole, with the same bits)
@@ -687,9 +687,11 @@ def row_counts(crow: torch.Tensor, long_from: int, short_below: int) -> tuple[in
     return _ROW_COUNT_MEMO.get((crow,), (long_from, short_below), compute)
 
 
-def sliced_rows(crow: torch.Tensor, column_slices: bool) -> int:
-    """Rows the column-sliced SpMM slices (degree >= its threshold)."""
-    return row_counts(crow, int(library().as_spmm_colslice_min_degree(int(bool(column_slices)))), 0)[0]
+def sliced_rows(crow: torch.Tensor, column_slices: bool, f: int, dtype: torch.dtype) -> int:
+    """Rows the column-sliced SpMM slices for F features of ``dtype``
+    (degree >= its threshold)."""
+    code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
+    return row_counts(crow, int(library().as_spmm_colslice_min_degree(int(bool(column_slices)), f, code)), 0)[0]
 
 
 def _maybe_validate(crow: torch.Tensor, col: torch.Tensor) -> None:

@@ -59,6 +59,14 @@ constexpr int kColsliceLongRow = 1024;     // slice length from which U = 16
 #define AS_COLSLICE_MIN_DEGREE 128
 #endif
 constexpr int64_t kColsliceMinDegree = AS_COLSLICE_MIN_DEGREE;
+// With fp32 rows of at most 64 features (256 bytes) a row's 8 partial rows
+// weigh twice as much against its gathers, and rows of 128-255 edges are
+// left whole: on the skewed 115M-edge benchmark graph at F = 64 that is
+// 1.92 ms against 2.00 (thresholds 192-320 all within 1 %); at F >= 128 the
+// same change costs 1-2 %.
+inline int64_t column_slice_degree(int64_t f, int64_t elem_bytes) {
+  return elem_bytes == 4 && f <= 64 ? 2 * kColsliceMinDegree : kColsliceMinDegree;
+}
 // With slices by edge count there is no cache gain, only the spread of long
 // rows over 8 waves.
 constexpr int64_t kEdgeSliceMinDegree = 1024;
@@ -951,7 +959,7 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
                         reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + capacity * row_bytes)};
 
-  const int64_t min_degree = slicing == kSliceColumns ? kColsliceMinDegree : kEdgeSliceMinDegree;
+  const int64_t min_degree = slicing == kSliceColumns ? column_slice_degree(f, E) : kEdgeSliceMinDegree;
   launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, off, s, slicing == kSliceEdges);
   // order: rows of degree >= min_degree (sliced) in 8 log2-degree buckets,
   // longest first; then the short rows, for 16-bit elements also in 8
@@ -1012,8 +1020,9 @@ size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f) {
   return as::colslice_fixed_bytes(n) + 2 * static_cast<size_t>(as::preferred_chunk_rows(n)) * as::colslice_row_bytes(f);
 }
 
-int64_t as_spmm_colslice_min_degree(int column_slices) {
-  return column_slices ? as::kColsliceMinDegree : as::kEdgeSliceMinDegree;
+int64_t as_spmm_colslice_min_degree(int column_slices, int64_t f, int dtype) {
+  if (!column_slices) return as::kEdgeSliceMinDegree;
+  return as::column_slice_degree(f, dtype == AS_DTYPE_F32 ? 4 : 2);
 }
 
 int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const float* val, const float* x, float* y,

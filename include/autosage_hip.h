@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 3
+#define AS_ABI_VERSION 4
 
 typedef enum as_status {
   AS_OK = 0,
@@ -152,9 +152,10 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col,
                              void* workspace, size_t workspace_bytes,
                              int64_t sliced_rows, void* stream);
 
-/* Degree from which rows are sliced: 128 for column slices
- * (column_slices != 0), 1024 for edge slices. */
-int64_t as_spmm_colslice_min_degree(int column_slices);
+/* Degree from which rows are sliced, for F features of type dtype
+ * (AS_DTYPE_*): with column slices (column_slices != 0) 256 for fp32 with
+ * F <= 64 and 128 otherwise; with edge slices 1024. */
+int64_t as_spmm_colslice_min_degree(int column_slices, int64_t f, int dtype);
 
 /* SpMM with bf16 or fp16 features, weights and output (dtype
  * AS_DTYPE_BF16 / AS_DTYPE_F16; val may be NULL).  The reference has no
@@ -177,7 +178,7 @@ int64_t as_spmm_colslice_min_degree(int column_slices);
  * summed several to a wavefront (a lane group each), the other rows one
  * wavefront each or sliced.
  * sliced_rows: as for as_spmm_csr_colslice_f32, with the degree
- * as_spmm_colslice_min_degree(column_slices); grouped_rows: the number of
+ * as_spmm_colslice_min_degree(column_slices, f, dtype); grouped_rows: the number of
  * rows of degree below as_spmm_rounded_16_group_degree(f), else -1.  Both
  * only size the launches; the result is the same for any values. */
 int as_spmm_csr_rounded_16(const int64_t* crow, const int64_t* col,

@@ -76,7 +76,10 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_last_error() == b"x, y and val must be 2-byte aligned"
     assert lib.as_spmm_csr_rounded_16(None, None, None, None, None, 4, 0, 8, 2, 0, None, 0, -1, -1, None) == 1
     assert lib.as_last_error() == b"null pointer argument"
-    assert lib.as_spmm_colslice_min_degree(1) == 128 and lib.as_spmm_colslice_min_degree(0) == 1024
+    # column slices from degree 256 for fp32 rows of at most 64 features, else 128; edge slices from 1024
+    assert [lib.as_spmm_colslice_min_degree(1, f, 0) for f in (1, 64, 65, 128)] == [256, 256, 128, 128]
+    assert [lib.as_spmm_colslice_min_degree(1, f, 1) for f in (8, 64, 128)] == [128, 128, 128]
+    assert lib.as_spmm_colslice_min_degree(0, 64, 0) == 1024 and lib.as_spmm_colslice_min_degree(0, 128, 2) == 1024
     # 16-bit SpMM, rows whole
     assert lib.as_spmm_csr_rows_16(None, None, None, None, None, 4, 0, 8, 3, None) == 1
     assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"

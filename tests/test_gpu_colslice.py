@@ -257,8 +257,8 @@ def test_sliced_rows_hint_only_sizes_the_launches():
     d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
     n, f = x.shape
     lib = _native.library()
-    exact = _native.sliced_rows(d_crow, True)
-    assert exact == int((np.diff(crow) >= lib.as_spmm_colslice_min_degree(1)).sum()) and exact >= 40
+    exact = _native.sliced_rows(d_crow, True, f, torch.float32)
+    assert exact == int((np.diff(crow) >= lib.as_spmm_colslice_min_degree(1, f, 0)).sum()) and exact >= 40
     ws = torch.empty(lib.as_spmm_colslice_workspace_bytes(n, f), dtype=torch.uint8, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     outs = []
@@ -277,7 +277,7 @@ def test_sliced_rows_hint_only_sizes_the_launches():
     limit = lib.as_spmm_rounded_16_group_degree(f)
     assert limit == 64
     for column_slices in (1, 0):
-        sliced, grouped = _native.row_counts(d_crow, lib.as_spmm_colslice_min_degree(column_slices), limit)
+        sliced, grouped = _native.row_counts(d_crow, lib.as_spmm_colslice_min_degree(column_slices, f, 1), limit)
         assert grouped == int((np.diff(crow) < limit).sum()) and 0 < grouped < n
         outs = []
         for hints in ((-1, -1), (0, 0), (sliced, grouped), (sliced + 500, n), (sliced, 0), (1, 3 * n), (-1, grouped)):
