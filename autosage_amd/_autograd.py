@@ -18,7 +18,9 @@ backward formulas built from the same native kernels:
 * ``p = softmax_row(s)``: ``ds = p·(dp − Σ_row dp·p)`` (native kernel).
 * the fused attention ``out = softmax_row(scale·s)·V``: the scores and
   probabilities are recomputed with the native ops and the three formulas
-  above are chained (``dV = Pᵀ·dOut``).
+  above are chained (``dV = Pᵀ·dOut``); the column-sliced attention (float32)
+  takes two native gather passes instead (``as_csr_attention_backward_f32``),
+  with no nnz-sized intermediate.
 
 The transposed CSR (rows of Aᵀ list the source rows in ascending order, a
 stable sort of the edges by column) is built with torch ops and memoised per
@@ -153,7 +155,7 @@ def _softmax_backward(ctx, grad_p: torch.Tensor):
 
 def _attention_setup(ctx, inputs, output) -> None:
     crow, col, query, key, value = inputs[:5]
-    ctx.save_for_backward(crow, col, query, key, value)
+    ctx.save_for_backward(crow, col, query, key, value, output)
     ctx.scale = float(inputs[5])
     ctx.sliced = False
 
@@ -164,14 +166,36 @@ def _attention_sliced_setup(ctx, inputs, output) -> None:
 
 
 def _attention_backward(ctx, grad_out: torch.Tensor):
-    """out = P·V with P = softmax_row(scale·SDDMM(Q, K)): the scores and P
-    are recomputed with the native ops, then
+    """out = P·V with P = softmax_row(scale·SDDMM(Q, K)).
+
+    The column-sliced op (float32, column slices allowed) takes the two-pass
+    native backward: pass 1 over the rows of A recomputes the scores with an
+    online maximum and sum and writes dQ and the row log-sum-exp; pass 2 over
+    the rows of Aᵀ writes dK and dV; t_r = <dOut[r], out[r]> comes from the
+    saved output.  Otherwise (the exact fused op, 16-bit inputs, column
+    slices off) the scores and P are recomputed with the native ops, then
     dV = Pᵀ·dOut, dP[e] = <dOut[row(e)], V[col(e)]>, dS = softmax'(P, dP)·scale,
     dQ = A_dS·K, dK = A_dSᵀ·Q (native SpMM / SDDMM / softmax backward)."""
-    from ._native import csr_row_softmax_backward_impl
+    from ._native import (
+        attention_backward_supported,
+        csr_attention_backward_impl,
+        csr_row_softmax_backward_impl,
+        row_sorted,
+    )
 
-    crow, col, query, key, value = ctx.saved_tensors
+    crow, col, query, key, value, out = ctx.saved_tensors
     grad_out = grad_out.contiguous()
+    if ctx.sliced and _column_slices_allowed() and attention_backward_supported(query, key, value, out, grad_out):
+        # the column-sliced op: two gather passes (over A, then over Aᵀ) with
+        # the row log-sum-exp of the first feeding the second; no scores,
+        # probabilities or their gradients in memory
+        col_s = row_sorted(crow, col)[0]
+        crow_t, col_t, _ = csr_transpose(crow, col_s)
+        grad_q, grad_k, grad_v = csr_attention_backward_impl(crow, col_s, crow_t, col_t, query, key, value, out,
+                                                             grad_out, ctx.scale)
+        needs = ctx.needs_input_grad
+        return (None, None, grad_q if needs[2] else None, grad_k if needs[3] else None,
+                grad_v if needs[4] else None, None)
     scores = _sddmm(crow, col, query, key)
     if ctx.scale != 1.0:
         scores = scores * ctx.scale

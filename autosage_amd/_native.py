@@ -93,6 +93,12 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_int,
          _c_ptr, _c_size, _c_ptr],
     ),
+    "as_csr_attention_backward_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "as_csr_attention_backward_f32": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64,
+         _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_size, _c_ptr],
+    ),
     "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "as_induced_sample_workspace_bytes": (_c_size, [_c_i64]),
     "as_induced_sample_count": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
@@ -575,6 +581,40 @@ def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
             )
     _raise(status, "autosage::csr_attention_colslice")
     return out
+
+
+def attention_backward_supported(query, key, value, out, grad_out) -> bool:
+    """Shapes the two-pass attention backward handles: float32, F_qk and F_v
+    multiples of 4 in [4, 256], 16-byte aligned dense tensors."""
+    fqk, fv = query.size(1), value.size(1)
+    tensors = (query, key, value, out, grad_out)
+    return (all(t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0 for t in tensors)
+            and fqk % 4 == 0 and 4 <= fqk <= 256 and fv % 4 == 0 and 4 <= fv <= 256)
+
+
+def csr_attention_backward_impl(crow, col, crow_t, col_t, query, key, value, out, grad_out, scale):
+    """(grad_q, grad_k, grad_v) of the attention from its saved inputs, its
+    output and dL/dout, in two native gather passes (over A and over its
+    transpose (crow_t, col_t))."""
+    n, fqk = query.shape
+    fv = value.size(1)
+    nnz = col.numel()
+    grad_q = torch.empty_like(query)
+    grad_k = torch.empty_like(key)
+    grad_v = torch.empty_like(value)
+    if n == 0:
+        return grad_q, grad_k, grad_v
+    lib = library()
+    ws = _workspace(min(lib.as_csr_attention_backward_workspace_bytes(n, nnz, fqk, fv), _colslice_workspace_cap()),
+                    query.device)
+    with torch.cuda.device(query.device):
+        status = lib.as_csr_attention_backward_f32(
+            _ptr(crow), _ptr(col), _ptr(crow_t), _ptr(col_t), _ptr(query), _ptr(key), _ptr(value), _ptr(out),
+            _ptr(grad_out), _ptr(grad_q), _ptr(grad_k), _ptr(grad_v), n, nnz, fqk, fv, float(scale), _ptr(ws),
+            ws.numel(), _stream(query.device),
+        )
+    _raise(status, "autosage::csr_attention (backward)")
+    return grad_q, grad_k, grad_v
 
 
 _VALIDATION_RULES = (

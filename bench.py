@@ -342,7 +342,8 @@ def main() -> int:
                         help="feature type of the SpMM workloads (cfg1-3, er), the SDDMM one (cfg4) and the "
                              "attention (cfg5); bf16/fp16 run the rounded 16-bit kernels")
     parser.add_argument("--backward", action="store_true",
-                        help="SpMM fp32: time forward + dX backward (flops and bytes of both products)")
+                        help="SpMM fp32: time forward + dX backward (flops and bytes of both products); cfg5: the "
+                             "attention forward + dQ, dK, dV")
     parser.add_argument("--hub-degree", type=int, default=12_000, help="hubsweep: degree of row 0")
     parser.add_argument("--other-degree", type=int, default=32, help="hubsweep: degree of every other row")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -873,15 +874,30 @@ def bench_other(args, device) -> dict:
             _, info = csr_attention_forward(crow, col, q, k, v, scale=0.125)
             chosen = info.get("variant", "stages")
             step = lambda: csr_attention_forward(crow, col, q, k, v, scale=0.125)[0]  # noqa: E731
+        passes = 1
+        if args.backward:
+            # one training step of the attention: the forward, then dQ, dK and
+            # dV through the op's backward (memoised transposed CSR, built in
+            # the warmup); flops and bytes count the forward's products twice
+            q, k, v = (t.detach().requires_grad_(True) for t in (q, k, v))
+            grad_out = torch.randn(w.rows, 128, device=device, dtype=dt)
+            forward = step
+
+            def step():
+                q.grad = k.grad = v.grad = None
+                forward().backward(grad_out)
+
+            passes = 2
+            chosen += " forward+backward"
         log(f"calibration (ms): {calib}; chosen {chosen}")
         ms, samples = time_steps(step, args.steps, args.warmup)
-        flops = 2.0 * w.nnz * (64 + 128)
-        algo = attention_bytes(w.rows, w.nnz, 64, 128, elem=q.element_size())
-        compulsory = attention_compulsory_bytes(w.rows, w.nnz, 64, 128, elem=q.element_size())
-        ref_numerator = (w.nnz + w.rows) * (64 + 128) * q.element_size()
+        flops = 2.0 * w.nnz * (64 + 128) * passes
+        algo = attention_bytes(w.rows, w.nnz, 64, 128, elem=q.element_size()) * passes
+        compulsory = attention_compulsory_bytes(w.rows, w.nnz, 64, 128, elem=q.element_size()) * passes
+        ref_numerator = (w.nnz + w.rows) * (64 + 128) * q.element_size() * passes
         type_name = {"f32": "fp32", "bf16": "bf16", "fp16": "fp16"}[args.dtype]
-        name = f"cfg5 CSR attention {type_name} Fqk=64 Fv=128 scale=1/8"
-        cpu = None if args.no_cpu_baseline else cpu_baseline_attention(w)
+        name = f"cfg5 CSR attention {type_name} Fqk=64 Fv=128 scale=1/8" + (" forward+backward" if args.backward else "")
+        cpu = None if args.no_cpu_baseline or args.backward else cpu_baseline_attention(w)
         if cpu is not None and dt != torch.float32:
             cpu["sample"] += "; fp32 (the reference's CPU composition in fp32)"
     traffic = profiled_traffic(name, chosen)

@@ -333,6 +333,31 @@ int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col,
                                  float scale, int dtype, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace for as_csr_attention_backward_f32. */
+size_t as_csr_attention_backward_workspace_bytes(int64_t n, int64_t nnz,
+                                                 int64_t f_qk, int64_t f_v);
+
+/* Gradients of out = softmax_row(scale · SDDMM(query, key)) · value (the
+ * attention of as_csr_attention_colslice_f32) in two gather passes, fp32:
+ * pass 1 over the rows of A (crow, col) recomputes the scores with an online
+ * maximum and sum and writes grad_q and the row log-sum-exp; pass 2 over the
+ * rows of the transposed graph (crow_t, col_t: the columns of A, sources
+ * ascending) writes grad_k and grad_v.  out is the forward result, grad_out
+ * dL/dout.  No reference counterpart: the reference registers no autograd
+ * and differentiates its torch composition (autosage/_auto.py:762-780).
+ * f_qk and f_v multiples of 4 in [4, 256]; all dense tensors 16-byte aligned;
+ * columns ascending within the rows of both graphs; a workspace smaller
+ * than the preferred size runs the sliced rows in more chunks. */
+int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col,
+                                  const int64_t* crow_t, const int64_t* col_t,
+                                  const float* query, const float* key,
+                                  const float* value, const float* out,
+                                  const float* grad_out, float* grad_q,
+                                  float* grad_k, float* grad_v, int64_t n,
+                                  int64_t nnz, int64_t f_qk, int64_t f_v,
+                                  float scale, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace for the induced-sample entry points (n int32). */
 size_t as_induced_sample_workspace_bytes(int64_t n);
 

@@ -125,3 +125,74 @@ def test_colslice_attention_backward_schedules(monkeypatch):
     assert all(torch.equal(a, b) for a, b in zip(off, fused))
     for a, b in zip(sliced, fused):
         assert torch.max(torch.abs(a - b)) <= 2e-5 * torch.max(torch.abs(b))
+
+
+@pytest.mark.parametrize("fqk, fv", [(64, 128), (32, 48), (128, 128), (256, 64), (4, 8)])
+def test_two_pass_attention_backward(fqk, fv):
+    """The column-sliced op's backward runs the two native passes: on a graph
+    with out- and in-degree hubs (both passes slice rows), empty rows and
+    columns out of order, every gradient is within 2e-5 of the fp64 autograd
+    gradients (max-norm) and of the recomputing chain (column slices off)."""
+    n = 2500
+    h_crow, h_col = case_graph(n, 9, seed=fqk + fv, hubs=3, hub_degree=1800, empty=0.05)
+    # A = H ∪ Hᵀ: symmetric, so its hubs are also hubs of Aᵀ
+    rows = np.concatenate([np.repeat(np.arange(n), np.diff(h_crow)), h_col])
+    cols = np.concatenate([h_col, np.repeat(np.arange(n), np.diff(h_crow))])
+    keys = np.unique(rows * n + cols)
+    r, c = keys // n, keys % n
+    crow = np.concatenate([[0], np.cumsum(np.bincount(r, minlength=n))]).astype(np.int64)
+    # columns out of order inside every row (the op sorts a copy)
+    rng = np.random.default_rng(fqk)
+    perm = np.concatenate([rng.permutation(np.arange(crow[i], crow[i + 1])) for i in range(n)])
+    col = c[perm].astype(np.int64)
+    assert np.diff(crow).max() >= 1800  # symmetric: the hubs are in- and out-degree hubs
+    q = (rng.standard_normal((n, fqk)) * 0.25).astype(np.float32)
+    k = (rng.standard_normal((n, fqk)) * 0.25).astype(np.float32)
+    v = rng.standard_normal((n, fv)).astype(np.float32)
+    g = rng.standard_normal((n, fv)).astype(np.float32)
+    d_crow, d_col = to_dev(crow, col)
+    leaves = [torch.from_numpy(a).cuda().requires_grad_(True) for a in (q, k, v)]
+    out = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *leaves, 0.125)
+    out.backward(torch.from_numpy(g).cuda())
+    ref, ref_leaves = _attention_fp64(crow, col, q, k, v, 0.125)
+    ref.backward(torch.from_numpy(g).double())
+    for got, leaf in zip(leaves, ref_leaves):
+        want = leaf.grad.numpy()
+        err = np.max(np.abs(got.grad.cpu().numpy() - want))
+        assert err <= 2e-5 * np.max(np.abs(want)), (err, np.max(np.abs(want)))
+    # deterministic
+    again = [torch.from_numpy(a).cuda().requires_grad_(True) for a in (q, k, v)]
+    torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *again, 0.125).backward(torch.from_numpy(g).cuda())
+    assert all(torch.equal(a.grad, b.grad) for a, b in zip(leaves, again))
+
+
+def test_two_pass_attention_backward_rows_without_edges_and_chunks(monkeypatch):
+    """Rows and columns without edges get zero gradients; a small workspace
+    (partial states for a few sliced rows) runs the sliced rows in chunks
+    with the same bits."""
+    n = 3000
+    crow, col = case_graph(n, 7, seed=4, hubs=30, hub_degree=900, empty=0.2)
+    col = col * (n - 100) // n  # columns n - 100 .. n - 1 get no edge (order kept, repeats allowed)
+    rng = np.random.default_rng(5)
+    arrays = [(rng.standard_normal((n, f)) * 0.25).astype(np.float32) for f in (64, 64, 128)]
+    g = torch.from_numpy(rng.standard_normal((n, 128)).astype(np.float32)).cuda()
+    d_crow, d_col = to_dev(crow, col)
+
+    def grads():
+        leaves = [torch.from_numpy(a).cuda().requires_grad_(True) for a in arrays]
+        torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *leaves, 0.125).backward(g)
+        return [leaf.grad for leaf in leaves]
+
+    first = grads()
+    empty_rows = torch.from_numpy(np.diff(crow) == 0).cuda()
+    assert torch.count_nonzero(first[0][empty_rows]).item() == 0
+    unused = torch.from_numpy(np.bincount(col, minlength=n) == 0).cuda()
+    assert unused.any() and torch.count_nonzero(first[1][unused]).item() == 0
+    assert torch.count_nonzero(first[2][unused]).item() == 0
+    from autosage_amd import _native
+
+    lib = _native.library()
+    fixed = lib.as_csr_attention_backward_workspace_bytes(n, 0, 64, 128) - 8 * (64 + 128) * 4 - 768
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((fixed + 3 * 8 * (64 + 128) * 4 + 768) / 2**20))
+    chunked = grads()
+    assert all(torch.equal(a, b) for a, b in zip(first, chunked))
