@@ -27,7 +27,7 @@ import torch
 from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
 # 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
@@ -67,6 +67,18 @@ _SIGNATURES = {
         _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_i64, _c_ptr]
     ),
     "as_spmm_colslice_min_degree": (_c_i64, [_c_int, _c_i64, _c_int]),
+    "as_spmm_colslice_plan_bytes": (_c_size, [_c_i64]),
+    "as_spmm_colslice_plan": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, ctypes.POINTER(ctypes.c_int64),
+         _c_ptr],
+    ),
+    "as_spmm_colslice_planned_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int, _c_i64]),
+    "as_spmm_csr_colslice_planned": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_i64,
+         _c_ptr, _c_size, _c_i64, _c_i64, _c_ptr],
+    ),
     "as_spmm_csr_rounded_16": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_i64,
@@ -297,6 +309,9 @@ def spmm_csr_colslice_impl(crow, col, val, x):
     if n == 0 or f == 0:
         return y
     lib = library()
+    if colslice_plans_enabled():
+        return _spmm_colslice_planned(crow, col, val, x, y, column_slices=True, sliced=sliced_rows(crow, True, f, x.dtype),
+                                      grouped=0)
     # the preferred size (two partial buffers of a quarter of the rows); a
     # smaller cap runs the pipeline in more, smaller chunks
     full = lib.as_spmm_colslice_workspace_bytes(n, f)
@@ -307,6 +322,64 @@ def spmm_csr_colslice_impl(crow, col, val, x):
             sliced_rows(crow, True, f, x.dtype), _stream(x.device),
         )
     _raise(status, "autosage::spmm_csr_colslice")
+    return y
+
+
+def colslice_plans_enabled() -> bool:
+    """Whether the column-sliced SpMM reuses a per-graph plan (slice points
+    and binned row order) across calls; ``AUTOSAGE_COLSLICE_PLAN=off`` builds
+    them on every call instead (same bits)."""
+    return os.getenv("AUTOSAGE_COLSLICE_PLAN", "on").lower() != "off"
+
+
+# A plan holds about 28 bytes per row (6.5 MB for a 233k-row graph).
+_PLAN_MEMO = GraphMemo("colslice_plan", max_entries=32, max_bytes=1 << 30)
+
+
+def colslice_plan(crow: torch.Tensor, col: torch.Tensor, f: int, dtype: torch.dtype,
+                  column_slices: bool) -> tuple[torch.Tensor, int]:
+    """(plan, tag) of the column-sliced SpMM for this graph (columns ascending
+    within rows for column slices), F and element type: the slice points and
+    the degree-binned row order, built on the device once per live,
+    unmodified (crow, col) pair and settings, then reused by every call
+    whatever X.  The build synchronises the stream once, so that a later
+    call on another stream finds the plan complete."""
+    lib = library()
+    code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
+    degree = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices)), f, code))
+
+    def compute() -> tuple[torch.Tensor, int]:
+        n = crow.numel() - 1
+        plan = _workspace(lib.as_spmm_colslice_plan_bytes(n), crow.device)
+        tag = ctypes.c_int64(0)
+        with torch.cuda.device(crow.device):
+            status = lib.as_spmm_colslice_plan(_ptr(crow), _ptr(col), n, col.numel(), f, code, int(bool(column_slices)),
+                                               _ptr(plan), plan.numel(), ctypes.byref(tag), _stream(crow.device))
+            _raise(status, "autosage column-sliced plan")
+            torch.cuda.current_stream(crow.device).synchronize()
+        return plan, int(tag.value)
+
+    # the plan depends on the slicing degree and on fp32 against 16-bit (the
+    # number of light buckets), not on F itself
+    return _PLAN_MEMO.get((crow, col), (degree, code != 0, bool(column_slices)), compute)
+
+
+def _spmm_colslice_planned(crow, col, val, x, y, column_slices: bool, sliced: int, grouped: int):
+    """The column-sliced SpMM on its per-graph plan: the workspace holds the
+    partial buffers only (the workspace cap counts the plan, as in the
+    unplanned call)."""
+    n, f = x.shape
+    code = 0 if x.dtype == torch.float32 else DTYPES_16[x.dtype]
+    lib = library()
+    plan, tag = colslice_plan(crow, col, f, x.dtype, column_slices)
+    needed = lib.as_spmm_colslice_planned_workspace_bytes(n, f, code, sliced)
+    ws = _workspace(max(min(needed, _colslice_workspace_cap() - plan.numel()), 0), x.device)
+    with torch.cuda.device(x.device):
+        status = lib.as_spmm_csr_colslice_planned(
+            _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, code, int(column_slices),
+            _ptr(plan), plan.numel(), tag, _ptr(ws), ws.numel(), sliced, grouped, _stream(x.device),
+        )
+    _raise(status, "autosage::spmm_csr_colslice" if code == 0 else "autosage::spmm_csr (16-bit)")
     return y
 
 
@@ -348,6 +421,8 @@ def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
     lib = library()
     threshold = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices)), f, DTYPES_16[x.dtype]))
     sliced, grouped = row_counts(crow, threshold, int(lib.as_spmm_rounded_16_group_degree(f)))
+    if colslice_plans_enabled():
+        return _spmm_colslice_planned(crow, col, val, x, y, bool(column_slices), sliced, grouped)
     # partial rows for the sliced rows only (a short workspace sums the rest
     # whole, with the same bits)
     needed = lib.as_spmm_rounded_16_workspace_bytes(n, f, sliced)

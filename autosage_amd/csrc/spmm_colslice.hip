@@ -898,19 +898,62 @@ inline int64_t grouped_degree(int64_t f, int64_t elem_bytes) {
   return kGroupedMaxBlocks * g;
 }
 
+// The per-graph part of a column-sliced call: slice points and the binned
+// row order.  A plan depends on the graph, the slicing degree and the number
+// of light buckets (and on nothing of X): `plan_tag` packs the last two, so
+// that an execution can check it was given a plan for its own settings.
+struct PlanView {
+  int32_t* off;
+  int32_t* order;
+  int32_t* counts;
+  void* bin_ws;
+};
+
+inline PlanView plan_view(void* base, int64_t n) {
+  char* p = static_cast<char*>(base);
+  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
+  PlanView v;
+  v.off = reinterpret_cast<int32_t*>(p);
+  p += align_up(rows * kSpmmBounds * sizeof(int32_t), 256);
+  v.order = reinterpret_cast<int32_t*>(p);
+  p += align_up(rows * sizeof(int32_t), 256);
+  v.counts = reinterpret_cast<int32_t*>(p);
+  p += 256;
+  v.bin_ws = p;
+  return v;
+}
+
+inline int64_t slicing_degree(Slicing slicing, int64_t f, int64_t elem_bytes) {
+  return slicing == kSliceColumns ? column_slice_degree(f, elem_bytes) : kEdgeSliceMinDegree;
+}
+
+// rows of degree >= the slicing degree in 8 log2-degree buckets, longest
+// first; then the short rows, for 16-bit elements also in 8 log2-degree
+// buckets (a wave of grouped short rows then holds rows of similar degree)
+inline int light_bucket_count(int64_t elem_bytes) { return elem_bytes == 2 ? kMaxHeavyBuckets : 1; }
+
+inline int64_t plan_tag_of(int64_t min_degree, int light_buckets) {
+  return (int64_t(1) << 48) | (static_cast<int64_t>(light_buckets) << 32) | min_degree;
+}
+
+inline int build_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree, int light_buckets,
+                      Slicing slicing, const PlanView& plan, hipStream_t s) {
+  launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, plan.off, s, slicing == kSliceEdges);
+  return launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, light_buckets, plan.order, plan.counts, plan.bin_ws,
+                         s);
+}
+
+// `plan`: built by build_plan for this graph, min_degree and light bucket
+// count (the caller's duty); the workspace holds the partial buffers only.
 template <typename T>
-int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
-                 int64_t nnz, int64_t f, Slicing slicing, void* workspace, size_t workspace_bytes,
-                 int64_t sliced_rows, int64_t grouped_rows, void* stream) {
-  int st = validate_spmm(crow, col, x, y, n, nnz, f);
-  if (st != AS_OK) return st;
-  if (n == 0 || f == 0) return AS_OK;
-  const size_t fixed = colslice_fixed_bytes(n);
+int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
+                     int64_t f, int64_t min_degree, const PlanView& plan, void* partials, size_t partial_bytes,
+                     int64_t sliced_rows, int64_t grouped_rows, hipStream_t s) {
   const size_t row_bytes = colslice_row_bytes(f);
-  if (workspace == nullptr || workspace_bytes < fixed + 2 * row_bytes)
-    return fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu workspace bytes, got %zu",
-                fixed + 2 * row_bytes, workspace_bytes);
-  if (!aligned(workspace, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  if (partials == nullptr || partial_bytes < 2 * row_bytes)
+    return fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu bytes of partial buffers, got %zu",
+                2 * row_bytes, partial_bytes);
+  if (!aligned(partials, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   constexpr int64_t E = static_cast<int64_t>(sizeof(T));
   constexpr int64_t P = 16 / E;  // elements per 16-byte lane
 
@@ -936,7 +979,7 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   // row of a chunk has partial rows.  16-bit: chunks of the preferred size
   // whatever the workspace; sliced rows past the capacity are summed whole,
   // with the same bits, so a workspace sized for the sliced rows suffices.
-  const int64_t fits = static_cast<int64_t>((workspace_bytes - fixed) / (2 * row_bytes));
+  const int64_t fits = static_cast<int64_t>(partial_bytes / (2 * row_bytes));
   int64_t chunk = preferred_chunk_rows(n);
   if (E == 4 && chunk > fits) chunk = fits;
   // blocks of a launch: 8 per group, at most tiles·(P·ceil(c/4) + ceil(c/32))
@@ -945,46 +988,26 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   if (chunk > max_rows) chunk = max_rows;
   if (chunk < 1) return fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
   const int64_t capacity = fits < chunk ? fits : chunk;
-
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const size_t rows = static_cast<size_t>(n);
-  int32_t* off = reinterpret_cast<int32_t*>(ws);
-  ws += align_up(rows * kSpmmBounds * sizeof(int32_t), 256);
-  int32_t* order = reinterpret_cast<int32_t*>(ws);
-  ws += align_up(rows * sizeof(int32_t), 256);
-  int32_t* counts = reinterpret_cast<int32_t*>(ws);
-  ws += 256;
-  void* bin_ws = ws;
-  double* buffers[2] = {reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed),
-                        reinterpret_cast<double*>(static_cast<char*>(workspace) + fixed + capacity * row_bytes)};
-
-  const int64_t min_degree = slicing == kSliceColumns ? column_slice_degree(f, E) : kEdgeSliceMinDegree;
-  launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, off, s, slicing == kSliceEdges);
-  // order: rows of degree >= min_degree (sliced) in 8 log2-degree buckets,
-  // longest first; then the short rows, for 16-bit elements also in 8
-  // log2-degree buckets (a wave of grouped short rows then holds rows of
-  // similar degree)
-  const int light_buckets = E == 2 ? kMaxHeavyBuckets : 1;
-  st = launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, light_buckets, order, counts, bin_ws, s);
-  if (st != AS_OK) return st;
+  double* buffers[2] = {static_cast<double*>(partials),
+                        reinterpret_cast<double*>(static_cast<char*>(partials) + capacity * row_bytes)};
 
   // grouped short rows: the light buckets from level L on, L the first whose
   // rows all have degree below the limit (light bucket L holds degrees up to
   // (min_degree - 1) >> L, and bucket L - 1 none below min_degree >> L; both
   // are powers of two, so these are exactly the rows below the limit)
+  const int light_buckets = light_bucket_count(E);
   GroupedRows grouped{nullptr};
   const int64_t limit = v >= 8 ? grouped_degree(f, E) : 0;
   if (limit > 0) {
     int level = 0;
     while (level < light_buckets && ((min_degree - 1) >> level) >= limit) ++level;
-    if (level < light_buckets) grouped.start = bin_bucket_start(bin_ws, n, kMaxHeavyBuckets + level);
+    if (level < light_buckets) grouped.start = bin_bucket_start(plan.bin_ws, n, kMaxHeavyBuckets + level);
   }
   const int64_t rows_per_wave = grouped.start != nullptr ? kWave / v : 1;
   if (grouped.start == nullptr) grouped_rows = 0;
 
   // launch k: slice work of chunk k beside the reduction of chunk k - 1
-  const StepArgs a{crow, col, val, x, y, f, order, counts, off, grouped};
+  const StepArgs a{crow, col, val, x, y, f, plan.order, plan.counts, plan.off, grouped};
   const int64_t chunks = (n + chunk - 1) / chunk;
   SliceChunk previous{0, 0, buffers[1], 1, 1, -1};
   for (int64_t k = 0; k <= chunks; ++k) {
@@ -1008,6 +1031,34 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   return AS_OK;
 }
 
+// One call with its plan built in the workspace's first colslice_fixed_bytes(n).
+template <typename T>
+int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
+                 int64_t nnz, int64_t f, Slicing slicing, void* workspace, size_t workspace_bytes,
+                 int64_t sliced_rows, int64_t grouped_rows, void* stream) {
+  int st = validate_spmm(crow, col, x, y, n, nnz, f);
+  if (st != AS_OK) return st;
+  if (n == 0 || f == 0) return AS_OK;
+  const size_t fixed = colslice_fixed_bytes(n);
+  const size_t row_bytes = colslice_row_bytes(f);
+  if (workspace == nullptr || workspace_bytes < fixed + 2 * row_bytes)
+    return fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu workspace bytes, got %zu",
+                fixed + 2 * row_bytes, workspace_bytes);
+  if (!aligned(workspace, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  constexpr int64_t E = static_cast<int64_t>(sizeof(T));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const PlanView plan = plan_view(workspace, n);
+  const int64_t min_degree = slicing_degree(slicing, f, E);
+  st = build_plan(crow, col, n, min_degree, light_bucket_count(E), slicing, plan, s);
+  if (st != AS_OK) return st;
+  return colslice_execute<T>(crow, col, val, x, y, n, f, min_degree, plan, static_cast<char*>(workspace) + fixed,
+                             workspace_bytes - fixed, sliced_rows, grouped_rows, s);
+}
+
+inline int elem_bytes_of(int dtype) {
+  return dtype == AS_DTYPE_F32 ? 4 : (dtype == AS_DTYPE_BF16 || dtype == AS_DTYPE_F16 ? 2 : 0);
+}
+
 }  // namespace
 
 }  // namespace as
@@ -1023,6 +1074,81 @@ size_t as_spmm_colslice_workspace_bytes(int64_t n, int64_t f) {
 int64_t as_spmm_colslice_min_degree(int column_slices, int64_t f, int dtype) {
   if (!column_slices) return as::kEdgeSliceMinDegree;
   return as::column_slice_degree(f, dtype == AS_DTYPE_F32 ? 4 : 2);
+}
+
+size_t as_spmm_colslice_plan_bytes(int64_t n) { return as::colslice_fixed_bytes(n); }
+
+int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t nnz, int64_t f, int dtype,
+                          int column_slices, void* plan, size_t plan_bytes, int64_t* plan_tag, void* stream) {
+  as::clear_error();
+  const int64_t e = as::elem_bytes_of(dtype);
+  if (e == 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (e == 4 && !column_slices)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "float32 features take column slices only (column_slices != 0)");
+  if (plan_tag == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "plan_tag must not be NULL");
+  if (n < 0 || nnz < 0 || f < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "n, nnz and f must be non-negative");
+  if (n > 0 && (crow == nullptr || (nnz > 0 && col == nullptr)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "crow and col must not be NULL");
+  if (plan == nullptr || plan_bytes < as::colslice_fixed_bytes(n))
+    return as::fail(AS_ERR_WORKSPACE, "a column-sliced plan needs %zu bytes, got %zu", as::colslice_fixed_bytes(n),
+                    plan_bytes);
+  if (!as::aligned(plan, 256)) return as::fail(AS_ERR_WORKSPACE, "the plan must be 256-byte aligned");
+  const as::Slicing slicing = column_slices ? as::kSliceColumns : as::kSliceEdges;
+  const int64_t min_degree = as::slicing_degree(slicing, f, e);
+  const int light = as::light_bucket_count(e);
+  *plan_tag = as::plan_tag_of(min_degree, light);
+  if (n == 0) return AS_OK;
+  const int st = as::build_plan(crow, col, n, min_degree, light, slicing, as::plan_view(plan, n),
+                                static_cast<hipStream_t>(stream));
+  if (st != AS_OK) return st;
+  return as::check_launch("spmm_colslice_plan");
+}
+
+size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype, int64_t sliced_rows) {
+  if (n < 0) n = 0;
+  if (f < 1) f = 1;
+  int64_t rows = as::preferred_chunk_rows(n);
+  if (dtype != AS_DTYPE_F32 && sliced_rows >= 0 && sliced_rows < rows) rows = sliced_rows > 0 ? sliced_rows : 1;
+  return 2 * static_cast<size_t>(rows) * as::colslice_row_bytes(f);
+}
+
+int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
+                                 int64_t n, int64_t nnz, int64_t f, int dtype, int column_slices, const void* plan,
+                                 size_t plan_bytes, int64_t plan_tag, void* workspace, size_t workspace_bytes,
+                                 int64_t sliced_rows, int64_t grouped_rows, void* stream) {
+  as::clear_error();
+  const int64_t e = as::elem_bytes_of(dtype);
+  if (e == 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (e == 4 && !column_slices)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "float32 features take column slices only (column_slices != 0)");
+  if (!as::aligned(x, e) || !as::aligned(y, e) || (val != nullptr && !as::aligned(val, e)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "x, y and val must be aligned to their element size");
+  int st = as::validate_spmm(crow, col, x, y, n, nnz, f);
+  if (st != AS_OK) return st;
+  if (n == 0 || f == 0) return AS_OK;
+  const as::Slicing slicing = column_slices ? as::kSliceColumns : as::kSliceEdges;
+  const int64_t min_degree = as::slicing_degree(slicing, f, e);
+  if (plan_tag != as::plan_tag_of(min_degree, as::light_bucket_count(e)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT,
+                    "the plan was built for other settings (plan tag %lld, these F, dtype and slicing need %lld)",
+                    (long long)plan_tag, (long long)as::plan_tag_of(min_degree, as::light_bucket_count(e)));
+  if (plan == nullptr || plan_bytes < as::colslice_fixed_bytes(n))
+    return as::fail(AS_ERR_WORKSPACE, "a column-sliced plan needs %zu bytes, got %zu", as::colslice_fixed_bytes(n),
+                    plan_bytes);
+  if (!as::aligned(plan, 256)) return as::fail(AS_ERR_WORKSPACE, "the plan must be 256-byte aligned");
+  const as::PlanView view = as::plan_view(const_cast<void*>(plan), n);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == AS_DTYPE_F32)
+    st = as::colslice_execute<float>(crow, col, val, x, y, n, f, min_degree, view, workspace, workspace_bytes,
+                                     sliced_rows, 0, s);
+  else if (dtype == AS_DTYPE_BF16)
+    st = as::colslice_execute<as::Bf16>(crow, col, val, x, y, n, f, min_degree, view, workspace, workspace_bytes,
+                                        sliced_rows, grouped_rows, s);
+  else
+    st = as::colslice_execute<as::Fp16>(crow, col, val, x, y, n, f, min_degree, view, workspace, workspace_bytes,
+                                        sliced_rows, grouped_rows, s);
+  if (st != AS_OK) return st;
+  return as::check_launch("spmm_csr_colslice_planned");
 }
 
 int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const float* val, const float* x, float* y,

@@ -16,6 +16,7 @@ builder's own measurements.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -541,6 +542,8 @@ def bench_spmm(args, device) -> dict:
         "graph_fingerprint": w.fingerprint(),
         "degree_stats": stats,
     }
+    if chosen == "colslice" or (half and chosen in ("rounded16:edges", "rounded16:columns")):
+        config["plan"] = plan_record(step, args, crow, col, f, x.dtype, chosen != "rounded16:edges", ms)
     if args.workload == "cfg3":
         config["tail_note"] = (
             f"{stats['frac_deg_gt_2000'] * 100:.2f} % of rows have degree > 2,000, not the spec's ~2 %: a truncated "
@@ -599,6 +602,45 @@ def bench_spmm(args, device) -> dict:
     else:
         result["cpu_baseline"] = None
     return result
+
+
+def plan_record(step, args, crow, col, f, dtype, column_slices: bool, ms: float) -> dict:
+    """What the column-sliced SpMM keeps per graph: its plan (slice points and
+    the degree-binned row order) is built once per graph and reused by every
+    call.  Records the build time (median of 5, HIP events on the launch
+    stream) and the step time with the plan rebuilt in every call."""
+    from autosage_amd import _native
+
+    if not _native.colslice_plans_enabled():
+        return {"reused": False, "note": "AUTOSAGE_COLSLICE_PLAN=off: slice points and binning run in every call"}
+    lib = _native.library()
+    sorted_col = _native.row_sorted(crow, col)[0]
+    code = 0 if dtype == torch.float32 else _native.DTYPES_16[dtype]
+    n = crow.numel() - 1
+    plan = torch.empty(lib.as_spmm_colslice_plan_bytes(n), dtype=torch.uint8, device=crow.device)
+    tag = ctypes.c_int64(0)
+    times = []
+    for _ in range(6):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        status = lib.as_spmm_colslice_plan(crow.data_ptr(), sorted_col.data_ptr(), n, sorted_col.numel(), f, code,
+                                           int(column_slices), plan.data_ptr(), plan.numel(), ctypes.byref(tag),
+                                           torch.cuda.current_stream().cuda_stream)
+        end.record()
+        end.synchronize()
+        if status != 0:
+            raise RuntimeError(lib.as_last_error().decode())
+        times.append(start.elapsed_time(end))
+    os.environ["AUTOSAGE_COLSLICE_PLAN"] = "off"
+    try:
+        unplanned, _ = time_steps(step, max(5, args.steps // 2), 2)
+    finally:
+        os.environ.pop("AUTOSAGE_COLSLICE_PLAN")
+    return {"reused": True, "build_ms": round(statistics.median(times[1:]), 4),
+            "ms_per_step_rebuilding_it": round(unplanned, 4),
+            "note": "slice points and the degree-binned row order are built once per graph (as_spmm_colslice_plan) "
+                    "and reused by every call, whatever X; ms_per_step_rebuilding_it times the same step with "
+                    "AUTOSAGE_COLSLICE_PLAN=off"}
 
 
 def bench_hubsweep(args, device) -> dict:

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 4
+#define AS_ABI_VERSION 5
 
 typedef enum as_status {
   AS_OK = 0,
@@ -156,6 +156,50 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col,
  * (AS_DTYPE_*): with column slices (column_slices != 0) 256 for fp32 with
  * F <= 64 and 128 otherwise; with edge slices 1024. */
 int64_t as_spmm_colslice_min_degree(int column_slices, int64_t f, int dtype);
+
+/* Bytes of a column-sliced plan for n rows (n·28 B of slice points and row
+ * order, plus the binning tables). */
+size_t as_spmm_colslice_plan_bytes(int64_t n);
+
+/* Builds the per-graph part of the column-sliced SpMM (as_spmm_csr_colslice_f32,
+ * as_spmm_csr_rounded_16) into `plan` (256-byte aligned): the slice points
+ * of every row of slicing degree and the degree-binned row order.  No
+ * reference counterpart: the reference bins the rows on every call
+ * (csrc/launcher_spmm.cu:49-59, at::nonzero); a plan is built once per graph
+ * and serves every later call with the same F, dtype and slicing, whatever
+ * X and the weights.  *plan_tag receives the settings the plan was built
+ * for (slicing degree, light buckets), checked by the planned call.
+ * dtype AS_DTYPE_F32 (column_slices != 0 only), AS_DTYPE_BF16 or
+ * AS_DTYPE_F16; the columns of the graph ascend within rows for column
+ * slices.  Asynchronous on `stream`. */
+int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n,
+                          int64_t nnz, int64_t f, int dtype, int column_slices,
+                          void* plan, size_t plan_bytes, int64_t* plan_tag,
+                          void* stream);
+
+/* Preferred workspace bytes of as_spmm_csr_colslice_planned: the two partial
+ * buffers only (for 16-bit types sized by sliced_rows as in
+ * as_spmm_rounded_16_workspace_bytes). */
+size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype,
+                                                int64_t sliced_rows);
+
+/* as_spmm_csr_colslice_f32 (dtype AS_DTYPE_F32, column_slices != 0) or
+ * as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16) with the slice
+ * points and row order read from a plan that as_spmm_colslice_plan built
+ * for this graph (same crow, col, n and nnz, unmodified since) with the
+ * same F, dtype and column_slices: the same bits, without the per-call
+ * slice point and binning launches.  A plan_tag of other settings returns
+ * AS_ERR_INVALID_ARGUMENT; a plan of another graph is not detected (the
+ * caller keys plans by graph).  The workspace holds the partial buffers
+ * only (any size down to two partial rows, as for the unplanned calls). */
+int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col,
+                                 const void* val, const void* x, void* y,
+                                 int64_t n, int64_t nnz, int64_t f, int dtype,
+                                 int column_slices, const void* plan,
+                                 size_t plan_bytes, int64_t plan_tag,
+                                 void* workspace, size_t workspace_bytes,
+                                 int64_t sliced_rows, int64_t grouped_rows,
+                                 void* stream);
 
 /* SpMM with bf16 or fp16 features, weights and output (dtype
  * AS_DTYPE_BF16 / AS_DTYPE_F16; val may be NULL).  The reference has no

@@ -80,6 +80,33 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert [lib.as_spmm_colslice_min_degree(1, f, 0) for f in (1, 64, 65, 128)] == [256, 256, 128, 128]
     assert [lib.as_spmm_colslice_min_degree(1, f, 1) for f in (8, 64, 128)] == [128, 128, 128]
     assert lib.as_spmm_colslice_min_degree(0, 64, 0) == 1024 and lib.as_spmm_colslice_min_degree(0, 128, 2) == 1024
+    # column-sliced plans: settings and sizes are checked before any device work
+    tag = ctypes.c_int64(0)
+    assert lib.as_spmm_colslice_plan(None, None, 4, 0, 64, 3, 1, None, 0, ctypes.byref(tag), None) == 1
+    assert lib.as_last_error() == b"dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16"
+    assert lib.as_spmm_colslice_plan(None, None, 4, 0, 64, 0, 0, None, 0, ctypes.byref(tag), None) == 1
+    assert lib.as_last_error() == b"float32 features take column slices only (column_slices != 0)"
+    assert lib.as_spmm_colslice_plan(256, 256, 4, 0, 64, 0, 1, 256, 16, ctypes.byref(tag), None) == 4
+    assert lib.as_last_error().startswith(b"a column-sliced plan needs ")
+    assert lib.as_spmm_colslice_plan_bytes(1000) >= 28 * 1000
+    # an empty graph builds an empty plan and reports the tag of its settings
+    tags = {}
+    for code, f, slices in [(0, 64, 1), (0, 128, 1), (1, 64, 1), (1, 128, 0), (2, 128, 0)]:
+        assert lib.as_spmm_colslice_plan(None, None, 0, 0, f, code, slices, 256, 1 << 20, ctypes.byref(tag), None) == 0
+        tags[(code, f, slices)] = tag.value
+    # fp32 F=64 slices from 256, F=128 from 128; bf16 and fp16 with edge slices share their tag
+    assert tags[(0, 64, 1)] != tags[(0, 128, 1)] and tags[(0, 128, 1)] != tags[(1, 64, 1)]
+    assert tags[(1, 128, 0)] == tags[(2, 128, 0)]
+    # a plan of other settings is refused before the plan or any pointer is read
+    fake = 256
+    assert lib.as_spmm_csr_colslice_planned(fake, fake, None, fake, fake, 4, 4, 128, 0, 1, fake, 1 << 20,
+                                            tags[(0, 64, 1)], fake, 1 << 20, -1, 0, None) == 1
+    assert lib.as_last_error().startswith(b"the plan was built for other settings")
+    assert lib.as_spmm_csr_colslice_planned(fake, fake, None, fake, fake, 4, 4, 128, 0, 0, fake, 1 << 20,
+                                            tags[(0, 128, 1)], fake, 1 << 20, -1, 0, None) == 1
+    # two partial buffers of a chunk's rows (all 1,000 rows here: chunks hold at least 4,096), 8 slices of F fp64
+    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 0, -1) == 2 * 1000 * 8 * 128 * 8
+    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 1, 10) == 2 * 10 * 8 * 128 * 8
     # 16-bit SpMM, rows whole
     assert lib.as_spmm_csr_rows_16(None, None, None, None, None, 4, 0, 8, 3, None) == 1
     assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"

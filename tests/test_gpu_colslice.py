@@ -303,3 +303,70 @@ def test_sliced_rows_hint_only_sizes_the_launches():
             assert status == 0, lib.as_last_error()
             torch.cuda.synchronize()
             assert torch.equal(y, outs[0]), rows
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_planned_calls_match_unplanned(dtype, monkeypatch):
+    """A plan (slice points and binned row order, built once per graph)
+    gives the bits of a call that builds them itself: fp32 and 16-bit, F of
+    either fp32 slicing degree (256 at F = 64, 128 above), column and edge
+    slices, a short partial workspace; a plan is built per (graph, settings),
+    and it goes with the graph."""
+    import gc
+
+    crow, col, val, x = _inputs(128, True, seed=31, rows=9000, degree=20, hubs=40, hub_degree=3000)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    d_val, d_x = d_val.to(dtype), d_x.to(dtype)
+    before = len(_native._PLAN_MEMO)
+    for f in (64, 128):
+        xf = d_x[:, :f].contiguous()
+        modes = [True] if dtype == torch.float32 else [True, False]
+        for column_slices in modes:
+            if dtype == torch.float32:
+                planned = _native.spmm_csr_colslice_impl(d_crow, d_col, d_val, xf)
+            else:
+                planned = _native.spmm_rounded_16_impl(d_crow, d_col, d_val, xf, column_slices)
+            monkeypatch.setenv("AUTOSAGE_COLSLICE_PLAN", "off")
+            if dtype == torch.float32:
+                unplanned = _native.spmm_csr_colslice_impl(d_crow, d_col, d_val, xf)
+            else:
+                unplanned = _native.spmm_rounded_16_impl(d_crow, d_col, d_val, xf, column_slices)
+            monkeypatch.delenv("AUTOSAGE_COLSLICE_PLAN")
+            assert torch.equal(planned, unplanned), (f, column_slices)
+            # a short workspace (partials for ~40 rows) with the same plan: more chunks, same bits
+            plan_bytes = _native.library().as_spmm_colslice_plan_bytes(crow.size - 1)
+            monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((plan_bytes + 40 * 8 * f * 8) / 2**20))
+            if dtype == torch.float32:
+                short = _native.spmm_csr_colslice_impl(d_crow, d_col, d_val, xf)
+            else:
+                short = _native.spmm_rounded_16_impl(d_crow, d_col, d_val, xf, column_slices)
+            monkeypatch.delenv("AUTOSAGE_COLSLICE_WORKSPACE_MB")
+            assert torch.equal(short, planned)
+    if dtype == torch.float32:
+        _assert_fp64_close(planned.cpu().numpy(), oracle.spmm_f64(crow, col, val, x[:, :128]))
+    # fp32 slices from 256 at F = 64 and 128 at F = 128: two plans; 16-bit:
+    # column slices from 128 at both F, edge slices from 1024: two plans
+    assert len(_native._PLAN_MEMO) == before + 2
+    del d_col
+    gc.collect()
+    assert len(_native._PLAN_MEMO) == before
+
+
+def test_planned_call_rejects_a_plan_of_other_settings():
+    crow, col, val, x = _inputs(64, False, seed=32, rows=2000)
+    d_crow, d_col, d_x = to_dev(crow, col, x)
+    lib = _native.library()
+    n, f = x.shape
+    plan64, tag64 = _native.colslice_plan(d_crow, d_col, 64, torch.float32, True)
+    _, tag128 = _native.colslice_plan(d_crow, d_col, 128, torch.float32, True)
+    assert tag64 != tag128
+    y = torch.empty_like(d_x)
+    ws = torch.empty(lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, -1), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (d_crow.data_ptr(), d_col.data_ptr(), 0, d_x.data_ptr(), y.data_ptr(), n, col.size, f, 0, 1,
+            plan64.data_ptr(), plan64.numel())
+    assert lib.as_spmm_csr_colslice_planned(*args, tag128, ws.data_ptr(), ws.numel(), -1, 0, stream) == 1
+    assert lib.as_last_error().startswith(b"the plan was built for other settings")
+    assert lib.as_spmm_csr_colslice_planned(*args, tag64, ws.data_ptr(), ws.numel(), -1, 0, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y, _native.spmm_csr_colslice_impl(d_crow, d_col, None, d_x))
