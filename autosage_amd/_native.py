@@ -95,21 +95,25 @@ _SIGNATURES = {
          _c_ptr],
     ),
     "as_csr_attention_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "as_csr_attention_plan_bytes": (_c_size, [_c_i64]),
+    "as_csr_attention_plan": (
+        _c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_int, _c_ptr, _c_size, ctypes.POINTER(ctypes.c_int64), _c_ptr]
+    ),
     "as_csr_attention_colslice_f32": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr,
-         _c_size, _c_ptr],
+         _c_i64, _c_ptr, _c_size, _c_ptr],
     ),
     "as_csr_attention_colslice_16": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_int,
-         _c_ptr, _c_size, _c_ptr],
+         _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
     ),
     "as_csr_attention_backward_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "as_csr_attention_backward_f32": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64,
-         _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_size, _c_ptr],
+         _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
     ),
     "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "as_induced_sample_workspace_bytes": (_c_size, [_c_i64]),
@@ -641,21 +645,46 @@ def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
     if n == 0:
         return out
     lib = library()
-    ws = _workspace(min(lib.as_csr_attention_colslice_workspace_bytes(n, nnz, fv), _colslice_workspace_cap()),
-                    query.device)
+    plan, tag = attention_plan(crow, col, query.dtype) if colslice_plans_enabled() else (None, 0)
+    # the workspace cap counts the plan, as in a call that builds it
+    size = min(lib.as_csr_attention_colslice_workspace_bytes(n, nnz, fv), _colslice_workspace_cap())
+    ws = _workspace(size - (plan.numel() if plan is not None else 0), query.device)
     with torch.cuda.device(query.device):
         if half:
             status = lib.as_csr_attention_colslice_16(
                 _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv,
-                float(scale), DTYPES_16[query.dtype], _ptr(ws), ws.numel(), _stream(query.device),
+                float(scale), DTYPES_16[query.dtype], _ptr(plan), tag, _ptr(ws), ws.numel(), _stream(query.device),
             )
         else:
             status = lib.as_csr_attention_colslice_f32(
                 _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv,
-                float(scale), _ptr(ws), ws.numel(), _stream(query.device),
+                float(scale), _ptr(plan), tag, _ptr(ws), ws.numel(), _stream(query.device),
             )
     _raise(status, "autosage::csr_attention_colslice")
     return out
+
+
+def attention_plan(crow: torch.Tensor, col: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, int]:
+    """(plan, tag) of the column-sliced attention on this graph (columns
+    ascending within rows) for ``dtype``: slice points and the binned row
+    order, built once per live, unmodified (crow, col) pair and element type
+    (fp32 or 16-bit), then reused whatever Q, K and V; an fp32 plan also
+    serves the backward's passes.  The build synchronises the stream once."""
+    lib = library()
+    code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
+
+    def compute() -> tuple[torch.Tensor, int]:
+        n = crow.numel() - 1
+        plan = _workspace(lib.as_csr_attention_plan_bytes(n), crow.device)
+        tag = ctypes.c_int64(0)
+        with torch.cuda.device(crow.device):
+            status = lib.as_csr_attention_plan(_ptr(crow), _ptr(col), n, col.numel(), code, _ptr(plan), plan.numel(),
+                                               ctypes.byref(tag), _stream(crow.device))
+            _raise(status, "autosage attention plan")
+            torch.cuda.current_stream(crow.device).synchronize()
+        return plan, int(tag.value)
+
+    return _PLAN_MEMO.get((crow, col), ("attention", code != 0), compute)
 
 
 def attention_backward_supported(query, key, value, out, grad_out) -> bool:
@@ -680,13 +709,21 @@ def csr_attention_backward_impl(crow, col, crow_t, col_t, query, key, value, out
     if n == 0:
         return grad_q, grad_k, grad_v
     lib = library()
-    ws = _workspace(min(lib.as_csr_attention_backward_workspace_bytes(n, nnz, fqk, fv), _colslice_workspace_cap()),
-                    query.device)
+    size = min(lib.as_csr_attention_backward_workspace_bytes(n, nnz, fqk, fv), _colslice_workspace_cap())
+    plan = plan_t = None
+    tag = tag_t = 0
+    if colslice_plans_enabled():
+        # fp32 plans of A and of Aᵀ (the forward's plan serves pass 1); the
+        # workspace then needs no plan region
+        plan, tag = attention_plan(crow, col, torch.float32)
+        plan_t, tag_t = attention_plan(crow_t, col_t, torch.float32)
+        size -= plan.numel()
+    ws = _workspace(size, query.device)
     with torch.cuda.device(query.device):
         status = lib.as_csr_attention_backward_f32(
             _ptr(crow), _ptr(col), _ptr(crow_t), _ptr(col_t), _ptr(query), _ptr(key), _ptr(value), _ptr(out),
-            _ptr(grad_out), _ptr(grad_q), _ptr(grad_k), _ptr(grad_v), n, nnz, fqk, fv, float(scale), _ptr(ws),
-            ws.numel(), _stream(query.device),
+            _ptr(grad_out), _ptr(grad_q), _ptr(grad_k), _ptr(grad_v), n, nnz, fqk, fv, float(scale), _ptr(plan), tag,
+            _ptr(plan_t), tag_t, _ptr(ws), ws.numel(), _stream(query.device),
         )
     _raise(status, "autosage::csr_attention (backward)")
     return grad_q, grad_k, grad_v

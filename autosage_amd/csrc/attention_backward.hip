@@ -553,11 +553,9 @@ size_t bwd_row_bytes(int64_t fqk, int64_t fv) {
   return static_cast<size_t>(kSlices) * (p1 > p2 ? p1 : p2) * sizeof(float);
 }
 
-size_t bwd_fixed_bytes(int64_t n) {
-  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
-  return align_up(rows * sizeof(float2), 256) + align_up(rows * kSliceBounds * sizeof(int32_t), 256) +
-         align_up(rows * sizeof(int32_t), 256) + 256 + bin_workspace_bytes(n);
-}
+// (lse, t) pairs, then a slice plan region for passes called without a plan
+size_t bwd_pairs_bytes(int64_t n) { return align_up(static_cast<size_t>(n > 0 ? n : 1) * sizeof(float2), 256); }
+size_t bwd_fixed_bytes(int64_t n) { return bwd_pairs_bytes(n) + slice_plan_bytes(n); }
 
 int64_t bwd_sliced_upper(int64_t n, int64_t nnz) {
   const int64_t u = nnz / kBwdSliceMinDegree;
@@ -657,8 +655,15 @@ int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col, const
                                   const int64_t* col_t, const float* query, const float* key, const float* value,
                                   const float* out, const float* grad_out, float* grad_q, float* grad_k,
                                   float* grad_v, int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v, float scale,
+                                  const void* plan, int64_t plan_tag, const void* plan_t, int64_t plan_t_tag,
                                   void* workspace, size_t workspace_bytes, void* stream) {
   as::clear_error();
+  const int64_t want = as::slice_plan_tag(as::kBwdSliceMinDegree, 1);
+  if ((plan != nullptr && plan_tag != want) || (plan_t != nullptr && plan_t_tag != want))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "a plan was built for other settings (this call needs plan tag %lld)",
+                    (long long)want);
+  if ((plan != nullptr && !as::aligned(plan, 256)) || (plan_t != nullptr && !as::aligned(plan_t, 256)))
+    return as::fail(AS_ERR_WORKSPACE, "plans must be 256-byte aligned");
   if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
   if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
   if (f_qk < 4 || f_qk > 256 || f_qk % 4 != 0 || f_v < 4 || f_v > 256 || f_v % 4 != 0)
@@ -673,7 +678,9 @@ int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col, const
                         static_cast<const void*>(grad_out), static_cast<const void*>(grad_q),
                         static_cast<const void*>(grad_k), static_cast<const void*>(grad_v)})
     if (!as::aligned(p, 16)) return as::fail(AS_ERR_UNSUPPORTED, "attention backward needs 16-byte aligned tensors");
-  const size_t fixed = as::bwd_fixed_bytes(n);
+  // the workspace holds a plan region only for a pass called without a plan
+  const bool own_plan = plan == nullptr || plan_t == nullptr;
+  const size_t fixed = own_plan ? as::bwd_fixed_bytes(n) : as::bwd_pairs_bytes(n);
   const size_t row_bytes = as::bwd_row_bytes(f_qk, f_v);
   if (workspace == nullptr || workspace_bytes < fixed + row_bytes + 3 * 256)
     return as::fail(AS_ERR_WORKSPACE, "attention backward needs at least %zu workspace bytes, got %zu",
@@ -686,29 +693,23 @@ int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col, const
   if (chunk < 1) chunk = 1;
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const size_t rows = static_cast<size_t>(n);
-  float2* lt = reinterpret_cast<float2*>(ws);
-  ws += as::align_up(rows * sizeof(float2), 256);
-  int32_t* off = reinterpret_cast<int32_t*>(ws);
-  ws += as::align_up(rows * as::kSliceBounds * sizeof(int32_t), 256);
-  int32_t* order = reinterpret_cast<int32_t*>(ws);
-  ws += as::align_up(rows * sizeof(int32_t), 256);
-  int32_t* counts = reinterpret_cast<int32_t*>(ws);
-  ws += 256;
-  void* bin_ws = ws;
+  float2* lt = static_cast<float2*>(workspace);
+  void* own = static_cast<char*>(workspace) + as::bwd_pairs_bytes(n);
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + fixed);
 
-  // pass 1 over A; then pass 2 over Aᵀ, which reuses the slice points, the
-  // order and the partial buffers (stream order)
+  // pass 1 over A; then pass 2 over Aᵀ.  A pass without a plan builds one in
+  // the workspace's plan region (pass 2 after pass 1 in stream order)
   for (int pass = 1; pass <= 2; ++pass) {
     const int64_t* pc = pass == 1 ? crow : crow_t;
     const int64_t* pcol = pass == 1 ? col : col_t;
-    as::launch_slice_points(pc, pcol, n, as::kBwdSliceMinDegree, off, s);
-    const int st = as::launch_bin_rows(pc, n, as::kBwdSliceMinDegree, as::kMaxHeavyBuckets, 1, order, counts, bin_ws, s);
-    if (st != AS_OK) return st;
-    const as::BwdArgs a{pc,     pcol,   query, key, value, grad_out, out,   lt,     grad_q,
-                        grad_k, grad_v, n,     f_qk, f_v,  scale,    order, counts, off};
+    const void* given = pass == 1 ? plan : plan_t;
+    const as::SlicePlan view = as::slice_plan_view(given != nullptr ? const_cast<void*>(given) : own, n);
+    if (given == nullptr) {
+      const int st = as::build_slice_plan(pc, pcol, n, as::kBwdSliceMinDegree, 1, false, view, s);
+      if (st != AS_OK) return st;
+    }
+    const as::BwdArgs a{pc,     pcol,   query, key,  value, grad_out,   out,         lt,      grad_q,
+                        grad_k, grad_v, n,     f_qk, f_v,   scale,      view.order, view.counts, view.off};
     if (pass == 1) as::dispatch_pass<1>(a, upper, chunk, part, s);
     else as::dispatch_pass<2>(a, upper, chunk, part, s);
   }

@@ -557,10 +557,14 @@ void launch_attention_k(int gv, const AttArgs<T>& a, int64_t upper, int64_t chun
   }
 }
 
-size_t att_fixed_bytes(int64_t n) {
-  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
-  return align_up(rows * kSliceBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
-         bin_workspace_bytes(n);
+size_t att_fixed_bytes(int64_t n) { return slice_plan_bytes(n); }
+
+// The plan settings of the attention on element type T: rows of degree >= 128
+// are sliced; short rows in 8 log2-degree buckets for 16-bit elements (the
+// grouped rows), in one for fp32.
+template <typename T>
+constexpr int att_light_buckets() {
+  return sizeof(T) == 2 ? kMaxHeavyBuckets : 1;
 }
 
 // Per sliced row of a chunk: 8 x (m, l, F_v accumulators), fp32.
@@ -576,15 +580,20 @@ int64_t att_sliced_upper(int64_t n, int64_t nnz) {
 // workspace, computes the slice points and the row order, launches.
 template <typename T>
 int attention_run(const int64_t* crow, const int64_t* col, const T* query, const T* key, const T* value, T* out,
-                  int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v, float scale, void* workspace,
-                  size_t workspace_bytes, void* stream, const char* what) {
+                  int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v, float scale, const void* plan, int64_t plan_tag,
+                  void* workspace, size_t workspace_bytes, void* stream, const char* what) {
+  if (plan != nullptr && plan_tag != slice_plan_tag(kAttSliceMinDegree, att_light_buckets<T>()))
+    return fail(AS_ERR_INVALID_ARGUMENT, "the plan was built for other settings (plan tag %lld, this call needs %lld)",
+                (long long)plan_tag, (long long)slice_plan_tag(kAttSliceMinDegree, att_light_buckets<T>()));
+  if (plan != nullptr && !aligned(plan, 256)) return fail(AS_ERR_WORKSPACE, "the plan must be 256-byte aligned");
   if (n == 0) return AS_OK;
   if (crow == nullptr || query == nullptr || key == nullptr || value == nullptr || out == nullptr ||
       (nnz > 0 && col == nullptr))
     return fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (!aligned(query, 16) || !aligned(key, 16) || !aligned(value, 16) || !aligned(out, 16))
     return fail(AS_ERR_UNSUPPORTED, "column-sliced attention needs 16-byte aligned Q, K, V and out");
-  const size_t fixed = att_fixed_bytes(n);
+  // with a plan the workspace holds the partial states only
+  const size_t fixed = plan != nullptr ? 0 : att_fixed_bytes(n);
   const size_t row_bytes = att_row_bytes(f_v);
   if (workspace == nullptr || workspace_bytes < fixed + row_bytes + 3 * 256)
     return fail(AS_ERR_WORKSPACE, "column-sliced attention needs at least %zu workspace bytes, got %zu",
@@ -597,16 +606,8 @@ int attention_run(const int64_t* crow, const int64_t* col, const T* query, const
   if (chunk < 1) chunk = 1;
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const size_t rows = static_cast<size_t>(n);
-  int32_t* off = reinterpret_cast<int32_t*>(ws);
-  ws += align_up(rows * kSliceBounds * sizeof(int32_t), 256);
-  int32_t* order = reinterpret_cast<int32_t*>(ws);
-  ws += align_up(rows * sizeof(int32_t), 256);
-  int32_t* counts = reinterpret_cast<int32_t*>(ws);
-  ws += 256;
-  void* bin_ws = ws;
-  ws = static_cast<char*>(workspace) + fixed;
+  const SlicePlan view = slice_plan_view(plan != nullptr ? const_cast<void*>(plan) : workspace, n);
+  char* ws = static_cast<char*>(workspace) + fixed;
   const size_t states = static_cast<size_t>(kSlices) * static_cast<size_t>(chunk);
   float* pm = reinterpret_cast<float*>(ws);
   ws += align_up(states * sizeof(float), 256);
@@ -614,16 +615,16 @@ int attention_run(const int64_t* crow, const int64_t* col, const T* query, const
   ws += align_up(states * sizeof(float), 256);
   float* pacc = reinterpret_cast<float*>(ws);
 
-  launch_slice_points(crow, col, n, kAttSliceMinDegree, off, s);
   // order: rows of degree >= 128 (sliced) longest first, then the others; for
   // 16-bit elements in 8 log2-degree buckets, longest first (light bucket b
   // holds degrees [128 / 2^(b+1), 128 / 2^b), the last one the empty rows)
   // (grouped rows take similar degrees together)
   constexpr bool kHalf = sizeof(T) == 2;
-  int st = launch_bin_rows(crow, n, kAttSliceMinDegree, kMaxHeavyBuckets, kHalf ? kMaxHeavyBuckets : 1, order, counts,
-                           bin_ws, s);
-  if (st != AS_OK) return st;
-  const AttArgs<T> a{crow, col, query, key, value, out, n, f_qk, f_v, scale, order, counts, off};
+  if (plan == nullptr) {
+    const int st = build_slice_plan(crow, col, n, kAttSliceMinDegree, att_light_buckets<T>(), false, view, s);
+    if (st != AS_OK) return st;
+  }
+  const AttArgs<T> a{crow, col, query, key, value, out, n, f_qk, f_v, scale, view.order, view.counts, view.off};
   // common widths with compile-time strides
   if (f_qk == 64 && f_v == 128) {
     launch_attention_t<T, kHalf ? 8 : 16, kHalf ? 16 : 32, 64, 128>(a, upper, chunk, pm, pl, pacc, s);
@@ -662,21 +663,48 @@ size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz, int64_t
   return as::att_fixed_bytes(n) + static_cast<size_t>(rows) * as::att_row_bytes(f_v) + 3 * 256;
 }
 
+size_t as_csr_attention_plan_bytes(int64_t n) { return as::slice_plan_bytes(n); }
+
+int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t nnz, int dtype, void* plan,
+                          size_t plan_bytes, int64_t* plan_tag, void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_F32 && dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (plan_tag == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "plan_tag must not be NULL");
+  if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
+  if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
+  if (n > 0 && (crow == nullptr || (nnz > 0 && col == nullptr)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "crow and col must not be NULL");
+  if (plan == nullptr || plan_bytes < as::slice_plan_bytes(n))
+    return as::fail(AS_ERR_WORKSPACE, "an attention plan needs %zu bytes, got %zu", as::slice_plan_bytes(n),
+                    plan_bytes);
+  if (!as::aligned(plan, 256)) return as::fail(AS_ERR_WORKSPACE, "the plan must be 256-byte aligned");
+  const int light = dtype == AS_DTYPE_F32 ? as::att_light_buckets<float>() : as::att_light_buckets<as::Bf16>();
+  *plan_tag = as::slice_plan_tag(as::kAttSliceMinDegree, light);
+  if (n == 0) return AS_OK;
+  const int st = as::build_slice_plan(crow, col, n, as::kAttSliceMinDegree, light, false, as::slice_plan_view(plan, n),
+                                      static_cast<hipStream_t>(stream));
+  if (st != AS_OK) return st;
+  return as::check_launch("csr_attention_plan");
+}
+
 int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col, const float* query, const float* key,
                                   const float* value, float* out, int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v,
-                                  float scale, void* workspace, size_t workspace_bytes, void* stream) {
+                                  float scale, const void* plan, int64_t plan_tag, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   as::clear_error();
   if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
   if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
   if (f_qk < 4 || f_qk > 256 || f_qk % 4 != 0 || f_v < 4 || f_v > 256 || f_v % 4 != 0)
     return as::fail(AS_ERR_UNSUPPORTED, "column-sliced attention needs F_qk and F_v in [4, 256], multiples of 4");
-  return as::attention_run<float>(crow, col, query, key, value, out, n, nnz, f_qk, f_v, scale, workspace,
-                                  workspace_bytes, stream, "csr_attention_colslice");
+  return as::attention_run<float>(crow, col, query, key, value, out, n, nnz, f_qk, f_v, scale, plan, plan_tag,
+                                  workspace, workspace_bytes, stream, "csr_attention_colslice");
 }
 
 int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col, const void* query, const void* key,
                                  const void* value, void* out, int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v,
-                                 float scale, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+                                 float scale, int dtype, const void* plan, int64_t plan_tag, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   as::clear_error();
   if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
     return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
@@ -687,11 +715,12 @@ int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col, const 
   if (dtype == AS_DTYPE_BF16)
     return as::attention_run<as::Bf16>(crow, col, static_cast<const as::Bf16*>(query),
                                        static_cast<const as::Bf16*>(key), static_cast<const as::Bf16*>(value),
-                                       static_cast<as::Bf16*>(out), n, nnz, f_qk, f_v, scale, workspace,
-                                       workspace_bytes, stream, "csr_attention_colslice (bf16)");
+                                       static_cast<as::Bf16*>(out), n, nnz, f_qk, f_v, scale, plan, plan_tag,
+                                       workspace, workspace_bytes, stream, "csr_attention_colslice (bf16)");
   return as::attention_run<as::Fp16>(crow, col, static_cast<const as::Fp16*>(query), static_cast<const as::Fp16*>(key),
                                      static_cast<const as::Fp16*>(value), static_cast<as::Fp16*>(out), n, nnz, f_qk,
-                                     f_v, scale, workspace, workspace_bytes, stream, "csr_attention_colslice (fp16)");
+                                     f_v, scale, plan, plan_tag, workspace, workspace_bytes, stream,
+                                     "csr_attention_colslice (fp16)");
 }
 
 }  // extern "C"

@@ -78,5 +78,54 @@ __device__ __forceinline__ void slice_range(const int32_t* __restrict__ off, int
   b = b < a ? a : (b > deg ? deg : b);
 }
 
+// A slice plan: the per-graph part of a column-sliced call, which depends on
+// the graph, the slicing degree and the number of light buckets only (not on
+// the features): the slice points of every row of slicing degree
+// (off[n·(S-1)]), the degree-binned row order (order[n]), the bucket counts
+// and the binning tables.  The tag packs the two settings, so that a call can
+// check that it was given a plan built for its own.
+struct SlicePlan {
+  int32_t* off;
+  int32_t* order;
+  int32_t* counts;
+  void* bin_ws;
+};
+
+template <int S = kSlices>
+inline size_t slice_plan_bytes(int64_t n) {
+  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
+  return align_up(rows * (S - 1) * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
+         bin_workspace_bytes(n);
+}
+
+template <int S = kSlices>
+inline SlicePlan slice_plan_view(void* base, int64_t n) {
+  char* p = static_cast<char*>(base);
+  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
+  SlicePlan v;
+  v.off = reinterpret_cast<int32_t*>(p);
+  p += align_up(rows * (S - 1) * sizeof(int32_t), 256);
+  v.order = reinterpret_cast<int32_t*>(p);
+  p += align_up(rows * sizeof(int32_t), 256);
+  v.counts = reinterpret_cast<int32_t*>(p);
+  p += 256;
+  v.bin_ws = p;
+  return v;
+}
+
+inline int64_t slice_plan_tag(int64_t min_degree, int light_buckets) {
+  return (int64_t(1) << 48) | (static_cast<int64_t>(light_buckets) << 32) | min_degree;
+}
+
+// order: rows of degree >= min_degree in 8 log2-degree buckets, longest
+// first, then the shorter rows in `light_buckets` log2-degree buckets
+template <int S = kSlices>
+inline int build_slice_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree,
+                            int light_buckets, bool by_edges, const SlicePlan& plan, hipStream_t s) {
+  launch_slice_points<S>(crow, col, n, min_degree, plan.off, s, by_edges);
+  return launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, light_buckets, plan.order, plan.counts, plan.bin_ws,
+                         s);
+}
+
 }  // namespace
 }  // namespace as

@@ -726,11 +726,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(AS_COLSL
   }
 }
 
-size_t colslice_fixed_bytes(int64_t n) {
-  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
-  return align_up(rows * kSpmmBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) + 256 +
-         bin_workspace_bytes(n);
-}
+size_t colslice_fixed_bytes(int64_t n) { return slice_plan_bytes<kSpmmSlices>(n); }
 
 size_t colslice_row_bytes(int64_t f) {
   return static_cast<size_t>(kSpmmSlices) * static_cast<size_t>(f) * sizeof(double);
@@ -898,30 +894,9 @@ inline int64_t grouped_degree(int64_t f, int64_t elem_bytes) {
   return kGroupedMaxBlocks * g;
 }
 
-// The per-graph part of a column-sliced call: slice points and the binned
-// row order.  A plan depends on the graph, the slicing degree and the number
-// of light buckets (and on nothing of X): `plan_tag` packs the last two, so
-// that an execution can check it was given a plan for its own settings.
-struct PlanView {
-  int32_t* off;
-  int32_t* order;
-  int32_t* counts;
-  void* bin_ws;
-};
-
-inline PlanView plan_view(void* base, int64_t n) {
-  char* p = static_cast<char*>(base);
-  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
-  PlanView v;
-  v.off = reinterpret_cast<int32_t*>(p);
-  p += align_up(rows * kSpmmBounds * sizeof(int32_t), 256);
-  v.order = reinterpret_cast<int32_t*>(p);
-  p += align_up(rows * sizeof(int32_t), 256);
-  v.counts = reinterpret_cast<int32_t*>(p);
-  p += 256;
-  v.bin_ws = p;
-  return v;
-}
+// The column-sliced SpMM's plan (colslice_common.h) over kSpmmSlices slices.
+using PlanView = SlicePlan;
+inline PlanView plan_view(void* base, int64_t n) { return slice_plan_view<kSpmmSlices>(base, n); }
 
 inline int64_t slicing_degree(Slicing slicing, int64_t f, int64_t elem_bytes) {
   return slicing == kSliceColumns ? column_slice_degree(f, elem_bytes) : kEdgeSliceMinDegree;
@@ -932,15 +907,11 @@ inline int64_t slicing_degree(Slicing slicing, int64_t f, int64_t elem_bytes) {
 // buckets (a wave of grouped short rows then holds rows of similar degree)
 inline int light_bucket_count(int64_t elem_bytes) { return elem_bytes == 2 ? kMaxHeavyBuckets : 1; }
 
-inline int64_t plan_tag_of(int64_t min_degree, int light_buckets) {
-  return (int64_t(1) << 48) | (static_cast<int64_t>(light_buckets) << 32) | min_degree;
-}
+inline int64_t plan_tag_of(int64_t min_degree, int light_buckets) { return slice_plan_tag(min_degree, light_buckets); }
 
 inline int build_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree, int light_buckets,
                       Slicing slicing, const PlanView& plan, hipStream_t s) {
-  launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, plan.off, s, slicing == kSliceEdges);
-  return launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, light_buckets, plan.order, plan.counts, plan.bin_ws,
-                         s);
+  return build_slice_plan<kSpmmSlices>(crow, col, n, min_degree, light_buckets, slicing == kSliceEdges, plan, s);
 }
 
 // `plan`: built by build_plan for this graph, min_degree and light bucket

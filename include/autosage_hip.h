@@ -336,9 +336,27 @@ int as_csr_attention_f32(const int64_t* crow, const int64_t* col,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
-/* Preferred bytes of workspace for as_csr_attention_colslice_f32. */
+/* Preferred bytes of workspace for as_csr_attention_colslice_f32 (called
+ * without a plan; with one, as_csr_attention_plan_bytes(n) less). */
 size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz,
                                                  int64_t f_v);
+
+/* Bytes of an attention plan for n rows. */
+size_t as_csr_attention_plan_bytes(int64_t n);
+
+/* Builds the per-graph part of the column-sliced attention into `plan`
+ * (256-byte aligned): the slice points of every row of degree >= 128 and
+ * the degree-binned row order.  No reference counterpart (the reference
+ * composes its attention from torch ops, autosage/_auto.py:762-780); a plan
+ * is built once per graph and serves every later attention call on it with
+ * the same element type (dtype AS_DTYPE_F32 / BF16 / F16), whatever Q, K
+ * and V.  An fp32 plan also serves the backward's passes over the graph,
+ * and the backward's pass over the transposed graph takes an fp32 plan of
+ * that graph.  *plan_tag receives the settings it was built for, checked by
+ * the calls.  Columns ascending within rows; asynchronous on `stream`. */
+int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n,
+                          int64_t nnz, int dtype, void* plan,
+                          size_t plan_bytes, int64_t* plan_tag, void* stream);
 
 /* Column-sliced attention, an alternative schedule for as_csr_attention_f32
  * (no reference counterpart; chosen by csr_attention_forward,
@@ -348,14 +366,19 @@ size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz,
  * column slices (one per XCD) with an online softmax per (row, slice) and
  * fp32 partial states merged per row; shorter rows run the online softmax in
  * one wave.  Deterministic; not bit-identical to as_csr_attention_f32.
+ * plan: NULL (the slice points and row order are built in the workspace in
+ * every call) or a plan of as_csr_attention_plan for this graph, unmodified
+ * since, with plan_tag (a tag of other settings returns
+ * AS_ERR_INVALID_ARGUMENT); the same bits either way.
  * A workspace smaller than the preferred size (256-byte aligned, at least
- * the slice points, row order and one row of partial states) runs the sliced
- * rows in more chunks. */
+ * the slice points and row order when plan is NULL and one row of partial
+ * states) runs the sliced rows in more chunks. */
 int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col,
                                   const float* query, const float* key,
                                   const float* value, float* out, int64_t n,
                                   int64_t nnz, int64_t f_qk, int64_t f_v,
-                                  float scale, void* workspace,
+                                  float scale, const void* plan,
+                                  int64_t plan_tag, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
 /* The column-sliced attention on bf16 or fp16 query, key, value and output
@@ -369,12 +392,14 @@ int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col,
  * probabilities to the feature type; there is no 16-bit kernel to replace.
  * f_qk and f_v multiples of 8 in [8, 512]; 16-byte aligned Q, K, V and out;
  * columns ascending within every row; the workspace of
- * as_csr_attention_colslice_workspace_bytes. */
+ * as_csr_attention_colslice_workspace_bytes; plan and plan_tag as for
+ * as_csr_attention_colslice_f32 (a plan built for this dtype). */
 int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col,
                                  const void* query, const void* key,
                                  const void* value, void* out, int64_t n,
                                  int64_t nnz, int64_t f_qk, int64_t f_v,
-                                 float scale, int dtype, void* workspace,
+                                 float scale, int dtype, const void* plan,
+                                 int64_t plan_tag, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
 /* Bytes of workspace for as_csr_attention_backward_f32. */
@@ -391,7 +416,11 @@ size_t as_csr_attention_backward_workspace_bytes(int64_t n, int64_t nnz,
  * and differentiates its torch composition (autosage/_auto.py:762-780).
  * f_qk and f_v multiples of 4 in [4, 256]; all dense tensors 16-byte aligned;
  * columns ascending within the rows of both graphs; a workspace smaller
- * than the preferred size runs the sliced rows in more chunks. */
+ * than the preferred size runs the sliced rows in more chunks.
+ * plan / plan_t: NULL, or fp32 plans of as_csr_attention_plan for the graph
+ * and for the transposed graph with their tags; a pass without a plan
+ * builds one in the workspace (as_csr_attention_plan_bytes(n) of the
+ * preferred size are that region, needed unless both plans are given). */
 int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col,
                                   const int64_t* crow_t, const int64_t* col_t,
                                   const float* query, const float* key,
@@ -399,7 +428,9 @@ int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col,
                                   const float* grad_out, float* grad_q,
                                   float* grad_k, float* grad_v, int64_t n,
                                   int64_t nnz, int64_t f_qk, int64_t f_v,
-                                  float scale, void* workspace,
+                                  float scale, const void* plan,
+                                  int64_t plan_tag, const void* plan_t,
+                                  int64_t plan_t_tag, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
 /* Bytes of workspace for the induced-sample entry points (n int32). */

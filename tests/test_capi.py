@@ -107,6 +107,24 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     # two partial buffers of a chunk's rows (all 1,000 rows here: chunks hold at least 4,096), 8 slices of F fp64
     assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 0, -1) == 2 * 1000 * 8 * 128 * 8
     assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 1, 10) == 2 * 10 * 8 * 128 * 8
+    # attention plans: fp32 and 16-bit tags differ (light buckets), and the
+    # forward and the backward refuse a tag of other settings before any device work
+    att = {}
+    for code in (0, 1, 2):
+        assert lib.as_csr_attention_plan(None, None, 0, 0, code, fake, 1 << 20, ctypes.byref(tag), None) == 0
+        att[code] = tag.value
+    assert att[0] != att[1] and att[1] == att[2]
+    assert lib.as_csr_attention_plan(None, None, 4, 0, 3, fake, 1 << 20, ctypes.byref(tag), None) == 1
+    assert lib.as_csr_attention_plan(fake, fake, 4, 4, 0, fake, 16, ctypes.byref(tag), None) == 4
+    assert lib.as_csr_attention_plan_bytes(1000) == lib.as_spmm_colslice_plan_bytes(1000)
+    assert lib.as_csr_attention_colslice_f32(fake, fake, fake, fake, fake, fake, 4, 4, 64, 64, 1.0, fake, att[1],
+                                             fake, 1 << 20, None) == 1
+    assert lib.as_last_error().startswith(b"the plan was built for other settings")
+    assert lib.as_csr_attention_colslice_16(fake, fake, fake, fake, fake, fake, 4, 4, 64, 64, 1.0, 1, fake, att[0],
+                                            fake, 1 << 20, None) == 1
+    assert lib.as_csr_attention_backward_f32(*([fake] * 12), 4, 4, 64, 64, 1.0, fake, att[0], fake, att[1], fake,
+                                             1 << 20, None) == 1
+    assert lib.as_last_error().startswith(b"a plan was built for other settings")
     # 16-bit SpMM, rows whole
     assert lib.as_spmm_csr_rows_16(None, None, None, None, None, 4, 0, 8, 3, None) == 1
     assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"

@@ -197,3 +197,43 @@ def test_two_pass_attention_backward_rows_without_edges_and_chunks(monkeypatch):
     monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((fixed + 3 * 8 * (64 + 128) * 4 + 768) / 2**20))
     chunked = grads()
     assert all(torch.equal(a, b) for a, b in zip(first, chunked))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_attention_plans_give_the_bits_of_per_call_set_up(dtype, monkeypatch):
+    """Per-graph plans (slice points and row order of A, and for the backward
+    of Aᵀ) give the bits of calls that build them each time, forward and
+    backward; the plans go with their graphs."""
+    import gc
+
+    from autosage_amd import _native
+
+    n = 3000
+    crow, col = case_graph(n, 9, seed=12, hubs=20, hub_degree=1200, empty=0.05)
+    rng = np.random.default_rng(13)
+    arrays = [(rng.standard_normal((n, f)) * 0.25).astype(np.float32) for f in (64, 64, 128)]
+    g = torch.from_numpy(rng.standard_normal((n, 128)).astype(np.float32)).cuda().to(dtype)
+    d_crow, d_col = to_dev(crow, col)
+    before = len(_native._PLAN_MEMO)
+
+    def run():
+        leaves = [torch.from_numpy(a).cuda().to(dtype).requires_grad_(True) for a in arrays]
+        out = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *leaves, 0.125)
+        out.backward(g)
+        return [out] + [leaf.grad for leaf in leaves]
+
+    planned = run()
+    # fp32: the plan of A (forward and pass 1) and of Aᵀ (pass 2); 16-bit: the
+    # forward's plan (its backward chains the native 16-bit stages)
+    assert len(_native._PLAN_MEMO) == before + (2 if dtype == torch.float32 else 1)
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_PLAN", "off")
+    unplanned = run()
+    monkeypatch.delenv("AUTOSAGE_COLSLICE_PLAN")
+    assert all(torch.equal(a, b) for a, b in zip(planned, unplanned))
+    assert torch.equal(planned[0], run()[0])
+    from autosage_amd import _autograd
+
+    del d_col
+    _autograd._TRANSPOSE_MEMO.clear()
+    gc.collect()
+    assert len(_native._PLAN_MEMO) == before
