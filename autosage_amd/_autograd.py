@@ -18,9 +18,9 @@ backward formulas built from the same native kernels:
 * ``p = softmax_row(s)``: ``ds = p·(dp − Σ_row dp·p)`` (native kernel).
 * the fused attention ``out = softmax_row(scale·s)·V``: the scores and
   probabilities are recomputed with the native ops and the three formulas
-  above are chained (``dV = Pᵀ·dOut``); the column-sliced attention (float32)
-  takes two native gather passes instead (``as_csr_attention_backward_f32``),
-  with no nnz-sized intermediate.
+  above are chained (``dV = Pᵀ·dOut``); the column-sliced attention takes two
+  native gather passes instead (``as_csr_attention_backward_f32`` / ``_16``:
+  float32, bf16 or fp16, fp32 sums), with no nnz-sized intermediate.
 
 The transposed CSR (rows of Aᵀ list the source rows in ascending order, a
 stable sort of the edges by column) is built with torch ops and memoised per
@@ -168,12 +168,13 @@ def _attention_sliced_setup(ctx, inputs, output) -> None:
 def _attention_backward(ctx, grad_out: torch.Tensor):
     """out = P·V with P = softmax_row(scale·SDDMM(Q, K)).
 
-    The column-sliced op (float32, column slices allowed) takes the two-pass
-    native backward: pass 1 over the rows of A recomputes the scores with an
-    online maximum and sum and writes dQ and the row log-sum-exp; pass 2 over
-    the rows of Aᵀ writes dK and dV; t_r = <dOut[r], out[r]> comes from the
-    saved output.  Otherwise (the exact fused op, 16-bit inputs, column
-    slices off) the scores and P are recomputed with the native ops, then
+    The column-sliced op (column slices allowed; float32, bf16 or fp16) takes
+    the two-pass native backward: pass 1 over the rows of A recomputes the
+    scores with an online maximum and sum and writes dQ and the row
+    log-sum-exp; pass 2 over the rows of Aᵀ writes dK and dV; t_r =
+    <dOut[r], out[r]> comes from the saved output (float32) or is summed in
+    pass 1 (16-bit, whose output is rounded).  Otherwise (the exact fused op,
+    column slices off) the scores and P are recomputed with the native ops, then
     dV = Pᵀ·dOut, dP[e] = <dOut[row(e)], V[col(e)]>, dS = softmax'(P, dP)·scale,
     dQ = A_dS·K, dK = A_dSᵀ·Q (native SpMM / SDDMM / softmax backward)."""
     from ._native import (

@@ -109,11 +109,16 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_int,
          _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
     ),
-    "as_csr_attention_backward_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "as_csr_attention_backward_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
     "as_csr_attention_backward_f32": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64,
          _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
+    ),
+    "as_csr_attention_backward_16": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64,
+         _c_i64, _c_i64, ctypes.c_float, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
     ),
     "as_csr_validate": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "as_induced_sample_workspace_bytes": (_c_size, [_c_i64]),
@@ -668,8 +673,9 @@ def attention_plan(crow: torch.Tensor, col: torch.Tensor, dtype: torch.dtype) ->
     """(plan, tag) of the column-sliced attention on this graph (columns
     ascending within rows) for ``dtype``: slice points and the binned row
     order, built once per live, unmodified (crow, col) pair and element type
-    (fp32 or 16-bit), then reused whatever Q, K and V; an fp32 plan also
-    serves the backward's passes.  The build synchronises the stream once."""
+    (fp32 or 16-bit), then reused whatever Q, K and V; it also serves the
+    backward's passes of the same element type.  The build synchronises the
+    stream once."""
     lib = library()
     code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
 
@@ -688,18 +694,28 @@ def attention_plan(crow: torch.Tensor, col: torch.Tensor, dtype: torch.dtype) ->
 
 
 def attention_backward_supported(query, key, value, out, grad_out) -> bool:
-    """Shapes the two-pass attention backward handles: float32, F_qk and F_v
-    multiples of 4 in [4, 256], 16-byte aligned dense tensors."""
+    """Shapes the two-pass attention backward handles: one element type for
+    all five tensors, float32 with F_qk and F_v multiples of 4 in [4, 256] or
+    bf16 / fp16 with multiples of 8 in [8, 512], 16-byte aligned dense
+    tensors."""
     fqk, fv = query.size(1), value.size(1)
     tensors = (query, key, value, out, grad_out)
-    return (all(t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0 for t in tensors)
-            and fqk % 4 == 0 and 4 <= fqk <= 256 and fv % 4 == 0 and 4 <= fv <= 256)
+    dtype = query.dtype
+    if dtype == torch.float32:
+        step, top = 4, 256
+    elif dtype in DTYPES_16:
+        step, top = 8, 512
+    else:
+        return False
+    return (all(t.dtype == dtype and t.is_contiguous() and t.data_ptr() % 16 == 0 for t in tensors)
+            and fqk % step == 0 and step <= fqk <= top and fv % step == 0 and step <= fv <= top)
 
 
 def csr_attention_backward_impl(crow, col, crow_t, col_t, query, key, value, out, grad_out, scale):
     """(grad_q, grad_k, grad_v) of the attention from its saved inputs, its
     output and dL/dout, in two native gather passes (over A and over its
-    transpose (crow_t, col_t))."""
+    transpose (crow_t, col_t)); float32, or bf16 / fp16 (fp32 sums, each
+    gradient rounded once)."""
     n, fqk = query.shape
     fv = value.size(1)
     nnz = col.numel()
@@ -709,22 +725,31 @@ def csr_attention_backward_impl(crow, col, crow_t, col_t, query, key, value, out
     if n == 0:
         return grad_q, grad_k, grad_v
     lib = library()
-    size = min(lib.as_csr_attention_backward_workspace_bytes(n, nnz, fqk, fv), _colslice_workspace_cap())
+    code = 0 if query.dtype == torch.float32 else DTYPES_16[query.dtype]
+    size = min(lib.as_csr_attention_backward_workspace_bytes(n, nnz, fqk, fv, code), _colslice_workspace_cap())
     plan = plan_t = None
     tag = tag_t = 0
     if colslice_plans_enabled():
-        # fp32 plans of A and of Aᵀ (the forward's plan serves pass 1); the
-        # workspace then needs no plan region
-        plan, tag = attention_plan(crow, col, torch.float32)
-        plan_t, tag_t = attention_plan(crow_t, col_t, torch.float32)
+        # plans of A and of Aᵀ for this element type (the forward's plan
+        # serves pass 1); the workspace then needs no plan region
+        plan, tag = attention_plan(crow, col, query.dtype)
+        plan_t, tag_t = attention_plan(crow_t, col_t, query.dtype)
         size -= plan.numel()
     ws = _workspace(size, query.device)
     with torch.cuda.device(query.device):
-        status = lib.as_csr_attention_backward_f32(
-            _ptr(crow), _ptr(col), _ptr(crow_t), _ptr(col_t), _ptr(query), _ptr(key), _ptr(value), _ptr(out),
-            _ptr(grad_out), _ptr(grad_q), _ptr(grad_k), _ptr(grad_v), n, nnz, fqk, fv, float(scale), _ptr(plan), tag,
-            _ptr(plan_t), tag_t, _ptr(ws), ws.numel(), _stream(query.device),
-        )
+        if code == 0:
+            status = lib.as_csr_attention_backward_f32(
+                _ptr(crow), _ptr(col), _ptr(crow_t), _ptr(col_t), _ptr(query), _ptr(key), _ptr(value), _ptr(out),
+                _ptr(grad_out), _ptr(grad_q), _ptr(grad_k), _ptr(grad_v), n, nnz, fqk, fv, float(scale), _ptr(plan),
+                tag, _ptr(plan_t), tag_t, _ptr(ws), ws.numel(), _stream(query.device),
+            )
+        else:
+            # 16-bit: pass 1 sums t itself, the output is not read
+            status = lib.as_csr_attention_backward_16(
+                _ptr(crow), _ptr(col), _ptr(crow_t), _ptr(col_t), _ptr(query), _ptr(key), _ptr(value),
+                _ptr(grad_out), _ptr(grad_q), _ptr(grad_k), _ptr(grad_v), n, nnz, fqk, fv, float(scale), code,
+                _ptr(plan), tag, _ptr(plan_t), tag_t, _ptr(ws), ws.numel(), _stream(query.device),
+            )
     _raise(status, "autosage::csr_attention (backward)")
     return grad_q, grad_k, grad_v
 

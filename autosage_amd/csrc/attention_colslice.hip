@@ -34,6 +34,7 @@
 #include "as_internal.h"
 #include "colslice_common.h"
 #include "elem16.h"
+#include "attention_lanes.h"
 
 namespace as {
 
@@ -44,12 +45,6 @@ constexpr int64_t kAttChunkRows = 131072;    // sliced rows per partial chunk
 constexpr int64_t kAttSliceBlocks = 4096;    // slice-kernel workgroups per slice
 constexpr int64_t kAttReduceBlocks = 8192;   // reduction workgroups
 
-// Elements of type T in one 16-byte lane.
-template <typename T>
-constexpr int lane_elems() {
-  return 16 / static_cast<int>(sizeof(T));
-}
-
 // Edges per online-softmax step.  8 for both element sizes: with 16-bit
 // elements 16 or 32 edges per step took the benchmark attention (Fqk 64,
 // Fv 128, 2.4M rows of median degree 16) from 7.84 to 8.85 and 9.93 ms.
@@ -59,26 +54,6 @@ constexpr int lane_elems() {
 template <typename T>
 constexpr int att_batch() {
   return sizeof(T) == 2 ? AS_ATT_BATCH_16 : 8;
-}
-
-template <int P>
-__device__ __forceinline__ void merge_softmax(float& m, float& l, float (&acc)[P], float mo, float lo,
-                                              const float (&ao)[P]) {
-  const float mn = fmaxf(m, mo);
-  if (mn == -INFINITY) return;  // both sides saw no edge
-  const float c1 = m == -INFINITY ? 0.f : expf(m - mn);
-  const float c2 = mo == -INFINITY ? 0.f : expf(mo - mn);
-  l = l * c1 + lo * c2;
-#pragma unroll
-  for (int v = 0; v < P; ++v) acc[v] = acc[v] * c1 + ao[v] * c2;
-  m = mn;
-}
-
-// The P elements of a 16-byte lane as exact fp32 values.
-template <typename T>
-__device__ __forceinline__ void lane_values(const RawVec<16>& r, float (&out)[lane_elems<T>()]) {
-#pragma unroll
-  for (int v = 0; v < lane_elems<T>(); ++v) out[v] = Elem<T>::get(r.w, v);
 }
 
 // Online softmax of one wave over edges [rs, re) of a row.  On return every
@@ -201,44 +176,6 @@ __device__ __forceinline__ void attend_edges(const int64_t* __restrict__ col, co
 #pragma unroll
     for (int v = 0; v < P; ++v) ao[v] = __shfl_xor(acc[v], o, kWave);
     merge_softmax<P>(m, l, acc, mo, lo, ao);
-  }
-}
-
-template <typename T, int GK>
-__device__ __forceinline__ void load_query_lanes(const T* __restrict__ query, int64_t row, int64_t fqk,
-                                                 float (&q)[lane_elems<T>()]) {
-  constexpr int P = lane_elems<T>();
-  const int kl = lane_id() % GK;
-  if (P * kl < fqk) {
-    lane_values<T>(load_raw<16>(reinterpret_cast<const char*>(query + row * fqk + P * kl)), q);
-  } else {
-#pragma unroll
-    for (int v = 0; v < P; ++v) q[v] = 0.f;
-  }
-}
-
-// N consecutive outputs (N = 4 or 8, 4·N-byte aligned for fp32, 2·N-byte
-// for 16-bit), each rounded once to T.
-template <typename T, int N>
-__device__ __forceinline__ void store_out(T* p, const float (&v)[N]) {
-  if constexpr (sizeof(T) == 4) {
-#pragma unroll
-    for (int i = 0; i < N; i += 4) {
-      FVec<4> o;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o.v[k] = v[i + k];
-      store_vec<4>(reinterpret_cast<float*>(p) + i, o);
-    }
-  } else {
-    uint32_t w[N / 2];
-#pragma unroll
-    for (int i = 0; i < N / 2; ++i)
-      w[i] = uint32_t(Elem<T>::bits(v[2 * i])) | (uint32_t(Elem<T>::bits(v[2 * i + 1])) << 16);
-    if constexpr (N == 8) {
-      *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
-    } else {
-      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
-    }
   }
 }
 
@@ -511,16 +448,6 @@ __global__ __launch_bounds__(kBlock) void att_reduce_kernel(AttArgs<T> a, int64_
   }
 }
 
-// Lanes per K (or V) row: one 16-byte lane per P elements, a power of two;
-// fp32 keeps at least 16 lanes (4 edges per gather), 16-bit at least 8.
-template <typename T>
-int lane_group(int64_t f) {
-  if constexpr (sizeof(T) == 4) {
-    return f <= 64 ? 16 : (f <= 128 ? 32 : 64);
-  } else {
-    return f <= 64 ? 8 : (f <= 128 ? 16 : (f <= 256 ? 32 : 64));
-  }
-}
 
 template <typename T, int GK, int GV, int FQK = 0, int FV = 0>
 void launch_attention_t(const AttArgs<T>& a, int64_t upper, int64_t chunk, float* pm, float* pl, float* pacc,

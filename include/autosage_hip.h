@@ -350,8 +350,8 @@ size_t as_csr_attention_plan_bytes(int64_t n);
  * composes its attention from torch ops, autosage/_auto.py:762-780); a plan
  * is built once per graph and serves every later attention call on it with
  * the same element type (dtype AS_DTYPE_F32 / BF16 / F16), whatever Q, K
- * and V.  An fp32 plan also serves the backward's passes over the graph,
- * and the backward's pass over the transposed graph takes an fp32 plan of
+ * and V.  It also serves the backward's pass over the graph (same element
+ * type), and the backward's pass over the transposed graph takes a plan of
  * that graph.  *plan_tag receives the settings it was built for, checked by
  * the calls.  Columns ascending within rows; asynchronous on `stream`. */
 int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n,
@@ -402,9 +402,11 @@ int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col,
                                  int64_t plan_tag, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
-/* Bytes of workspace for as_csr_attention_backward_f32. */
+/* Bytes of workspace for as_csr_attention_backward_f32 (dtype AS_DTYPE_F32)
+ * or as_csr_attention_backward_16 (AS_DTYPE_BF16 / AS_DTYPE_F16). */
 size_t as_csr_attention_backward_workspace_bytes(int64_t n, int64_t nnz,
-                                                 int64_t f_qk, int64_t f_v);
+                                                 int64_t f_qk, int64_t f_v,
+                                                 int dtype);
 
 /* Gradients of out = softmax_row(scale · SDDMM(query, key)) · value (the
  * attention of as_csr_attention_colslice_f32) in two gather passes, fp32:
@@ -418,7 +420,8 @@ size_t as_csr_attention_backward_workspace_bytes(int64_t n, int64_t nnz,
  * columns ascending within the rows of both graphs; a workspace smaller
  * than the preferred size runs the sliced rows in more chunks.
  * plan / plan_t: NULL, or fp32 plans of as_csr_attention_plan for the graph
- * and for the transposed graph with their tags; a pass without a plan
+ * and for the transposed graph with their tags (the 16-bit entry takes plans
+ * of its dtype); a pass without a plan
  * builds one in the workspace (as_csr_attention_plan_bytes(n) of the
  * preferred size are that region, needed unless both plans are given). */
 int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col,
@@ -432,6 +435,29 @@ int as_csr_attention_backward_f32(const int64_t* crow, const int64_t* col,
                                   int64_t plan_tag, const void* plan_t,
                                   int64_t plan_t_tag, void* workspace,
                                   size_t workspace_bytes, void* stream);
+
+/* as_csr_attention_backward_f32 for bf16 / fp16 query, key, value, grad_out
+ * and gradients (dtype AS_DTYPE_BF16 / AS_DTYPE_F16; the attention of
+ * as_csr_attention_colslice_16).  Inputs converted exactly to fp32, every
+ * sum in fp32, each gradient rounded once to the element type.  The output
+ * is not an argument: pass 1 sums t_r = Σ p·dP itself (the rounded 16-bit
+ * output would carry 2^-9 of relative error into it) and keeps
+ * Σ w·dP·K and Σ w·K apart (dQ = scale·(Σ w·dP·K − t·Σ w·K)/l).  No
+ * reference counterpart (its torch composition works in the feature type).
+ * f_qk and f_v multiples of 8 in [8, 512]; plans (of this dtype, for the
+ * graph and for its transpose) and workspace as for the fp32 entry, sized
+ * with this dtype.  Short rows of both passes run several to a wave. */
+int as_csr_attention_backward_16(const int64_t* crow, const int64_t* col,
+                                 const int64_t* crow_t, const int64_t* col_t,
+                                 const void* query, const void* key,
+                                 const void* value, const void* grad_out,
+                                 void* grad_q, void* grad_k, void* grad_v,
+                                 int64_t n, int64_t nnz, int64_t f_qk,
+                                 int64_t f_v, float scale, int dtype,
+                                 const void* plan, int64_t plan_tag,
+                                 const void* plan_t, int64_t plan_t_tag,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /* Bytes of workspace for the induced-sample entry points (n int32). */
 size_t as_induced_sample_workspace_bytes(int64_t n);

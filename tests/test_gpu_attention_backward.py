@@ -127,6 +127,23 @@ def test_colslice_attention_backward_schedules(monkeypatch):
         assert torch.max(torch.abs(a - b)) <= 2e-5 * torch.max(torch.abs(b))
 
 
+def _symmetric_hub_graph(n, seed):
+    """A = H ∪ Hᵀ for a hub graph H: symmetric, so its hubs are also hubs of
+    Aᵀ (both backward passes slice rows), with empty rows and the columns of
+    every row shuffled (the op sorts a copy)."""
+    h_crow, h_col = case_graph(n, 9, seed=seed, hubs=3, hub_degree=1800, empty=0.05)
+    rows = np.concatenate([np.repeat(np.arange(n), np.diff(h_crow)), h_col])
+    cols = np.concatenate([h_col, np.repeat(np.arange(n), np.diff(h_crow))])
+    keys = np.unique(rows * n + cols)
+    r, c = keys // n, keys % n
+    crow = np.concatenate([[0], np.cumsum(np.bincount(r, minlength=n))]).astype(np.int64)
+    rng = np.random.default_rng(seed)
+    perm = np.concatenate([rng.permutation(np.arange(crow[i], crow[i + 1])) for i in range(n)])
+    col = c[perm].astype(np.int64)
+    assert np.diff(crow).max() >= 1800
+    return crow, col, rng
+
+
 @pytest.mark.parametrize("fqk, fv", [(64, 128), (32, 48), (128, 128), (256, 64), (4, 8)])
 def test_two_pass_attention_backward(fqk, fv):
     """The column-sliced op's backward runs the two native passes: on a graph
@@ -135,18 +152,7 @@ def test_two_pass_attention_backward(fqk, fv):
     gradients (max-norm), and a second run gives the same bits.  The
     comparison with the recomputing chain is in the schedules test above."""
     n = 2500
-    h_crow, h_col = case_graph(n, 9, seed=fqk + fv, hubs=3, hub_degree=1800, empty=0.05)
-    # A = H ∪ Hᵀ: symmetric, so its hubs are also hubs of Aᵀ
-    rows = np.concatenate([np.repeat(np.arange(n), np.diff(h_crow)), h_col])
-    cols = np.concatenate([h_col, np.repeat(np.arange(n), np.diff(h_crow))])
-    keys = np.unique(rows * n + cols)
-    r, c = keys // n, keys % n
-    crow = np.concatenate([[0], np.cumsum(np.bincount(r, minlength=n))]).astype(np.int64)
-    # columns out of order inside every row (the op sorts a copy)
-    rng = np.random.default_rng(fqk)
-    perm = np.concatenate([rng.permutation(np.arange(crow[i], crow[i + 1])) for i in range(n)])
-    col = c[perm].astype(np.int64)
-    assert np.diff(crow).max() >= 1800  # symmetric: the hubs are in- and out-degree hubs
+    crow, col, rng = _symmetric_hub_graph(n, seed=fqk + fv)
     q = (rng.standard_normal((n, fqk)) * 0.25).astype(np.float32)
     k = (rng.standard_normal((n, fqk)) * 0.25).astype(np.float32)
     v = rng.standard_normal((n, fv)).astype(np.float32)
@@ -193,8 +199,9 @@ def test_two_pass_attention_backward_rows_without_edges_and_chunks(monkeypatch):
     from autosage_amd import _native
 
     lib = _native.library()
-    fixed = lib.as_csr_attention_backward_workspace_bytes(n, 0, 64, 128) - 8 * (64 + 128) * 4 - 768
-    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((fixed + 3 * 8 * (64 + 128) * 4 + 768) / 2**20))
+    # the preferred size less one row of partials and the alignment slack (5·256 bytes)
+    fixed = lib.as_csr_attention_backward_workspace_bytes(n, 0, 64, 128, 0) - 8 * (64 + 128) * 4 - 1280
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((fixed + 3 * 8 * (64 + 128) * 4 + 1280) / 2**20))
     chunked = grads()
     assert all(torch.equal(a, b) for a, b in zip(first, chunked))
 
@@ -223,9 +230,8 @@ def test_attention_plans_give_the_bits_of_per_call_set_up(dtype, monkeypatch):
         return [out] + [leaf.grad for leaf in leaves]
 
     planned = run()
-    # fp32: the plan of A (forward and pass 1) and of Aᵀ (pass 2); 16-bit: the
-    # forward's plan (its backward chains the native 16-bit stages)
-    assert len(_native._PLAN_MEMO) == before + (2 if dtype == torch.float32 else 1)
+    # the plan of A (forward and pass 1) and of Aᵀ (pass 2)
+    assert len(_native._PLAN_MEMO) == before + 2
     monkeypatch.setenv("AUTOSAGE_COLSLICE_PLAN", "off")
     unplanned = run()
     monkeypatch.delenv("AUTOSAGE_COLSLICE_PLAN")
@@ -237,3 +243,50 @@ def test_attention_plans_give_the_bits_of_per_call_set_up(dtype, monkeypatch):
     _autograd._TRANSPOSE_MEMO.clear()
     gc.collect()
     assert len(_native._PLAN_MEMO) == before
+
+
+# Rounding of a gradient to the 16-bit type: at most half an ulp, 2^-9 of the
+# value for bf16 and 2^-11 for fp16 (normal range); the bars allow twice that
+# plus fp32 error relative to the largest gradient.
+UNIT_16 = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -10}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fqk, fv", [(64, 128), (32, 48), (128, 128), (256, 64), (8, 8), (512, 16)])
+def test_two_pass_attention_backward_16(dtype, fqk, fv, monkeypatch):
+    """bf16 / fp16: the two native passes in fp32, each gradient rounded once.
+    Every element is within UNIT_16·|exact| + 2e-5·max|exact| of fp64 autograd
+    of the composition on the same (exactly converted) 16-bit inputs; the
+    result is deterministic and at least as accurate (root-mean-square error)
+    as the chain of native 16-bit stages (column slices off), which rounds
+    scores and probabilities."""
+    n = 2500
+    crow, col, rng = _symmetric_hub_graph(n, seed=fqk + 7 * fv)
+    arrays = [torch.from_numpy((rng.standard_normal((n, f)) * s_).astype(np.float32)).to(dtype)
+              for f, s_ in ((fqk, 0.25), (fqk, 0.25), (fv, 1.0), (fv, 1.0))]
+    q, k, v, g = arrays
+    d_crow, d_col = to_dev(crow, col)
+
+    def grads():
+        leaves = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+        torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *leaves, 0.125).backward(g.cuda())
+        return [leaf.grad for leaf in leaves]
+
+    got = grads()
+    assert all(t.dtype == dtype for t in got)
+    ref, ref_leaves = _attention_fp64(crow, col, *(t.float().numpy() for t in (q, k, v)), 0.125)
+    ref.backward(g.double())
+    errors = []
+    for t, leaf in zip(got, ref_leaves):
+        want = leaf.grad.numpy()
+        err = np.abs(t.cpu().double().numpy() - want)
+        bar = UNIT_16[dtype] * np.abs(want) + 2e-5 * np.max(np.abs(want))
+        assert np.all(err <= bar), (float(np.max(err - bar)), float(np.max(np.abs(want))))
+        errors.append(float(np.sqrt(np.mean(err ** 2))))
+    assert all(torch.equal(a, b) for a, b in zip(got, grads()))
+    # root-mean-square errors: both results carry the final rounding, the
+    # chain also the rounding of every score and probability
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
+    chained = grads()
+    for t, leaf, e in zip(chained, ref_leaves, errors):
+        assert e <= float(np.sqrt(np.mean((t.cpu().double().numpy() - leaf.grad.numpy()) ** 2)))
