@@ -115,26 +115,21 @@ def profiled_traffic(workload: str, variant: str):
     WRITE_SIZE runs for this exact workload and variant, read from the
     ``<!-- traffic: {...} -->`` record of a summary under profiles/; None when
     no record matches."""
-    same_workload = None
     for path in sorted((ROOT / "profiles").glob("*.md")):
         for line in path.read_text(encoding="utf-8").splitlines():
             line = line.strip()
             if line.startswith("<!-- traffic:") and line.endswith("-->"):
                 record = json.loads(line[len("<!-- traffic:"):-3])
-                if record.get("workload") != workload:
-                    continue
-                if record.get("variant") == variant:
+                if record.get("workload") == workload and record.get("variant") == variant:
                     return record
-                same_workload = same_workload or record
-    # Calibration can pick another variant of near-equal time than the one the
-    # counters were taken on; the record then says which variant it measured.
-    if same_workload is None and workload.endswith(" shuffled columns") and variant == "colslice":
+    if workload.endswith(" shuffled columns") and variant == "colslice":
         # the column-sliced kernels run on the row-sorted copy, which is the
         # unshuffled graph: the same launches and the same traffic
         base = profiled_traffic(workload[: -len(" shuffled columns")], variant)
-        if base is not None and base.get("variant") == variant:
+        if base is not None:
             return {**base, "source": base["source"] + " (row-sorted copy = the unshuffled graph)"}
-    return same_workload
+    # no record of this variant: the line falls back to the compulsory bytes
+    return None
 
 
 def time_steps(fn, steps: int, warmup: int) -> tuple[float, list[float]]:
@@ -631,11 +626,15 @@ def plan_record(step, args, crow, col, f, dtype, column_slices: bool, ms: float)
         if status != 0:
             raise RuntimeError(lib.as_last_error().decode())
         times.append(start.elapsed_time(end))
+    previous = os.environ.get("AUTOSAGE_COLSLICE_PLAN")
     os.environ["AUTOSAGE_COLSLICE_PLAN"] = "off"
     try:
         unplanned, _ = time_steps(step, max(5, args.steps // 2), 2)
     finally:
-        os.environ.pop("AUTOSAGE_COLSLICE_PLAN")
+        if previous is None:
+            os.environ.pop("AUTOSAGE_COLSLICE_PLAN")
+        else:
+            os.environ["AUTOSAGE_COLSLICE_PLAN"] = previous
     return {"reused": True, "build_ms": round(statistics.median(times[1:]), 4),
             "ms_per_step_rebuilding_it": round(unplanned, 4),
             "note": "slice points and the degree-binned row order are built once per graph (as_spmm_colslice_plan) "
