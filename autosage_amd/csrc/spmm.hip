@@ -369,13 +369,17 @@ struct SpmmArgs {
 
 int rows_per_wave(int layout) { return layout == kSub16 ? 4 : layout == kSub32 ? 2 : 1; }
 
-// Mean degree below which float4 sub-wave rows are used for short rows
-// (when vec4 is allowed).  Off by default: one wave per row with SGPR column
-// broadcast measured faster on every graph tried, including 16 nonzeros per
-// row (1.21 vs 1.30 ms on 2^20 rows, F = 128), because the sub-wave form
-// needs one vector load of the column index per edge.
+// Mean degree below which float4 sub-wave rows (16 or 32 lanes per row,
+// several rows per wave) are used for short rows when vec4 is allowed; the
+// same sums in the same order as one wave per row.  On graphs of a few
+// edges per row a wave per row leaves most of its lanes and issue slots
+// idle: the reference's Erdos-Renyi graph (200k rows, mean degree 4) takes
+// 40.1 against 68.4 us at F = 64 and 72.4 against 96.8 us at F = 128.  At
+// mean degree 8 (16,384 rows) both take 17.2 us; at 16 (2^20 rows,
+// F = 128) one wave per row with SGPR column broadcast is faster (1.22
+// against 1.26 ms), since the sub-wave form loads each column index per lane.
 #ifndef AS_SUBWAVE_MAX_MEAN_DEGREE
-#define AS_SUBWAVE_MAX_MEAN_DEGREE 0
+#define AS_SUBWAVE_MAX_MEAN_DEGREE 12
 #endif
 constexpr int64_t kSubwaveMaxMeanDegree = AS_SUBWAVE_MAX_MEAN_DEGREE;
 

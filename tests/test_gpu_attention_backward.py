@@ -173,7 +173,8 @@ def test_two_pass_attention_backward(fqk, fv):
     assert all(torch.equal(a.grad, b.grad) for a, b in zip(leaves, again))
 
 
-def test_two_pass_attention_backward_rows_without_edges_and_chunks(monkeypatch):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_two_pass_attention_backward_rows_without_edges_and_chunks(dtype, monkeypatch):
     """Rows and columns without edges get zero gradients; a small workspace
     (partial states for a few sliced rows) runs the sliced rows in chunks
     with the same bits."""
@@ -182,11 +183,12 @@ def test_two_pass_attention_backward_rows_without_edges_and_chunks(monkeypatch):
     col = col * (n - 100) // n  # columns n - 100 .. n - 1 get no edge (order kept, repeats allowed)
     rng = np.random.default_rng(5)
     arrays = [(rng.standard_normal((n, f)) * 0.25).astype(np.float32) for f in (64, 64, 128)]
-    g = torch.from_numpy(rng.standard_normal((n, 128)).astype(np.float32)).cuda()
+    g = torch.from_numpy(rng.standard_normal((n, 128)).astype(np.float32)).cuda().to(dtype)
     d_crow, d_col = to_dev(crow, col)
+    half = dtype != torch.float32
 
     def grads():
-        leaves = [torch.from_numpy(a).cuda().requires_grad_(True) for a in arrays]
+        leaves = [torch.from_numpy(a).cuda().to(dtype).requires_grad_(True) for a in arrays]
         torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *leaves, 0.125).backward(g)
         return [leaf.grad for leaf in leaves]
 
@@ -199,9 +201,11 @@ def test_two_pass_attention_backward_rows_without_edges_and_chunks(monkeypatch):
     from autosage_amd import _native
 
     lib = _native.library()
-    # the preferred size less one row of partials and the alignment slack (5·256 bytes)
-    fixed = lib.as_csr_attention_backward_workspace_bytes(n, 0, 64, 128, 0) - 8 * (64 + 128) * 4 - 1280
-    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((fixed + 3 * 8 * (64 + 128) * 4 + 1280) / 2**20))
+    # the preferred size less one row of partials (8 slices of the larger of
+    # pass 1's and pass 2's states) and the alignment slack (5·256 bytes)
+    row = 8 * max(64 * (2 if half else 1) + 3, 64 + 128) * 4
+    fixed = lib.as_csr_attention_backward_workspace_bytes(n, 0, 64, 128, 1 if half else 0) - row - 1280
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((fixed + 3 * row + 1280) / 2**20))
     chunked = grads()
     assert all(torch.equal(a, b) for a, b in zip(first, chunked))
 

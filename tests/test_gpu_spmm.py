@@ -46,6 +46,37 @@ def test_spmm_csr_bitwise(features, weighted, vec4, monkeypatch):
     assert bitwise_equal(got, ref), mismatch_report(got, ref)
 
 
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("features", [4, 16, 64, 68, 128, 132])
+def test_spmm_csr_short_rows_bitwise(features, weighted):
+    """Graphs of mean degree below 12 with float4 lanes take the sub-wave
+    rows (16 or 32 lanes per row, several rows per wave; F > 128 one wave per
+    row): the same sequential sums, so bitwise equal to the oracle, with empty
+    rows, a hub row and rows of different lengths in one wave."""
+    crow, col = case_graph(5000, 3, seed=features, hubs=1, hub_degree=900, empty=0.2)
+    assert col.size < 12 * 5000
+    rng = np.random.default_rng(features + 7)
+    val = rng.standard_normal(col.size).astype(np.float32) if weighted else None
+    x = rng.standard_normal((5000, features)).astype(np.float32)
+    ref = oracle.spmm_seq(crow, col, val, x)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    got = torch.ops.autosage.spmm_csr(d_crow, d_col, d_val, d_x)
+    torch.cuda.synchronize()
+    assert bitwise_equal(got, ref), mismatch_report(got, ref)
+    # the reference's Erdos-Renyi graph (200k rows, mean degree 4), sampled rows
+    if features == 64 and not weighted:
+        w = synth.erdos_renyi(seed=0, features=64)
+        d = to_dev(w.crow, w.col, None, w.dense["x"])
+        y = torch.ops.autosage.spmm_csr(*d).cpu().numpy()
+        rows = np.random.default_rng(0).choice(w.rows, 2000, replace=False)
+        for r in rows[:200]:
+            cols = w.col[w.crow[r]:w.crow[r + 1]]
+            want = np.zeros(64, dtype=np.float32)
+            for c in cols:
+                want = want + w.dense["x"][c]  # sequential fp32 adds in edge order
+            assert np.array_equal(y[r].view(np.uint32), want.view(np.uint32)), r
+
+
 @pytest.mark.parametrize("vec4", ["1", "0"])
 @pytest.mark.parametrize("tile", [64, 128])
 @pytest.mark.parametrize("waves", [2, 4, 8])
