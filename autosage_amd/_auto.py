@@ -28,7 +28,8 @@ from typing import Any, Callable, Optional
 
 import torch
 
-from ._cache import ScheduleCache, device_signature, graph_signature_memo, log_probe
+from . import _env
+from ._cache import cached_result, ScheduleCache, device_signature, graph_signature_memo, log_probe
 from .config import SchedulerConfig
 from .ops import _normalize_csr, load_native, native_load_error, native_op, spmm_csr, validate_if_requested
 
@@ -273,6 +274,26 @@ def _cached_native_available(operation: str, choice: str, candidate) -> bool:
     return native_op(operation + ("_split" if candidate is not None else "")) is not None
 
 
+def _cached_record(crow, col, width: int, operation: str, config: SchedulerConfig, *, weighted: bool = False,
+                   dtype=None) -> Optional[dict[str, Any]]:
+    """The cached result for this device, graph, width, operation and
+    configuration (``_auto.py:291-300`` of the reference: device and graph
+    signatures, canonical-JSON key, schema and tuning-signature check), or
+    None.  Memoised per live, unmodified (crow, col) pair while the schedule
+    file is unchanged, so a repeated call skips the signatures and the key."""
+
+    def lookup(cache: ScheduleCache) -> Optional[dict[str, Any]]:
+        device = device_signature()
+        graph = graph_signature_memo(crow, col, width, operation, weighted=weighted, dtype=dtype)
+        record = cache.lookup(device, graph)
+        if record is None or not _cache_hit_allowed(record.get("result", {}), config):
+            return None
+        return record["result"]
+
+    extra = (operation, int(width), bool(weighted), str(dtype), config, torch.cuda.current_device())
+    return cached_result(crow, col, extra, lookup)
+
+
 def _cpu_info(operation: str) -> dict[str, Any]:
     return {
         "operation": operation,
@@ -409,7 +430,7 @@ def _replay_miss(operation: str, baseline_name: str) -> dict[str, Any]:
 
 
 def _verbose(tag: str, result: dict[str, Any], verbose: bool) -> None:
-    if verbose or os.getenv("AUTOSAGE_VERBOSE") == "1":
+    if verbose or _env.get("AUTOSAGE_VERBOSE") == "1":
         print(
             f"[autosage:{tag}] rows={result['probe_rows']} nnz={result['probe_nonzeros']} "
             f"baseline={result['baseline_probe_ms']} ms auto={result['autosage_probe_ms']} "
@@ -441,18 +462,17 @@ def spmm_csr_auto(
 
     _require_native()
     config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=k)
-    device = device_signature()
-    graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
-    cache = ScheduleCache()
     if config.cache:
-        record = cache.lookup(device, graph)
-        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
-            result = record["result"]
+        result = _cached_record(crow, col, x.size(1), "spmm", config, weighted=val is not None, dtype=x.dtype)
+        if result is not None:
             choice, candidate = result.get("choice", "baseline"), result.get("candidate")
             if _cached_native_available("spmm_csr", choice, candidate):
                 return _run_spmm_choice(choice, candidate, crow, col, val, x), {**result, "from_cache": True}
     if config.replay_only:
         return _run_spmm_choice("baseline", None, crow, col, val, x), _replay_miss("spmm", "torch.sparse.mm(csr)")
+    device = device_signature()
+    graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
+    cache = ScheduleCache()
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -509,16 +529,14 @@ def _spmm_auto_16(crow, col, val, x, config: SchedulerConfig, verbose: bool) -> 
     graph and the fastest is cached under the usual key, which includes the
     dtype.  The PyTorch
     baseline cannot be run for these types here (see _BASELINE_16_NOTE)."""
+    if config.cache:
+        result = _cached_record(crow, col, x.size(1), "spmm", config, weighted=val is not None, dtype=x.dtype)
+        if result is not None and result.get("candidate") in _ROUNDED16_ALL:
+            return (_run_spmm_choice("autosage", result["candidate"], crow, col, val, x),
+                    {**result, "from_cache": True})
     device = device_signature()
     graph = graph_signature_memo(crow, col, x.size(1), "spmm", weighted=val is not None, dtype=x.dtype)
     cache = ScheduleCache()
-    if config.cache:
-        record = cache.lookup(device, graph)
-        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
-            result = record["result"]
-            if result.get("candidate") in _ROUNDED16_ALL:
-                return (_run_spmm_choice("autosage", result["candidate"], crow, col, val, x),
-                        {**result, "from_cache": True})
     if config.replay_only:
         info = _replay_miss("spmm", "torch.sparse.mm(csr)")
         info.update(choice="autosage", candidate=ROUNDED16, reason="cache miss; " + _BASELINE_16_NOTE)
@@ -737,18 +755,17 @@ def sddmm_csr_auto(
 
     _require_native()
     config = SchedulerConfig.from_env(guardrail=guardrail, candidate_count=6)
-    device = device_signature()
-    graph = graph_signature_memo(crow, col, query.size(1), "sddmm", dtype=query.dtype)
-    cache = ScheduleCache()
     if config.cache:
-        record = cache.lookup(device, graph)
-        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
-            result = record["result"]
+        result = _cached_record(crow, col, query.size(1), "sddmm", config, dtype=query.dtype)
+        if result is not None:
             choice, candidate = result.get("choice", "baseline"), result.get("candidate")
             if _cached_native_available("sddmm_csr", choice, candidate):
                 return _run_sddmm_choice(choice, candidate, crow, col, query, key), {**result, "from_cache": True}
     if config.replay_only:
         return _run_sddmm_choice("baseline", None, crow, col, query, key), _replay_miss("sddmm", "gather-dot")
+    device = device_signature()
+    graph = graph_signature_memo(crow, col, query.size(1), "sddmm", dtype=query.dtype)
+    cache = ScheduleCache()
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -813,17 +830,15 @@ def _sddmm_auto_16(crow, col, query, key, config: SchedulerConfig, verbose: bool
     whatever the split, so the split points of ``_SDDMM_16_OPTIONS`` are
     timed once on the full graph and the faster is cached under the usual key
     (which includes the dtype)."""
+    options = [list(o) for o in _SDDMM_16_OPTIONS]
+    if config.cache:
+        result = _cached_record(crow, col, query.size(1), "sddmm", config, dtype=query.dtype)
+        if result is not None and result.get("choice") == "autosage" and result.get("candidate") in options:
+            return (_run_sddmm_choice("autosage", result["candidate"], crow, col, query, key),
+                    {**result, "from_cache": True})
     device = device_signature()
     graph = graph_signature_memo(crow, col, query.size(1), "sddmm", dtype=query.dtype)
     cache = ScheduleCache()
-    options = [list(o) for o in _SDDMM_16_OPTIONS]
-    if config.cache:
-        record = cache.lookup(device, graph)
-        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
-            result = record["result"]
-            if result.get("choice") == "autosage" and result.get("candidate") in options:
-                return (_run_sddmm_choice("autosage", result["candidate"], crow, col, query, key),
-                        {**result, "from_cache": True})
     if config.replay_only:
         info = _replay_miss("sddmm", "gather-dot")
         info.update(choice="autosage", candidate=options[0], reason="cache miss; " + _SDDMM_16_NOTE)
@@ -912,15 +927,14 @@ def _attention_variant(crow, col, q, k, v, scale: float) -> tuple[str, dict[str,
     config = SchedulerConfig.from_env()
     if not _attention_colslice_eligible(crow, col, q, v, config):
         return "fused", {"variant": "fused", "from_cache": False}
-    device = device_signature()
-    graph = graph_signature_memo(crow, col, q.size(1), f"attention:fv={v.size(1)}", dtype=q.dtype)
-    cache = ScheduleCache()
+    operation = f"attention:fv={v.size(1)}"
     if config.cache:
-        record = cache.lookup(device, graph)
-        if record is not None and _cache_hit_allowed(record.get("result", {}), config):
-            result = record["result"]
-            if result.get("variant") in ("fused", "colslice"):
-                return result["variant"], {**result, "from_cache": True}
+        result = _cached_record(crow, col, q.size(1), operation, config, dtype=q.dtype)
+        if result is not None and result.get("variant") in ("fused", "colslice"):
+            return result["variant"], {**result, "from_cache": True}
+    device = device_signature()
+    graph = graph_signature_memo(crow, col, q.size(1), operation, dtype=q.dtype)
+    cache = ScheduleCache()
     times = {}
     for name, op in (("fused", native_op("csr_attention")), ("colslice", native_op("csr_attention_colslice"))):
         times[name] = _time_cuda(lambda o=op: o(crow, col, q, k, v, scale), warmup=1, iterations=3)["best_ms"]
@@ -939,7 +953,7 @@ def _attention_variant(crow, col, q, k, v, scale: float) -> tuple[str, dict[str,
 
 
 def _fused_default() -> bool:
-    return os.getenv("AUTOSAGE_FUSED_ATTENTION", "1") == "1"
+    return _env.get("AUTOSAGE_FUSED_ATTENTION", "1") == "1"
 
 
 def csr_attention_forward(

@@ -24,6 +24,9 @@ from typing import Any, Optional
 
 import torch
 
+from . import _env
+from ._memo import GraphMemo
+
 CACHE_SCHEMA_VERSION = 1
 _HASH_EDGE = 1024  # entries hashed from each end of a long index vector
 
@@ -36,25 +39,45 @@ _SIGNATURE_MEMO_SIZE = 64
 _FILE_MEMO: dict[str, tuple[int, int, dict]] = {}
 
 
+_DIRECTORY_MEMO: dict[Optional[str], Path] = {}
+
+
 def cache_directory() -> Path:
-    configured = os.getenv("AUTOSAGE_CACHE_DIR")
-    return Path(configured).expanduser() if configured else Path.home() / ".cache" / "autosage"
+    configured = _env.get("AUTOSAGE_CACHE_DIR")
+    path = _DIRECTORY_MEMO.get(configured)
+    if path is None:
+        path = Path(configured).expanduser() if configured else Path.home() / ".cache" / "autosage"
+        _DIRECTORY_MEMO[configured] = path
+    return path
+
+
+def schedule_file() -> Path:
+    """The schedule cache file of the current ``AUTOSAGE_CACHE_DIR``."""
+    return cache_directory() / "schedules.json"
+
+
+_DEVICE_MEMO: dict[int, dict[str, Any]] = {}
 
 
 def device_signature(device: Optional[int] = None) -> dict[str, Any]:
     if not torch.cuda.is_available():
         return {"type": "cpu", "torch": torch.__version__}
     index = torch.cuda.current_device() if device is None else device
-    props = torch.cuda.get_device_properties(index)
-    return {
-        "type": "cuda",
-        "name": props.name,
-        "compute_capability": [props.major, props.minor],
-        "multiprocessors": props.multi_processor_count,
-        "total_memory": int(props.total_memory),
-        "cuda": torch.version.cuda,
-        "torch": torch.__version__,
-    }
+    signature = _DEVICE_MEMO.get(index)
+    if signature is None:
+        # a device's properties do not change while the process runs
+        props = torch.cuda.get_device_properties(index)
+        signature = {
+            "type": "cuda",
+            "name": props.name,
+            "compute_capability": [props.major, props.minor],
+            "multiprocessors": props.multi_processor_count,
+            "total_memory": int(props.total_memory),
+            "cuda": torch.version.cuda,
+            "torch": torch.__version__,
+        }
+        _DEVICE_MEMO[index] = signature
+    return {**signature, "compute_capability": list(signature["compute_capability"])}
 
 
 def _hash_slice(tensor: torch.Tensor) -> torch.Tensor:
@@ -148,22 +171,23 @@ def _file_stamp(path: Path) -> Optional[tuple[int, int]]:
 
 class ScheduleCache:
     def __init__(self, path: Optional[os.PathLike[str] | str] = None):
-        self.path = Path(path) if path is not None else cache_directory() / "schedules.json"
+        self.path = Path(path) if path is not None else schedule_file()
         self._records = self._load_memo()
 
     def _load_memo(self) -> dict[str, dict[str, Any]]:
         """``_load`` unless the file is unchanged (same mtime and size) since
-        this process last parsed or wrote it."""
+        this process last parsed or wrote it.  The records are shared with
+        the memo and copied before ``store`` changes them."""
         stamp = _file_stamp(self.path)
         key = str(self.path)
         with _MEMO_LOCK:
             memo = _FILE_MEMO.get(key)
             if stamp is not None and memo is not None and memo[:2] == stamp:
-                return dict(memo[2])
+                return memo[2]
         records = self._load()
         if stamp is not None:
             with _MEMO_LOCK:
-                _FILE_MEMO[key] = (*stamp, dict(records))
+                _FILE_MEMO[key] = (*stamp, records)
         return records
 
     @staticmethod
@@ -187,12 +211,14 @@ class ScheduleCache:
 
     def store(self, device: dict[str, Any], graph: dict[str, Any], result: dict[str, Any]) -> None:
         self.path.parent.mkdir(parents=True, exist_ok=True)
-        self._records[self._key(device, graph)] = {
+        records = dict(self._records)  # the loaded records may be shared with the memo
+        records[self._key(device, graph)] = {
             "timestamp": int(time.time()),
             "device": device,
             "graph": graph,
             "result": result,
         }
+        self._records = records
         payload = {"schema_version": CACHE_SCHEMA_VERSION, "records": self._records}
         fd, temporary = tempfile.mkstemp(prefix="schedules-", suffix=".json", dir=self.path.parent)
         try:
@@ -206,11 +232,31 @@ class ScheduleCache:
         stamp = _file_stamp(self.path)
         if stamp is not None:
             with _MEMO_LOCK:
-                _FILE_MEMO[str(self.path)] = (*stamp, dict(self._records))
+                _FILE_MEMO[str(self.path)] = (*stamp, self._records)
+
+
+# The cache record a repeated call replays, per live (crow, col) pair and the
+# call's settings, so that a steady-state call skips the device and graph
+# signatures, the canonical-JSON key and the record lookup.  The schedule
+# file's stamp (mtime, size) is part of the key: a file written since (by this
+# or another process) is looked up again.
+_DECISION_MEMO = GraphMemo("cached_decision", max_entries=64)
+
+
+def cached_result(crow: torch.Tensor, col: torch.Tensor, extra: tuple,
+                  lookup) -> Optional[dict[str, Any]]:
+    """``lookup(cache)`` (the cached result or None) memoised per live,
+    unmodified (crow, col), ``extra`` (the caller's settings) and the current
+    schedule file and its stamp."""
+    path = schedule_file()
+    stamp = _file_stamp(path)
+    if stamp is None:
+        return lookup(ScheduleCache(path))
+    return _DECISION_MEMO.get((crow, col), (extra, str(path), stamp), lambda: lookup(ScheduleCache(path)))
 
 
 def log_probe(event: dict[str, Any]) -> None:
-    if os.getenv("AUTOSAGE_LOG_PROBES", "1") != "1":
+    if _env.get("AUTOSAGE_LOG_PROBES", "1") != "1":
         return
     path = cache_directory() / "probe_logs.jsonl"
     path.parent.mkdir(parents=True, exist_ok=True)

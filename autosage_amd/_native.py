@@ -24,6 +24,7 @@ from typing import Optional
 
 import torch
 
+from . import _env
 from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
@@ -186,14 +187,14 @@ def _raise(status: int, what: str) -> None:
 
 
 def _env_vec4() -> bool:
-    value = os.getenv("AUTOSAGE_VEC4")
+    value = _env.get("AUTOSAGE_VEC4")
     if value is None:
         return True
     return value.strip().lower() not in {"0", "false", "no", "off"}
 
 
 def _env_hub_mode() -> int:
-    value = (os.getenv("AUTOSAGE_HUB_MODE") or "exact").strip().lower()
+    value = (_env.get("AUTOSAGE_HUB_MODE") or "exact").strip().lower()
     if value in {"exact", "0"}:
         return HUB_EXACT
     if value in {"split64", "1"}:
@@ -298,7 +299,7 @@ def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_th
 
 
 def _colslice_workspace_cap() -> int:
-    return int(float(os.getenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", "4096")) * 2**20)
+    return int(float(_env.get("AUTOSAGE_COLSLICE_WORKSPACE_MB", "4096")) * 2**20)
 
 
 def spmm_csr_colslice_impl(crow, col, val, x):
@@ -338,7 +339,7 @@ def colslice_plans_enabled() -> bool:
     """Whether the column-sliced SpMM reuses a per-graph plan (slice points
     and binned row order) across calls; ``AUTOSAGE_COLSLICE_PLAN=off`` builds
     them on every call instead (same bits)."""
-    return os.getenv("AUTOSAGE_COLSLICE_PLAN", "on").lower() != "off"
+    return _env.get("AUTOSAGE_COLSLICE_PLAN", "on").lower() != "off"
 
 
 # A plan holds about 28 bytes per row (6.5 MB for a 233k-row graph).
@@ -872,7 +873,7 @@ def sliced_rows(crow: torch.Tensor, column_slices: bool, f: int, dtype: torch.dt
 
 
 def _maybe_validate(crow: torch.Tensor, col: torch.Tensor) -> None:
-    if os.getenv("AUTOSAGE_VALIDATE") == "1":
+    if _env.get("AUTOSAGE_VALIDATE") == "1":
         validate_csr(crow, col)
 
 

@@ -17,18 +17,19 @@ keeps SpMM results bit-identical to the sequential CSR product.
 
 from __future__ import annotations
 
-import os
 from dataclasses import dataclass
 from typing import Optional
 
+from . import _env
+
 
 def _optional_int(name: str) -> Optional[int]:
-    raw = os.getenv(name)
+    raw = _env.get(name)
     return None if raw in (None, "") else int(raw)
 
 
 def _boolean(name: str, default: bool) -> bool:
-    raw = os.getenv(name)
+    raw = _env.get(name)
     if raw is None:
         return default
     word = raw.strip().lower()
@@ -102,7 +103,22 @@ class SchedulerConfig:
 
     @classmethod
     def from_env(cls, *, guardrail: float = 0.95, candidate_count: int = 6) -> "SchedulerConfig":
-        env = os.getenv
+        """The configuration the environment gives now (read on every call,
+        as the reference does); the parsed value is memoised per set of raw
+        environment values, so an unchanged environment costs twenty dict
+        lookups.  Invalid values raise on every call."""
+        key = (_env.raw(_ENV_NAMES), float(guardrail), int(candidate_count))
+        config = _FROM_ENV_MEMO.get(key)
+        if config is None:
+            config = cls._parse_env(guardrail, candidate_count)
+            if len(_FROM_ENV_MEMO) > 64:
+                _FROM_ENV_MEMO.clear()
+            _FROM_ENV_MEMO[key] = config
+        return config
+
+    @classmethod
+    def _parse_env(cls, guardrail: float, candidate_count: int) -> "SchedulerConfig":
+        env = _env.get
         return cls(
             guardrail=float(guardrail),
             probe_fraction=float(env("AUTOSAGE_PROBE_FRAC", "0.03")),
@@ -123,3 +139,13 @@ class SchedulerConfig:
             full_graph_check=_boolean("AUTOSAGE_FULL_CHECK", True),
             column_slices=(env("AUTOSAGE_COLUMN_SLICES") or "auto").strip().lower(),
         )
+
+
+# Every environment variable from_env reads.
+_ENV_NAMES = (
+    "AUTOSAGE_PROBE_FRAC", "AUTOSAGE_PROBE_MIN_ROWS", "AUTOSAGE_PROBE_ITERS", "AUTOSAGE_PROBE_CAP_MS",
+    "AUTOSAGE_MIN_PROBE_ROWS", "AUTOSAGE_MIN_PROBE_NNZ", "AUTOSAGE_HUB_CTA", "AUTOSAGE_VEC4", "AUTOSAGE_CACHE",
+    "AUTOSAGE_REPLAY_ONLY", "AUTOSAGE_FTILE", "AUTOSAGE_WPB", "AUTOSAGE_HUB_T", "AUTOSAGE_HUB_MODE",
+    "AUTOSAGE_FULL_CHECK", "AUTOSAGE_COLUMN_SLICES",
+)
+_FROM_ENV_MEMO: dict = {}

