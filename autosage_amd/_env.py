@@ -16,34 +16,59 @@ import os
 from typing import Optional
 
 _KEYS: dict[str, bytes] = {}
+_NAME_KEYS: dict[tuple, tuple] = {}
 _VALUES: dict[bytes, str] = {}
 _MAX_VALUES = 4096
+# (os.environ object, its encoded mapping or None, encodekey, decodevalue)
+_STATE: Optional[tuple] = None
 
 
-def get(name: str, default: Optional[str] = None) -> Optional[str]:
-    """``os.environ.get(name, default)``."""
+def _state() -> tuple:
+    global _STATE
     env = os.environ
-    data = getattr(env, "_data", None)
-    encode = getattr(env, "encodekey", None)
-    decode = getattr(env, "decodevalue", None)
-    if not isinstance(data, dict) or encode is None or decode is None:
-        return env.get(name, default)
+    state = _STATE
+    if state is None or state[0] is not env:
+        data = getattr(env, "_data", None)
+        encode = getattr(env, "encodekey", None)
+        decode = getattr(env, "decodevalue", None)
+        usable = isinstance(data, dict) and encode is not None and decode is not None
+        state = (env, data if usable else None, encode, decode)
+        _STATE = state
+    return state
+
+
+def _key(name: str, encode) -> bytes:
     key = _KEYS.get(name)
     if key is None:
         key = encode(name)
         _KEYS[name] = key
-    raw = data.get(key)
-    if raw is None:
+    return key
+
+
+def get(name: str, default: Optional[str] = None) -> Optional[str]:
+    """``os.environ.get(name, default)``."""
+    env, data, encode, decode = _state()
+    if data is None:
+        return env.get(name, default)
+    raw_value = data.get(_key(name, encode))
+    if raw_value is None:
         return default
-    value = _VALUES.get(raw)
+    value = _VALUES.get(raw_value)
     if value is None:
-        value = decode(raw)
+        value = decode(raw_value)
         if len(_VALUES) < _MAX_VALUES:
-            _VALUES[raw] = value
+            _VALUES[raw_value] = value
     return value
 
 
 def raw(names: tuple[str, ...]) -> tuple:
-    """The current values of ``names`` (None when unset), cheap enough to key
-    a memo of what is parsed from them."""
-    return tuple(get(n) for n in names)
+    """The current values of ``names`` (None when unset), undecoded where the
+    platform allows: a cheap key for a memo of what is parsed from them."""
+    env, data, encode, _ = _state()
+    if data is None:
+        return tuple(env.get(n) for n in names)
+    keys = _NAME_KEYS.get(names)
+    if keys is None:
+        keys = tuple(_key(n, encode) for n in names)
+        _NAME_KEYS[names] = keys
+    return tuple(map(data.get, keys))

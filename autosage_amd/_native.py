@@ -17,6 +17,7 @@ as ``TORCH_CHECK`` does.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 from pathlib import Path
@@ -176,6 +177,18 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+_NO_GUARD = contextlib.nullcontext()
+
+
+def _on(device: torch.device):
+    """``torch.cuda.device(device)``, or nothing when that device is already
+    the current one (the common case; entering the guard costs microseconds
+    on every call)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _NO_GUARD
+    return torch.cuda.device(device)
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -268,7 +281,7 @@ def spmm_csr_impl(crow, col, val, x):
     n, f = x.shape
     if n == 0 or f == 0:
         return y
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         status = library().as_spmm_csr_f32(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, int(_env_vec4()), _stream(x.device)
         )
@@ -288,7 +301,7 @@ def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_th
         return y
     lib = library()
     ws = _workspace(lib.as_spmm_split_workspace_bytes(n), x.device)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         status = lib.as_spmm_csr_split_f32(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, int(feature_tile),
             int(warps_per_block), int(hub_threshold), int(_env_vec4()), _env_hub_mode(), _ptr(ws), ws.numel(),
@@ -326,7 +339,7 @@ def spmm_csr_colslice_impl(crow, col, val, x):
     # smaller cap runs the pipeline in more, smaller chunks
     full = lib.as_spmm_colslice_workspace_bytes(n, f)
     ws = _workspace(min(full, _colslice_workspace_cap()), x.device)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         status = lib.as_spmm_csr_colslice_f32(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, _ptr(ws), ws.numel(),
             sliced_rows(crow, True, f, x.dtype), _stream(x.device),
@@ -362,7 +375,7 @@ def colslice_plan(crow: torch.Tensor, col: torch.Tensor, f: int, dtype: torch.dt
         n = crow.numel() - 1
         plan = _workspace(lib.as_spmm_colslice_plan_bytes(n), crow.device)
         tag = ctypes.c_int64(0)
-        with torch.cuda.device(crow.device):
+        with _on(crow.device):
             status = lib.as_spmm_colslice_plan(_ptr(crow), _ptr(col), n, col.numel(), f, code, int(bool(column_slices)),
                                                _ptr(plan), plan.numel(), ctypes.byref(tag), _stream(crow.device))
             _raise(status, "autosage column-sliced plan")
@@ -384,7 +397,7 @@ def _spmm_colslice_planned(crow, col, val, x, y, column_slices: bool, sliced: in
     plan, tag = colslice_plan(crow, col, f, x.dtype, column_slices)
     needed = lib.as_spmm_colslice_planned_workspace_bytes(n, f, code, sliced)
     ws = _workspace(max(min(needed, _colslice_workspace_cap() - plan.numel()), 0), x.device)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         status = lib.as_spmm_csr_colslice_planned(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, code, int(column_slices),
             _ptr(plan), plan.numel(), tag, _ptr(ws), ws.numel(), sliced, grouped, _stream(x.device),
@@ -407,7 +420,7 @@ def spmm_rows_16_impl(crow, col, val, x):
     n, f = x.shape
     if n == 0 or f == 0:
         return y
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         status = library().as_spmm_csr_rows_16(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, DTYPES_16[x.dtype],
             _stream(x.device),
@@ -437,7 +450,7 @@ def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
     # whole, with the same bits)
     needed = lib.as_spmm_rounded_16_workspace_bytes(n, f, sliced)
     ws = _workspace(min(needed, _colslice_workspace_cap()), x.device)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         status = lib.as_spmm_csr_rounded_16(
             _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, DTYPES_16[x.dtype],
             int(bool(column_slices)), _ptr(ws), ws.numel(), sliced, grouped, _stream(x.device),
@@ -474,7 +487,7 @@ def sddmm_csr_impl(crow, col, query, key):
     out = torch.empty(nnz, dtype=query.dtype, device=query.device)
     if n == 0 or nnz == 0:
         return out
-    with torch.cuda.device(query.device):
+    with _on(query.device):
         status = library().as_sddmm_csr_f32(
             _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, _stream(query.device)
         )
@@ -498,7 +511,7 @@ def sddmm_csr_split_impl(crow, col, query, key, warps_per_block, hub_threshold):
         return out
     lib = library()
     ws = _workspace(lib.as_sddmm_split_workspace_bytes(n), query.device)
-    with torch.cuda.device(query.device):
+    with _on(query.device):
         status = lib.as_sddmm_csr_split_f32(
             _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, int(warps_per_block),
             int(hub_threshold), _ptr(ws), ws.numel(), _stream(query.device),
@@ -527,7 +540,7 @@ def sddmm_rounded_16_impl(crow, col, query, key, warps_per_block: int, hub_thres
         return out
     lib = library()
     ws = _workspace(lib.as_sddmm_split_workspace_bytes(n), query.device)
-    with torch.cuda.device(query.device):
+    with _on(query.device):
         status = lib.as_sddmm_csr_rounded_16(
             _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, DTYPES_16[query.dtype],
             int(warps_per_block), int(hub_threshold), _ptr(ws), ws.numel(), _stream(query.device),
@@ -547,7 +560,7 @@ def csr_row_softmax_impl(crow, scores):
     n = crow.numel() - 1
     if n <= 0 or scores.numel() == 0:
         return probs
-    with torch.cuda.device(scores.device):
+    with _on(scores.device):
         if scores.dtype in DTYPES_16:
             # fp32 softmax of the exactly converted scores, rounded once
             status = library().as_csr_row_softmax_16(
@@ -577,7 +590,7 @@ def csr_row_softmax_backward_impl(crow, probs, grad):
     if n <= 0 or probs.numel() == 0:
         return out.zero_()
     dtype = 0 if probs.dtype == torch.float32 else DTYPES_16[probs.dtype]
-    with torch.cuda.device(probs.device):
+    with _on(probs.device):
         status = library().as_csr_row_softmax_backward(
             _ptr(crow), _ptr(probs), _ptr(grad), _ptr(out), n, probs.numel(), dtype, _stream(probs.device)
         )
@@ -604,7 +617,7 @@ def csr_attention_impl(crow, col, query, key, value, scale=1.0):
         return spmm_csr_impl(crow, col, csr_row_softmax_impl(crow, scores), value)
     lib = library()
     ws = _workspace(lib.as_csr_attention_workspace_bytes(n, nnz), query.device)
-    with torch.cuda.device(query.device):
+    with _on(query.device):
         status = lib.as_csr_attention_f32(
             _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv, float(scale),
             _ptr(ws), ws.numel(), _stream(query.device),
@@ -655,7 +668,7 @@ def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
     # the workspace cap counts the plan, as in a call that builds it
     size = min(lib.as_csr_attention_colslice_workspace_bytes(n, nnz, fv), _colslice_workspace_cap())
     ws = _workspace(size - (plan.numel() if plan is not None else 0), query.device)
-    with torch.cuda.device(query.device):
+    with _on(query.device):
         if half:
             status = lib.as_csr_attention_colslice_16(
                 _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv,
@@ -684,7 +697,7 @@ def attention_plan(crow: torch.Tensor, col: torch.Tensor, dtype: torch.dtype) ->
         n = crow.numel() - 1
         plan = _workspace(lib.as_csr_attention_plan_bytes(n), crow.device)
         tag = ctypes.c_int64(0)
-        with torch.cuda.device(crow.device):
+        with _on(crow.device):
             status = lib.as_csr_attention_plan(_ptr(crow), _ptr(col), n, col.numel(), code, _ptr(plan), plan.numel(),
                                                ctypes.byref(tag), _stream(crow.device))
             _raise(status, "autosage attention plan")
@@ -737,7 +750,7 @@ def csr_attention_backward_impl(crow, col, crow_t, col_t, query, key, value, out
         plan_t, tag_t = attention_plan(crow_t, col_t, query.dtype)
         size -= plan.numel()
     ws = _workspace(size, query.device)
-    with torch.cuda.device(query.device):
+    with _on(query.device):
         if code == 0:
             status = lib.as_csr_attention_backward_f32(
                 _ptr(crow), _ptr(col), _ptr(crow_t), _ptr(col_t), _ptr(query), _ptr(key), _ptr(value), _ptr(out),
@@ -782,7 +795,7 @@ def csr_flags(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = Non
     if n < 0:
         raise ValueError("crow must contain N + 1 entries")
     flags = torch.zeros(1, dtype=torch.int32, device=crow.device)
-    with torch.cuda.device(crow.device):
+    with _on(crow.device):
         status = library().as_csr_validate(_ptr(crow), _ptr(col), n, col.numel(), n if n_cols is None else n_cols,
                                            _ptr(flags), _stream(crow.device))
     _raise(status, "csr_validate")
@@ -892,7 +905,7 @@ def induced_sample(crow: torch.Tensor, col: torch.Tensor, val: Optional[torch.Te
     lib = library()
     ws = _workspace(lib.as_induced_sample_workspace_bytes(n), crow.device)
     new_crow = torch.empty(s + 1, dtype=torch.long, device=crow.device)
-    with torch.cuda.device(crow.device):
+    with _on(crow.device):
         stream = _stream(crow.device)
         _raise(lib.as_induced_sample_count(_ptr(crow), _ptr(col), n, _ptr(selected), s, _ptr(new_crow), _ptr(ws),
                                            ws.numel(), stream), "induced_sample")
@@ -916,7 +929,7 @@ def bin_rows_by_degree(crow: torch.Tensor, threshold: int) -> tuple[torch.Tensor
     counts = torch.zeros(4, dtype=torch.int32, device=crow.device)
     lib = library()
     ws = _workspace(lib.as_bin_workspace_bytes(n), crow.device)
-    with torch.cuda.device(crow.device):
+    with _on(crow.device):
         status = lib.as_bin_rows_by_degree(
             _ptr(crow), n, int(threshold), _ptr(order), _ptr(counts), _ptr(ws), ws.numel(), _stream(crow.device)
         )

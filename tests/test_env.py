@@ -20,7 +20,14 @@ def test_get_follows_os_environ(monkeypatch):
         assert _env.get(name) == os.environ.get(name) == value
     monkeypatch.delenv(name)
     assert _env.get(name, "gone") == "gone"
-    assert _env.raw((name, "PATH")) == (None, os.environ.get("PATH"))
+    # raw values key memos: equal exactly when the values are
+    monkeypatch.setenv(name, "a")
+    first = _env.raw((name, "PATH"))
+    assert first == _env.raw((name, "PATH"))
+    monkeypatch.setenv(name, "b")
+    assert _env.raw((name, "PATH")) != first
+    monkeypatch.delenv(name)
+    assert _env.raw((name,)) == (None,)
 
 
 def test_from_env_sees_every_change(monkeypatch):
