@@ -521,9 +521,37 @@ struct SliceChunk {
 
 // Where the grouped short rows (16-bit, degree below 4·G) start in the order:
 // the start of a light degree bucket of the binning, read on the device.
+// Device-side bucket boundaries of the binned order, read by the step
+// kernels: where the grouped short rows start, and where the rows of the
+// cooperative ("mega") degree end.
 struct GroupedRows {
   const int32_t* start;  // null: no grouped rows
+  const int32_t* mega_end = nullptr;  // null: no cooperative rows
 };
+
+// Rows of degree >= T·2^kMegaLevel (T the slicing degree; 8192 at T = 128)
+// are the first heavy buckets of the order.  On graphs of at most
+// kMegaMaxNnz edges all waves of a slice workgroup share one (row, slice) of
+// such a row, each summing an equal run of its edges; the fp64 partials are
+// added in wave order through LDS, so a hub row's slice no longer rests on
+// one wave.  Wide lanes only (V >= 8).  The reference's hub sweep (20,000
+// rows, one row of 12,000 edges, the others 32) takes 74.7 against 152.5 us;
+// on larger graphs the other rows fill the GPU beside the hub slices and the
+// workgroup's waiting costs more than it saves (the skewed 115M-edge graph at
+// F = 128: 3.494 against 3.449 ms), so it stays off there.  Which rows
+// cooperate depends only on N, nnz and the degrees, never on a launch hint.
+#ifndef AS_COLSLICE_MEGA_LEVEL
+#define AS_COLSLICE_MEGA_LEVEL 6
+#endif
+constexpr int kMegaLevel = AS_COLSLICE_MEGA_LEVEL;
+constexpr int64_t kMegaMaxNnz = int64_t(1) << 24;
+
+// An fp64 sum kept in LDS (plain stores, where partial rows in memory take
+// non-temporal ones).
+struct LdsSum {
+  double v;
+};
+__device__ __forceinline__ void store_out(LdsSum* p, double v) { p->v = v; }
 
 #ifndef AS_COLSLICE_SLICE_GROUPS
 #define AS_COLSLICE_SLICE_GROUPS 4096
@@ -576,7 +604,7 @@ __device__ __forceinline__ void colslice_slice_block(int64_t mb, const int64_t* 
                                                      const int32_t* __restrict__ order,
                                                      const int32_t* __restrict__ counts,
                                                      const int32_t* __restrict__ off, const SliceChunk& c,
-                                                     int64_t chunk_stride) {
+                                                     int64_t chunk_stride, const int32_t* __restrict__ mega_end) {
   constexpr int64_t kTile = 16 * V / static_cast<int64_t>(sizeof(T));  // features of a wide tile
   const int64_t gs = c.slice_groups;
   const int64_t phase_blocks = kSlices * gs;
@@ -587,7 +615,42 @@ __device__ __forceinline__ void colslice_slice_block(int64_t mb, const int64_t* 
   const int64_t in_phase = in_tile - phase * phase_blocks;
   const int slice = static_cast<int>(phase * kSlices + in_phase % kSlices);
   const int64_t sliced = first_short(counts, c) - c.item_begin;
-  for (int64_t local = (in_phase / kSlices) * kWavesPerBlock + wave_in_block(); local < sliced;
+  int64_t mega = 0;
+  if constexpr (V >= 8) {
+    if (mega_end != nullptr) {
+      mega = uniform_i64(static_cast<int64_t>(*mega_end)) - c.item_begin;
+      mega = mega < 0 ? 0 : (mega > sliced ? sliced : mega);
+    }
+    // cooperative rows: the whole workgroup on one (row, slice), block-strided
+    __shared__ LdsSum sums[kWavesPerBlock * kTile];
+    const int w = wave_in_block();
+    for (int64_t local = in_phase / kSlices; local < mega; local += gs) {
+      const int64_t row = uniform_i64(order[c.item_begin + local]);
+      const int64_t rs = uniform_i64(crow[row]);
+      const int64_t deg = uniform_i64(crow[row + 1]) - rs;
+      int64_t a, b;
+      slice_range<kSpmmSlices>(off, row, slice, deg, a, b);
+      a = uniform_i64(a);
+      b = uniform_i64(b);
+      if (a >= b) continue;  // the same for the whole workgroup
+      const int64_t pa = a + (b - a) * w / kWavesPerBlock;
+      const int64_t pb = a + (b - a) * (w + 1) / kWavesPerBlock;
+      // this wave's sums of the tile, addressed by absolute feature index
+      slice_wide<T, V, HAS_VAL, OFF32>(col, val, x, sums + w * kTile - tile * kTile, F, rs + pa, rs + pb,
+                                       tile * kTile);
+      __syncthreads();
+      const int64_t width = F - tile * kTile < kTile ? F - tile * kTile : kTile;
+      double* out = c.partial + (slice * chunk_stride + local) * F + tile * kTile;
+      for (int64_t f = threadIdx.x; f < width; f += kBlock) {
+        double total = sums[f].v;
+#pragma unroll
+        for (int k = 1; k < kWavesPerBlock; ++k) total += sums[k * kTile + f].v;
+        store_out(out + f, total);
+      }
+      __syncthreads();
+    }
+  }
+  for (int64_t local = mega + (in_phase / kSlices) * kWavesPerBlock + wave_in_block(); local < sliced;
        local += gs * kWavesPerBlock) {
     const int64_t row = uniform_i64(order[c.item_begin + local]);
     const int64_t rs = uniform_i64(crow[row]);
@@ -719,7 +782,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(AS_COLSL
   const int64_t work = g - before;
   if (work < MG) {
     colslice_slice_block<T, V, HAS_VAL, OFF32>(work * kSlices + within, crow, col, val, x, F, order, counts, off, m,
-                                               chunk_stride);
+                                               chunk_stride, grouped.mega_end);
   } else {
     colslice_short_block<T, V, HAS_VAL, OFF32>((work - MG) * kSlices + within, crow, col, val, x, y, F, order,
                                                counts, m, grouped);
@@ -918,7 +981,7 @@ inline int build_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_
 // count (the caller's duty); the workspace holds the partial buffers only.
 template <typename T>
 int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
-                     int64_t f, int64_t min_degree, const PlanView& plan, void* partials, size_t partial_bytes,
+                     int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials, size_t partial_bytes,
                      int64_t sliced_rows, int64_t grouped_rows, hipStream_t s) {
   const size_t row_bytes = colslice_row_bytes(f);
   if (partials == nullptr || partial_bytes < 2 * row_bytes)
@@ -974,6 +1037,10 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
     while (level < light_buckets && ((min_degree - 1) >> level) >= limit) ++level;
     if (level < light_buckets) grouped.start = bin_bucket_start(plan.bin_ws, n, kMaxHeavyBuckets + level);
   }
+  // cooperative rows (wide lanes, graphs of at most kMegaMaxNnz edges):
+  // heavy buckets 0 .. K-1-kMegaLevel
+  if (v >= 8 && nnz <= kMegaMaxNnz && kMegaLevel >= 1 && kMegaLevel < kMaxHeavyBuckets)
+    grouped.mega_end = bin_bucket_start(plan.bin_ws, n, kMaxHeavyBuckets - kMegaLevel);
   const int64_t rows_per_wave = grouped.start != nullptr ? kWave / v : 1;
   if (grouped.start == nullptr) grouped_rows = 0;
 
@@ -1022,7 +1089,7 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   const int64_t min_degree = slicing_degree(slicing, f, E);
   st = build_plan(crow, col, n, min_degree, light_bucket_count(E), slicing, plan, s);
   if (st != AS_OK) return st;
-  return colslice_execute<T>(crow, col, val, x, y, n, f, min_degree, plan, static_cast<char*>(workspace) + fixed,
+  return colslice_execute<T>(crow, col, val, x, y, n, nnz, f, min_degree, plan, static_cast<char*>(workspace) + fixed,
                              workspace_bytes - fixed, sliced_rows, grouped_rows, s);
 }
 
@@ -1110,13 +1177,13 @@ int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col, const 
   const as::PlanView view = as::plan_view(const_cast<void*>(plan), n);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == AS_DTYPE_F32)
-    st = as::colslice_execute<float>(crow, col, val, x, y, n, f, min_degree, view, workspace, workspace_bytes,
+    st = as::colslice_execute<float>(crow, col, val, x, y, n, nnz, f, min_degree, view, workspace, workspace_bytes,
                                      sliced_rows, 0, s);
   else if (dtype == AS_DTYPE_BF16)
-    st = as::colslice_execute<as::Bf16>(crow, col, val, x, y, n, f, min_degree, view, workspace, workspace_bytes,
+    st = as::colslice_execute<as::Bf16>(crow, col, val, x, y, n, nnz, f, min_degree, view, workspace, workspace_bytes,
                                         sliced_rows, grouped_rows, s);
   else
-    st = as::colslice_execute<as::Fp16>(crow, col, val, x, y, n, f, min_degree, view, workspace, workspace_bytes,
+    st = as::colslice_execute<as::Fp16>(crow, col, val, x, y, n, nnz, f, min_degree, view, workspace, workspace_bytes,
                                         sliced_rows, grouped_rows, s);
   if (st != AS_OK) return st;
   return as::check_launch("spmm_csr_colslice_planned");

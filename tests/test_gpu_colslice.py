@@ -370,3 +370,43 @@ def test_planned_call_rejects_a_plan_of_other_settings():
     assert lib.as_spmm_csr_colslice_planned(*args, tag64, ws.data_ptr(), ws.numel(), -1, 0, stream) == 0
     torch.cuda.synchronize()
     assert torch.equal(y, _native.spmm_csr_colslice_impl(d_crow, d_col, None, d_x))
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("features", [64, 128, 256, 33])
+def test_colslice_cooperative_hub_rows(features, weighted, monkeypatch):
+    """Rows of degree >= 2^6 times the slicing degree (8,192 edges at 128,
+    16,384 at 256 for F <= 64) run each (row, slice) on all waves of a
+    workgroup, their fp64 sums added in wave order: within the fp64 bound,
+    deterministic, and the same bits with a short workspace (many chunks) and
+    without the per-graph plan.  F = 33 (narrow lanes) keeps one wave per
+    (row, slice)."""
+    crow, col, val, x = _inputs(features, weighted, seed=features + 40, rows=30000, degree=3, hubs=6,
+                                hub_degree=24000, empty=0.2)
+    deg = np.diff(crow)
+    assert (deg >= 16384).sum() == 6 and deg[deg < 24000].max() < 100
+    d = to_dev(crow, col, val, x)
+    first = torch.ops.autosage.spmm_csr_colslice(*d)
+    _assert_fp64_close(first.cpu().numpy(), oracle.spmm_f64(crow, col, val, x))
+    assert torch.equal(first, torch.ops.autosage.spmm_csr_colslice(*d))
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_PLAN", "off")
+    assert torch.equal(first, torch.ops.autosage.spmm_csr_colslice(*d))
+    monkeypatch.delenv("AUTOSAGE_COLSLICE_PLAN")
+    # partial rows for two sliced rows at a time
+    plan_bytes = _native.library().as_spmm_colslice_plan_bytes(crow.size - 1)
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((plan_bytes + 4 * 8 * features * 8) / 2**20))
+    assert torch.equal(first, torch.ops.autosage.spmm_csr_colslice(*d))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rounded16_cooperative_hub_rows(dtype):
+    """16-bit features with column slices (slicing degree 128): the
+    cooperative hub rows give the bits of the rounded fp64 oracle."""
+    crow, col = case_graph(30000, 3, seed=41, hubs=6, hub_degree=24000, empty=0.2)
+    rng = np.random.default_rng(42)
+    x = torch.from_numpy(rng.standard_normal((30000, 128)).astype(np.float32)).to(dtype)
+    val = torch.from_numpy(rng.standard_normal(col.size).astype(np.float32)).to(dtype)
+    want = oracle.spmm_rounded_16(crow, col, val, x, dtype)
+    d_crow, d_col = to_dev(crow, col)
+    got = _native.spmm_rounded_16_impl(d_crow, d_col, val.cuda(), x.cuda(), column_slices=True)
+    assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
