@@ -1015,13 +1015,20 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
   // with the same bits, so a workspace sized for the sliced rows suffices.
   const int64_t fits = static_cast<int64_t>(partial_bytes / (2 * row_bytes));
   int64_t chunk = preferred_chunk_rows(n);
-  if (E == 4 && chunk > fits) chunk = fits;
+  // a graph holds at most nnz / min_degree sliced rows; when they fit one
+  // partial buffer the whole graph is one chunk (fewer launches, and short
+  // rows run beside the hub rows' slices)
+  const int64_t upper = min_degree > 0 && nnz / min_degree < n ? nnz / min_degree : n;
+  if (upper <= chunk && (E != 4 || upper <= fits)) chunk = n;
+  if (E == 4 && (chunk < upper ? chunk : upper) > fits) chunk = fits;
   // blocks of a launch: 8 per group, at most tiles·(P·ceil(c/4) + ceil(c/32))
   // work groups for c rows, and reduce groups at most a quarter of those
   const int64_t max_rows = (kMaxBlocksPerLaunch * 4 / 5 / (kSlices * tiles) - 2) * 32 / (8 * kPhases + 1);
   if (chunk > max_rows) chunk = max_rows;
   if (chunk < 1) return fail(AS_ERR_UNSUPPORTED, "F = %lld is too wide for the column-sliced SpMM", (long long)f);
-  const int64_t capacity = fits < chunk ? fits : chunk;
+  // partial rows per buffer: a chunk's sliced rows are at most min(chunk, upper)
+  int64_t capacity = fits < chunk ? fits : chunk;
+  if (E == 4 && capacity > upper) capacity = upper > 0 ? upper : 1;
   double* buffers[2] = {static_cast<double*>(partials),
                         reinterpret_cast<double*>(static_cast<char*>(partials) + capacity * row_bytes)};
 
