@@ -128,7 +128,7 @@ def test_attention_forward_runs_one_16_bit_kernel(dtype):
     err_fused = np.abs(out.cpu().double().numpy() - exact).max()
     err_staged = np.abs(staged.cpu().double().numpy() - exact).max()
     assert err_fused <= err_staged
-    # the backward chains the native 16-bit stages
+    # the backward: the two native gather passes, gradients in the input type
     qq, kk, vv = (t.clone().requires_grad_(True) for t in d)
     y = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, qq, kk, vv, 0.125)
     y.float().sum().backward()
