@@ -819,7 +819,8 @@ def sddmm_csr_auto(
 
 
 # Split points timed for 16-bit SDDMM: (waves per block, hub threshold).
-_SDDMM_16_OPTIONS = ([4, 1024], [8, 4096])
+# None: sddmm_csr's own schedule (blocks of 64 edges in CSR order)
+_SDDMM_16_OPTIONS = (None, [4, 1024], [8, 4096])
 _SDDMM_16_NOTE = ("bf16/fp16 SDDMM is native (fp64 sums of exact products, rounded); the gather-dot baseline "
                   "rounds every product to the 16-bit type and is not a candidate")
 
@@ -827,10 +828,10 @@ _SDDMM_16_NOTE = ("bf16/fp16 SDDMM is native (fp64 sums of exact products, round
 def _sddmm_auto_16(crow, col, query, key, config: SchedulerConfig, verbose: bool) -> tuple[torch.Tensor, dict]:
     """bf16 / fp16 query and key (the reference runs its gather-dot baseline
     for them, ``_auto.py:575-581``).  Every output is the rounded fp64 sum
-    whatever the split, so the split points of ``_SDDMM_16_OPTIONS`` are
-    timed once on the full graph and the faster is cached under the usual key
-    (which includes the dtype)."""
-    options = [list(o) for o in _SDDMM_16_OPTIONS]
+    whatever the schedule, so the schedules of ``_SDDMM_16_OPTIONS`` (edge
+    blocks, and two degree splits) are timed once on the full graph and the
+    fastest is cached under the usual key (which includes the dtype)."""
+    options = [None if o is None else list(o) for o in _SDDMM_16_OPTIONS]
     if config.cache:
         result = _cached_record(crow, col, query.size(1), "sddmm", config, dtype=query.dtype)
         if result is not None and result.get("choice") == "autosage" and result.get("candidate") in options:

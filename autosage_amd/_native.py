@@ -29,7 +29,7 @@ from . import _env
 from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
 # 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
@@ -95,6 +95,11 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_ptr, _c_size,
          _c_ptr],
+    ),
+    "as_sddmm_edges_16_workspace_bytes": (_c_size, [_c_i64]),
+    "as_sddmm_csr_edges_16": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_size, _c_ptr],
     ),
     "as_csr_attention_colslice_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_csr_attention_plan_bytes": (_c_size, [_c_i64]),
@@ -460,9 +465,10 @@ def spmm_rounded_16_impl(crow, col, val, x, column_slices: bool):
 
 
 # Schedule of sddmm_csr on 16-bit inputs: any schedule gives the same bits,
-# so the whole-graph op takes the split one (hub rows in 2048-edge chunks).
-SDDMM_16_WAVES = 4
-SDDMM_16_HUB_THRESHOLD = 1024
+# so the whole-graph op takes blocks of 64 edges in CSR order, faster than
+# the split schedule (rows by degree, hub rows in 2048-edge chunks) on every
+# graph measured: 14 % on the 50M-edge hub graph (bf16, F = 64), 28 % on
+# the 124M-edge attention graph, 11 % on the skewed 115M-edge graph.
 
 
 # fp32 sddmm_csr: every output keeps the reference kernel's dot order on any
@@ -476,7 +482,7 @@ SDDMM_WAVES = 4
 def sddmm_csr_impl(crow, col, query, key):
     check_sddmm_inputs(crow, col, query, key, allow_16=True)
     if query.dtype in DTYPES_16:
-        return sddmm_rounded_16_impl(crow, col, query, key, SDDMM_16_WAVES, SDDMM_16_HUB_THRESHOLD)
+        return sddmm_edges_16_impl(crow, col, query, key)
     if col.numel() >= SDDMM_HUB_THRESHOLD:
         return sddmm_csr_split_impl(crow, col, query, key, SDDMM_WAVES, SDDMM_HUB_THRESHOLD)
     _maybe_validate(crow, col)
@@ -546,6 +552,30 @@ def sddmm_rounded_16_impl(crow, col, query, key, warps_per_block: int, hub_thres
             int(warps_per_block), int(hub_threshold), _ptr(ws), ws.numel(), _stream(query.device),
         )
     _raise(status, "autosage::sddmm_csr (16-bit)")
+    return out
+
+
+def sddmm_edges_16_impl(crow, col, query, key):
+    """SDDMM on bf16/fp16 query and key over blocks of 64 edges in CSR order
+    (no degree split): the same bits as ``sddmm_rounded_16_impl``."""
+    check_sddmm_inputs(crow, col, query, key, allow_16=True)
+    _check(query.dtype in DTYPES_16, "query and key must be bfloat16 or float16")
+    _maybe_validate(crow, col)
+    nnz = col.numel()
+    n, f = query.shape
+    if f == 0:
+        return torch.zeros(nnz, dtype=query.dtype, device=query.device)
+    out = torch.empty(nnz, dtype=query.dtype, device=query.device)
+    if n == 0 or nnz == 0:
+        return out
+    lib = library()
+    ws = _workspace(lib.as_sddmm_edges_16_workspace_bytes(nnz), query.device)
+    with _on(query.device):
+        status = lib.as_sddmm_csr_edges_16(
+            _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, DTYPES_16[query.dtype],
+            _ptr(ws), ws.numel(), _stream(query.device),
+        )
+    _raise(status, "autosage::sddmm_csr (16-bit, edge blocks)")
     return out
 
 

@@ -590,6 +590,306 @@ void launch_sddmm16(const Sddmm16Args& a, int waves, int64_t hub_threshold, int6
   }
 }
 
+// ---- 16-bit SDDMM by blocks of edges ---------------------------------------
+// The same dot products as above (the same lane layout, fp64 sums and
+// butterfly: the same bits) over the edges in CSR order, 64 at a time, with
+// no regard to rows: wave w takes blocks [w·B, w·B + B) of 64 edges.  Every
+// gather instruction then carries 64/G edges however short the rows are (a
+// wave per row issues one partly filled gather for a row of a few edges and
+// waits for it), and long rows need no schedule of their own.  The query row
+// is gathered per edge (consecutive edges share it, so those gathers hit
+// the caches).
+//
+// Rows of the edges: the wave loads the ends of the 64 rows from r, the row
+// of the block's first edge, and lane i finds the row of edge b + i by a
+// binary search over them (ds_bpermute).  A block spanning more than 64 rows
+// (empty rows) takes further rounds of 64.  r comes from a table for the
+// wave's first block (edge_wave_rows_kernel, one binary search over crow per
+// wave) and is the row of the previous block's last edge after that.
+// 2 blocks a wave: cfg4 (50M edges, median degree 8) bf16 F = 64 takes
+// 0.975 ms against 0.986 at 4 and 1.000 at 8 (the split schedule: 1.133);
+// the 2.4M-row, 124M-edge attention graph at F = 64 1.988 against 2.000 and
+// 2.032 (split: 2.756); the skewed 115M-edge graph at F = 128 2.890 against
+// 2.930 and 3.011 (split: 3.257).
+#ifndef AS_SDDMM16_EDGE_BLOCKS
+#define AS_SDDMM16_EDGE_BLOCKS 2
+#endif
+constexpr int64_t kEdgeBlocksPerWave = AS_SDDMM16_EDGE_BLOCKS;
+constexpr int64_t kEdgesPerWave = kWave * kEdgeBlocksPerWave;
+constexpr int kEdgeWaves = 4;  // waves per workgroup
+
+int64_t edge_waves(int64_t nnz) { return (nnz + kEdgesPerWave - 1) / kEdgesPerWave; }
+
+size_t sddmm_edges_ws(int64_t nnz) {
+  return align_up(static_cast<size_t>(edge_waves(nnz) > 0 ? edge_waves(nnz) : 1) * sizeof(int32_t), 256);
+}
+
+// rows[w] = the row holding edge w·kEdgesPerWave: the last r < n with
+// crow[r] <= e (rows before it that are empty end at or before e).
+__global__ __launch_bounds__(256) void edge_wave_rows_kernel(const int64_t* __restrict__ crow, int64_t n,
+                                                             int64_t waves, int32_t* __restrict__ rows) {
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (w >= waves) return;
+  const int64_t e = w * kEdgesPerWave;
+  int64_t lo = 0;
+  int64_t hi = n - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (crow[mid] <= e) lo = mid;
+    else hi = mid - 1;
+  }
+  rows[w] = static_cast<int32_t>(lo);
+}
+
+// Lane i: the row of edge b + min(i, cnt - 1), given r, the row of edge b.
+// Every lane of the wave must be active.  The rounds end at the last row
+// whatever crow holds, and the result is clamped to [0, n).
+__device__ __forceinline__ int block_edge_rows(const int64_t* __restrict__ crow, int64_t n, int64_t b, int cnt,
+                                               int64_t r) {
+  const int lane = lane_id();
+  const int i = lane < cnt ? lane : cnt - 1;
+  int row = -1;
+  for (int64_t rr = r;; rr += kWave) {
+    // rel: where row rr + lane ends (row n - 1 for lanes past it), relative
+    // to b, clamped to [0, 64]
+    const int64_t left = n - 1 - rr;  // >= 0
+    const int lim = left < kWave ? static_cast<int>(left) : kWave;
+    const int64_t d = crow[rr + 1 + (lane < lim ? lane : lim)] - b;
+    const int rel = d < 0 ? 0 : (d > kWave ? kWave : static_cast<int>(d));
+    // pos = #{l : rel_l <= i}, the ends being non-decreasing in l
+    int pos = 0;
+#pragma unroll
+    for (int s = kWave / 2; s >= 1; s >>= 1) {
+      const int v = __builtin_amdgcn_ds_bpermute((pos + s - 1) * 4, rel);
+      pos = v <= i ? pos + s : pos;
+    }
+    const int rel_last = __builtin_amdgcn_readlane(rel, kWave - 1);
+    if (pos == kWave - 1 && rel_last <= i) pos = kWave;
+    if (row < 0 && pos < kWave) row = static_cast<int>(rr + pos);
+    if (rel_last >= cnt || rr + kWave >= n) break;
+  }
+  const int last = static_cast<int>(n - 1);
+  return row < 0 || row > last ? last : row;
+}
+
+// Byte offset of 16-byte chunk lane_off of row `row` of a [*, F] matrix.
+template <bool OFF32>
+__device__ __forceinline__ const char* chunk_at(const char* base, int row, uint32_t row_bytes, uint32_t lane_off) {
+  if constexpr (OFF32) {
+    return base + (__umul24(static_cast<uint32_t>(row), row_bytes) + lane_off);
+  } else {
+    return base + static_cast<int64_t>(row) * row_bytes + lane_off;
+  }
+}
+
+// The dot products of one block of cnt <= 64 edges starting at edge b,
+// vector lanes: lane j of lane group g holds chunks j + G·m of the edge's
+// query and key rows.  my_c / my_row: lane i holds the column / row of edge
+// b + i.
+template <typename T, int G, int MB, bool OFF32>
+__device__ __forceinline__ void edge_block16_vec(const char* __restrict__ kb, const char* __restrict__ qb,
+                                                 uint16_t* __restrict__ out, int64_t F, int64_t b, int cnt, int my_c,
+                                                 int my_row) {
+  constexpr int NG = kWave / G;  // edges per gather instruction
+  // key (and query) gathers in flight per lane and chunk; fewer at 32 lanes
+  // an edge, which would spill at 4
+  constexpr int UE = MB == 1 ? (G >= 32 ? 2 : (4 < G ? 4 : G)) : 1;
+  constexpr int kSub = NG * UE;  // edges per sub-pass, divides 64
+  static_assert(kWave % kSub == 0, "a sub-pass stays inside its block of 64 edges");
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int j = lane % G;
+  const int64_t chunks = F / 8;
+  const uint32_t row_bytes = static_cast<uint32_t>(F * sizeof(T));
+  uint32_t lane_off[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) lane_off[m] = static_cast<uint32_t>((j + G * m < chunks ? j + G * m : 0) * 16);
+  for (int u0 = 0; u0 < cnt; u0 += kSub) {
+    RawVec<16> kv[UE][MB];
+    RawVec<16> qv[UE][MB];
+#pragma unroll
+    for (int u = 0; u < UE; ++u) {
+      if (u0 + u * NG < cnt) {
+        const int addr = (u0 + u * NG + g) * 4;  // an edge of this block (< 64)
+        const int c = __builtin_amdgcn_ds_bpermute(addr, my_c);
+        const int rw = __builtin_amdgcn_ds_bpermute(addr, my_row);
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          kv[u][m] = load_raw<16>(chunk_at<OFF32>(kb, c, row_bytes, lane_off[m]));
+          qv[u][m] = load_raw<16>(chunk_at<OFF32>(qb, rw, row_bytes, lane_off[m]));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UE; ++u) {
+      if (u0 + u * NG < cnt) {
+        double acc = 0.0;
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          if (j + G * m < chunks) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+              acc = __builtin_fma(static_cast<double>(Elem<T>::get(qv[u][m].w, p)),
+                                  static_cast<double>(Elem<T>::get(kv[u][m].w, p)), acc);
+          }
+        }
+#pragma unroll
+        for (int o = 1; o < G; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+        const int idx = u0 + u * NG + g;
+        if (j == 0 && idx < cnt) out[b + idx] = Elem<T>::bits(acc);
+      }
+    }
+  }
+}
+
+// A wave whose edges [b0, b1) all lie in row `row` (long rows): the lane's
+// query chunks are loaded once and the blocks need no row lookup.  The same
+// products, sums and butterfly.
+template <typename T, int G, int MB, bool OFF32>
+__device__ __forceinline__ void one_row_edges16_vec(const int64_t* __restrict__ col, const char* __restrict__ kb,
+                                                    const char* __restrict__ qb, uint16_t* __restrict__ out,
+                                                    int64_t F, int64_t b0, int64_t b1, int row) {
+  constexpr int NG = kWave / G;
+  constexpr int UE = MB == 1 ? (4 < G ? 4 : G) : 1;
+  constexpr int kSub = NG * UE;
+  static_assert(kWave % kSub == 0, "a sub-pass stays inside its block of 64 edges");
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int j = lane % G;
+  const int64_t chunks = F / 8;
+  const uint32_t row_bytes = static_cast<uint32_t>(F * sizeof(T));
+  uint32_t lane_off[MB];
+  RawVec<16> q[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    lane_off[m] = static_cast<uint32_t>((j + G * m < chunks ? j + G * m : 0) * 16);
+    q[m] = load_raw<16>(chunk_at<OFF32>(qb, row, row_bytes, lane_off[m]));
+  }
+  int next_c = b0 + lane < b1 ? static_cast<int>(col[b0 + lane]) : 0;
+  for (int64_t b = b0; b < b1; b += kWave) {
+    const int cnt = b1 - b < kWave ? static_cast<int>(b1 - b) : kWave;
+    const int my_c = next_c;
+    if (b + kWave < b1) next_c = b + kWave + lane < b1 ? static_cast<int>(col[b + kWave + lane]) : 0;
+    for (int u0 = 0; u0 < cnt; u0 += kSub) {
+      RawVec<16> kv[UE][MB];
+#pragma unroll
+      for (int u = 0; u < UE; ++u) {
+        if (u0 + u * NG < cnt) {
+          const int c = __builtin_amdgcn_ds_bpermute((u0 + u * NG + g) * 4, my_c);
+#pragma unroll
+          for (int m = 0; m < MB; ++m) kv[u][m] = load_raw<16>(chunk_at<OFF32>(kb, c, row_bytes, lane_off[m]));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UE; ++u) {
+        if (u0 + u * NG < cnt) {
+          double acc = 0.0;
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            if (j + G * m < chunks) {
+#pragma unroll
+              for (int p = 0; p < 8; ++p)
+                acc = __builtin_fma(static_cast<double>(Elem<T>::get(q[m].w, p)),
+                                    static_cast<double>(Elem<T>::get(kv[u][m].w, p)), acc);
+            }
+          }
+#pragma unroll
+          for (int o = 1; o < G; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+          const int idx = u0 + u * NG + g;
+          if (j == 0 && idx < cnt) out[b + idx] = Elem<T>::bits(acc);
+        }
+      }
+    }
+  }
+}
+
+template <typename T, int G, int MB, bool VEC, bool OFF32>
+__global__ __launch_bounds__(kEdgeWaves * kWave) __attribute__((amdgpu_waves_per_eu(8))) void sddmm16_edges_kernel(
+    const int64_t* __restrict__ crow, const int64_t* __restrict__ col, const T* __restrict__ query,
+    const T* __restrict__ key, uint16_t* __restrict__ out, int64_t n, int64_t nnz, int64_t F,
+    const int32_t* __restrict__ wave_rows, int64_t waves, int64_t wave_base) {
+  const int64_t w = wave_base + static_cast<int64_t>(blockIdx.x) * kEdgeWaves + wave_in_block();
+  if (w >= waves) return;  // wave-uniform
+  const int lane = lane_id();
+  const int64_t b0 = uniform_i64(w * kEdgesPerWave);
+  const int64_t b1 = uniform_i64(b0 + kEdgesPerWave < nnz ? b0 + kEdgesPerWave : nnz);
+  int64_t r = uniform_i64(wave_rows[w]);
+  const char* __restrict__ kb = reinterpret_cast<const char*>(key);
+  const char* __restrict__ qb = reinterpret_cast<const char*>(query);
+  if constexpr (VEC) {
+    if (uniform_i64(crow[r + 1]) >= b1) {  // every edge of the wave is in row r
+      one_row_edges16_vec<T, G, MB, OFF32>(col, kb, qb, out, F, b0, b1, static_cast<int>(r));
+      return;
+    }
+  }
+  int next_c = b0 + lane < b1 ? static_cast<int>(col[b0 + lane]) : 0;
+  for (int64_t b = b0; b < b1; b += kWave) {
+    const int cnt = b1 - b < kWave ? static_cast<int>(b1 - b) : kWave;
+    const int my_c = next_c;
+    if (b + kWave < b1) next_c = b + kWave + lane < b1 ? static_cast<int>(col[b + kWave + lane]) : 0;
+    const int my_row = block_edge_rows(crow, n, b, cnt, r);
+    r = __builtin_amdgcn_readlane(my_row, cnt - 1);
+    if constexpr (VEC) {
+      edge_block16_vec<T, G, MB, OFF32>(kb, qb, out, F, b, cnt, my_c, my_row);
+    } else {
+      // element lanes: lane l adds features l, l + 64, ... of each edge in
+      // turn (the order of dots16_scalar)
+      for (int idx = 0; idx < cnt; ++idx) {
+        const int64_t c = __builtin_amdgcn_readlane(my_c, idx);
+        const int64_t rw = __builtin_amdgcn_readlane(my_row, idx);
+        const T* __restrict__ kr = key + c * F;
+        const T* __restrict__ qr = query + rw * F;
+        double acc = 0.0;
+        for (int64_t f = lane; f < F; f += kWave)
+          acc = __builtin_fma(static_cast<double>(Elem<T>::at(qr, f)), static_cast<double>(Elem<T>::at(kr, f)), acc);
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+        if (lane == 0) out[b + idx] = Elem<T>::bits(acc);
+      }
+    }
+  }
+}
+
+template <typename T>
+void launch_sddmm16_edges(const Sddmm16Args& a, int64_t nnz, int32_t* wave_rows, hipStream_t s) {
+  const int64_t waves = edge_waves(nnz);
+  hipLaunchKernelGGL(edge_wave_rows_kernel, dim3(static_cast<unsigned>((waves + 255) / 256)), dim3(256), 0, s,
+                     a.crow, a.n, waves, wave_rows);
+  int g, mb;
+  sddmm16_shape(a, g, mb);
+  const bool off32 = a.n <= (int64_t(1) << 24) && a.n * a.f * 2 <= (int64_t(1) << 32);
+  const int64_t blocks = (waves + kEdgeWaves - 1) / kEdgeWaves;
+  for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
+    const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
+    const dim3 grid(static_cast<unsigned>(nb));
+    const dim3 block(kEdgeWaves * kWave);
+#define AS_E16(G, MB, VEC, OFF)                                                                              \
+  hipLaunchKernelGGL((sddmm16_edges_kernel<T, G, MB, VEC, OFF>), grid, block, 0, s, a.crow, a.col,           \
+                     static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<uint16_t*>(a.out), a.n, \
+                     nnz, a.f, wave_rows, waves, b0 * kEdgeWaves)
+#define AS_E16_V(G, MB)                  \
+  do {                                   \
+    if (off32) AS_E16(G, MB, true, true); \
+    else AS_E16(G, MB, true, false);      \
+  } while (0)
+    if (mb == 2) {
+      AS_E16_V(32, 2);
+    } else {
+      switch (g) {
+        case 1: AS_E16_V(1, 1); break;
+        case 2: AS_E16_V(2, 1); break;
+        case 4: AS_E16_V(4, 1); break;
+        case 8: AS_E16_V(8, 1); break;
+        case 16: AS_E16_V(16, 1); break;
+        case 32: AS_E16_V(32, 1); break;
+        default: AS_E16(64, 1, false, false); break;
+      }
+    }
+#undef AS_E16_V
+#undef AS_E16
+  }
+}
+
 int validate_sddmm(const SddmmArgs& a, int64_t nnz) {
   if (a.n < 0 || a.n > INT32_MAX || a.f < 0)
     return fail(AS_ERR_INVALID_ARGUMENT, "SDDMM dimensions exceed the kernel index range");
@@ -713,6 +1013,35 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void*
   else
     as::launch_sddmm16<as::Fp16>(a, waves_per_block, hub_threshold, item_upper, order, counts, chunk_off, s);
   return as::check_launch("sddmm_csr_rounded_16");
+}
+
+size_t as_sddmm_edges_16_workspace_bytes(int64_t nnz) { return as::sddmm_edges_ws(nnz < 0 ? 0 : nnz); }
+
+int as_sddmm_csr_edges_16(const int64_t* crow, const int64_t* col, const void* query, const void* key, void* out,
+                          int64_t n, int64_t nnz, int64_t f, int dtype, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  as::clear_error();
+  if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
+  if (!as::aligned(query, 2) || !as::aligned(key, 2) || !as::aligned(out, 2))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "query, key and out must be 2-byte aligned");
+  const as::SddmmArgs shape{crow, col, static_cast<const float*>(query), static_cast<const float*>(key),
+                            static_cast<float*>(out), n, f};
+  int st = as::validate_sddmm(shape, nnz);
+  if (st != AS_OK) return st;
+  if (n == 0 || nnz == 0) return AS_OK;
+  if (f == 0) return as::fail(AS_ERR_UNSUPPORTED, "SDDMM with zero features is handled by the caller");
+  if (workspace == nullptr || workspace_bytes < as::sddmm_edges_ws(nnz))
+    return as::fail(AS_ERR_WORKSPACE, "16-bit SDDMM by edge blocks needs %zu workspace bytes, got %zu",
+                    as::sddmm_edges_ws(nnz), workspace_bytes);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const as::Sddmm16Args a{crow, col, query, key, out, n, f};
+  int32_t* wave_rows = static_cast<int32_t*>(workspace);
+  if (dtype == AS_DTYPE_BF16)
+    as::launch_sddmm16_edges<as::Bf16>(a, nnz, wave_rows, s);
+  else
+    as::launch_sddmm16_edges<as::Fp16>(a, nnz, wave_rows, s);
+  return as::check_launch("sddmm_csr_edges_16");
 }
 
 }  // extern "C"

@@ -842,7 +842,8 @@ def bench_other(args, device) -> dict:
         crow = torch.from_numpy(w.crow).to(device)
         col = torch.from_numpy(w.col).to(device)
         # bf16 / fp16: the rounded 16-bit SDDMM (fp64 sums of exact products);
-        # the split points are the ones its scheduler times
+        # the schedules are the ones its scheduler times (sddmm_csr's own, in
+        # blocks of 64 edges, and two degree splits)
         dt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
         q = torch.from_numpy(w.dense["q"]).to(device).to(dt)
         k = torch.from_numpy(w.dense["k"]).to(device).to(dt)
@@ -852,8 +853,8 @@ def bench_other(args, device) -> dict:
         for waves, thr in splits:
             variants[f"{waves},{thr}"] = (
                 lambda a=waves, b=thr: torch.ops.autosage.sddmm_csr_split(crow, col, q, k, a, b))
-        if dt == torch.float32:
-            variants["whole"] = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)
+        whole = "whole" if dt == torch.float32 else "edges"
+        variants[whole] = lambda: torch.ops.autosage.sddmm_csr(crow, col, q, k)
         calib = {}
         chosen = calibrate(variants, calib) if args.variant in ("calibrated", "auto") else args.variant
         step = variants[chosen]
@@ -867,7 +868,7 @@ def bench_other(args, device) -> dict:
             _, info = sddmm_csr_auto(crow, col, q, k)
             cand = info.get("candidate")
             chosen = "baseline" if info.get("choice") != "autosage" else (
-                "whole" if cand is None else ",".join(map(str, cand)))
+                whole if cand is None else ",".join(map(str, cand)))
             step = lambda: sddmm_csr_auto(crow, col, q, k)[0]  # noqa: E731
         ms, samples = time_steps(step, args.steps, args.warmup)
         flops = 2.0 * w.nnz * f

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 5
+#define AS_ABI_VERSION 6
 
 typedef enum as_status {
   AS_OK = 0,
@@ -270,6 +270,22 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col,
                             int waves_per_block, int64_t hub_threshold,
                             void* workspace, size_t workspace_bytes,
                             void* stream);
+
+/* Bytes of workspace as_sddmm_csr_edges_16 needs for nnz edges. */
+size_t as_sddmm_edges_16_workspace_bytes(int64_t nnz);
+
+/* The SDDMM of as_sddmm_csr_rounded_16 (the same bits) on another schedule:
+ * the edges in CSR order in blocks of 64, a few blocks per wavefront,
+ * whatever the row lengths, each edge's row found from crow inside the
+ * wavefront; no degree split.  Same arguments as as_sddmm_csr_rounded_16
+ * without the split settings.  Replaces sddmm_csr (csrc/sddmm_csr_op.cu:108-134)
+ * for the 16-bit types the reference leaves to its gather-dot baseline
+ * (autosage/_auto.py:575-581). */
+int as_sddmm_csr_edges_16(const int64_t* crow, const int64_t* col,
+                          const void* query, const void* key, void* out,
+                          int64_t n, int64_t nnz, int64_t f, int dtype,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 /* Row softmax of bf16 or fp16 scores (dtype AS_DTYPE_BF16 / AS_DTYPE_F16):
  * the scores convert exactly to fp32, the softmax is computed in fp32 (rows

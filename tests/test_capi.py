@@ -150,6 +150,20 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_last_error() == b"query, key and out must be 2-byte aligned"
     assert lib.as_sddmm_csr_rounded_16(None, None, None, None, None, 4, 5, 8, 2, 4, 1024, None, 0, None) == 1
     assert lib.as_last_error() == b"null crow pointer"
+    # the same checks for the edge-block schedule, then its workspace (one
+    # int32 per wavefront of 128 edges, in 256-byte units)
+    assert lib.as_sddmm_csr_edges_16(None, None, None, None, None, 4, 0, 8, 3, None, 0, None) == 1
+    assert lib.as_last_error() == b"dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16"
+    assert lib.as_sddmm_csr_edges_16(None, None, 1, None, None, 4, 0, 8, 2, None, 0, None) == 1
+    assert lib.as_last_error() == b"query, key and out must be 2-byte aligned"
+    assert lib.as_sddmm_csr_edges_16(None, None, None, None, None, 4, 5, 8, 2, None, 0, None) == 1
+    assert lib.as_last_error() == b"null crow pointer"
+    assert lib.as_sddmm_csr_edges_16(None, None, None, None, None, 0, 0, 8, 2, None, 0, None) == 0
+    fake = 256
+    assert lib.as_sddmm_csr_edges_16(fake, fake, fake, fake, fake, 4, 5, 8, 1, fake, 255, None) == 4
+    assert lib.as_last_error().startswith(b"16-bit SDDMM by edge blocks needs 256 workspace bytes")
+    assert [lib.as_sddmm_edges_16_workspace_bytes(e) for e in (0, 1, 128 * 64, 128 * 64 + 1, -5)] == [
+        256, 256, 256, 512, 256]
     assert [lib.as_spmm_rounded_16_group_degree(f) for f in (8, 64, 72, 128, 136, 512, 7, 0)] == [
         32, 32, 64, 64, 128, 128, 0, 0]
     # n == 0 is a no-op success
@@ -164,6 +178,7 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_spmm_csr_colslice_f32(None, None, None, None, None, 4, 0, big, None, 0, -1, None) == 3
     assert lib.as_sddmm_csr_f32(None, None, None, None, None, 4, 0, big, None) == 3
     assert lib.as_sddmm_csr_rounded_16(None, None, None, None, None, 4, 0, big, 1, 4, 1024, None, 0, None) == 3
+    assert lib.as_sddmm_csr_edges_16(None, None, None, None, None, 4, 0, big, 1, None, 0, None) == 3
     assert lib.as_csr_attention_f32(None, None, None, None, None, None, 4, 0, 8, big, 1.0, None, 0, None) == 3
     assert lib.as_last_error() == b"F_qk and F_v must be below 2^28 (32-bit lane offsets)"
     assert lib.as_spmm_csr_f32(None, None, None, None, None, 4, 0, -1, 1, None) == 1

@@ -11,7 +11,8 @@ rounded result only for a sum that close to a tie (random inputs do not
 produce one).  So the bar is bit-identity with the oracle
 (``oracle.spmm_rounded_16``, an fp64 sum in CSR order) for every schedule:
 column slices (ascending columns), edge slices (shuffled columns), grouped
-and one-wave short rows, hub rows, empty rows, any F.
+and one-wave short rows, hub rows, empty rows, any F; for the SDDMM, rows
+split by degree and blocks of 64 edges whatever the rows.
 """
 
 from __future__ import annotations
@@ -243,6 +244,43 @@ def test_rounded_sddmm_equals_oracle_on_every_split(dtype, features):
         assert _same_bits(torch.ops.autosage.sddmm_csr_split(d_crow, d_col, d_q, d_k, waves, threshold), want)
 
 
+def _edge_block_graphs(rows_seed: int):
+    """Row layouts for the edge-block schedule: hub rows and 8 % empty rows;
+    90 % empty rows (blocks of 64 edges spanning far more than 64 rows); one
+    edge per row (exactly 64 rows a block); runs of hundreds of empty rows
+    between short rows and a hub as the last row; fewer edges than a block."""
+    rng = np.random.default_rng(rows_seed)
+    yield "hubs", case_graph(3000, 9, seed=rows_seed, hubs=3, hub_degree=2500, empty=0.08)
+    yield "mostly empty", case_graph(5000, 3, seed=rows_seed + 1, empty=0.9)
+    n = 700
+    yield "one edge a row", (np.arange(n + 1, dtype=np.int64), np.sort(rng.integers(0, n, n)).astype(np.int64))
+    deg = np.zeros(900, dtype=np.int64)
+    deg[[0, 130, 131, 400, 650]] = [3, 1, 70, 2, 5]
+    deg[-1] = 4000
+    crow = np.concatenate(([0], np.cumsum(deg))).astype(np.int64)
+    col = np.concatenate([np.sort(rng.integers(0, deg.size, d)) for d in deg]).astype(np.int64)
+    yield "empty runs, hub last", (crow, col)
+    yield "one block", (np.array([0, 5, 5, 20], dtype=np.int64), np.sort(rng.integers(0, 3, 20)).astype(np.int64))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("features", [1, 7, 8, 16, 24, 64, 128, 136, 264, 512, 520])
+def test_rounded_sddmm_edge_blocks(dtype, features):
+    """``sddmm_edges_16_impl``: blocks of 64 edges whatever the rows, each
+    edge's row found from crow in the wavefront; bitwise the oracle's (and
+    so the split schedules') result on every layout."""
+    for name, (crow, col) in _edge_block_graphs(features):
+        n = crow.size - 1
+        rng = np.random.default_rng(features + 3)
+        q = torch.from_numpy(rng.standard_normal((n, features)).astype(np.float32)).to(dtype)
+        k = torch.from_numpy(rng.standard_normal((n, features)).astype(np.float32)).to(dtype)
+        want = oracle.sddmm_rounded_16(crow, col, q, k, dtype)
+        d_crow, d_col = to_dev(crow, col)
+        got = _native.sddmm_edges_16_impl(d_crow, d_col, q.cuda(), k.cuda())
+        assert got.dtype == dtype
+        assert _same_bits(got, want), (name, (got.float().cpu() - want.float()).abs().max())
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_rounded_sddmm_edge_cases(dtype):
     # rows that are not 16-byte aligned take the element lanes
@@ -293,7 +331,7 @@ def test_sddmm_scheduler_on_16_bit_inputs(dtype, monkeypatch, tmp_path):
     d_crow, d_col = to_dev(crow, col)
     out, info = sddmm_csr_auto(d_crow, d_col, q.cuda(), k.cuda())
     assert info["operation"] == "sddmm" and info["choice"] == "autosage" and info["from_cache"] is False
-    assert info["candidate"] in ([4, 1024], [8, 4096]) and len(info["candidates"]) == 2
+    assert info["candidate"] in (None, [4, 1024], [8, 4096]) and len(info["candidates"]) == 3
     assert info["baseline_probe_ms"] is None and _same_bits(out, want)
     out2, info2 = sddmm_csr_auto(d_crow, d_col, q.cuda(), k.cuda())
     assert info2["from_cache"] is True and info2["candidate"] == info["candidate"]
