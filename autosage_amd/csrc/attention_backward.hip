@@ -37,7 +37,6 @@ namespace as {
 
 namespace {
 
-constexpr int64_t kBwdSliceMinDegree = 128;
 constexpr int kBwdBatch = 8;
 constexpr int64_t kBwdChunkRows = 131072;
 constexpr int64_t kBwdSliceBlocks = 4096;
@@ -958,8 +957,9 @@ size_t bwd_row_bytes(int64_t fqk, int64_t fv, bool two) {
 size_t bwd_pairs_bytes(int64_t n) { return align_up(static_cast<size_t>(n > 0 ? n : 1) * sizeof(float2), 256); }
 size_t bwd_fixed_bytes(int64_t n) { return bwd_pairs_bytes(n) + slice_plan_bytes(n); }
 
-int64_t bwd_sliced_upper(int64_t n, int64_t nnz) {
-  const int64_t u = nnz / kBwdSliceMinDegree;
+// Upper bound on the rows of degree >= `degree` (the sliced rows).
+int64_t bwd_sliced_upper(int64_t n, int64_t nnz, int64_t degree) {
+  const int64_t u = nnz / degree;
   return u < n ? u : n;
 }
 
@@ -1071,7 +1071,9 @@ int backward_run(const int64_t* crow, const int64_t* col, const int64_t* crow_t,
   // 16-bit: short rows in 8 log2-degree buckets (the grouped rows), as in the
   // forward's plan
   constexpr int kLight = sums_t<T>() ? kMaxHeavyBuckets : 1;
-  const int64_t want = slice_plan_tag(kBwdSliceMinDegree, kLight);
+  // the forward's slicing degree: the two share the per-graph plans
+  constexpr int64_t kDegree = att_slice_degree<T>();
+  const int64_t want = slice_plan_tag(kDegree, kLight);
   if ((plan != nullptr && plan_tag != want) || (plan_t != nullptr && plan_t_tag != want))
     return fail(AS_ERR_INVALID_ARGUMENT, "a plan was built for other settings (this call needs plan tag %lld)",
                 (long long)want);
@@ -1096,7 +1098,7 @@ int backward_run(const int64_t* crow, const int64_t* col, const int64_t* crow_t,
     return fail(AS_ERR_WORKSPACE, "attention backward needs at least %zu workspace bytes, got %zu",
                 fixed + row_bytes + kBwdPartSlack, workspace_bytes);
   if (!aligned(workspace, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  const int64_t upper = bwd_sliced_upper(n, nnz);
+  const int64_t upper = bwd_sliced_upper(n, nnz, kDegree);
   int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed - kBwdPartSlack) / row_bytes);
   if (chunk > kBwdChunkRows) chunk = kBwdChunkRows;
   if (chunk > upper) chunk = upper;
@@ -1115,7 +1117,7 @@ int backward_run(const int64_t* crow, const int64_t* col, const int64_t* crow_t,
     const void* given = pass == 1 ? plan : plan_t;
     const SlicePlan view = slice_plan_view(given != nullptr ? const_cast<void*>(given) : own, n);
     if (given == nullptr) {
-      const int st = build_slice_plan(pc, pcol, n, kBwdSliceMinDegree, kLight, false, view, s);
+      const int st = build_slice_plan(pc, pcol, n, kDegree, kLight, false, view, s);
       if (st != AS_OK) return st;
     }
     const BwdArgs<T> a{pc,     pcol,   query, key,  value, grad_out, out,        lt,          grad_q,
@@ -1137,7 +1139,8 @@ size_t as_csr_attention_backward_workspace_bytes(int64_t n, int64_t nnz, int64_t
   if (nnz < 0) nnz = 0;
   if (f_qk < 4) f_qk = 4;
   if (f_v < 4) f_v = 4;
-  int64_t rows = as::bwd_sliced_upper(n, nnz);
+  int64_t rows = as::bwd_sliced_upper(
+      n, nnz, dtype == AS_DTYPE_F32 ? as::att_slice_degree<float>() : as::att_slice_degree<as::Bf16>());
   if (rows > as::kBwdChunkRows) rows = as::kBwdChunkRows;
   if (rows < 1) rows = 1;
   return as::bwd_fixed_bytes(n) + static_cast<size_t>(rows) * as::bwd_row_bytes(f_qk, f_v, dtype != AS_DTYPE_F32) +

@@ -2,7 +2,8 @@
 // an alternative schedule for the fused attention (attention.hip) on graphs
 // whose columns ascend within every row.
 //
-// Rows of degree >= 128 are cut into the 8 column slices of colslice_common.h;
+// Rows of degree >= D (att_slice_degree: 128 for fp32, 512 for 16-bit
+// elements) are cut into the 8 column slices of colslice_common.h;
 // workgroup g works on slice g % 8, so each XCD gathers K and V rows only
 // from its eighth of the columns and its L2 caches eight times as many
 // distinct rows as when every XCD gathers from all of them.  One wave per
@@ -40,7 +41,6 @@ namespace as {
 
 namespace {
 
-constexpr int64_t kAttSliceMinDegree = 128;  // rows below are not sliced
 constexpr int64_t kAttChunkRows = 131072;    // sliced rows per partial chunk
 constexpr int64_t kAttSliceBlocks = 4096;    // slice-kernel workgroups per slice
 constexpr int64_t kAttReduceBlocks = 8192;   // reduction workgroups
@@ -486,8 +486,8 @@ void launch_attention_k(int gv, const AttArgs<T>& a, int64_t upper, int64_t chun
 
 size_t att_fixed_bytes(int64_t n) { return slice_plan_bytes(n); }
 
-// The plan settings of the attention on element type T: rows of degree >= 128
-// are sliced; short rows in 8 log2-degree buckets for 16-bit elements (the
+// The plan settings of the attention on element type T: rows of degree >=
+// att_slice_degree<T>() are sliced; short rows in 8 log2-degree buckets for 16-bit elements (the
 // grouped rows), in one for fp32.
 template <typename T>
 constexpr int att_light_buckets() {
@@ -497,9 +497,9 @@ constexpr int att_light_buckets() {
 // Per sliced row of a chunk: 8 x (m, l, F_v accumulators), fp32.
 size_t att_row_bytes(int64_t fv) { return static_cast<size_t>(kSlices) * (static_cast<size_t>(fv) + 2) * sizeof(float); }
 
-// Upper bound on the sliced rows: degree >= kAttSliceMinDegree.
-int64_t att_sliced_upper(int64_t n, int64_t nnz) {
-  const int64_t u = nnz / kAttSliceMinDegree;
+// Upper bound on the rows of degree >= `degree` (the sliced rows).
+int64_t att_sliced_upper(int64_t n, int64_t nnz, int64_t degree) {
+  const int64_t u = nnz / degree;
   return u < n ? u : n;
 }
 
@@ -509,9 +509,10 @@ template <typename T>
 int attention_run(const int64_t* crow, const int64_t* col, const T* query, const T* key, const T* value, T* out,
                   int64_t n, int64_t nnz, int64_t f_qk, int64_t f_v, float scale, const void* plan, int64_t plan_tag,
                   void* workspace, size_t workspace_bytes, void* stream, const char* what) {
-  if (plan != nullptr && plan_tag != slice_plan_tag(kAttSliceMinDegree, att_light_buckets<T>()))
+  constexpr int64_t kDegree = att_slice_degree<T>();
+  if (plan != nullptr && plan_tag != slice_plan_tag(kDegree, att_light_buckets<T>()))
     return fail(AS_ERR_INVALID_ARGUMENT, "the plan was built for other settings (plan tag %lld, this call needs %lld)",
-                (long long)plan_tag, (long long)slice_plan_tag(kAttSliceMinDegree, att_light_buckets<T>()));
+                (long long)plan_tag, (long long)slice_plan_tag(kDegree, att_light_buckets<T>()));
   if (plan != nullptr && !aligned(plan, 256)) return fail(AS_ERR_WORKSPACE, "the plan must be 256-byte aligned");
   if (n == 0) return AS_OK;
   if (crow == nullptr || query == nullptr || key == nullptr || value == nullptr || out == nullptr ||
@@ -526,7 +527,7 @@ int attention_run(const int64_t* crow, const int64_t* col, const T* query, const
     return fail(AS_ERR_WORKSPACE, "column-sliced attention needs at least %zu workspace bytes, got %zu",
                 fixed + row_bytes + 3 * 256, workspace_bytes);
   if (!aligned(workspace, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  const int64_t upper = att_sliced_upper(n, nnz);
+  const int64_t upper = att_sliced_upper(n, nnz, kDegree);
   int64_t chunk = static_cast<int64_t>((workspace_bytes - fixed - 3 * 256) / row_bytes);
   if (chunk > kAttChunkRows) chunk = kAttChunkRows;
   if (chunk > upper) chunk = upper;
@@ -542,13 +543,13 @@ int attention_run(const int64_t* crow, const int64_t* col, const T* query, const
   ws += align_up(states * sizeof(float), 256);
   float* pacc = reinterpret_cast<float*>(ws);
 
-  // order: rows of degree >= 128 (sliced) longest first, then the others; for
-  // 16-bit elements in 8 log2-degree buckets, longest first (light bucket b
-  // holds degrees [128 / 2^(b+1), 128 / 2^b), the last one the empty rows)
+  // order: rows of degree >= D = kDegree (sliced) longest first, then the
+  // others; for 16-bit elements in 8 log2-degree buckets, longest first (light
+  // bucket b holds degrees [D / 2^(b+1), D / 2^b), the last one the empty rows)
   // (grouped rows take similar degrees together)
   constexpr bool kHalf = sizeof(T) == 2;
   if (plan == nullptr) {
-    const int st = build_slice_plan(crow, col, n, kAttSliceMinDegree, att_light_buckets<T>(), false, view, s);
+    const int st = build_slice_plan(crow, col, n, kDegree, att_light_buckets<T>(), false, view, s);
     if (st != AS_OK) return st;
   }
   const AttArgs<T> a{crow, col, query, key, value, out, n, f_qk, f_v, scale, view.order, view.counts, view.off};
@@ -583,7 +584,8 @@ size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz, int64_t
   if (n < 0) n = 0;
   if (nnz < 0) nnz = 0;
   if (f_v < 4) f_v = 4;
-  int64_t rows = as::att_sliced_upper(n, nnz);
+  // the fp32 slicing degree, the lowest: enough for every element type
+  int64_t rows = as::att_sliced_upper(n, nnz, as::att_slice_degree<float>());
   if (rows > as::kAttChunkRows) rows = as::kAttChunkRows;
   if (rows < 1) rows = 1;
   // + 256 bytes per partial array for alignment
@@ -606,10 +608,12 @@ int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n, in
     return as::fail(AS_ERR_WORKSPACE, "an attention plan needs %zu bytes, got %zu", as::slice_plan_bytes(n),
                     plan_bytes);
   if (!as::aligned(plan, 256)) return as::fail(AS_ERR_WORKSPACE, "the plan must be 256-byte aligned");
-  const int light = dtype == AS_DTYPE_F32 ? as::att_light_buckets<float>() : as::att_light_buckets<as::Bf16>();
-  *plan_tag = as::slice_plan_tag(as::kAttSliceMinDegree, light);
+  const bool f32 = dtype == AS_DTYPE_F32;
+  const int light = f32 ? as::att_light_buckets<float>() : as::att_light_buckets<as::Bf16>();
+  const int64_t degree = f32 ? as::att_slice_degree<float>() : as::att_slice_degree<as::Bf16>();
+  *plan_tag = as::slice_plan_tag(degree, light);
   if (n == 0) return AS_OK;
-  const int st = as::build_slice_plan(crow, col, n, as::kAttSliceMinDegree, light, false, as::slice_plan_view(plan, n),
+  const int st = as::build_slice_plan(crow, col, n, degree, light, false, as::slice_plan_view(plan, n),
                                       static_cast<hipStream_t>(stream));
   if (st != AS_OK) return st;
   return as::check_launch("csr_attention_plan");

@@ -10,6 +10,26 @@
 namespace as {
 namespace {
 
+// Rows of at least this degree are cut into column slices; shorter rows run
+// whole (one wave each for fp32, several to a wave for 16-bit elements).
+// On the 2.4M-row, 124M-edge benchmark attention (Fqk 64, Fv 128, median
+// degree 16) fp32 is fastest from 128 (forward 11.17 ms, forward + backward
+// 35.86; 512: 11.27 / 36.29) and bf16 from 512 (forward 5.68 against 6.07 at
+// 128, forward + backward 19.63 against 21.23; 1024: 5.69 / 19.54): K and V
+// do not fit the caches there, and the grouped short-row kernels run longer
+// rows at the fabric rate without the partial states.  The forward and the
+// backward share the per-graph plans built with it.
+#ifndef AS_ATT_SLICE_MIN_DEGREE
+#define AS_ATT_SLICE_MIN_DEGREE 128
+#endif
+#ifndef AS_ATT_SLICE_MIN_DEGREE_16
+#define AS_ATT_SLICE_MIN_DEGREE_16 512
+#endif
+template <typename T>
+constexpr int64_t att_slice_degree() {
+  return sizeof(T) == 2 ? AS_ATT_SLICE_MIN_DEGREE_16 : AS_ATT_SLICE_MIN_DEGREE;
+}
+
 // Elements of type T in one 16-byte lane.
 template <typename T>
 constexpr int lane_elems() {

@@ -361,8 +361,8 @@ size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz,
 size_t as_csr_attention_plan_bytes(int64_t n);
 
 /* Builds the per-graph part of the column-sliced attention into `plan`
- * (256-byte aligned): the slice points of every row of degree >= 128 and
- * the degree-binned row order.  No reference counterpart (the reference
+ * (256-byte aligned): the slice points of every row of degree >= 128
+ * (fp32) or >= 512 (bf16 / fp16) and the degree-binned row order.  No reference counterpart (the reference
  * composes its attention from torch ops, autosage/_auto.py:762-780); a plan
  * is built once per graph and serves every later attention call on it with
  * the same element type (dtype AS_DTYPE_F32 / BF16 / F16), whatever Q, K
@@ -409,7 +409,8 @@ int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col,
  * f_qk and f_v multiples of 8 in [8, 512]; 16-byte aligned Q, K, V and out;
  * columns ascending within every row; the workspace of
  * as_csr_attention_colslice_workspace_bytes; plan and plan_tag as for
- * as_csr_attention_colslice_f32 (a plan built for this dtype). */
+ * as_csr_attention_colslice_f32 (a plan built for this dtype).  Rows are
+ * sliced from degree 512; shorter rows run several to a wavefront. */
 int as_csr_attention_colslice_16(const int64_t* crow, const int64_t* col,
                                  const void* query, const void* key,
                                  const void* value, void* out, int64_t n,

@@ -114,6 +114,8 @@ def test_argument_errors_are_reported_without_a_launch(lib):
         assert lib.as_csr_attention_plan(None, None, 0, 0, code, fake, 1 << 20, ctypes.byref(tag), None) == 0
         att[code] = tag.value
     assert att[0] != att[1] and att[1] == att[2]
+    # the slicing degree in the tag's low 32 bits: 128 for fp32, 512 for 16-bit
+    assert (att[0] & 0xFFFFFFFF, att[1] & 0xFFFFFFFF) == (128, 512)
     assert lib.as_csr_attention_plan(None, None, 4, 0, 3, fake, 1 << 20, ctypes.byref(tag), None) == 1
     assert lib.as_csr_attention_plan(fake, fake, 4, 4, 0, fake, 16, ctypes.byref(tag), None) == 4
     assert lib.as_csr_attention_plan_bytes(1000) == lib.as_spmm_colslice_plan_bytes(1000)
