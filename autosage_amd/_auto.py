@@ -305,6 +305,22 @@ def _cpu_info(operation: str) -> dict[str, Any]:
     }
 
 
+def _op_call(name: str, args: tuple, differentiable: tuple):
+    """``torch.ops.autosage.<name>(*args)``, or None when the ops are not
+    registered.  With nothing for autograd to record (grad mode off, or no
+    tensor of ``differentiable`` requiring grad) the op's CUDA implementation
+    is called directly: the function the op dispatches to, without the
+    autograd wrapper and the dispatcher (~4 us a call)."""
+    op = native_op(name)
+    if op is None:
+        return None
+    if not torch.is_grad_enabled() or not any(t is not None and t.requires_grad for t in differentiable):
+        from ._native import implementation
+
+        return implementation(name)(*args)
+    return op(*args)
+
+
 def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
     if choice == "autosage" and candidate in _ROUNDED16_ALL:
         from ._native import columns_ascending, spmm_rounded_16_impl, spmm_rows_16_impl
@@ -318,24 +334,31 @@ def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
     if choice == "autosage" and candidate == COLSLICE:
         # any column order: a graph whose columns do not ascend runs on its
         # row-sorted copy, made once per graph
-        return native_op("spmm_csr_colslice")(crow, col, val, x)
+        out = _op_call("spmm_csr_colslice", (crow, col, val, x), (val, x))
+        if out is None:
+            raise RuntimeError("native operator autosage::spmm_csr_colslice is not registered")
+        return out
     if choice == "autosage":
-        split, core = native_op("spmm_csr_split"), native_op("spmm_csr")
-        if split is not None and candidate is not None:
-            return split(crow, col, val, x, *map(int, candidate))
-        if core is not None:
-            return core(crow, col, val, x)
+        out = None
+        if candidate is not None:
+            out = _op_call("spmm_csr_split", (crow, col, val, x, *map(int, candidate)), (val, x))
+        if out is None:
+            out = _op_call("spmm_csr", (crow, col, val, x), (val, x))
+        if out is not None:
+            return out
     baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
     return baseline()
 
 
 def _run_sddmm_choice(choice, candidate, crow, col, query, key) -> torch.Tensor:
     if choice == "autosage":
-        split, core = native_op("sddmm_csr_split"), native_op("sddmm_csr")
-        if split is not None and candidate is not None:
-            return split(crow, col, query, key, *map(int, candidate))
-        if core is not None:
-            return core(crow, col, query, key)
+        out = None
+        if candidate is not None:
+            out = _op_call("sddmm_csr_split", (crow, col, query, key, *map(int, candidate)), (query, key))
+        if out is None:
+            out = _op_call("sddmm_csr", (crow, col, query, key), (query, key))
+        if out is not None:
+            return out
     baseline, _ = _prepare_sddmm_baseline(crow, col, query, key)
     return baseline()
 

@@ -51,9 +51,17 @@ def cache_directory() -> Path:
     return path
 
 
+_FILE_PATH_MEMO: dict[Path, Path] = {}
+
+
 def schedule_file() -> Path:
     """The schedule cache file of the current ``AUTOSAGE_CACHE_DIR``."""
-    return cache_directory() / "schedules.json"
+    directory = cache_directory()
+    path = _FILE_PATH_MEMO.get(directory)
+    if path is None:
+        path = directory / "schedules.json"
+        _FILE_PATH_MEMO[directory] = path
+    return path
 
 
 _DEVICE_MEMO: dict[int, dict[str, Any]] = {}
