@@ -296,9 +296,10 @@ def spmm_csr_impl(crow, col, val, x):
     _maybe_validate(crow, col)
     if x.dtype in DTYPES_16:
         # the same bits on every schedule: rows whole on small graphs and on
-        # graphs without a row to slice (one launch), else edge slices (with
-        # 2-byte features the fp64 partials of column slices cost more than
-        # their cache gain: 1.99 against 2.36 ms on the skewed graph)
+        # graphs without a row to slice (one launch), else edge slices (any
+        # column order; column slices, which need ascending columns, are
+        # within 1-5 % of them on the skewed graph at F >= 128 and slower at
+        # F = 64; spmm_csr_auto times both)
         if col.numel() <= ROWS_16_MAX_NNZ or sliced_rows(crow, False, x.size(1), x.dtype) == 0:
             return spmm_rows_16_impl(crow, col, val, x)
         return spmm_rounded_16_impl(crow, col, val, x, column_slices=False)

@@ -64,7 +64,14 @@ constexpr int64_t kColsliceMinDegree = AS_COLSLICE_MIN_DEGREE;
 // left whole: on the skewed 115M-edge benchmark graph at F = 64 that is
 // 1.92 ms against 2.00 (thresholds 192-320 all within 1 %); at F >= 128 the
 // same change costs 1-2 %.
+// With 2-byte elements a row's fp64 partials weigh four times as much
+// against its gathers as with fp32 (8·8·F bytes against 2·F a gathered row),
+// and rows are sliced from degree 512: the skewed graph in bf16 takes 1.900
+// ms at F = 128 and 4.290 at F = 256 with column slices from 512, against
+// 2.160 / 4.497 from 128 and 1.922 / 4.466 with edge slices (F = 64: 1.056
+// against 1.347 and 1.007; the scheduler times both).
 inline int64_t column_slice_degree(int64_t f, int64_t elem_bytes) {
+  if (elem_bytes == 2) return 4 * kColsliceMinDegree;
   return elem_bytes == 4 && f <= 64 ? 2 * kColsliceMinDegree : kColsliceMinDegree;
 }
 // With slices by edge count there is no cache gain, only the spread of long

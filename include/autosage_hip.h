@@ -154,7 +154,8 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col,
 
 /* Degree from which rows are sliced, for F features of type dtype
  * (AS_DTYPE_*): with column slices (column_slices != 0) 256 for fp32 with
- * F <= 64 and 128 otherwise; with edge slices 1024. */
+ * F <= 64, 128 for wider fp32 rows and 512 for bf16 / fp16; with edge slices
+ * 1024. */
 int64_t as_spmm_colslice_min_degree(int column_slices, int64_t f, int dtype);
 
 /* Bytes of a column-sliced plan for n rows (n·28 B of slice points and row

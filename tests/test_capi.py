@@ -78,7 +78,7 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_last_error() == b"null pointer argument"
     # column slices from degree 256 for fp32 rows of at most 64 features, else 128; edge slices from 1024
     assert [lib.as_spmm_colslice_min_degree(1, f, 0) for f in (1, 64, 65, 128)] == [256, 256, 128, 128]
-    assert [lib.as_spmm_colslice_min_degree(1, f, 1) for f in (8, 64, 128)] == [128, 128, 128]
+    assert [lib.as_spmm_colslice_min_degree(1, f, 1) for f in (8, 64, 128)] == [512, 512, 512]
     assert lib.as_spmm_colslice_min_degree(0, 64, 0) == 1024 and lib.as_spmm_colslice_min_degree(0, 128, 2) == 1024
     # column-sliced plans: settings and sizes are checked before any device work
     tag = ctypes.c_int64(0)

@@ -271,7 +271,7 @@ def test_sliced_rows_hint_only_sizes_the_launches():
     torch.cuda.synchronize()
     for y in outs[1:]:
         assert torch.equal(y, outs[0])
-    # 16-bit features, column and edge slices (thresholds 128 and 1024), with
+    # 16-bit features, column and edge slices (thresholds 512 and 1024), with
     # the count of grouped short rows (degree below 64 for F = 128) too
     xb = d_x.to(torch.bfloat16)
     limit = lib.as_spmm_rounded_16_group_degree(f)
@@ -400,11 +400,14 @@ def test_colslice_cooperative_hub_rows(features, weighted, monkeypatch):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_rounded16_cooperative_hub_rows(dtype):
-    """16-bit features with column slices (slicing degree 128): the
-    cooperative hub rows give the bits of the rounded fp64 oracle."""
-    crow, col = case_graph(30000, 3, seed=41, hubs=6, hub_degree=24000, empty=0.2)
+    """16-bit features with column slices (slicing degree 512, so rows of
+    32,768 edges and more cooperate): the cooperative hub rows give the bits
+    of the rounded fp64 oracle."""
+    n = 50000
+    crow, col = case_graph(n, 3, seed=41, hubs=4, hub_degree=40000, empty=0.2)
+    assert np.diff(crow).max() >= 512 * 64
     rng = np.random.default_rng(42)
-    x = torch.from_numpy(rng.standard_normal((30000, 128)).astype(np.float32)).to(dtype)
+    x = torch.from_numpy(rng.standard_normal((n, 128)).astype(np.float32)).to(dtype)
     val = torch.from_numpy(rng.standard_normal(col.size).astype(np.float32)).to(dtype)
     want = oracle.spmm_rounded_16(crow, col, val, x, dtype)
     d_crow, d_col = to_dev(crow, col)
