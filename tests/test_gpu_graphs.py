@@ -38,6 +38,32 @@ def test_native_ops_replay_in_a_hip_graph():
         lambda: ops.csr_attention(d_crow, d_col, d_q, d_k, d_x, 0.125),
         lambda: ops.csr_attention_colslice(d_crow, d_col, d_q, d_k, d_x, 0.125),
     ]
+    _replay_matches_eager(calls, lambda: (d_x.mul_(2.0), d_q.mul_(0.5)))
+
+
+def test_16_bit_ops_replay_in_a_hip_graph():
+    """bf16: the SDDMM in blocks of 64 edges, the rounded SpMM (rows whole,
+    and column slices on the graph's plan, built by the eager call) and the
+    16-bit column-sliced attention."""
+    crow, col = case_graph(6000, 20, seed=5, hubs=12, hub_degree=4000, empty=0.05)
+    rng = np.random.default_rng(5)
+    x, q, k = (torch.from_numpy(rng.standard_normal((6000, f)).astype(np.float32)).to(torch.bfloat16).cuda()
+               for f in (128, 64, 64))
+    d_crow, d_col = to_dev(crow, col)
+    ops = torch.ops.autosage
+    calls = [
+        lambda: ops.sddmm_csr(d_crow, d_col, q, k),
+        lambda: ops.spmm_csr(d_crow, d_col, None, x),
+        lambda: ops.spmm_csr_colslice(d_crow, d_col, None, x),
+        lambda: ops.csr_attention_colslice(d_crow, d_col, q, k, x, 0.125),
+    ]
+    _replay_matches_eager(calls, lambda: (x.mul_(2.0), q.mul_(0.5)))
+
+
+def _replay_matches_eager(calls, change_inputs):
+    """Captures ``calls`` in one graph and checks three replays (eager work
+    and a sync between them) against eager results, then a replay after
+    ``change_inputs`` against fresh eager results."""
     # eager results, and warm-up on a side stream (default priority) as
     # graph capture wants
     eager = [c() for c in calls]
@@ -61,8 +87,7 @@ def test_native_ops_replay_in_a_hip_graph():
         for i, (got, want) in enumerate(zip(captured, eager)):
             assert torch.equal(got, want), (replay, i)
     # inputs changed in place: the replay sees them
-    d_x.mul_(2.0)
-    d_q.mul_(0.5)
+    change_inputs()
     fresh = [c() for c in calls]
     graph.replay()
     torch.cuda.synchronize()
