@@ -29,7 +29,7 @@ from . import _env
 from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
 # 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
@@ -74,6 +74,16 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, ctypes.POINTER(ctypes.c_int64),
          _c_ptr],
+    ),
+    "as_spmm_colslice_plan_rect": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size,
+         ctypes.POINTER(ctypes.c_int64), _c_ptr],
+    ),
+    "as_spmm_csr_colslice_planned_rect": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size,
+         _c_i64, _c_ptr, _c_size, _c_i64, _c_i64, _c_ptr],
     ),
     "as_spmm_colslice_planned_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int, _c_i64]),
     "as_spmm_csr_colslice_planned": (
@@ -234,14 +244,18 @@ def _check(cond: bool, message: str) -> None:
         raise RuntimeError(message)
 
 
-def check_spmm_inputs(crow, col, val, x, allow_16: bool = False) -> None:
+def check_spmm_inputs(crow, col, val, x, allow_16: bool = False, rect: bool = False) -> None:
+    """Raises ``RuntimeError`` unless the inputs suit the native SpMM.
+    ``rect``: crow may have any number of rows (a row shard against the
+    whole X), else it has x.size(0) + 1 entries."""
     # every condition at once (device indices as ints, no device objects);
     # on a failure the checks below name the first one that fails
     xd = x.dtype
     if (crow.is_cuda and col.is_cuda and x.is_cuda and crow.dtype is torch.long and col.dtype is torch.long
             and crow.dim() == 1 and col.dim() == 1 and x.dim() == 2 and x.is_contiguous()
             and crow.is_contiguous() and col.is_contiguous()
-            and crow.get_device() == x.get_device() == col.get_device() and crow.numel() == x.size(0) + 1
+            and crow.get_device() == x.get_device() == col.get_device()
+            and (crow.numel() == x.size(0) + 1 or (rect and crow.numel() >= 1))
             and (xd is torch.float32 or (allow_16 and xd in DTYPES_16))
             and (val is None or (val.is_cuda and val.get_device() == x.get_device() and val.dtype is xd
                                  and val.is_contiguous() and val.numel() == col.numel()))):
@@ -252,7 +266,10 @@ def check_spmm_inputs(crow, col, val, x, allow_16: bool = False) -> None:
     _check(x.dim() == 2 and x.is_contiguous(), "x must be contiguous with shape [N, F]")
     _check(crow.is_contiguous() and col.is_contiguous(), "crow and col must be contiguous")
     _check(crow.device == x.device and col.device == x.device, "crow, col, and x must be on the same CUDA device")
-    _check(crow.numel() == x.size(0) + 1, "crow must contain N + 1 entries")
+    if rect:
+        _check(crow.numel() >= 1, "crow must contain at least one entry")
+    else:
+        _check(crow.numel() == x.size(0) + 1, "crow must contain N + 1 entries")
     if allow_16:
         _check(x.dtype == torch.float32 or x.dtype in DTYPES_16, "x must be float32, bfloat16 or float16")
     else:
@@ -386,13 +403,15 @@ _PLAN_MEMO = GraphMemo("colslice_plan", max_entries=32, max_bytes=1 << 30)
 
 
 def colslice_plan(crow: torch.Tensor, col: torch.Tensor, f: int, dtype: torch.dtype,
-                  column_slices: bool) -> tuple[torch.Tensor, int]:
+                  column_slices: bool, n_cols: Optional[int] = None) -> tuple[torch.Tensor, int]:
     """(plan, tag) of the column-sliced SpMM for this graph (columns ascending
     within rows for column slices), F and element type: the slice points and
     the degree-binned row order, built on the device once per live,
     unmodified (crow, col) pair and settings, then reused by every call
-    whatever X.  The build synchronises the stream once, so that a later
-    call on another stream finds the plan complete."""
+    whatever X.  ``n_cols``: the column space of a row shard (the rows of
+    the whole X); None for a square graph.  The build synchronises the
+    stream once, so that a later call on another stream finds the plan
+    complete."""
     lib = library()
     code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
     degree = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices)), f, code))
@@ -402,34 +421,90 @@ def colslice_plan(crow: torch.Tensor, col: torch.Tensor, f: int, dtype: torch.dt
         plan = _workspace(lib.as_spmm_colslice_plan_bytes(n), crow.device)
         tag = ctypes.c_int64(0)
         with _on(crow.device):
-            status = lib.as_spmm_colslice_plan(_ptr(crow), _ptr(col), n, col.numel(), f, code, int(bool(column_slices)),
-                                               _ptr(plan), plan.numel(), ctypes.byref(tag), _stream(crow.device))
+            if n_cols is None:
+                status = lib.as_spmm_colslice_plan(_ptr(crow), _ptr(col), n, col.numel(), f, code,
+                                                   int(bool(column_slices)), _ptr(plan), plan.numel(),
+                                                   ctypes.byref(tag), _stream(crow.device))
+            else:
+                status = lib.as_spmm_colslice_plan_rect(_ptr(crow), _ptr(col), n, int(n_cols), col.numel(), f, code,
+                                                        int(bool(column_slices)), _ptr(plan), plan.numel(),
+                                                        ctypes.byref(tag), _stream(crow.device))
             _raise(status, "autosage column-sliced plan")
             torch.cuda.current_stream(crow.device).synchronize()
         return plan, int(tag.value)
 
     # the plan depends on the slicing degree and on fp32 against 16-bit (the
     # number of light buckets), not on F itself
-    return _PLAN_MEMO.get((crow, col), (degree, code != 0, bool(column_slices)), compute)
+    return _PLAN_MEMO.get((crow, col), (degree, code != 0, bool(column_slices), n_cols), compute)
 
 
-def _spmm_colslice_planned(crow, col, val, x, y, column_slices: bool, sliced: int, grouped: int):
+def _spmm_colslice_planned(crow, col, val, x, y, column_slices: bool, sliced: int, grouped: int,
+                           n_cols: Optional[int] = None):
     """The column-sliced SpMM on its per-graph plan: the workspace holds the
     partial buffers only (the workspace cap counts the plan, as in the
-    unplanned call)."""
-    n, f = x.shape
+    unplanned call).  ``n_cols``: as for ``colslice_plan``."""
+    n = crow.numel() - 1
+    f = x.size(1)
     code = 0 if x.dtype == torch.float32 else DTYPES_16[x.dtype]
     lib = library()
-    plan, tag = colslice_plan(crow, col, f, x.dtype, column_slices)
+    plan, tag = colslice_plan(crow, col, f, x.dtype, column_slices, n_cols)
     needed = lib.as_spmm_colslice_planned_workspace_bytes(n, f, code, sliced)
     ws = _workspace(max(min(needed, _colslice_workspace_cap() - plan.numel()), 0), x.device)
     with _on(x.device):
-        status = lib.as_spmm_csr_colslice_planned(
-            _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, code, int(column_slices),
-            _ptr(plan), plan.numel(), tag, _ptr(ws), ws.numel(), sliced, grouped, _stream(x.device),
-        )
+        if n_cols is None:
+            status = lib.as_spmm_csr_colslice_planned(
+                _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, code, int(column_slices),
+                _ptr(plan), plan.numel(), tag, _ptr(ws), ws.numel(), sliced, grouped, _stream(x.device),
+            )
+        else:
+            status = lib.as_spmm_csr_colslice_planned_rect(
+                _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, int(n_cols), col.numel(), f, code,
+                int(column_slices), _ptr(plan), plan.numel(), tag, _ptr(ws), ws.numel(), sliced, grouped,
+                _stream(x.device),
+            )
     _raise(status, "autosage::spmm_csr_colslice" if code == 0 else "autosage::spmm_csr (16-bit)")
     return y
+
+
+def spmm_csr_rect_impl(crow, col, val, x, exact: bool = False):
+    """Y = A·X for an n × n_cols CSR A (n = crow.numel() - 1 rows, n_cols =
+    x.size(0)); Y has n rows.  This is the product of one row shard of a
+    larger graph (its rows, crow rebased to 0, the columns unchanged) with
+    the whole X.
+
+    ``exact``: fp32 only, one wave per row in CSR order (the sequential
+    fp32 product of ``spmm_csr``, bit-identical to the same rows of the whole
+    graph's product).  Otherwise the column-sliced schedule: fp32 with fp64
+    partials per column slice, 16-bit rounded once; the slices cut the
+    whole column space [0, n_cols), so every row is summed as in the whole
+    graph (a graph whose columns do not ascend runs on its row-sorted copy)."""
+    check_spmm_inputs(crow, col, val, x, allow_16=not exact, rect=True)
+    n = crow.numel() - 1
+    n_cols, f = x.shape
+    _check(n <= 2**31 - 1 and n_cols <= 2**31 - 1, "crow and x must have fewer than 2^31 rows")
+    y = torch.empty((n, f), dtype=x.dtype, device=x.device)
+    if n == 0 or f == 0:
+        return y
+    if _env.get("AUTOSAGE_VALIDATE") == "1":
+        validate_csr(crow, col, n_cols)
+    if exact:
+        with _on(x.device):
+            status = library().as_spmm_csr_f32(
+                _ptr(crow), _ptr(col), _ptr(val), _ptr(x), _ptr(y), n, col.numel(), f, int(_env_vec4()),
+                _stream(x.device),
+            )
+        _raise(status, "autosage row-shard SpMM")
+        return y
+    sorted_col, perm = row_sorted(crow, col, n_cols)
+    val = _row_sorted_weights(col, val, perm)
+    col = sorted_col
+    lib = library()
+    if x.dtype == torch.float32:
+        return _spmm_colslice_planned(crow, col, val, x, y, column_slices=True,
+                                      sliced=sliced_rows(crow, True, f, x.dtype), grouped=0, n_cols=n_cols)
+    threshold = int(lib.as_spmm_colslice_min_degree(1, f, DTYPES_16[x.dtype]))
+    sliced, grouped = row_counts(crow, threshold, int(lib.as_spmm_rounded_16_group_degree(f)))
+    return _spmm_colslice_planned(crow, col, val, x, y, True, sliced, grouped, n_cols=n_cols)
 
 
 # 16-bit spmm_csr on graphs of at most this many edges, or without a row of
@@ -865,21 +940,23 @@ def validate_csr(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = 
     _raise_for_flags(csr_flags(crow, col, n_cols))
 
 
-def columns_ascending(crow: torch.Tensor, col: torch.Tensor) -> bool:
+def columns_ascending(crow: torch.Tensor, col: torch.Tensor, n_cols: Optional[int] = None) -> bool:
     """Whether the columns of every row are in non-decreasing order (what
     the column slices of the sliced kernels are cut along).  Memoised per
     live, unmodified (crow, col) tensor pair; raises ``ValueError`` for a
-    malformed graph."""
+    malformed graph.  ``n_cols``: the column count of a row shard (None: a
+    square graph)."""
 
     def compute() -> bool:
-        bad = csr_flags(crow, col)
+        bad = csr_flags(crow, col, n_cols)
         _raise_for_flags(bad)
         return not bad & _UNSORTED_FLAG
 
-    return _ASCENDING_MEMO.get((crow, col), None, compute)
+    return _ASCENDING_MEMO.get((crow, col), n_cols, compute)
 
 
-def row_sorted(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+def row_sorted(crow: torch.Tensor, col: torch.Tensor,
+               n_cols: Optional[int] = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
     """(col', perm) with the columns of every row in ascending order:
     ``col'[k] = col[perm[k]]`` and ``perm`` permutes edges only inside their
     row (stable, so equal columns keep their order).  ``perm`` is None and
@@ -888,23 +965,25 @@ def row_sorted(crow: torch.Tensor, col: torch.Tensor) -> tuple[torch.Tensor, Opt
     per row, so the column-sliced products over it are products of the
     original graph.  Built on the device once per live, unmodified graph
     (one sort of the nnz (row, column) keys) and memoised."""
-    if columns_ascending(crow, col):
+    if columns_ascending(crow, col, n_cols):
         return col, None
 
     def compute():
         n = crow.numel() - 1
+        width = n if n_cols is None else int(n_cols)
         counts = (crow[1:] - crow[:-1]).to(torch.long)
         rows = torch.repeat_interleave(torch.arange(n, device=crow.device, dtype=torch.long), counts,
                                        output_size=col.numel())
         # rows ascend already, so (row, column) keys sort each row's columns
-        # in place; n < 2^31 keeps row·n + column inside int64
-        keys = rows.mul_(n).add_(col)
+        # in place; rows and columns below 2^31 keep row·width + column
+        # inside int64
+        keys = rows.mul_(width).add_(col)
         sorted_keys, perm = torch.sort(keys, stable=True)
         del keys
-        col_sorted = sorted_keys.remainder_(n) if n > 0 else sorted_keys
+        col_sorted = sorted_keys.remainder_(width) if width > 0 else sorted_keys
         return col_sorted.contiguous(), perm
 
-    return _ROW_SORTED_MEMO.get((crow, col), None, compute)
+    return _ROW_SORTED_MEMO.get((crow, col), n_cols, compute)
 
 
 def _row_sorted_weights(col: torch.Tensor, val: Optional[torch.Tensor], perm: Optional[torch.Tensor]):

@@ -1,6 +1,7 @@
 // Column slices shared by the column-sliced SpMM and attention.
 //
-// The column space [0, N) of a square graph is cut into S equal ranges (S a
+// The column space [0, N) of a square graph (or of the graph a row shard was
+// cut from) is cut into S equal ranges (S a
 // multiple of kSlices = 8, the XCD count of an MI355X; slice s runs on XCD
 // s % 8).  With columns ascending inside every row, the edges of row r in
 // slice s form the contiguous range
@@ -27,12 +28,14 @@ __device__ __forceinline__ int64_t slice_start(int64_t n_cols, int b) {
 
 // Rows shorter than `min_degree` are never sliced and keep no slice points.
 // by_edges: slice b of a row of d edges starts at edge floor(d·b / S) (equal
-// runs of edges, for graphs whose columns do not ascend).
+// runs of edges, for graphs whose columns do not ascend).  n_cols: the
+// column space the slices cut (n for a square graph; the full graph's N for
+// a shard of its rows).
 template <int S>
 __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __restrict__ crow,
                                                               const int64_t* __restrict__ col, int64_t n,
-                                                              int64_t min_degree, int32_t* __restrict__ off,
-                                                              bool by_edges) {
+                                                              int64_t n_cols, int64_t min_degree,
+                                                              int32_t* __restrict__ off, bool by_edges) {
   constexpr int kBounds = S - 1;
   const int64_t total = n * kBounds;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -47,7 +50,7 @@ __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __r
       off[t] = static_cast<int32_t>((hi - lo) * b / S);
       continue;
     }
-    const int64_t start = slice_start<S>(n, b);
+    const int64_t start = slice_start<S>(n_cols, b);
     while (lo < hi) {
       const int64_t mid = lo + ((hi - lo) >> 1);
       if (col[mid] < start) lo = mid + 1;
@@ -59,12 +62,12 @@ __global__ __launch_bounds__(kBlock) void slice_points_kernel(const int64_t* __r
 
 template <int S = kSlices>
 inline void launch_slice_points(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree,
-                                int32_t* off, hipStream_t s, bool by_edges = false) {
+                                int32_t* off, hipStream_t s, bool by_edges = false, int64_t n_cols = -1) {
   int64_t blocks = (n * (S - 1) + kBlock - 1) / kBlock;
   if (blocks > kGridStrideBlocks) blocks = kGridStrideBlocks;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(slice_points_kernel<S>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, crow, col, n,
-                     min_degree, off, by_edges);
+                     n_cols < 0 ? n : n_cols, min_degree, off, by_edges);
 }
 
 // Edge range [a, b) of `slice` (of S) in a row of `deg` edges, relative to
@@ -118,11 +121,13 @@ inline int64_t slice_plan_tag(int64_t min_degree, int light_buckets) {
 }
 
 // order: rows of degree >= min_degree in 8 log2-degree buckets, longest
-// first, then the shorter rows in `light_buckets` log2-degree buckets
+// first, then the shorter rows in `light_buckets` log2-degree buckets.
+// n_cols < 0: a square graph (n columns).
 template <int S = kSlices>
 inline int build_slice_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree,
-                            int light_buckets, bool by_edges, const SlicePlan& plan, hipStream_t s) {
-  launch_slice_points<S>(crow, col, n, min_degree, plan.off, s, by_edges);
+                            int light_buckets, bool by_edges, const SlicePlan& plan, hipStream_t s,
+                            int64_t n_cols = -1) {
+  launch_slice_points<S>(crow, col, n, min_degree, plan.off, s, by_edges, n_cols);
   return launch_bin_rows(crow, n, min_degree, kMaxHeavyBuckets, light_buckets, plan.order, plan.counts, plan.bin_ws,
                          s);
 }

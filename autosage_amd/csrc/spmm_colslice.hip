@@ -804,12 +804,22 @@ size_t colslice_row_bytes(int64_t f) {
 
 // Rows per chunk when the workspace allows: the pipeline overlaps the
 // reduction of chunk k with the slice work of chunk k + 1, so all but the
-// last chunk's reduction is hidden.
+// last chunk's reduction is hidden.  Chunks hold at least 32,768 rows: on
+// smaller graphs each extra launch waits for its own longest (row, slice)
+// and the chunks' rows are of one degree range each (the order is binned by
+// degree), so one chunk is faster.  The reference's hub sweep (20,000 rows)
+// takes 0.059 against 0.076 ms as one chunk, and an eighth of the rows of the
+// skewed 115M-edge graph (29,000 rows against all 232,965 columns) 0.44
+// against 0.47 ms at F = 128 fp32 and 0.27 against 0.31 ms in bf16; the
+// whole skewed graph keeps its four chunks of 58,000 rows.
 #ifndef AS_COLSLICE_CHUNKS
 #define AS_COLSLICE_CHUNKS 4
 #endif
 constexpr int64_t kColsliceChunks = AS_COLSLICE_CHUNKS;
-constexpr int64_t kColsliceMinChunkRows = 4096;
+#ifndef AS_COLSLICE_MIN_CHUNK_ROWS
+#define AS_COLSLICE_MIN_CHUNK_ROWS 32768
+#endif
+constexpr int64_t kColsliceMinChunkRows = AS_COLSLICE_MIN_CHUNK_ROWS;
 
 int64_t preferred_chunk_rows(int64_t n) {
   int64_t c = (n + kColsliceChunks - 1) / kColsliceChunks;
@@ -979,17 +989,20 @@ inline int light_bucket_count(int64_t elem_bytes) { return elem_bytes == 2 ? kMa
 
 inline int64_t plan_tag_of(int64_t min_degree, int light_buckets) { return slice_plan_tag(min_degree, light_buckets); }
 
-inline int build_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t min_degree, int light_buckets,
-                      Slicing slicing, const PlanView& plan, hipStream_t s) {
-  return build_slice_plan<kSpmmSlices>(crow, col, n, min_degree, light_buckets, slicing == kSliceEdges, plan, s);
+// n_cols: the column space (rows of X); n for a square graph.
+inline int build_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t n_cols, int64_t min_degree,
+                      int light_buckets, Slicing slicing, const PlanView& plan, hipStream_t s) {
+  return build_slice_plan<kSpmmSlices>(crow, col, n, min_degree, light_buckets, slicing == kSliceEdges, plan, s,
+                                       n_cols);
 }
 
 // `plan`: built by build_plan for this graph, min_degree and light bucket
 // count (the caller's duty); the workspace holds the partial buffers only.
+// n rows of A and Y, n_cols rows of X.
 template <typename T>
 int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
-                     int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials, size_t partial_bytes,
-                     int64_t sliced_rows, int64_t grouped_rows, hipStream_t s) {
+                     int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials,
+                     size_t partial_bytes, int64_t sliced_rows, int64_t grouped_rows, hipStream_t s) {
   const size_t row_bytes = colslice_row_bytes(f);
   if (partials == nullptr || partial_bytes < 2 * row_bytes)
     return fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu bytes of partial buffers, got %zu",
@@ -1012,7 +1025,8 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
   }
   const int64_t tiles = v >= 8 ? (f + P * v - 1) / (P * v) : 1;
   // every X byte offset fits 32 bits, row index and row bytes fit 24 bits
-  const bool off32 = n <= (int64_t(1) << 24) && f * E < (int64_t(1) << 24) && n * f * E <= (int64_t(1) << 32);
+  const bool off32 =
+      n_cols <= (int64_t(1) << 24) && f * E < (int64_t(1) << 24) && n_cols * f * E <= (int64_t(1) << 32);
   const int vr = (f % 2 == 0 && aligned(y, static_cast<size_t>(2 * E))) ? 2 : 1;
 
   // two partial buffers of `capacity` rows each (chunk k writes buffer
@@ -1101,10 +1115,11 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const PlanView plan = plan_view(workspace, n);
   const int64_t min_degree = slicing_degree(slicing, f, E);
-  st = build_plan(crow, col, n, min_degree, light_bucket_count(E), slicing, plan, s);
+  st = build_plan(crow, col, n, n, min_degree, light_bucket_count(E), slicing, plan, s);
   if (st != AS_OK) return st;
-  return colslice_execute<T>(crow, col, val, x, y, n, nnz, f, min_degree, plan, static_cast<char*>(workspace) + fixed,
-                             workspace_bytes - fixed, sliced_rows, grouped_rows, s);
+  return colslice_execute<T>(crow, col, val, x, y, n, n, nnz, f, min_degree, plan,
+                             static_cast<char*>(workspace) + fixed, workspace_bytes - fixed, sliced_rows, grouped_rows,
+                             s);
 }
 
 inline int elem_bytes_of(int dtype) {
@@ -1130,9 +1145,11 @@ int64_t as_spmm_colslice_min_degree(int column_slices, int64_t f, int dtype) {
 
 size_t as_spmm_colslice_plan_bytes(int64_t n) { return as::colslice_fixed_bytes(n); }
 
-int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t nnz, int64_t f, int dtype,
-                          int column_slices, void* plan, size_t plan_bytes, int64_t* plan_tag, void* stream) {
+int as_spmm_colslice_plan_rect(const int64_t* crow, const int64_t* col, int64_t n, int64_t n_cols, int64_t nnz,
+                               int64_t f, int dtype, int column_slices, void* plan, size_t plan_bytes,
+                               int64_t* plan_tag, void* stream) {
   as::clear_error();
+  if (n_cols < 0 || n_cols > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "n_cols exceeds kernel index range");
   const int64_t e = as::elem_bytes_of(dtype);
   if (e == 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16");
   if (e == 4 && !column_slices)
@@ -1150,10 +1167,16 @@ int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n, in
   const int light = as::light_bucket_count(e);
   *plan_tag = as::plan_tag_of(min_degree, light);
   if (n == 0) return AS_OK;
-  const int st = as::build_plan(crow, col, n, min_degree, light, slicing, as::plan_view(plan, n),
+  const int st = as::build_plan(crow, col, n, n_cols, min_degree, light, slicing, as::plan_view(plan, n),
                                 static_cast<hipStream_t>(stream));
   if (st != AS_OK) return st;
   return as::check_launch("spmm_colslice_plan");
+}
+
+int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t nnz, int64_t f, int dtype,
+                          int column_slices, void* plan, size_t plan_bytes, int64_t* plan_tag, void* stream) {
+  return as_spmm_colslice_plan_rect(crow, col, n, n < 0 ? 0 : n, nnz, f, dtype, column_slices, plan, plan_bytes,
+                                    plan_tag, stream);
 }
 
 size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype, int64_t sliced_rows) {
@@ -1164,11 +1187,13 @@ size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype,
   return 2 * static_cast<size_t>(rows) * as::colslice_row_bytes(f);
 }
 
-int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
-                                 int64_t n, int64_t nnz, int64_t f, int dtype, int column_slices, const void* plan,
-                                 size_t plan_bytes, int64_t plan_tag, void* workspace, size_t workspace_bytes,
-                                 int64_t sliced_rows, int64_t grouped_rows, void* stream) {
+int as_spmm_csr_colslice_planned_rect(const int64_t* crow, const int64_t* col, const void* val, const void* x,
+                                      void* y, int64_t n, int64_t n_cols, int64_t nnz, int64_t f, int dtype,
+                                      int column_slices, const void* plan, size_t plan_bytes, int64_t plan_tag,
+                                      void* workspace, size_t workspace_bytes, int64_t sliced_rows,
+                                      int64_t grouped_rows, void* stream) {
   as::clear_error();
+  if (n_cols < 0 || n_cols > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "n_cols exceeds kernel index range");
   const int64_t e = as::elem_bytes_of(dtype);
   if (e == 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16");
   if (e == 4 && !column_slices)
@@ -1191,16 +1216,25 @@ int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col, const 
   const as::PlanView view = as::plan_view(const_cast<void*>(plan), n);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == AS_DTYPE_F32)
-    st = as::colslice_execute<float>(crow, col, val, x, y, n, nnz, f, min_degree, view, workspace, workspace_bytes,
-                                     sliced_rows, 0, s);
+    st = as::colslice_execute<float>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
+                                     workspace_bytes, sliced_rows, 0, s);
   else if (dtype == AS_DTYPE_BF16)
-    st = as::colslice_execute<as::Bf16>(crow, col, val, x, y, n, nnz, f, min_degree, view, workspace, workspace_bytes,
-                                        sliced_rows, grouped_rows, s);
+    st = as::colslice_execute<as::Bf16>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
+                                        workspace_bytes, sliced_rows, grouped_rows, s);
   else
-    st = as::colslice_execute<as::Fp16>(crow, col, val, x, y, n, nnz, f, min_degree, view, workspace, workspace_bytes,
-                                        sliced_rows, grouped_rows, s);
+    st = as::colslice_execute<as::Fp16>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
+                                        workspace_bytes, sliced_rows, grouped_rows, s);
   if (st != AS_OK) return st;
   return as::check_launch("spmm_csr_colslice_planned");
+}
+
+int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
+                                 int64_t n, int64_t nnz, int64_t f, int dtype, int column_slices, const void* plan,
+                                 size_t plan_bytes, int64_t plan_tag, void* workspace, size_t workspace_bytes,
+                                 int64_t sliced_rows, int64_t grouped_rows, void* stream) {
+  return as_spmm_csr_colslice_planned_rect(crow, col, val, x, y, n, n < 0 ? 0 : n, nnz, f, dtype, column_slices,
+                                           plan, plan_bytes, plan_tag, workspace, workspace_bytes, sliced_rows,
+                                           grouped_rows, stream);
 }
 
 int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const float* val, const float* x, float* y,

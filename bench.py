@@ -340,6 +340,10 @@ def main() -> int:
     parser.add_argument("--backward", action="store_true",
                         help="SpMM fp32: time forward + dX backward (flops and bytes of both products); cfg5: the "
                              "attention forward + dQ, dK, dV")
+    parser.add_argument("--shards", type=int, default=0,
+                        help="SpMM workloads: cut the graph into this many nnz-balanced row shards (one GPU's share "
+                             "each when the graph is split by rows over that many GPUs) and time each shard's "
+                             "product with the whole X on this GPU; the line is the slowest shard")
     parser.add_argument("--hub-degree", type=int, default=12_000, help="hubsweep: degree of row 0")
     parser.add_argument("--other-degree", type=int, default=32, help="hubsweep: degree of every other row")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -373,6 +377,10 @@ def main() -> int:
         del src, dst
     if args.probe_overhead:
         result = probe_overhead(args, device)
+    elif args.shards > 0:
+        if args.workload not in ("cfg1", "cfg2", "cfg3", "er"):
+            raise SystemExit("--shards is for the SpMM workloads (cfg1, cfg2, cfg3, er)")
+        result = bench_shards(args, device)
     elif args.workload in ("cfg1", "cfg2", "cfg3", "er"):
         result = bench_spmm(args, device)
     elif args.workload == "hubsweep":
@@ -597,6 +605,101 @@ def bench_spmm(args, device) -> dict:
     else:
         result["cpu_baseline"] = None
     return result
+
+
+def bench_shards(args, device) -> dict:
+    """One GPU's share of an SpMM workload split by rows over ``--shards``
+    GPUs: the graph is cut at nnz-balanced row prefixes
+    (``autosage_amd.shard.cut_rows``) and each shard's product with the whole
+    X (``spmm_csr_shard``: the column-sliced schedule, fp32 or 16-bit) is
+    timed on this GPU in turn, at its real shape (its rows, all N columns).
+    The line's step is the slowest shard; the table lists every shard and
+    the whole graph's step for comparison.  The all-gather of X that a
+    multi-GPU run needs before the product is not run (one GPU)."""
+    from autosage_amd import shard, synth
+    from autosage_amd._auto import spmm_csr_auto
+
+    t0 = time.time()
+    f = args.features or {"cfg1": 64, "cfg2": 128, "cfg3": 128, "er": 64}[args.workload]
+    if args.workload == "er":
+        w = synth.erdos_renyi(seed=args.seed, features=f)
+    else:
+        w = {"cfg1": synth.config1, "cfg2": synth.config2, "cfg3": synth.config3}[args.workload](
+            seed=args.seed, features=f)
+    log(f"generated {args.workload}: {w.degree_stats()} in {time.time() - t0:.1f}s")
+    n, nnz = w.rows, w.nnz
+    crow = torch.from_numpy(w.crow).to(device)
+    col = torch.from_numpy(w.col).to(device)
+    val = None if w.val is None else torch.from_numpy(w.val).to(device)
+    x = torch.from_numpy(w.dense["x"]).to(device)
+    half = args.dtype != "f32"
+    elem = 2 if half else 4
+    if half:
+        dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+        x = x.to(dt)
+        val = None if val is None else val.to(dt)
+    weighted = val is not None
+    cuts = shard.cut_rows(crow, args.shards)
+    table = []
+    for k, (r0, r1) in enumerate(zip(cuts, cuts[1:])):
+        s_crow, s_col, s_val = shard.shard_csr(crow, col, val, r0, r1)
+        nnz_k = s_col.numel()
+
+        def step(s_crow=s_crow, s_col=s_col, s_val=s_val):
+            return shard.spmm_csr_shard(s_crow, s_col, s_val, x)
+
+        ms, samples = time_steps(step, args.steps, args.warmup)
+        deg = (s_crow[1:] - s_crow[:-1])
+        table.append({"shard": k, "rows": [r0, r1], "nnz": nnz_k, "max_degree": int(deg.max()) if r1 > r0 else 0,
+                      "ms": round(ms, 4), "gflops": round(2.0 * nnz_k * f / (ms * 1e-3) / 1e9, 2),
+                      "per_call_ms": [round(s_, 4) for s_ in samples]})
+        log(f"shard {k}: rows [{r0}, {r1}), nnz {nnz_k}: {ms:.4f} ms")
+    whole_ms, _ = time_steps(lambda: spmm_csr_auto(crow, col, val, x)[0], args.steps, args.warmup)
+    slowest = max(table, key=lambda r: r["ms"])
+    rows_k = slowest["rows"][1] - slowest["rows"][0]
+    nnz_k = slowest["nnz"]
+    type_name = {"f32": "fp32", "bf16": "bf16", "fp16": "fp16"}[args.dtype]
+    workload_name = (f"{args.workload} SpMM {type_name} F={f}" + (" weighted" if weighted else " unweighted")
+                     + f", row shard {slowest['shard']} of {args.shards}")
+    algo = (elem * f * nnz_k + elem * f * rows_k + 8 * nnz_k + 8 * (rows_k + 1)
+            + (elem * nnz_k if weighted else 0))
+    # the shard's compulsory bytes: the X rows its columns reach (all of X
+    # on these graphs, bounded by N), its Y rows, its index stream
+    compulsory = (elem * f * n + elem * f * rows_k + 8 * nnz_k + 8 * (rows_k + 1)
+                  + (elem * nnz_k if weighted else 0))
+    traffic = profiled_traffic(workload_name, "colslice")
+    return {
+        "metric": METRIC,
+        "value": slowest["gflops"],
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": slowest["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic",
+        "config": {
+            "workload": workload_name,
+            "rows": rows_k,
+            "nnz": nnz_k,
+            "columns": n,
+            "features": f,
+            "variant": "colslice",
+            "graph_fingerprint": w.fingerprint(),
+            "cut": "nnz-balanced row prefixes: shard k starts at the first row r with crow[r] >= ceil(k*nnz/P)",
+            "note": "one GPU's share of the graph split by rows over P GPUs, at its real shape (its rows, all N "
+                    "columns, the whole X resident); the all-gather of X a multi-GPU run needs first is not run",
+        },
+        "roofline": roofline_record(slowest["ms"], algo, compulsory, traffic, (nnz_k + rows_k) * f * elem),
+        "shards": table,
+        "sum_of_shard_ms": round(sum(r["ms"] for r in table), 4),
+        "whole_graph_ms": round(whole_ms, 4),
+        "allgather_bytes_per_gpu": (args.shards - 1) * n * f * elem // args.shards,
+        "cpu_baseline": None,
+    }
 
 
 def plan_record(step, args, crow, col, f, dtype, column_slices: bool, ms: float) -> dict:

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 6
+#define AS_ABI_VERSION 7
 
 typedef enum as_status {
   AS_OK = 0,
@@ -201,6 +201,32 @@ int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col,
                                  void* workspace, size_t workspace_bytes,
                                  int64_t sliced_rows, int64_t grouped_rows,
                                  void* stream);
+
+/* Row shards.  No reference counterpart: the reference runs one graph on one
+ * GPU.  A graph split by rows over several GPUs gives each GPU the CSR of
+ * its rows [r0, r1) (crow rebased to start at 0, the columns unchanged) and
+ * the whole of X, n_cols = N rows; Y holds the shard's n = r1 - r0 rows.
+ * These two entries are as_spmm_colslice_plan and
+ * as_spmm_csr_colslice_planned for such an n × n_cols CSR: the column
+ * slices cut [0, n_cols), so a shard's slice points, and with them its
+ * rows' sums, are those of the same rows in the whole graph (a shard of at
+ * most 2^24 edges adds its hub rows' wave sums through LDS, which can move
+ * the fp64 sum of a row by less than 2^-52 of its largest partial).  The
+ * square entries are these with n_cols = n. */
+int as_spmm_colslice_plan_rect(const int64_t* crow, const int64_t* col,
+                               int64_t n, int64_t n_cols, int64_t nnz,
+                               int64_t f, int dtype, int column_slices,
+                               void* plan, size_t plan_bytes,
+                               int64_t* plan_tag, void* stream);
+int as_spmm_csr_colslice_planned_rect(const int64_t* crow, const int64_t* col,
+                                      const void* val, const void* x, void* y,
+                                      int64_t n, int64_t n_cols, int64_t nnz,
+                                      int64_t f, int dtype, int column_slices,
+                                      const void* plan, size_t plan_bytes,
+                                      int64_t plan_tag, void* workspace,
+                                      size_t workspace_bytes,
+                                      int64_t sliced_rows,
+                                      int64_t grouped_rows, void* stream);
 
 /* SpMM with bf16 or fp16 features, weights and output (dtype
  * AS_DTYPE_BF16 / AS_DTYPE_F16; val may be NULL).  The reference has no

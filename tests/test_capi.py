@@ -104,7 +104,21 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_last_error().startswith(b"the plan was built for other settings")
     assert lib.as_spmm_csr_colslice_planned(fake, fake, None, fake, fake, 4, 4, 128, 0, 0, fake, 1 << 20,
                                             tags[(0, 128, 1)], fake, 1 << 20, -1, 0, None) == 1
-    # two partial buffers of a chunk's rows (all 1,000 rows here: chunks hold at least 4,096), 8 slices of F fp64
+    # the row-shard forms take the column count separately and refuse a bad one before any pointer is read
+    rect_tag = ctypes.c_int64(0)
+    assert lib.as_spmm_colslice_plan_rect(None, None, 0, 5, 0, 128, 0, 1, 256, 1 << 20, ctypes.byref(rect_tag),
+                                          None) == 0
+    assert rect_tag.value == tags[(0, 128, 1)]
+    assert lib.as_spmm_colslice_plan_rect(None, None, 0, -1, 0, 128, 0, 1, 256, 1 << 20, ctypes.byref(rect_tag),
+                                          None) == 1
+    assert lib.as_last_error() == b"n_cols exceeds kernel index range"
+    assert lib.as_spmm_csr_colslice_planned_rect(fake, fake, None, fake, fake, 4, 1 << 31, 4, 128, 0, 1, fake,
+                                                 1 << 20, tags[(0, 128, 1)], fake, 1 << 20, -1, 0, None) == 1
+    assert lib.as_last_error() == b"n_cols exceeds kernel index range"
+    assert lib.as_spmm_csr_colslice_planned_rect(fake, fake, None, fake, fake, 4, 9, 4, 128, 0, 1, fake, 1 << 20,
+                                                 tags[(0, 64, 1)], fake, 1 << 20, -1, 0, None) == 1
+    assert lib.as_last_error().startswith(b"the plan was built for other settings")
+    # two partial buffers of a chunk's rows (all 1,000 rows here: chunks hold at least 32,768), 8 slices of F fp64
     assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 0, -1) == 2 * 1000 * 8 * 128 * 8
     assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 1, 10) == 2 * 10 * 8 * 128 * 8
     # attention plans: fp32 and 16-bit tags differ (light buckets), and the
