@@ -796,8 +796,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(AS_COLSL
   }
 }
 
-size_t colslice_fixed_bytes(int64_t n) { return slice_plan_bytes<kSpmmSlices>(n); }
-
 size_t colslice_row_bytes(int64_t f) {
   return static_cast<size_t>(kSpmmSlices) * static_cast<size_t>(f) * sizeof(double);
 }
@@ -974,9 +972,69 @@ inline int64_t grouped_degree(int64_t f, int64_t elem_bytes) {
   return kGroupedMaxBlocks * g;
 }
 
-// The column-sliced SpMM's plan (colslice_common.h) over kSpmmSlices slices.
+// Row blocks (fp32).  The rows of a graph of at least 2·kColsliceMinChunkRows
+// rows run as B blocks of consecutive rows (B = min(kColsliceRowBlocks,
+// n / kColsliceMinChunkRows)), one block after the other, each with its own
+// degree-binned order and as one chunk where the workspace allows.  A launch
+// then mixes long and short rows of its block, where chunks of one
+// degree-binned order are each one degree range (the longest rows first, the
+// shortest last).  Which rows a block holds changes no result: a row's sums
+// depend only on its own edges and slice points.  On the skewed 115M-edge
+// graph, one block against 4: F = 128 3.426 against 3.360 ms, F = 256 6.957
+// against 6.820, F = 64 1.776 against 1.771 (2 blocks: 3.376, 6.819, 1.761;
+// 3: 3.405, 6.784, 1.787; 6: 3.378, 6.858, 1.806).  16-bit elements keep one
+// block: bf16 F = 128 1.908 against 1.916 ms with 4, F = 256 4.243 against
+// 4.275.
+#ifndef AS_COLSLICE_ROW_BLOCKS
+#define AS_COLSLICE_ROW_BLOCKS 4
+#endif
+constexpr int64_t kColsliceRowBlocks = AS_COLSLICE_ROW_BLOCKS;
+
+inline int64_t row_blocks(int64_t n, int64_t elem_bytes) {
+  if (elem_bytes != 4) return 1;
+  int64_t b = n / kColsliceMinChunkRows;
+  if (b > kColsliceRowBlocks) b = kColsliceRowBlocks;
+  return b < 1 ? 1 : b;
+}
+inline int64_t block_begin(int64_t n, int64_t blocks, int64_t b) { return n * b / blocks; }
+inline int64_t block_rows_max(int64_t n, int64_t blocks) { return (n + blocks - 1) / blocks; }
+
+// The column-sliced SpMM's plan over kSpmmSlices slices: the slice points of
+// every row (off[n·(S-1)], as in colslice_common.h) and the order (order[n]),
+// block b's rows at [r_b, r_{b+1}) of it, as row indices relative to r_b;
+// then per block its bucket counts (256 bytes) and binning tables.  One size
+// serves both block counts (fp32 and 16-bit plans).
 using PlanView = SlicePlan;
-inline PlanView plan_view(void* base, int64_t n) { return slice_plan_view<kSpmmSlices>(base, n); }
+
+inline size_t block_tables_bytes(int64_t n, int64_t blocks) {
+  return static_cast<size_t>(blocks) * (256 + bin_workspace_bytes(block_rows_max(n, blocks)));
+}
+
+size_t colslice_fixed_bytes(int64_t n) {
+  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
+  const size_t one = block_tables_bytes(n, 1);
+  const size_t many = block_tables_bytes(n, row_blocks(n, 4));
+  return align_up(rows * kSpmmBounds * sizeof(int32_t), 256) + align_up(rows * sizeof(int32_t), 256) +
+         (one > many ? one : many);
+}
+
+// Block b (of row_blocks(n, elem_bytes)) of the plan: off and order start at
+// its first row.
+inline PlanView block_view(void* base, int64_t n, int64_t elem_bytes, int64_t b) {
+  char* p = static_cast<char*>(base);
+  const size_t rows = static_cast<size_t>(n > 0 ? n : 1);
+  const int64_t blocks = row_blocks(n, elem_bytes);
+  const int64_t r0 = block_begin(n, blocks, b);
+  PlanView v;
+  v.off = reinterpret_cast<int32_t*>(p) + r0 * kSpmmBounds;
+  p += align_up(rows * kSpmmBounds * sizeof(int32_t), 256);
+  v.order = reinterpret_cast<int32_t*>(p) + r0;
+  p += align_up(rows * sizeof(int32_t), 256);
+  p += static_cast<size_t>(b) * (256 + bin_workspace_bytes(block_rows_max(n, blocks)));
+  v.counts = reinterpret_cast<int32_t*>(p);
+  v.bin_ws = p + 256;
+  return v;
+}
 
 inline int64_t slicing_degree(Slicing slicing, int64_t f, int64_t elem_bytes) {
   return slicing == kSliceColumns ? column_slice_degree(f, elem_bytes) : kEdgeSliceMinDegree;
@@ -989,20 +1047,32 @@ inline int light_bucket_count(int64_t elem_bytes) { return elem_bytes == 2 ? kMa
 
 inline int64_t plan_tag_of(int64_t min_degree, int light_buckets) { return slice_plan_tag(min_degree, light_buckets); }
 
-// n_cols: the column space (rows of X); n for a square graph.
+// n_cols: the column space (rows of X); n for a square graph.  The slice
+// points of all rows in one launch, then the binning of each row block.
 inline int build_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t n_cols, int64_t min_degree,
-                      int light_buckets, Slicing slicing, const PlanView& plan, hipStream_t s) {
-  return build_slice_plan<kSpmmSlices>(crow, col, n, min_degree, light_buckets, slicing == kSliceEdges, plan, s,
-                                       n_cols);
+                      int light_buckets, Slicing slicing, int64_t elem_bytes, void* plan, hipStream_t s) {
+  launch_slice_points<kSpmmSlices>(crow, col, n, min_degree, block_view(plan, n, elem_bytes, 0).off, s,
+                                   slicing == kSliceEdges, n_cols);
+  const int64_t blocks = row_blocks(n, elem_bytes);
+  for (int64_t b = 0; b < blocks; ++b) {
+    const int64_t r0 = block_begin(n, blocks, b);
+    const PlanView v = block_view(plan, n, elem_bytes, b);
+    const int st = launch_bin_rows(crow + r0, block_begin(n, blocks, b + 1) - r0, min_degree, kMaxHeavyBuckets,
+                                   light_buckets, v.order, v.counts, v.bin_ws, s);
+    if (st != AS_OK) return st;
+  }
+  return AS_OK;
 }
 
-// `plan`: built by build_plan for this graph, min_degree and light bucket
+// One row block (or a whole graph of one block): `plan` is its view of a
+// plan that build_plan built for this graph, min_degree and light bucket
 // count (the caller's duty); the workspace holds the partial buffers only.
-// n rows of A and Y, n_cols rows of X.
+// n rows of A and Y, n_cols rows of X; nnz: the whole graph's edges (an
+// upper bound for a block's); chunk: preferred rows per chunk.
 template <typename T>
 int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
                      int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials,
-                     size_t partial_bytes, int64_t sliced_rows, int64_t grouped_rows, hipStream_t s) {
+                     size_t partial_bytes, int64_t sliced_rows, int64_t grouped_rows, int64_t chunk, hipStream_t s) {
   const size_t row_bytes = colslice_row_bytes(f);
   if (partials == nullptr || partial_bytes < 2 * row_bytes)
     return fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu bytes of partial buffers, got %zu",
@@ -1035,7 +1105,6 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
   // whatever the workspace; sliced rows past the capacity are summed whole,
   // with the same bits, so a workspace sized for the sliced rows suffices.
   const int64_t fits = static_cast<int64_t>(partial_bytes / (2 * row_bytes));
-  int64_t chunk = preferred_chunk_rows(n);
   // a graph holds at most nnz / min_degree sliced rows; when they fit one
   // partial buffer the whole graph is one chunk (fewer launches, and short
   // rows run beside the hub rows' slices)
@@ -1097,6 +1166,32 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
   return AS_OK;
 }
 
+// The whole call over the row blocks of `plan`, one block after the other;
+// a block is one chunk where the workspace allows.  The launch-sizing hints
+// of a block are the graph's scaled to its rows.
+template <typename T>
+int colslice_execute_blocks(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
+                            int64_t n, int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, void* plan,
+                            void* partials, size_t partial_bytes, int64_t sliced_rows, int64_t grouped_rows,
+                            hipStream_t s) {
+  constexpr int64_t E = static_cast<int64_t>(sizeof(T));
+  const int64_t blocks = row_blocks(n, E);
+  if (blocks == 1)
+    return colslice_execute<T>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, block_view(plan, n, E, 0),
+                               partials, partial_bytes, sliced_rows, grouped_rows, preferred_chunk_rows(n), s);
+  for (int64_t b = 0; b < blocks; ++b) {
+    const int64_t r0 = block_begin(n, blocks, b);
+    const int64_t rows = block_begin(n, blocks, b + 1) - r0;
+    const int64_t sliced = sliced_rows < 0 ? -1 : (sliced_rows * rows + n - 1) / n;
+    const int64_t grouped = grouped_rows < 0 ? -1 : (grouped_rows * rows + n - 1) / n;
+    const int st = colslice_execute<T>(crow + r0, col, val, x, static_cast<T*>(y) + r0 * f, rows, n_cols, nnz, f,
+                                       min_degree, block_view(plan, n, E, b), partials, partial_bytes, sliced, grouped,
+                                       rows, s);
+    if (st != AS_OK) return st;
+  }
+  return AS_OK;
+}
+
 // One call with its plan built in the workspace's first colslice_fixed_bytes(n).
 template <typename T>
 int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
@@ -1113,13 +1208,12 @@ int colslice_run(const int64_t* crow, const int64_t* col, const void* val, const
   if (!aligned(workspace, 256)) return fail(AS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   constexpr int64_t E = static_cast<int64_t>(sizeof(T));
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const PlanView plan = plan_view(workspace, n);
   const int64_t min_degree = slicing_degree(slicing, f, E);
-  st = build_plan(crow, col, n, n, min_degree, light_bucket_count(E), slicing, plan, s);
+  st = build_plan(crow, col, n, n, min_degree, light_bucket_count(E), slicing, E, workspace, s);
   if (st != AS_OK) return st;
-  return colslice_execute<T>(crow, col, val, x, y, n, n, nnz, f, min_degree, plan,
-                             static_cast<char*>(workspace) + fixed, workspace_bytes - fixed, sliced_rows, grouped_rows,
-                             s);
+  return colslice_execute_blocks<T>(crow, col, val, x, y, n, n, nnz, f, min_degree, workspace,
+                                    static_cast<char*>(workspace) + fixed, workspace_bytes - fixed, sliced_rows,
+                                    grouped_rows, s);
 }
 
 inline int elem_bytes_of(int dtype) {
@@ -1167,7 +1261,7 @@ int as_spmm_colslice_plan_rect(const int64_t* crow, const int64_t* col, int64_t 
   const int light = as::light_bucket_count(e);
   *plan_tag = as::plan_tag_of(min_degree, light);
   if (n == 0) return AS_OK;
-  const int st = as::build_plan(crow, col, n, n_cols, min_degree, light, slicing, as::plan_view(plan, n),
+  const int st = as::build_plan(crow, col, n, n_cols, min_degree, light, slicing, e, plan,
                                 static_cast<hipStream_t>(stream));
   if (st != AS_OK) return st;
   return as::check_launch("spmm_colslice_plan");
@@ -1213,17 +1307,17 @@ int as_spmm_csr_colslice_planned_rect(const int64_t* crow, const int64_t* col, c
     return as::fail(AS_ERR_WORKSPACE, "a column-sliced plan needs %zu bytes, got %zu", as::colslice_fixed_bytes(n),
                     plan_bytes);
   if (!as::aligned(plan, 256)) return as::fail(AS_ERR_WORKSPACE, "the plan must be 256-byte aligned");
-  const as::PlanView view = as::plan_view(const_cast<void*>(plan), n);
+  void* view = const_cast<void*>(plan);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == AS_DTYPE_F32)
-    st = as::colslice_execute<float>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
-                                     workspace_bytes, sliced_rows, 0, s);
+    st = as::colslice_execute_blocks<float>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
+                                            workspace_bytes, sliced_rows, 0, s);
   else if (dtype == AS_DTYPE_BF16)
-    st = as::colslice_execute<as::Bf16>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
-                                        workspace_bytes, sliced_rows, grouped_rows, s);
+    st = as::colslice_execute_blocks<as::Bf16>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
+                                               workspace_bytes, sliced_rows, grouped_rows, s);
   else
-    st = as::colslice_execute<as::Fp16>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
-                                        workspace_bytes, sliced_rows, grouped_rows, s);
+    st = as::colslice_execute_blocks<as::Fp16>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
+                                               workspace_bytes, sliced_rows, grouped_rows, s);
   if (st != AS_OK) return st;
   return as::check_launch("spmm_csr_colslice_planned");
 }

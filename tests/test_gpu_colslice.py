@@ -413,3 +413,33 @@ def test_rounded16_cooperative_hub_rows(dtype):
     d_crow, d_col = to_dev(crow, col)
     got = _native.spmm_rounded_16_impl(d_crow, d_col, val.cuda(), x.cuda(), column_slices=True)
     assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("features", [64, 128, 33])
+def test_colslice_row_blocks(features, weighted, monkeypatch):
+    """fp32 graphs of at least 65,536 rows run as row blocks (each with its
+    own binned order): within the fp64 bound, and the same bits as the
+    per-call plan, as row shards of one block each (``autosage_amd.shard``)
+    and as a short workspace (several chunks per block).  Hub rows of 9,000
+    edges take the cooperative form (graphs of at most 2^24 edges)."""
+    from autosage_amd import shard
+
+    rows = 140_000
+    crow, col, val, x = _inputs(features, weighted, seed=features + 60, rows=rows, degree=6, hubs=5,
+                                hub_degree=9000, empty=0.1)
+    d = to_dev(crow, col, val, x)
+    first = torch.ops.autosage.spmm_csr_colslice(*d)
+    _assert_fp64_close(first.cpu().numpy(), oracle.spmm_f64(crow, col, val, x))
+    pieces = []
+    cuts = shard.cut_rows(d[0], 3)
+    for r0, r1 in zip(cuts, cuts[1:]):
+        s_crow, s_col, s_val = shard.shard_csr(d[0], d[1], d[2], r0, r1)
+        pieces.append(shard.spmm_csr_shard(s_crow, s_col, s_val, d[3]))
+    assert torch.equal(first, torch.cat(pieces))
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_PLAN", "off")
+    assert torch.equal(first, torch.ops.autosage.spmm_csr_colslice(*d))
+    monkeypatch.delenv("AUTOSAGE_COLSLICE_PLAN")
+    plan_bytes = _native.library().as_spmm_colslice_plan_bytes(rows)
+    monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((plan_bytes + 2 * 3000 * 8 * features * 8) / 2**20))
+    assert torch.equal(first, torch.ops.autosage.spmm_csr_colslice(*d))
