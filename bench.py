@@ -107,6 +107,10 @@ def roofline_record(ms: float, algorithmic: int, compulsory: int, traffic, refer
         gbps = k["bytes"] / (k["ms_per_step"] * 1e-3) / 1e9
         record["dominant_kernel"] = {"name": k["name"], "bytes": k["bytes"], "ms_per_step": k["ms_per_step"],
                                      "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+    if measured and "l2_hit_rate" in traffic:
+        record["l2_hit_rate"] = traffic["l2_hit_rate"]
+    if measured and "note" in traffic:
+        record["note"] = traffic["note"]
     return record
 
 
