@@ -111,6 +111,12 @@ def roofline_record(ms: float, algorithmic: int, compulsory: int, traffic, refer
         record["l2_hit_rate"] = traffic["l2_hit_rate"]
     if measured and "note" in traffic:
         record["note"] = traffic["note"]
+    if measured and "all_cached_ms" in traffic:
+        # the same launches on the same graph with every gather of a (row,
+        # slice) aimed at one X row (all L2 hits): what the gather path
+        # itself allows
+        record["all_cached_ceiling"] = {"ms": traffic["all_cached_ms"],
+                                        "frac": round(traffic["all_cached_ms"] / ms, 4)}
     return record
 
 
