@@ -97,6 +97,7 @@ _SIGNATURES = {
          _c_i64, _c_ptr],
     ),
     "as_spmm_rounded_16_group_degree": (_c_i64, [_c_i64]),
+    "as_spmm_colslice_group_degree": (_c_i64, [_c_i64, _c_int]),
     "as_spmm_rounded_16_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_spmm_csr_rows_16": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr]),
     "as_csr_row_softmax_16": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_int, _c_ptr]),
@@ -376,8 +377,8 @@ def spmm_csr_colslice_impl(crow, col, val, x):
         return y
     lib = library()
     if colslice_plans_enabled():
-        return _spmm_colslice_planned(crow, col, val, x, y, column_slices=True, sliced=sliced_rows(crow, True, f, x.dtype),
-                                      grouped=0)
+        sliced, grouped = colslice_row_counts(crow, f, x.dtype)
+        return _spmm_colslice_planned(crow, col, val, x, y, column_slices=True, sliced=sliced, grouped=grouped)
     # the preferred size (two partial buffers of a quarter of the rows); a
     # smaller cap runs the pipeline in more, smaller chunks
     full = lib.as_spmm_colslice_workspace_bytes(n, f)
@@ -498,12 +499,7 @@ def spmm_csr_rect_impl(crow, col, val, x, exact: bool = False):
     sorted_col, perm = row_sorted(crow, col, n_cols)
     val = _row_sorted_weights(col, val, perm)
     col = sorted_col
-    lib = library()
-    if x.dtype == torch.float32:
-        return _spmm_colslice_planned(crow, col, val, x, y, column_slices=True,
-                                      sliced=sliced_rows(crow, True, f, x.dtype), grouped=0, n_cols=n_cols)
-    threshold = int(lib.as_spmm_colslice_min_degree(1, f, DTYPES_16[x.dtype]))
-    sliced, grouped = row_counts(crow, threshold, int(lib.as_spmm_rounded_16_group_degree(f)))
+    sliced, grouped = colslice_row_counts(crow, f, x.dtype)
     return _spmm_colslice_planned(crow, col, val, x, y, True, sliced, grouped, n_cols=n_cols)
 
 
@@ -1006,6 +1002,15 @@ def row_counts(crow: torch.Tensor, long_from: int, short_below: int) -> tuple[in
         return int(counts[0]), int(counts[1])
 
     return _ROW_COUNT_MEMO.get((crow,), (long_from, short_below), compute)
+
+
+def colslice_row_counts(crow: torch.Tensor, f: int, dtype: torch.dtype) -> tuple[int, int]:
+    """(sliced rows, grouped short rows) of the column-sliced SpMM with column
+    slices for F features of ``dtype``: its launch-sizing hints."""
+    lib = library()
+    code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
+    return row_counts(crow, int(lib.as_spmm_colslice_min_degree(1, f, code)),
+                      int(lib.as_spmm_colslice_group_degree(f, code)))
 
 
 def sliced_rows(crow: torch.Tensor, column_slices: bool, f: int, dtype: torch.dtype) -> int:

@@ -420,6 +420,21 @@ __device__ __forceinline__ void slice_wide(const int64_t* __restrict__ col, cons
 #endif
 constexpr int kGroupedMaxBlocks = AS_COLSLICE_GROUPED_BLOCKS;  // grouped rows have fewer than 4·G edges (0: none)
 
+// Element types and lane widths with a grouped form: 16-bit elements with
+// wide lanes, fp32 with up to AS_COLSLICE_GROUPED_F32 lanes per edge.  fp32
+// short rows grouped (two rows a wave at F >= 128, four at F = 64, rows below
+// 4·G edges), against one wave per short row, on the skewed 115M-edge graph:
+// F = 128 3.293 against 3.366 ms, F = 256 6.752 against 6.826, F = 64 1.750
+// against 1.761 (grouping F = 64 only: 1.750 / 3.351 / 6.803; the short rows
+// then also run in log2-degree buckets).
+#ifndef AS_COLSLICE_GROUPED_F32
+#define AS_COLSLICE_GROUPED_F32 32
+#endif
+template <typename T, int V>
+constexpr bool grouped_lanes() {
+  return sizeof(T) == 2 ? V >= 8 : (AS_COLSLICE_GROUPED_F32 != 0 && V >= 8 && V <= AS_COLSLICE_GROUPED_F32);
+}
+
 template <typename T, int G, bool HAS_VAL, int U, bool OFF32>
 __device__ __forceinline__ void short_rows_grouped(const int64_t* __restrict__ crow, const int64_t* __restrict__ col,
                                                    const T* __restrict__ val, const T* __restrict__ x,
@@ -693,7 +708,7 @@ __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* 
   const int64_t fs = first_short(counts, c);
   const int64_t end = c.item_begin + c.items;
   int64_t split = end;  // grouped rows: [split, end)
-  if constexpr (sizeof(T) == 2 && V >= 8) {
+  if constexpr (grouped_lanes<T, V>()) {
     if (grouped.start != nullptr) {
       split = *grouped.start;
       split = split < fs ? fs : (split > end ? end : split);
@@ -710,8 +725,8 @@ __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* 
       slice_row<T, V, HAS_VAL, 8>(col, val, x, y + row * F, F, rs, rs + deg);
     }
   }
-  // 16-bit wide lanes: 64/V grouped rows per wave
-  if constexpr (sizeof(T) == 2 && V >= 8) {
+  // grouped rows: 64/V per wave
+  if constexpr (grouped_lanes<T, V>()) {
     constexpr int64_t kRows = kWave / V;
     for (int64_t item0 = split + w * kRows; item0 < end; item0 += waves * kRows) {
       short_rows_grouped<T, V, HAS_VAL, 1, OFF32>(crow, col, val, x, y, F, order, item0, end, tile * kTile);
@@ -964,9 +979,14 @@ int rows16_run(const int64_t* crow, const int64_t* col, const void* val, const v
   return AS_OK;
 }
 
-// Degree limit of the grouped short rows (16-bit elements, 16-byte lanes):
-// 4·G for the G lanes per edge that F takes; 0 when rows are not grouped.
+// Degree limit of the grouped short rows (16-byte lanes): 4·G for the G lanes
+// per edge that F takes; 0 when rows are not grouped.
 inline int64_t grouped_degree(int64_t f, int64_t elem_bytes) {
+  if (elem_bytes == 4) {
+    if (f <= 0 || f % 4 != 0) return 0;
+    const int64_t g = f <= 64 ? 16 : 32;
+    return g <= AS_COLSLICE_GROUPED_F32 ? kGroupedMaxBlocks * g : 0;
+  }
   if (elem_bytes != 2 || f <= 0 || f % 8 != 0) return 0;
   const int64_t g = f <= 64 ? 8 : (f <= 128 ? 16 : 32);
   return kGroupedMaxBlocks * g;
@@ -1043,7 +1063,9 @@ inline int64_t slicing_degree(Slicing slicing, int64_t f, int64_t elem_bytes) {
 // rows of degree >= the slicing degree in 8 log2-degree buckets, longest
 // first; then the short rows, for 16-bit elements also in 8 log2-degree
 // buckets (a wave of grouped short rows then holds rows of similar degree)
-inline int light_bucket_count(int64_t elem_bytes) { return elem_bytes == 2 ? kMaxHeavyBuckets : 1; }
+inline int light_bucket_count(int64_t elem_bytes) {
+  return elem_bytes == 2 || AS_COLSLICE_GROUPED_F32 != 0 ? kMaxHeavyBuckets : 1;
+}
 
 inline int64_t plan_tag_of(int64_t min_degree, int light_buckets) { return slice_plan_tag(min_degree, light_buckets); }
 
@@ -1342,6 +1364,11 @@ int as_spmm_csr_colslice_f32(const int64_t* crow, const int64_t* col, const floa
 }
 
 int64_t as_spmm_rounded_16_group_degree(int64_t f) { return as::grouped_degree(f, 2); }
+
+int64_t as_spmm_colslice_group_degree(int64_t f, int dtype) {
+  const int64_t e = as::elem_bytes_of(dtype);
+  return e == 0 ? 0 : as::grouped_degree(f, e);
+}
 
 int as_spmm_csr_rows_16(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
                         int64_t nnz, int64_t f, int dtype, void* stream) {

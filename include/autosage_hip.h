@@ -279,6 +279,13 @@ int as_spmm_csr_rows_16(const int64_t* crow, const int64_t* col, const void* val
  * F is not a multiple of 8). */
 int64_t as_spmm_rounded_16_group_degree(int64_t f);
 
+/* Degree below which the column-sliced SpMM (as_spmm_csr_colslice_planned,
+ * as_spmm_csr_colslice_f32, as_spmm_csr_rounded_16) sums short rows several to
+ * a wavefront, for F features of type dtype (AS_DTYPE_*): 4·G for the G lanes
+ * per edge, 0 when they run one per wavefront.  The count of such rows is
+ * the planned call's `grouped_rows` launch-sizing hint. */
+int64_t as_spmm_colslice_group_degree(int64_t f, int dtype);
+
 /* SDDMM with bf16 or fp16 query, key and output (dtype AS_DTYPE_BF16 /
  * AS_DTYPE_F16): out[e] is the fp64 sum of the exact products
  * query[row(e), f]·key[col[e], f], rounded to fp32 and then to the element
