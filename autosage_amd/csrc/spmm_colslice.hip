@@ -1333,7 +1333,7 @@ int as_spmm_csr_colslice_planned_rect(const int64_t* crow, const int64_t* col, c
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == AS_DTYPE_F32)
     st = as::colslice_execute_blocks<float>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
-                                            workspace_bytes, sliced_rows, 0, s);
+                                            workspace_bytes, sliced_rows, grouped_rows, s);
   else if (dtype == AS_DTYPE_BF16)
     st = as::colslice_execute_blocks<as::Bf16>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, view, workspace,
                                                workspace_bytes, sliced_rows, grouped_rows, s);

@@ -192,7 +192,11 @@ size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype,
  * slice point and binning launches.  A plan_tag of other settings returns
  * AS_ERR_INVALID_ARGUMENT; a plan of another graph is not detected (the
  * caller keys plans by graph).  The workspace holds the partial buffers
- * only (any size down to two partial rows, as for the unplanned calls). */
+ * only (any size down to two partial rows, as for the unplanned calls).
+ * sliced_rows / grouped_rows: launch-sizing hints for every dtype, the
+ * rows of degree >= as_spmm_colslice_min_degree(column_slices, f, dtype) and
+ * of degree < as_spmm_colslice_group_degree(f, dtype), or -1; the result is
+ * the same for any value. */
 int as_spmm_csr_colslice_planned(const int64_t* crow, const int64_t* col,
                                  const void* val, const void* x, void* y,
                                  int64_t n, int64_t nnz, int64_t f, int dtype,
