@@ -118,6 +118,12 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.as_spmm_csr_colslice_planned_rect(fake, fake, None, fake, fake, 4, 9, 4, 128, 0, 1, fake, 1 << 20,
                                                  tags[(0, 64, 1)], fake, 1 << 20, -1, 0, None) == 1
     assert lib.as_last_error().startswith(b"the plan was built for other settings")
+    # short rows below 4·G edges run grouped (G lanes per edge: fp32 16 at F <= 64, else 32; 16-bit 8 / 16 / 32)
+    assert [lib.as_spmm_colslice_group_degree(f, 0) for f in (64, 128, 256, 66)] == [64, 128, 128, 0]
+    for f in (64, 128, 256, 520):
+        for code in (1, 2):
+            assert lib.as_spmm_colslice_group_degree(f, code) == lib.as_spmm_rounded_16_group_degree(f)
+    assert lib.as_spmm_colslice_group_degree(64, 3) == 0
     # two partial buffers of a chunk's rows (all 1,000 rows here: chunks hold at least 32,768), 8 slices of F fp64
     assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 0, -1) == 2 * 1000 * 8 * 128 * 8
     assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 1, 10) == 2 * 10 * 8 * 128 * 8
