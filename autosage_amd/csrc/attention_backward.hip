@@ -38,6 +38,16 @@ namespace as {
 namespace {
 
 constexpr int kBwdBatch = 8;
+// Edges per step of a wave that walks one (row, slice) or row with 16-bit
+// elements: 8, as fp32 (16, as the forward takes, gave the benchmark
+// attention's bf16 forward + backward 19.73 against 19.62 ms).
+#ifndef AS_BWD_BATCH_16
+#define AS_BWD_BATCH_16 8
+#endif
+template <typename T>
+constexpr int bwd_batch() {
+  return sizeof(T) == 2 ? AS_BWD_BATCH_16 : kBwdBatch;
+}
 constexpr int64_t kBwdChunkRows = 131072;
 constexpr int64_t kBwdSliceBlocks = 4096;
 constexpr int64_t kBwdReduceBlocks = 8192;
@@ -139,7 +149,7 @@ __device__ __forceinline__ void bwd_q_edges(const int64_t* __restrict__ col, con
   constexpr bool TWO = sums_t<T>();
   constexpr int EK = kWave / GK;
   constexpr int EV = kWave / GV;
-  constexpr int E = kBwdBatch;
+  constexpr int E = bwd_batch<T>();
   static_assert(E % EK == 0 && E % EV == 0, "a batch holds whole gather instructions");
   const int64_t fqk = FQK > 0 ? FQK : fqk_rt;
   const int64_t fv = FV > 0 ? FV : fv_rt;
@@ -282,7 +292,7 @@ __device__ __forceinline__ void bwd_kv_edges(const int64_t* __restrict__ src, co
   constexpr int P = lane_elems<T>();
   constexpr int EK = kWave / GK;
   constexpr int EV = kWave / GV;
-  constexpr int E = kBwdBatch;
+  constexpr int E = bwd_batch<T>();
   static_assert(E % EK == 0 && E % EV == 0, "a batch holds whole gather instructions");
   const int64_t fqk = FQK > 0 ? FQK : fqk_rt;
   const int64_t fv = FV > 0 ? FV : fv_rt;

@@ -45,11 +45,15 @@ constexpr int64_t kAttChunkRows = 131072;    // sliced rows per partial chunk
 constexpr int64_t kAttSliceBlocks = 4096;    // slice-kernel workgroups per slice
 constexpr int64_t kAttReduceBlocks = 8192;   // reduction workgroups
 
-// Edges per online-softmax step.  8 for both element sizes: with 16-bit
-// elements 16 or 32 edges per step took the benchmark attention (Fqk 64,
-// Fv 128, 2.4M rows of median degree 16) from 7.84 to 8.85 and 9.93 ms.
+// Edges per online-softmax step of a wave that walks one row or (row, slice)
+// alone.  fp32: 8.  16-bit: 16, which keeps as many gathered bytes in flight
+// per wave as fp32 with 8; with 16-bit elements the short rows run grouped
+// (attend_rows_grouped, its own step), so this step serves the sliced rows:
+// the benchmark attention (Fqk 64, Fv 128, 2.4M rows, rows sliced from
+// degree 512) takes 5.63 against 5.78 ms in bf16.  (Before the short rows were
+// grouped, 16 and 32 edges per step took it from 7.84 to 8.85 and 9.93 ms.)
 #ifndef AS_ATT_BATCH_16
-#define AS_ATT_BATCH_16 8
+#define AS_ATT_BATCH_16 16
 #endif
 template <typename T>
 constexpr int att_batch() {
