@@ -443,3 +443,34 @@ def test_colslice_row_blocks(features, weighted, monkeypatch):
     plan_bytes = _native.library().as_spmm_colslice_plan_bytes(rows)
     monkeypatch.setenv("AUTOSAGE_COLSLICE_WORKSPACE_MB", str((plan_bytes + 2 * 3000 * 8 * features * 8) / 2**20))
     assert torch.equal(first, torch.ops.autosage.spmm_csr_colslice(*d))
+
+
+@pytest.mark.parametrize("features", [300, 128])
+def test_colslice_row_blocks_with_empty_blocks_and_feature_tiles(features):
+    """Row blocks of a graph whose middle rows have no edges at all (two of
+    its four blocks empty, the others holding hub rows and short rows), at a
+    width of several feature tiles (F = 300: three tiles of 128) and at one:
+    within the fp64 bound, the empty rows zero, and the same bits as the
+    graph's row shards (one block each)."""
+    from autosage_amd import shard
+
+    rows = 140_000
+    crow, col, val, x = _inputs(features, True, seed=features + 70, rows=rows, degree=7, hubs=4,
+                                hub_degree=5000, empty=0.05)
+    deg = np.diff(crow)
+    deg[rows // 4: 3 * rows // 4] = 0  # blocks 1 and 2 of 4 hold no edge
+    keep = np.concatenate([np.arange(crow[r], crow[r + 1]) for r in range(rows) if deg[r] > 0])
+    new_crow = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    col, val = col[keep], val[keep]
+    assert new_crow[-1] == col.size
+    d = to_dev(new_crow, col, val, x)
+    got = torch.ops.autosage.spmm_csr_colslice(*d)
+    host = got.cpu().numpy()
+    _assert_fp64_close(host, oracle.spmm_f64(new_crow, col, val, x))
+    assert not host[rows // 4: 3 * rows // 4].any()
+    cuts = [0, rows // 3, 2 * rows // 3, rows]
+    pieces = []
+    for r0, r1 in zip(cuts, cuts[1:]):
+        s_crow, s_col, s_val = shard.shard_csr(d[0], d[1], d[2], r0, r1)
+        pieces.append(shard.spmm_csr_shard(s_crow, s_col, s_val, d[3]))
+    assert torch.equal(got, torch.cat(pieces))
