@@ -430,6 +430,13 @@ constexpr int kGroupedMaxBlocks = AS_COLSLICE_GROUPED_BLOCKS;  // grouped rows h
 #ifndef AS_COLSLICE_GROUPED_F32
 #define AS_COLSLICE_GROUPED_F32 32
 #endif
+// Gathers in flight per lane group and step in the grouped fp32 rows (must
+// divide G): 2 on the skewed graph at F = 64 / 128 / 256 1.760 / 3.270 /
+// 6.765 ms, against 1.761 / 3.298 / 6.773 with 1 and 1.761 / 3.313 / 6.830
+// with 4.  16-bit rows keep 1.
+#ifndef AS_COLSLICE_GROUPED_U_F32
+#define AS_COLSLICE_GROUPED_U_F32 2
+#endif
 template <typename T, int V>
 constexpr bool grouped_lanes() {
   return sizeof(T) == 2 ? V >= 8 : (AS_COLSLICE_GROUPED_F32 != 0 && V >= 8 && V <= AS_COLSLICE_GROUPED_F32);
@@ -728,8 +735,9 @@ __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* 
   // grouped rows: 64/V per wave
   if constexpr (grouped_lanes<T, V>()) {
     constexpr int64_t kRows = kWave / V;
+    constexpr int kU = sizeof(T) == 2 ? 1 : AS_COLSLICE_GROUPED_U_F32;
     for (int64_t item0 = split + w * kRows; item0 < end; item0 += waves * kRows) {
-      short_rows_grouped<T, V, HAS_VAL, 1, OFF32>(crow, col, val, x, y, F, order, item0, end, tile * kTile);
+      short_rows_grouped<T, V, HAS_VAL, kU, OFF32>(crow, col, val, x, y, F, order, item0, end, tile * kTile);
     }
   }
 }
