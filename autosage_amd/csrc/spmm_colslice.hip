@@ -430,12 +430,17 @@ constexpr int kGroupedMaxBlocks = AS_COLSLICE_GROUPED_BLOCKS;  // grouped rows h
 #ifndef AS_COLSLICE_GROUPED_F32
 #define AS_COLSLICE_GROUPED_F32 32
 #endif
-// Gathers in flight per lane group and step in the grouped fp32 rows (must
-// divide G): 2 on the skewed graph at F = 64 / 128 / 256 1.760 / 3.270 /
+// Gathers in flight per lane group and step in the grouped rows (must divide
+// G).  fp32: 2 on the skewed graph at F = 64 / 128 / 256 1.760 / 3.270 /
 // 6.765 ms, against 1.761 / 3.298 / 6.773 with 1 and 1.761 / 3.313 / 6.830
-// with 4.  16-bit rows keep 1.
+// with 4.  16-bit: 1 (bf16 with 2: skewed graph F = 128 1.907 against 1.909
+// ms, F = 256 4.204 against 4.230, the 16.8M-edge uniform graph 0.646
+// against 0.624).
 #ifndef AS_COLSLICE_GROUPED_U_F32
 #define AS_COLSLICE_GROUPED_U_F32 2
+#endif
+#ifndef AS_COLSLICE_GROUPED_U_16
+#define AS_COLSLICE_GROUPED_U_16 1
 #endif
 template <typename T, int V>
 constexpr bool grouped_lanes() {
@@ -735,7 +740,7 @@ __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* 
   // grouped rows: 64/V per wave
   if constexpr (grouped_lanes<T, V>()) {
     constexpr int64_t kRows = kWave / V;
-    constexpr int kU = sizeof(T) == 2 ? 1 : AS_COLSLICE_GROUPED_U_F32;
+    constexpr int kU = sizeof(T) == 2 ? AS_COLSLICE_GROUPED_U_16 : AS_COLSLICE_GROUPED_U_F32;
     for (int64_t item0 = split + w * kRows; item0 < end; item0 += waves * kRows) {
       short_rows_grouped<T, V, HAS_VAL, kU, OFF32>(crow, col, val, x, y, F, order, item0, end, tile * kTile);
     }
