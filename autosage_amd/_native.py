@@ -108,6 +108,13 @@ _SIGNATURES = {
          _c_ptr],
     ),
     "as_sddmm_edges_16_workspace_bytes": (_c_size, [_c_i64]),
+    "as_sddmm_csr_edges_16_rect": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_size, _c_ptr],
+    ),
+    "as_csr_attention_plan_rect": (
+        _c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_size, ctypes.POINTER(ctypes.c_int64), _c_ptr],
+    ),
     "as_sddmm_csr_edges_16": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_size, _c_ptr],
@@ -805,13 +812,15 @@ def csr_attention_colslice_impl(crow, col, query, key, value, scale=1.0):
     return out
 
 
-def attention_plan(crow: torch.Tensor, col: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, int]:
+def attention_plan(crow: torch.Tensor, col: torch.Tensor, dtype: torch.dtype,
+                   n_cols: Optional[int] = None) -> tuple[torch.Tensor, int]:
     """(plan, tag) of the column-sliced attention on this graph (columns
     ascending within rows) for ``dtype``: slice points and the binned row
     order, built once per live, unmodified (crow, col) pair and element type
     (fp32 or 16-bit), then reused whatever Q, K and V; it also serves the
-    backward's passes of the same element type.  The build synchronises the
-    stream once."""
+    backward's passes of the same element type.  ``n_cols``: the column
+    space of a row shard (the rows of the whole K and V); None for a square
+    graph.  The build synchronises the stream once."""
     lib = library()
     code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
 
@@ -820,13 +829,115 @@ def attention_plan(crow: torch.Tensor, col: torch.Tensor, dtype: torch.dtype) ->
         plan = _workspace(lib.as_csr_attention_plan_bytes(n), crow.device)
         tag = ctypes.c_int64(0)
         with _on(crow.device):
-            status = lib.as_csr_attention_plan(_ptr(crow), _ptr(col), n, col.numel(), code, _ptr(plan), plan.numel(),
-                                               ctypes.byref(tag), _stream(crow.device))
+            if n_cols is None:
+                status = lib.as_csr_attention_plan(_ptr(crow), _ptr(col), n, col.numel(), code, _ptr(plan),
+                                                   plan.numel(), ctypes.byref(tag), _stream(crow.device))
+            else:
+                status = lib.as_csr_attention_plan_rect(_ptr(crow), _ptr(col), n, int(n_cols), col.numel(), code,
+                                                        _ptr(plan), plan.numel(), ctypes.byref(tag),
+                                                        _stream(crow.device))
             _raise(status, "autosage attention plan")
             torch.cuda.current_stream(crow.device).synchronize()
         return plan, int(tag.value)
 
-    return _PLAN_MEMO.get((crow, col), ("attention", code != 0), compute)
+    return _PLAN_MEMO.get((crow, col), ("attention", code != 0, n_cols), compute)
+
+
+def _check_rect_pair(crow, col, rows: torch.Tensor, whole: torch.Tensor, what: str) -> None:
+    """Inputs of a row shard's SDDMM or attention: ``rows`` holds the shard's
+    rows of the query (crow.numel() - 1 of them), ``whole`` the whole key."""
+    _check(crow.is_cuda and col.is_cuda and rows.is_cuda and whole.is_cuda, f"{what}: inputs must be CUDA tensors")
+    _check(crow.dtype == torch.long and col.dtype == torch.long, "crow and col must use torch.long indices")
+    _check(crow.dim() == 1 and col.dim() == 1 and crow.numel() >= 1, "crow and col must be one-dimensional")
+    _check(rows.dim() == 2 and whole.dim() == 2 and rows.size(1) == whole.size(1),
+           f"{what}: query and key must have the same feature width")
+    _check(rows.size(0) == crow.numel() - 1, f"{what}: query must hold one row per row of the shard")
+    _check(rows.dtype == whole.dtype and (rows.dtype == torch.float32 or rows.dtype in DTYPES_16),
+           f"{what}: query and key must share float32, bfloat16 or float16")
+    _check(crow.device == rows.device and col.device == rows.device and whole.device == rows.device,
+           f"{what}: inputs must be on one CUDA device")
+    _check(crow.is_contiguous() and col.is_contiguous() and rows.is_contiguous() and whole.is_contiguous(),
+           f"{what}: inputs must be contiguous")
+    _check(crow.numel() - 1 <= 2**31 - 1 and whole.size(0) <= 2**31 - 1, f"{what}: too many rows")
+
+
+def sddmm_csr_rect_impl(crow, col, query, key):
+    """out[e] = <query[r], key[col_e]> for the edges of a row shard: ``query``
+    holds the shard's rows, ``key`` the whole key (any number of rows).  fp32
+    keeps the reference kernel's dot order (``sddmm_csr``'s bits); bf16 /
+    fp16 the fp64 sum of the exact products, rounded once to fp32 and then to
+    the element type."""
+    _check_rect_pair(crow, col, query, key, "row-shard SDDMM")
+    if _env.get("AUTOSAGE_VALIDATE") == "1":
+        validate_csr(crow, col, key.size(0))
+    n, f = query.shape
+    nnz = col.numel()
+    if f == 0:
+        return torch.zeros(nnz, dtype=query.dtype, device=query.device)
+    out = torch.empty(nnz, dtype=query.dtype, device=query.device)
+    if n == 0 or nnz == 0:
+        return out
+    lib = library()
+    with _on(query.device):
+        if query.dtype in DTYPES_16:
+            ws = _workspace(lib.as_sddmm_edges_16_workspace_bytes(nnz), query.device)
+            status = lib.as_sddmm_csr_edges_16_rect(
+                _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, key.size(0), nnz, f,
+                DTYPES_16[query.dtype], _ptr(ws), ws.numel(), _stream(query.device),
+            )
+        elif nnz >= SDDMM_HUB_THRESHOLD:
+            # fp32 kernels address the key through the column indices only
+            ws = _workspace(lib.as_sddmm_split_workspace_bytes(n), query.device)
+            status = lib.as_sddmm_csr_split_f32(
+                _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f, SDDMM_WAVES,
+                SDDMM_HUB_THRESHOLD, _ptr(ws), ws.numel(), _stream(query.device),
+            )
+        else:
+            status = lib.as_sddmm_csr_f32(_ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(out), n, nnz, f,
+                                          _stream(query.device))
+    _raise(status, "autosage row-shard SDDMM")
+    return out
+
+
+def csr_attention_rect_impl(crow, col, query, key, value, scale=1.0):
+    """The column-sliced attention of a row shard: ``query`` holds the
+    shard's rows, ``key`` and ``value`` the whole graph's rows; the slices cut
+    the whole column space, so every row is computed as in the whole graph
+    (a graph whose columns do not ascend runs on its row-sorted copy)."""
+    _check_rect_pair(crow, col, query, key, "row-shard attention")
+    _check(value.is_cuda and value.device == query.device and value.dtype == query.dtype and value.dim() == 2
+           and value.is_contiguous() and value.size(0) == key.size(0),
+           "row-shard attention: value must be contiguous with key's rows and query's dtype")
+    if not attention_colslice_supported(query, value) or key.data_ptr() % 16 != 0:
+        raise ValueError("row-shard attention needs F_qk and F_v multiples of 4 in [4, 256] (float32) or of 8 "
+                         "in [8, 512] (bfloat16 / float16) and 16-byte aligned rows")
+    n_cols = key.size(0)
+    col = row_sorted(crow, col, n_cols)[0]
+    n, fqk = query.shape
+    fv = value.size(1)
+    nnz = col.numel()
+    out = torch.empty((n, fv), dtype=value.dtype, device=value.device)
+    if n == 0:
+        return out
+    lib = library()
+    # a shard always runs on a plan: a call without one would cut the
+    # slices over its own row count
+    plan, tag = attention_plan(crow, col, query.dtype, n_cols)
+    size = min(lib.as_csr_attention_colslice_workspace_bytes(n, nnz, fv), _colslice_workspace_cap())
+    ws = _workspace(max(size - plan.numel(), 1), query.device)
+    with _on(query.device):
+        if query.dtype in DTYPES_16:
+            status = lib.as_csr_attention_colslice_16(
+                _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv,
+                float(scale), DTYPES_16[query.dtype], _ptr(plan), tag, _ptr(ws), ws.numel(), _stream(query.device),
+            )
+        else:
+            status = lib.as_csr_attention_colslice_f32(
+                _ptr(crow), _ptr(col), _ptr(query), _ptr(key), _ptr(value), _ptr(out), n, nnz, fqk, fv,
+                float(scale), _ptr(plan), tag, _ptr(ws), ws.numel(), _stream(query.device),
+            )
+    _raise(status, "autosage row-shard attention")
+    return out
 
 
 def attention_backward_supported(query, key, value, out, grad_out) -> bool:

@@ -15,7 +15,8 @@
 //
 // Gathers use float4 lanes: G lanes per edge for K (G = 16/32/64 for
 // F_qk <= 64/128/256) and for V, 64/G edges per gather instruction.  A batch
-// of 8 edges issues all its K and V gathers first; the scores are reduced
+// of 8 edges (16 with 16-bit elements) issues all its K and V gathers first;
+// the scores are reduced
 // inside each K lane group, broadcast through SGPRs and picked up by the V
 // lane group that holds the same edge; each V lane group keeps its own
 // online-softmax state, merged in a fixed butterfly order at the end.
@@ -598,9 +599,10 @@ size_t as_csr_attention_colslice_workspace_bytes(int64_t n, int64_t nnz, int64_t
 
 size_t as_csr_attention_plan_bytes(int64_t n) { return as::slice_plan_bytes(n); }
 
-int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t nnz, int dtype, void* plan,
-                          size_t plan_bytes, int64_t* plan_tag, void* stream) {
+int as_csr_attention_plan_rect(const int64_t* crow, const int64_t* col, int64_t n, int64_t n_cols, int64_t nnz,
+                               int dtype, void* plan, size_t plan_bytes, int64_t* plan_tag, void* stream) {
   as::clear_error();
+  if (n_cols < 0 || n_cols > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "n_cols exceeds kernel index range");
   if (dtype != AS_DTYPE_F32 && dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
     return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_F32, AS_DTYPE_BF16 or AS_DTYPE_F16");
   if (plan_tag == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "plan_tag must not be NULL");
@@ -618,9 +620,14 @@ int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n, in
   *plan_tag = as::slice_plan_tag(degree, light);
   if (n == 0) return AS_OK;
   const int st = as::build_slice_plan(crow, col, n, degree, light, false, as::slice_plan_view(plan, n),
-                                      static_cast<hipStream_t>(stream));
+                                      static_cast<hipStream_t>(stream), n_cols);
   if (st != AS_OK) return st;
   return as::check_launch("csr_attention_plan");
+}
+
+int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t nnz, int dtype, void* plan,
+                          size_t plan_bytes, int64_t* plan_tag, void* stream) {
+  return as_csr_attention_plan_rect(crow, col, n, n < 0 ? 0 : n, nnz, dtype, plan, plan_bytes, plan_tag, stream);
 }
 
 int as_csr_attention_colslice_f32(const int64_t* crow, const int64_t* col, const float* query, const float* key,

@@ -513,9 +513,16 @@ struct Sddmm16Args {
   const void* q;
   const void* k;
   void* out;
-  int64_t n;
+  int64_t n;       // rows of the graph and of the query
   int64_t f;
+  int64_t n_keys;  // rows of the key (n for a square graph)
 };
+
+// Every query and key byte offset fits 32 bits, and every row index 24 bits.
+inline bool sddmm16_off32(const Sddmm16Args& a) {
+  const int64_t rows = a.n > a.n_keys ? a.n : a.n_keys;
+  return rows <= (int64_t(1) << 24) && rows * a.f * 2 <= (int64_t(1) << 32);
+}
 
 template <typename T, int G, int MB, bool VEC, bool OFF32>
 void launch_sddmm16_v(const Sddmm16Args& a, dim3 grid, dim3 block, int64_t hub_threshold, const int32_t* order,
@@ -559,8 +566,7 @@ void launch_sddmm16(const Sddmm16Args& a, int waves, int64_t hub_threshold, int6
   for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
     const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
     const dim3 grid(static_cast<unsigned>(nb));
-  // every key byte offset fits 32 bits (and the row index 24 bits)
-  const bool off32 = a.n <= (int64_t(1) << 24) && a.n * a.f * 2 <= (int64_t(1) << 32);
+  const bool off32 = sddmm16_off32(a);
 #define AS_S16(G, MB, VEC)                                                                                      \
   do {                                                                                                         \
     if (off32)                                                                                                 \
@@ -857,7 +863,7 @@ void launch_sddmm16_edges(const Sddmm16Args& a, int64_t nnz, int32_t* wave_rows,
                      a.crow, a.n, waves, wave_rows);
   int g, mb;
   sddmm16_shape(a, g, mb);
-  const bool off32 = a.n <= (int64_t(1) << 24) && a.n * a.f * 2 <= (int64_t(1) << 32);
+  const bool off32 = sddmm16_off32(a);
   const int64_t blocks = (waves + kEdgeWaves - 1) / kEdgeWaves;
   for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
     const int64_t nb = blocks - b0 < kMaxBlocksPerLaunch ? blocks - b0 : kMaxBlocksPerLaunch;
@@ -990,7 +996,7 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void*
     return as::fail(AS_ERR_WORKSPACE, "16-bit SDDMM needs %zu workspace bytes, got %zu", as::sddmm_split_ws(n),
                     workspace_bytes);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const as::Sddmm16Args a{crow, col, query, key, out, n, f};
+  const as::Sddmm16Args a{crow, col, query, key, out, n, f, n};
   char* ws = static_cast<char*>(workspace);
   int32_t* order = reinterpret_cast<int32_t*>(ws);
   const size_t order_bytes = as::align_up(static_cast<size_t>(n) * sizeof(int32_t), 256);
@@ -1017,10 +1023,11 @@ int as_sddmm_csr_rounded_16(const int64_t* crow, const int64_t* col, const void*
 
 size_t as_sddmm_edges_16_workspace_bytes(int64_t nnz) { return as::sddmm_edges_ws(nnz < 0 ? 0 : nnz); }
 
-int as_sddmm_csr_edges_16(const int64_t* crow, const int64_t* col, const void* query, const void* key, void* out,
-                          int64_t n, int64_t nnz, int64_t f, int dtype, void* workspace, size_t workspace_bytes,
-                          void* stream) {
+int as_sddmm_csr_edges_16_rect(const int64_t* crow, const int64_t* col, const void* query, const void* key,
+                               void* out, int64_t n, int64_t n_keys, int64_t nnz, int64_t f, int dtype,
+                               void* workspace, size_t workspace_bytes, void* stream) {
   as::clear_error();
+  if (n_keys < 0 || n_keys > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "n_keys exceeds kernel index range");
   if (dtype != AS_DTYPE_BF16 && dtype != AS_DTYPE_F16)
     return as::fail(AS_ERR_INVALID_ARGUMENT, "dtype must be AS_DTYPE_BF16 or AS_DTYPE_F16");
   if (!as::aligned(query, 2) || !as::aligned(key, 2) || !as::aligned(out, 2))
@@ -1035,13 +1042,20 @@ int as_sddmm_csr_edges_16(const int64_t* crow, const int64_t* col, const void* q
     return as::fail(AS_ERR_WORKSPACE, "16-bit SDDMM by edge blocks needs %zu workspace bytes, got %zu",
                     as::sddmm_edges_ws(nnz), workspace_bytes);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const as::Sddmm16Args a{crow, col, query, key, out, n, f};
+  const as::Sddmm16Args a{crow, col, query, key, out, n, f, n_keys};
   int32_t* wave_rows = static_cast<int32_t*>(workspace);
   if (dtype == AS_DTYPE_BF16)
     as::launch_sddmm16_edges<as::Bf16>(a, nnz, wave_rows, s);
   else
     as::launch_sddmm16_edges<as::Fp16>(a, nnz, wave_rows, s);
   return as::check_launch("sddmm_csr_edges_16");
+}
+
+int as_sddmm_csr_edges_16(const int64_t* crow, const int64_t* col, const void* query, const void* key, void* out,
+                          int64_t n, int64_t nnz, int64_t f, int dtype, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  return as_sddmm_csr_edges_16_rect(crow, col, query, key, out, n, n < 0 ? 0 : n, nnz, f, dtype, workspace,
+                                    workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -14,9 +14,11 @@ graph splits over P GPUs by rows and no sum crosses GPUs:
   links before the product);
 * its product is rows [r_k, r_{k+1}) of the whole graph's product.
 
-This module runs one shard on one GPU at its real shape.  The exchange of X
-between GPUs is not part of it.  The reference runs a graph on one GPU and
-has no counterpart (its product is ``autosage/ops.py:146-164``).
+This module runs one shard on one GPU at its real shape, for the SpMM, the
+SDDMM and the attention (the shard's rows of Q, the whole K and V).  The
+exchange of X (or K and V) between GPUs is not part of it.  The reference
+runs a graph on one GPU and has no counterpart (its ops are
+``autosage/ops.py:146-164`` and ``autosage/_auto.py:544-780``).
 """
 
 from __future__ import annotations
@@ -96,3 +98,65 @@ def spmm_csr_shard(crow: torch.Tensor, col: torch.Tensor, val: Optional[torch.Te
     if crow.device != x.device or col.device != x.device or (val is not None and val.device != x.device):
         raise ValueError("crow, col, val and x must be on the same device")
     return _native.spmm_csr_rect_impl(crow, col, val, x.contiguous(), exact=exact)
+
+
+def _shard_edge_rows(crow: torch.Tensor) -> torch.Tensor:
+    counts = (crow[1:] - crow[:-1]).to(torch.long)
+    return torch.repeat_interleave(torch.arange(crow.numel() - 1, device=crow.device, dtype=torch.long), counts)
+
+
+def sddmm_csr_shard(crow: torch.Tensor, col: torch.Tensor, query: torch.Tensor, key: torch.Tensor) -> torch.Tensor:
+    """out[e] = <query[r], key[col_e]> over a shard's edges: ``query`` holds
+    the shard's rows of the whole query (n_k × F), ``key`` the whole key
+    (N × F); the result is the whole graph's SDDMM output on the shard's
+    edges, in CSR order.  On a GPU the native kernels (fp32 in the
+    reference kernel's dot order, bf16 / fp16 rounded once); on the CPU the
+    reference's gather-dot (``autosage/_auto.py:79-92``)."""
+    if crow.dtype not in (torch.int32, torch.int64) or col.dtype not in (torch.int32, torch.int64):
+        raise TypeError("crow and col must use integer indices")
+    if query.dim() != 2 or key.dim() != 2 or query.size(1) != key.size(1):
+        raise ValueError("query and key must have shapes [n_k, F] and [N, F]")
+    if query.size(0) != crow.numel() - 1:
+        raise ValueError("query must hold one row per row of the shard")
+    crow = crow.to(torch.long).contiguous()
+    col = col.to(torch.long).contiguous()
+    if not query.is_cuda:
+        rows = _shard_edge_rows(crow)
+        return (query.index_select(0, rows) * key.index_select(0, col)).sum(dim=1)
+    if not load_native():
+        raise RuntimeError(f"AutoSAGE HIP library is not loaded: {native_load_error()}")
+    return _native.sddmm_csr_rect_impl(crow, col, query.contiguous(), key.contiguous())
+
+
+def csr_attention_shard(crow: torch.Tensor, col: torch.Tensor, query: torch.Tensor, key: torch.Tensor,
+                        value: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """softmax_r(scale·<query[r], key[c]>)·value over a shard's rows:
+    ``query`` holds the shard's rows (n_k × F_qk), ``key`` and ``value`` the
+    whole graph's (N × F_qk, N × F_v); the result is the shard's rows of the
+    attention output.  On a GPU the column-sliced attention (fp32, or bf16 /
+    fp16 computed in fp32 and rounded once) with the column slices over the
+    whole column space; on the CPU the reference's composition of
+    gather-dot, row softmax and CSR product (``autosage/_auto.py:762-780``)."""
+    if crow.dtype not in (torch.int32, torch.int64) or col.dtype not in (torch.int32, torch.int64):
+        raise TypeError("crow and col must use integer indices")
+    if value.dim() != 2 or value.size(0) != key.size(0):
+        raise ValueError("value must have one row per row of key")
+    crow = crow.to(torch.long).contiguous()
+    col = col.to(torch.long).contiguous()
+    if not query.is_cuda:
+        scores = sddmm_csr_shard(crow, col, query * scale, key)
+        rows = _shard_edge_rows(crow)
+        n = crow.numel() - 1
+        maxima = torch.full((n,), -torch.inf, dtype=scores.dtype)
+        maxima.scatter_reduce_(0, rows, scores, reduce="amax", include_self=True)
+        exps = (scores - maxima.index_select(0, rows)).exp()
+        sums = torch.zeros_like(maxima).scatter_add_(0, rows, exps)
+        probs = exps / sums.index_select(0, rows)
+        a = torch.sparse_csr_tensor(crow, col, probs, size=(n, key.size(0)), dtype=value.dtype)
+        return torch.sparse.mm(a, value.contiguous())
+    if not load_native():
+        raise RuntimeError(f"AutoSAGE HIP library is not loaded: {native_load_error()}")
+    if query.dim() != 2 or query.size(0) != crow.numel() - 1:
+        raise ValueError("query must hold one row per row of the shard")
+    return _native.csr_attention_rect_impl(crow, col, query.contiguous(), key.contiguous(), value.contiguous(),
+                                           scale)

@@ -388,9 +388,12 @@ def main() -> int:
     if args.probe_overhead:
         result = probe_overhead(args, device)
     elif args.shards > 0:
-        if args.workload not in ("cfg1", "cfg2", "cfg3", "er"):
-            raise SystemExit("--shards is for the SpMM workloads (cfg1, cfg2, cfg3, er)")
-        result = bench_shards(args, device)
+        if args.workload in ("cfg4", "cfg5"):
+            result = bench_shards_other(args, device)
+        elif args.workload in ("cfg1", "cfg2", "cfg3", "er"):
+            result = bench_shards(args, device)
+        else:
+            raise SystemExit("--shards is for the SpMM (cfg1-3, er), SDDMM (cfg4) and attention (cfg5) workloads")
     elif args.workload in ("cfg1", "cfg2", "cfg3", "er"):
         result = bench_spmm(args, device)
     elif args.workload == "hubsweep":
@@ -708,6 +711,111 @@ def bench_shards(args, device) -> dict:
         "sum_of_shard_ms": round(sum(r["ms"] for r in table), 4),
         "whole_graph_ms": round(whole_ms, 4),
         "allgather_bytes_per_gpu": (args.shards - 1) * n * f * elem // args.shards,
+        "cpu_baseline": None,
+    }
+
+
+def bench_shards_other(args, device) -> dict:
+    """One GPU's share of the SDDMM (cfg4) or attention (cfg5) workload
+    split by rows over ``--shards`` GPUs, as ``bench_shards`` does for the
+    SpMM: each shard's rows of Q against the whole K (and V), timed on this
+    GPU in turn (``sddmm_csr_shard``: fp32 in the reference kernel's dot
+    order, 16-bit by edge blocks; ``csr_attention_shard``: the column-sliced
+    attention over the whole column space).  The line's step is the slowest
+    shard; the all-gather of K (and V) a multi-GPU run needs first is not
+    run."""
+    from autosage_amd import shard, synth
+
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+    elem = 4 if dt == torch.float32 else 2
+    t0 = time.time()
+    if args.workload == "cfg4":
+        f = args.features or 64
+        w = synth.config4(seed=args.seed, features=f)
+        fqk, fv = f, 0
+    else:
+        w = synth.config5(seed=args.seed)
+        fqk, fv = 64, 128
+    log(f"generated {args.workload}: {w.degree_stats()} in {time.time() - t0:.1f}s")
+    n, nnz = w.rows, w.nnz
+    crow = torch.from_numpy(w.crow).to(device)
+    col = torch.from_numpy(w.col).to(device)
+    q = torch.from_numpy(w.dense["q"]).to(device).to(dt)
+    k = torch.from_numpy(w.dense["k"]).to(device).to(dt)
+    v = torch.from_numpy(w.dense["v"]).to(device).to(dt) if fv else None
+    if fv:
+        def whole():
+            return torch.ops.autosage.csr_attention_colslice(crow, col, q, k, v, 0.125)
+
+        def part(s_crow, s_col, r0, r1):
+            return shard.csr_attention_shard(s_crow, s_col, q[r0:r1], k, v, 0.125)
+    else:
+        def whole():
+            return torch.ops.autosage.sddmm_csr(crow, col, q, k)
+
+        def part(s_crow, s_col, r0, r1):
+            return shard.sddmm_csr_shard(s_crow, s_col, q[r0:r1], k)
+    flops_per_edge = 2 * (fqk + fv)
+    cuts = shard.cut_rows(crow, args.shards)
+    table = []
+    for idx, (r0, r1) in enumerate(zip(cuts, cuts[1:])):
+        s_crow, s_col, _ = shard.shard_csr(crow, col, None, r0, r1)
+        nnz_k = s_col.numel()
+        ms, samples = time_steps(lambda s_crow=s_crow, s_col=s_col, r0=r0, r1=r1: part(s_crow, s_col, r0, r1),
+                                 args.steps, args.warmup)
+        table.append({"shard": idx, "rows": [r0, r1], "nnz": nnz_k, "ms": round(ms, 4),
+                      "gflops": round(flops_per_edge * nnz_k / (ms * 1e-3) / 1e9, 2),
+                      "per_call_ms": [round(s_, 4) for s_ in samples]})
+        log(f"shard {idx}: rows [{r0}, {r1}), nnz {nnz_k}: {ms:.4f} ms")
+    whole_ms, _ = time_steps(whole, args.steps, args.warmup)
+    slowest = max(table, key=lambda r: r["ms"])
+    rows_k = slowest["rows"][1] - slowest["rows"][0]
+    nnz_k = slowest["nnz"]
+    type_name = {"f32": "fp32", "bf16": "bf16", "fp16": "fp16"}[args.dtype]
+    if fv:
+        workload_name = f"cfg5 CSR attention {type_name} Fqk=64 Fv=128 scale=1/8"
+        algo = attention_bytes(rows_k, nnz_k, fqk, fv, elem)
+        compulsory = elem * (fqk * rows_k + fqk * n + fv * n + fv * rows_k) + 8 * nnz_k + 8 * (rows_k + 1)
+        gathered = elem * (fqk + fv) * n
+        variant = "colslice" if dt == torch.float32 else "colslice16"
+    else:
+        workload_name = f"cfg4 SDDMM {type_name} F={fqk}"
+        algo = sddmm_bytes(rows_k, nnz_k, fqk, elem)
+        compulsory = elem * fqk * (rows_k + n) + elem * nnz_k + 8 * nnz_k + 8 * (rows_k + 1)
+        gathered = elem * fqk * n
+        variant = "edges" if dt != torch.float32 else "4,1024"
+    workload_name += f", row shard {slowest['shard']} of {args.shards}"
+    traffic = profiled_traffic(workload_name, variant)
+    return {
+        "metric": METRIC,
+        "value": slowest["gflops"],
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": slowest["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic",
+        "config": {
+            "workload": workload_name,
+            "rows": rows_k,
+            "nnz": nnz_k,
+            "columns": n,
+            "variant": variant,
+            "graph_fingerprint": w.fingerprint(),
+            "cut": "nnz-balanced row prefixes: shard k starts at the first row r with crow[r] >= ceil(k*nnz/P)",
+            "note": "one GPU's share of the graph split by rows over P GPUs, at its real shape (its rows of Q, "
+                    "the whole K (and V) resident); the all-gather a multi-GPU run needs first is not run",
+        },
+        "roofline": roofline_record(slowest["ms"], algo, compulsory, traffic,
+                                    (nnz_k + rows_k) * (fqk + fv) * elem),
+        "shards": table,
+        "sum_of_shard_ms": round(sum(r["ms"] for r in table), 4),
+        "whole_graph_ms": round(whole_ms, 4),
+        "allgather_bytes_per_gpu": (args.shards - 1) * gathered // args.shards,
         "cpu_baseline": None,
     }
 

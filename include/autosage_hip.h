@@ -325,6 +325,16 @@ int as_sddmm_csr_edges_16(const int64_t* crow, const int64_t* col,
                           void* workspace, size_t workspace_bytes,
                           void* stream);
 
+/* as_sddmm_csr_edges_16 for a row shard (no reference counterpart; see the
+ * row-shard entries of the column-sliced SpMM): n rows of the shard's CSR
+ * and of `query` (its rows of the whole query), `key` the whole key of
+ * n_keys rows.  The square entry is this with n_keys = n. */
+int as_sddmm_csr_edges_16_rect(const int64_t* crow, const int64_t* col,
+                               const void* query, const void* key, void* out,
+                               int64_t n, int64_t n_keys, int64_t nnz,
+                               int64_t f, int dtype, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* Row softmax of bf16 or fp16 scores (dtype AS_DTYPE_BF16 / AS_DTYPE_F16):
  * the scores convert exactly to fp32, the softmax is computed in fp32 (rows
  * of at most 64 edges by 16-lane groups, longer rows by a wavefront with a
@@ -411,6 +421,16 @@ size_t as_csr_attention_plan_bytes(int64_t n);
 int as_csr_attention_plan(const int64_t* crow, const int64_t* col, int64_t n,
                           int64_t nnz, int dtype, void* plan,
                           size_t plan_bytes, int64_t* plan_tag, void* stream);
+
+/* as_csr_attention_plan for a row shard (no reference counterpart): the
+ * slice points cut the whole column space [0, n_cols) of the graph the
+ * shard's n rows come from.  With this plan the column-sliced attention
+ * entries run the shard: query and out hold its n rows, key and value the
+ * whole n_cols rows.  The square entry is this with n_cols = n. */
+int as_csr_attention_plan_rect(const int64_t* crow, const int64_t* col,
+                               int64_t n, int64_t n_cols, int64_t nnz,
+                               int dtype, void* plan, size_t plan_bytes,
+                               int64_t* plan_tag, void* stream);
 
 /* Column-sliced attention, an alternative schedule for as_csr_attention_f32
  * (no reference counterpart; chosen by csr_attention_forward,

@@ -113,3 +113,31 @@ def test_shard_rejects_columns_beyond_x_when_validating(monkeypatch):
     with pytest.raises(ValueError, match="invalid CSR graph"):
         shard.spmm_csr_shard(s_crow, s_col, None, d_x[:200])
     assert shard.spmm_csr_shard(s_crow, s_col, None, d_x).shape == (100, 64)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_sddmm_and_attention_shards_are_the_whole_graph_outputs(dtype):
+    """The shard SDDMM (the shard's rows of Q against the whole K) gives the
+    whole graph's SDDMM on the shard's edges bit for bit (the same per-edge
+    arithmetic), and the shard attention (column slices over the whole column
+    space) the whole graph's column-sliced attention rows bit for bit."""
+    rows = 5000
+    crow, col = case_graph(rows, 9, seed=95, hubs=4, hub_degree=3000, empty=0.05)
+    rng = np.random.default_rng(96)
+    q = torch.from_numpy(rng.standard_normal((rows, 64)).astype(np.float32)).to(dtype).cuda()
+    k = torch.from_numpy(rng.standard_normal((rows, 64)).astype(np.float32)).to(dtype).cuda()
+    v = torch.from_numpy(rng.standard_normal((rows, 128)).astype(np.float32)).to(dtype).cuda()
+    d_crow, d_col = to_dev(crow, col)
+    whole_scores = torch.ops.autosage.sddmm_csr(d_crow, d_col, q, k)
+    whole_att = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, q, k, v, 0.125)
+    cuts = shard.cut_rows(d_crow, 5)
+    scores, att = [], []
+    for r0, r1 in zip(cuts, cuts[1:]):
+        s_crow, s_col, _ = shard.shard_csr(d_crow, d_col, None, r0, r1)
+        scores.append(shard.sddmm_csr_shard(s_crow, s_col, q[r0:r1], k))
+        att.append(shard.csr_attention_shard(s_crow, s_col, q[r0:r1], k, v, 0.125))
+    assert torch.equal(torch.cat(scores), whole_scores)
+    assert torch.equal(torch.cat(att), whole_att)
+    if dtype == torch.float32:
+        want = oracle.sddmm_ref(crow, col, q.cpu().numpy(), k.cpu().numpy())
+        assert np.array_equal(torch.cat(scores).cpu().numpy().view(np.uint32), want.view(np.uint32))

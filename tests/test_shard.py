@@ -87,3 +87,33 @@ def test_cpu_shards_are_the_rows_of_the_whole_product(weighted):
         assert np.array_equal(got.numpy(), want[r0:r1])
         pieces.append(got)
     assert np.array_equal(torch.cat(pieces).numpy(), want)
+
+
+def test_cpu_sddmm_and_attention_shards_are_the_whole_graph_rows():
+    """The CPU shard SDDMM / attention (the reference's gather-dot and
+    composition on the shard's rows) give the whole graph's outputs on the
+    shard's edges and rows: bitwise against the same composition over all
+    rows (one shard of everything), which is within the reference's bar
+    (1e-5 relative, 1e-6 absolute) of the oracle's reference-order
+    attention."""
+    crow, col = synth.random_csr(1200, 8, seed=8, hub_rows=3, hub_degree=700, empty_fraction=0.05)
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((crow.size - 1, 16)).astype(np.float32)
+    k = rng.standard_normal((crow.size - 1, 16)).astype(np.float32)
+    v = rng.standard_normal((crow.size - 1, 24)).astype(np.float32)
+    t_crow, t_col = torch.from_numpy(crow), torch.from_numpy(col)
+    tq, tk, tv = (torch.from_numpy(a) for a in (q, k, v))
+    whole_scores = oracle.torch_gather_dot(t_crow, t_col, tq, tk).numpy()
+    whole_att = shard.csr_attention_shard(t_crow, t_col, tq, tk, tv, 0.125).numpy()
+    ref_att = oracle.attention_ref(crow, col, q, k, v, 0.125)
+    assert np.all(np.abs(whole_att - ref_att) <= 1e-5 * np.abs(ref_att) + 1e-6)
+    cuts = shard.cut_rows(t_crow, 4)
+    for r0, r1 in zip(cuts, cuts[1:]):
+        s_crow, s_col, _ = shard.shard_csr(t_crow, t_col, None, r0, r1)
+        got = shard.sddmm_csr_shard(s_crow, s_col, tq[r0:r1], tk).numpy()
+        assert np.array_equal(got, whole_scores[crow[r0]:crow[r1]])
+        att = shard.csr_attention_shard(s_crow, s_col, tq[r0:r1], tk, tv, 0.125).numpy()
+        assert att.shape == (r1 - r0, 24)
+        assert np.array_equal(att, whole_att[r0:r1])
+    with pytest.raises(ValueError):
+        shard.sddmm_csr_shard(t_crow, t_col, tq[:5], tk)
