@@ -39,14 +39,22 @@ namespace {
 
 constexpr int kBwdBatch = 8;
 // Edges per step of a wave that walks one (row, slice) or row with 16-bit
-// elements: 8, as fp32 (16, as the forward takes, gave the benchmark
-// attention's bf16 forward + backward 19.73 against 19.62 ms).
+// elements.  Pass 2 (dK, dV): 8, as fp32 (16 in both passes gave the
+// benchmark attention's bf16 forward + backward 19.73 against 19.62 ms).
+// Pass 1 (dQ): 16, as the forward takes, 19.55-19.57 against 19.69-19.73 ms.
 #ifndef AS_BWD_BATCH_16
 #define AS_BWD_BATCH_16 8
 #endif
 template <typename T>
 constexpr int bwd_batch() {
   return sizeof(T) == 2 ? AS_BWD_BATCH_16 : kBwdBatch;
+}
+#ifndef AS_BWD_Q_BATCH_16
+#define AS_BWD_Q_BATCH_16 16
+#endif
+template <typename T>
+constexpr int bwd_q_batch() {
+  return sizeof(T) == 2 ? AS_BWD_Q_BATCH_16 : kBwdBatch;
 }
 constexpr int64_t kBwdChunkRows = 131072;
 constexpr int64_t kBwdSliceBlocks = 4096;
@@ -149,7 +157,7 @@ __device__ __forceinline__ void bwd_q_edges(const int64_t* __restrict__ col, con
   constexpr bool TWO = sums_t<T>();
   constexpr int EK = kWave / GK;
   constexpr int EV = kWave / GV;
-  constexpr int E = bwd_batch<T>();
+  constexpr int E = bwd_q_batch<T>();
   static_assert(E % EK == 0 && E % EV == 0, "a batch holds whole gather instructions");
   const int64_t fqk = FQK > 0 ? FQK : fqk_rt;
   const int64_t fv = FV > 0 ? FV : fv_rt;
