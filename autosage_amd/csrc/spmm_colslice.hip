@@ -42,6 +42,7 @@
 // 2^-52 of the largest partial, which changes the rounded result only for a
 // sum that close to a tie.
 #include <type_traits>
+#include <vector>
 
 #include "as_device.h"
 #include "as_internal.h"
@@ -782,9 +783,19 @@ __device__ __forceinline__ void colslice_reduce_block(int64_t rb, int64_t R, con
   }
 }
 
+// The rows a launch reduces: those of the previous chunk, which may belong to
+// the previous row block (its CSR offset, plan view and Y rows).
+struct ReduceRows {
+  const int64_t* crow;
+  const int32_t* off;
+  const int32_t* order;
+  const int32_t* counts;
+  void* y;
+};
+
 // One launch of the pipeline: the slice and short work of chunk `m` and the
 // reduction of the previous chunk `r`, whose partials a previous launch
-// wrote.  Of the TG groups of 8 blocks, RG evenly spread ones reduce, so the
+// wrote.  A chunk's partial rows are `capacity` apart between slices.  Of the TG groups of 8 blocks, RG evenly spread ones reduce, so the
 // HBM-streaming reduction runs beside the latency-bound gathers; the others,
 // in order, are the MG slice groups and then the short groups.  Group g
 // reduces iff floor((g+1)·RG/TG) > floor(g·RG/TG); floor(g·RG/TG) groups
@@ -804,20 +815,20 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(AS_COLSL
                                                                const int32_t* __restrict__ order,
                                                                const int32_t* __restrict__ counts,
                                                                const int32_t* __restrict__ off, SliceChunk m,
-                                                               SliceChunk r, int64_t chunk_stride, int64_t TG,
+                                                               SliceChunk r, ReduceRows rr, int64_t TG,
                                                                int64_t RG, int64_t MG, GroupedRows grouped) {
   const int64_t g = blockIdx.x / kSlices;
   const int64_t within = blockIdx.x % kSlices;
   const int64_t before = g * RG / TG;
   if ((g + 1) * RG / TG > before) {
-    colslice_reduce_block<T, VR>(before * kSlices + within, RG * kSlices, crow, off, order, counts, y, F, r,
-                                 chunk_stride);
+    colslice_reduce_block<T, VR>(before * kSlices + within, RG * kSlices, rr.crow, rr.off, rr.order, rr.counts,
+                                 static_cast<T*>(rr.y), F, r, r.capacity);
     return;
   }
   const int64_t work = g - before;
   if (work < MG) {
     colslice_slice_block<T, V, HAS_VAL, OFF32>(work * kSlices + within, crow, col, val, x, F, order, counts, off, m,
-                                               chunk_stride, grouped.mega_end);
+                                               m.capacity, grouped.mega_end);
   } else {
     colslice_short_block<T, V, HAS_VAL, OFF32>((work - MG) * kSlices + within, crow, col, val, x, y, F, order,
                                                counts, m, grouped);
@@ -872,46 +883,46 @@ struct GroupCounts {
 
 template <typename T, int V, bool HAS_VAL, int VR, bool OFF32>
 void launch_one(dim3 grid, hipStream_t s, const StepArgs& a, const SliceChunk& m, const SliceChunk& r,
-                int64_t stride, const GroupCounts& n) {
+                const ReduceRows& rr, const GroupCounts& n) {
   hipLaunchKernelGGL((colslice_step_kernel<T, V, HAS_VAL, VR, OFF32>), grid, dim3(kBlock), 0, s, a.crow, a.col,
                      static_cast<const T*>(a.val), static_cast<const T*>(a.x), static_cast<T*>(a.y), a.f, a.order,
-                     a.counts, a.off, m, r, stride, n.TG, n.RG, n.MG, a.grouped);
+                     a.counts, a.off, m, r, rr, n.TG, n.RG, n.MG, a.grouped);
 }
 
 // OFF32 only matters for the ds_bpermute form of the wide lanes (V <= 16);
 // V = 8 exists for 16-bit elements and V = 2 for fp32 only.
 template <typename T, bool HAS_VAL, int VR>
 void launch_step_v(int v, bool off32, dim3 grid, hipStream_t s, const StepArgs& a, const SliceChunk& m,
-                   const SliceChunk& r, int64_t stride, const GroupCounts& n) {
+                   const SliceChunk& r, const ReduceRows& rr, const GroupCounts& n) {
   constexpr bool kHalf = sizeof(T) == 2;
   switch (v) {
     case 32:
-      launch_one<T, 32, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
+      launch_one<T, 32, HAS_VAL, VR, false>(grid, s, a, m, r, rr, n);
       break;
     case 16:
-      if (off32) launch_one<T, 16, HAS_VAL, VR, true>(grid, s, a, m, r, stride, n);
-      else launch_one<T, 16, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
+      if (off32) launch_one<T, 16, HAS_VAL, VR, true>(grid, s, a, m, r, rr, n);
+      else launch_one<T, 16, HAS_VAL, VR, false>(grid, s, a, m, r, rr, n);
       break;
     case 8:
       if constexpr (kHalf) {
-        if (off32) launch_one<T, 8, HAS_VAL, VR, true>(grid, s, a, m, r, stride, n);
-        else launch_one<T, 8, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
+        if (off32) launch_one<T, 8, HAS_VAL, VR, true>(grid, s, a, m, r, rr, n);
+        else launch_one<T, 8, HAS_VAL, VR, false>(grid, s, a, m, r, rr, n);
       }
       break;
     case 2:
-      if constexpr (!kHalf) launch_one<T, 2, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
+      if constexpr (!kHalf) launch_one<T, 2, HAS_VAL, VR, false>(grid, s, a, m, r, rr, n);
       break;
     default:
-      launch_one<T, 1, HAS_VAL, VR, false>(grid, s, a, m, r, stride, n);
+      launch_one<T, 1, HAS_VAL, VR, false>(grid, s, a, m, r, rr, n);
       break;
   }
 }
 
 // Launch of slice work `m` (items may be 0) beside the reduction of `r`
-// (items may be 0).
+// (items may be 0) over the rows `rr` names.
 template <typename T>
 void launch_step(int v, bool off32, int vr, bool has_val, int64_t tiles, hipStream_t s, const StepArgs& a,
-                 const SliceChunk& m, const SliceChunk& r, int64_t stride) {
+                 const SliceChunk& m, const SliceChunk& r, const ReduceRows& rr) {
   // groups of 8 blocks: slice groups per (tile, phase), short groups per tile
   const int64_t MG = m.items > 0 ? tiles * kPhases * m.slice_groups : 0;
   const int64_t SG = m.items > 0 ? tiles * m.short_groups : 0;
@@ -930,11 +941,11 @@ void launch_step(int v, bool off32, int vr, bool has_val, int64_t tiles, hipStre
   if (n.TG == 0) return;
   const dim3 grid(static_cast<unsigned>(n.TG * kSlices));
   if (has_val) {
-    if (vr == 2) launch_step_v<T, true, 2>(v, off32, grid, s, a, m, r, stride, n);
-    else launch_step_v<T, true, 1>(v, off32, grid, s, a, m, r, stride, n);
+    if (vr == 2) launch_step_v<T, true, 2>(v, off32, grid, s, a, m, r, rr, n);
+    else launch_step_v<T, true, 1>(v, off32, grid, s, a, m, r, rr, n);
   } else {
-    if (vr == 2) launch_step_v<T, false, 2>(v, off32, grid, s, a, m, r, stride, n);
-    else launch_step_v<T, false, 1>(v, off32, grid, s, a, m, r, stride, n);
+    if (vr == 2) launch_step_v<T, false, 2>(v, off32, grid, s, a, m, r, rr, n);
+    else launch_step_v<T, false, 1>(v, off32, grid, s, a, m, r, rr, n);
   }
 }
 
@@ -1104,10 +1115,33 @@ inline int build_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_
 // count (the caller's duty); the workspace holds the partial buffers only.
 // n rows of A and Y, n_cols rows of X; nnz: the whole graph's edges (an
 // upper bound for a block's); chunk: preferred rows per chunk.
+// How a call's chunks are launched: the lane form, the feature tiles and the
+// partial rows of each of the two buffers (the same for every row block of a
+// call, since they depend on F, the alignments and the workspace only).
+struct StepShape {
+  int v;
+  bool off32;
+  int vr;
+  int64_t tiles;
+  int64_t fits;
+  bool operator==(const StepShape& o) const {
+    return v == o.v && off32 == o.off32 && vr == o.vr && tiles == o.tiles && fits == o.fits;
+  }
+};
+
+// A chunk of the pipeline with the pointers and plan view of its row block.
+struct ChunkWork {
+  StepArgs a;
+  SliceChunk c;
+};
+
+// Appends the chunks of rows [0, n) of `crow` (one row block, or the graph)
+// to `out`; their partial buffers are assigned when they are launched.
 template <typename T>
-int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
-                     int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials,
-                     size_t partial_bytes, int64_t sliced_rows, int64_t grouped_rows, int64_t chunk, hipStream_t s) {
+int colslice_chunks(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
+                    int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials,
+                    size_t partial_bytes, int64_t sliced_rows, int64_t grouped_rows, int64_t chunk, StepShape& shape,
+                    std::vector<ChunkWork>& out) {
   const size_t row_bytes = colslice_row_bytes(f);
   if (partials == nullptr || partial_bytes < 2 * row_bytes)
     return fail(AS_ERR_WORKSPACE, "column-sliced SpMM needs at least %zu bytes of partial buffers, got %zu",
@@ -1154,8 +1188,6 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
   // partial rows per buffer: a chunk's sliced rows are at most min(chunk, upper)
   int64_t capacity = fits < chunk ? fits : chunk;
   if (E == 4 && capacity > upper) capacity = upper > 0 ? upper : 1;
-  double* buffers[2] = {static_cast<double*>(partials),
-                        reinterpret_cast<double*>(static_cast<char*>(partials) + capacity * row_bytes)};
 
   // grouped short rows: the light buckets from level L on, L the first whose
   // rows all have degree below the limit (light bucket L holds degrees up to
@@ -1176,13 +1208,13 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
   const int64_t rows_per_wave = grouped.start != nullptr ? kWave / v : 1;
   if (grouped.start == nullptr) grouped_rows = 0;
 
-  // launch k: slice work of chunk k beside the reduction of chunk k - 1
+  shape = StepShape{v, off32, vr, tiles, fits};
+
   const StepArgs a{crow, col, val, x, y, f, plan.order, plan.counts, plan.off, grouped};
   const int64_t chunks = (n + chunk - 1) / chunk;
-  SliceChunk previous{0, 0, buffers[1], 1, 1, -1};
-  for (int64_t k = 0; k <= chunks; ++k) {
-    SliceChunk current{k * chunk, 0, buffers[k % 2], 1, 1, -1, capacity};
-    if (k < chunks) current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
+  for (int64_t k = 0; k < chunks; ++k) {
+    SliceChunk current{k * chunk, 0, nullptr, 1, 1, -1, capacity};
+    current.items = n - current.item_begin < chunk ? n - current.item_begin : chunk;
     // the sliced rows come first in the order, the grouped ones last
     const int64_t chunk_end = current.item_begin + current.items;
     const int64_t grouped_begin = grouped_rows < 0 || grouped_rows > n ? chunk_end : n - grouped_rows;
@@ -1190,20 +1222,66 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
     int64_t sliced_here = sliced_rows < 0 ? -1 : (sliced_rows > current.item_begin ? sliced_rows - current.item_begin : 0);
     if (sliced_here > capacity) sliced_here = capacity;
     chunk_groups(current, sliced_here, chunk_end > from ? chunk_end - from : 0, rows_per_wave);
-#if AS_COLSLICE_OVERLAP
-    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, previous, capacity);
-#else
-    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, current, SliceChunk{0, 0, nullptr, 1, 1, -1}, capacity);
-    launch_step<T>(v, off32, vr, val != nullptr, tiles, s, a, SliceChunk{0, 0, nullptr, 1, 1, -1}, current, capacity);
-#endif
-    previous = current;
+    out.push_back(ChunkWork{a, current});
   }
   return AS_OK;
 }
 
-// The whole call over the row blocks of `plan`, one block after the other;
-// a block is one chunk where the workspace allows.  The launch-sizing hints
-// of a block are the graph's scaled to its rows.
+// Launches chunks [begin, end) of `work` as a pipeline: launch k runs the slice
+// and short work of chunk k beside the reduction of chunk k - 1, which may
+// belong to the previous row block; chunk k writes partial buffer k % 2.
+template <typename T>
+void colslice_pipeline(const StepShape& sh, bool has_val, const std::vector<ChunkWork>& work, size_t begin,
+                       size_t end, void* partials, size_t row_bytes, hipStream_t s) {
+  if (end <= begin) return;
+  double* buffers[2] = {static_cast<double*>(partials),
+                        reinterpret_cast<double*>(static_cast<char*>(partials) + sh.fits * row_bytes)};
+  const SliceChunk none{0, 0, nullptr, 1, 1, -1};
+  for (size_t k = begin; k <= end; ++k) {
+    SliceChunk m = k < end ? work[k].c : none;
+    SliceChunk r = k > begin ? work[k - 1].c : none;
+    if (k < end) m.partial = buffers[(k - begin) % 2];
+    if (k > begin) r.partial = buffers[(k - begin - 1) % 2];
+    const StepArgs& a = work[k < end ? k : end - 1].a;
+    const StepArgs& ra = work[k > begin ? k - 1 : begin].a;
+    const ReduceRows rr{ra.crow, ra.off, ra.order, ra.counts, ra.y};
+#if AS_COLSLICE_OVERLAP
+    launch_step<T>(sh.v, sh.off32, sh.vr, has_val, sh.tiles, s, a, m, r, rr);
+#else
+    if (k < end) {
+      const ReduceRows own{a.crow, a.off, a.order, a.counts, a.y};
+      launch_step<T>(sh.v, sh.off32, sh.vr, has_val, sh.tiles, s, a, m, none, own);
+      launch_step<T>(sh.v, sh.off32, sh.vr, has_val, sh.tiles, s, a, none, m, own);
+    }
+#endif
+  }
+}
+
+template <typename T>
+int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
+                     int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials,
+                     size_t partial_bytes, int64_t sliced_rows, int64_t grouped_rows, int64_t chunk, hipStream_t s) {
+  std::vector<ChunkWork> work;
+  StepShape sh{};
+  const int st = colslice_chunks<T>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, plan, partials,
+                                    partial_bytes, sliced_rows, grouped_rows, chunk, sh, work);
+  if (st != AS_OK) return st;
+  colslice_pipeline<T>(sh, val != nullptr, work, 0, work.size(), partials, colslice_row_bytes(f), s);
+  return AS_OK;
+}
+
+// The whole call over the row blocks of `plan`; a block is one chunk where
+// the workspace allows.  The launch-sizing hints of a block are the graph's
+// scaled to its rows.  Each block is a pipeline of its own: its last chunk's
+// reduction is a launch of its own.  AS_COLSLICE_FUSE_BLOCKS=1 makes the
+// blocks' chunks one pipeline instead (the reduction of a block's last chunk
+// beside the next block's slice work; 4 blocks of one chunk: 5 launches
+// instead of 8), with the same bits; on the skewed 115M-edge graph that
+// measured 1.741 / 3.281 / 6.765 ms at F = 64 / 128 / 256 against 1.750 /
+// 3.271 / 6.745, so it is off.
+#ifndef AS_COLSLICE_FUSE_BLOCKS
+#define AS_COLSLICE_FUSE_BLOCKS 0
+#endif
 template <typename T>
 int colslice_execute_blocks(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
                             int64_t n, int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, void* plan,
@@ -1214,16 +1292,31 @@ int colslice_execute_blocks(const int64_t* crow, const int64_t* col, const void*
   if (blocks == 1)
     return colslice_execute<T>(crow, col, val, x, y, n, n_cols, nnz, f, min_degree, block_view(plan, n, E, 0),
                                partials, partial_bytes, sliced_rows, grouped_rows, preferred_chunk_rows(n), s);
+  std::vector<ChunkWork> work;
+  std::vector<size_t> ends;
+  std::vector<StepShape> shapes;
+  bool same_shape = true;
   for (int64_t b = 0; b < blocks; ++b) {
     const int64_t r0 = block_begin(n, blocks, b);
     const int64_t rows = block_begin(n, blocks, b + 1) - r0;
     const int64_t sliced = sliced_rows < 0 ? -1 : (sliced_rows * rows + n - 1) / n;
     const int64_t grouped = grouped_rows < 0 ? -1 : (grouped_rows * rows + n - 1) / n;
-    const int st = colslice_execute<T>(crow + r0, col, val, x, static_cast<T*>(y) + r0 * f, rows, n_cols, nnz, f,
-                                       min_degree, block_view(plan, n, E, b), partials, partial_bytes, sliced, grouped,
-                                       rows, s);
+    StepShape sh{};
+    const int st = colslice_chunks<T>(crow + r0, col, val, x, static_cast<T*>(y) + r0 * f, rows, n_cols, nnz, f,
+                                      min_degree, block_view(plan, n, E, b), partials, partial_bytes, sliced,
+                                      grouped, rows, sh, work);
     if (st != AS_OK) return st;
+    same_shape = same_shape && (b == 0 || sh == shapes[0]);
+    shapes.push_back(sh);
+    ends.push_back(work.size());
   }
+  const size_t row_bytes = colslice_row_bytes(f);
+  if (AS_COLSLICE_FUSE_BLOCKS && same_shape) {
+    colslice_pipeline<T>(shapes[0], val != nullptr, work, 0, work.size(), partials, row_bytes, s);
+    return AS_OK;
+  }
+  for (size_t b = 0, begin = 0; b < ends.size(); begin = ends[b++])
+    colslice_pipeline<T>(shapes[b], val != nullptr, work, begin, ends[b], partials, row_bytes, s);
   return AS_OK;
 }
 
