@@ -1034,10 +1034,19 @@ inline int64_t grouped_degree(int64_t f, int64_t elem_bytes) {
 #endif
 constexpr int64_t kColsliceRowBlocks = AS_COLSLICE_ROW_BLOCKS;
 
+// 16-bit elements keep one block (of 4 chunks): on the skewed 115M-edge graph
+// in bf16, 4 row blocks took 1.080 / 1.927 / 4.363 ms at F = 64 / 128 / 256,
+// and 1.068 / 1.902 / 4.325 as one pipeline (AS_COLSLICE_FUSE_BLOCKS=1),
+// against 1.061 / 1.909 / 4.314 with one block.
+#ifndef AS_COLSLICE_ROW_BLOCKS_16
+#define AS_COLSLICE_ROW_BLOCKS_16 1
+#endif
+static_assert(AS_COLSLICE_ROW_BLOCKS_16 >= 1 && AS_COLSLICE_ROW_BLOCKS_16 <= AS_COLSLICE_ROW_BLOCKS,
+              "the plan holds the tables of at most AS_COLSLICE_ROW_BLOCKS blocks");
 inline int64_t row_blocks(int64_t n, int64_t elem_bytes) {
-  if (elem_bytes != 4) return 1;
+  const int64_t most = elem_bytes == 4 ? kColsliceRowBlocks : AS_COLSLICE_ROW_BLOCKS_16;
   int64_t b = n / kColsliceMinChunkRows;
-  if (b > kColsliceRowBlocks) b = kColsliceRowBlocks;
+  if (b > most) b = most;
   return b < 1 ? 1 : b;
 }
 inline int64_t block_begin(int64_t n, int64_t blocks, int64_t b) { return n * b / blocks; }
