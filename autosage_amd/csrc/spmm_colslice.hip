@@ -1036,7 +1036,7 @@ constexpr int64_t kColsliceRowBlocks = AS_COLSLICE_ROW_BLOCKS;
 
 // 16-bit elements keep one block (of 4 chunks): on the skewed 115M-edge graph
 // in bf16, 4 row blocks took 1.080 / 1.927 / 4.363 ms at F = 64 / 128 / 256,
-// and 1.068 / 1.902 / 4.325 as one pipeline (AS_COLSLICE_FUSE_BLOCKS=1),
+// and 1.068 / 1.902 / 4.325 as one pipeline,
 // against 1.061 / 1.909 / 4.314 with one block.
 #ifndef AS_COLSLICE_ROW_BLOCKS_16
 #define AS_COLSLICE_ROW_BLOCKS_16 1
@@ -1281,15 +1281,15 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
 
 // The whole call over the row blocks of `plan`; a block is one chunk where
 // the workspace allows.  The launch-sizing hints of a block are the graph's
-// scaled to its rows.  Each block is a pipeline of its own: its last chunk's
-// reduction is a launch of its own.  AS_COLSLICE_FUSE_BLOCKS=1 makes the
-// blocks' chunks one pipeline instead (the reduction of a block's last chunk
-// beside the next block's slice work; 4 blocks of one chunk: 5 launches
-// instead of 8), with the same bits; on the skewed 115M-edge graph that
-// measured 1.741 / 3.281 / 6.765 ms at F = 64 / 128 / 256 against 1.750 /
-// 3.271 / 6.745, so it is off.
-#ifndef AS_COLSLICE_FUSE_BLOCKS
-#define AS_COLSLICE_FUSE_BLOCKS 0
+// scaled to its rows.  For F up to AS_COLSLICE_FUSE_BLOCKS_MAX_F the blocks'
+// chunks form one pipeline (the reduction of a block's last chunk beside the
+// next block's slice work; 4 blocks of one chunk: 5 launches instead of 8);
+// wider rows run each block as a pipeline of its own, whose last chunk's
+// reduction is a launch of its own.  Same bits either way.  On the skewed
+// 115M-edge graph one pipeline measured 1.741 / 3.281 / 6.765 ms at F = 64 /
+// 128 / 256 against 1.750 / 3.271 / 6.745 with one per block.
+#ifndef AS_COLSLICE_FUSE_BLOCKS_MAX_F
+#define AS_COLSLICE_FUSE_BLOCKS_MAX_F 64
 #endif
 template <typename T>
 int colslice_execute_blocks(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y,
@@ -1320,7 +1320,7 @@ int colslice_execute_blocks(const int64_t* crow, const int64_t* col, const void*
     ends.push_back(work.size());
   }
   const size_t row_bytes = colslice_row_bytes(f);
-  if (AS_COLSLICE_FUSE_BLOCKS && same_shape) {
+  if (f <= AS_COLSLICE_FUSE_BLOCKS_MAX_F && same_shape) {
     colslice_pipeline<T>(shapes[0], val != nullptr, work, 0, work.size(), partials, row_bytes, s);
     return AS_OK;
   }
