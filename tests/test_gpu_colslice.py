@@ -445,12 +445,13 @@ def test_colslice_row_blocks(features, weighted, monkeypatch):
     assert torch.equal(first, torch.ops.autosage.spmm_csr_colslice(*d))
 
 
-@pytest.mark.parametrize("features", [300, 128])
+@pytest.mark.parametrize("features", [300, 128, 64])
 def test_colslice_row_blocks_with_empty_blocks_and_feature_tiles(features):
     """Row blocks of a graph whose middle rows have no edges at all (two of
     its four blocks empty, the others holding hub rows and short rows), at a
-    width of several feature tiles (F = 300: three tiles of 128) and at one:
-    within the fp64 bound, the empty rows zero, and the same bits as the
+    width of several feature tiles (F = 300: three tiles of 128) and at one
+    (F = 128; F = 64, where the blocks run as one pipeline): within the fp64
+    bound, the empty rows zero, and the same bits as the
     graph's row shards (one block each)."""
     from autosage_amd import shard
 
