@@ -29,7 +29,7 @@ from . import _env
 from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
 # 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
@@ -51,6 +51,19 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_int, _c_int,
          _c_ptr, _c_size, _c_ptr],
+    ),
+    "as_spmm_fslice_plan_bytes": (_c_size, [_c_i64, _c_i64]),
+    "as_spmm_fslice_plan_workspace_bytes": (_c_size, [_c_i64]),
+    "as_spmm_fslice_plan": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr, _c_size, ctypes.POINTER(ctypes.c_int64),
+         _c_ptr],
+    ),
+    "as_spmm_fslice_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
+    "as_spmm_csr_fslice_f32": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_i64, _c_ptr, _c_size,
+         _c_ptr],
     ),
     "as_spmm_csr_split_f32_static": (
         _c_int,
@@ -360,6 +373,68 @@ def spmm_csr_split_impl(crow, col, val, x, feature_tile, warps_per_block, hub_th
         )
     _raise(status, "autosage::spmm_csr_split")
     return y
+
+
+# A plan holds 4 bytes per edge and per row (460 MB for a 115M-edge graph).
+_FSLICE_PLAN_MEMO = GraphMemo("fslice_plan", max_entries=8, max_bytes=4 << 30)
+FSLICE_FLAG_BAD_COLUMN = 1
+FSLICE_FLAG_LONG_ROW = 2
+
+
+def fslice_plan(crow: torch.Tensor, col: torch.Tensor, n_cols: int) -> tuple[torch.Tensor, int]:
+    """(plan, tag) of the feature-sliced SpMM for this graph: the rows sorted
+    by degree and the columns as int32, built on the device once per live,
+    unmodified (crow, col) pair and column count, then reused whatever X, F
+    and the weights.  The build synchronises the stream once and raises on a
+    column outside [0, n_cols) or a row of 2^31 or more edges."""
+    lib = library()
+
+    def compute() -> tuple[torch.Tensor, int]:
+        n = crow.numel() - 1
+        nnz = col.numel()
+        plan = _workspace(lib.as_spmm_fslice_plan_bytes(n, nnz), crow.device)
+        scratch = _workspace(lib.as_spmm_fslice_plan_workspace_bytes(n), crow.device)
+        tag = ctypes.c_int64(0)
+        with _on(crow.device):
+            status = lib.as_spmm_fslice_plan(_ptr(crow), _ptr(col), n, int(n_cols), nnz, _ptr(plan), plan.numel(),
+                                             _ptr(scratch), scratch.numel(), ctypes.byref(tag), _stream(crow.device))
+            _raise(status, "autosage feature-sliced plan")
+            flags = int(plan[:4].view(torch.int32).item())  # synchronises the stream
+        del scratch
+        _check(not flags & FSLICE_FLAG_BAD_COLUMN, f"col values must be in [0, {int(n_cols)})")
+        _check(not flags & FSLICE_FLAG_LONG_ROW, "rows of 2^31 or more edges are not supported")
+        return plan, int(tag.value)
+
+    return _FSLICE_PLAN_MEMO.get((crow, col), int(n_cols), compute)
+
+
+def _spmm_fslice(crow, col, val, x, n_rows: int) -> torch.Tensor:
+    """Feature-sliced exact SpMM of an n_rows × x.size(0) CSR (the bits of
+    spmm_csr: CSR-order fp32 chains)."""
+    f = x.size(1)
+    y = torch.empty((n_rows, f), dtype=x.dtype, device=x.device)
+    if n_rows == 0 or f == 0:
+        return y
+    lib = library()
+    n_cols = x.size(0)
+    plan, tag = fslice_plan(crow, col, n_cols)
+    ws = _workspace(lib.as_spmm_fslice_workspace_bytes(n_cols, f), x.device)
+    with _on(x.device):
+        status = lib.as_spmm_csr_fslice_f32(
+            _ptr(crow), _ptr(val), _ptr(x), _ptr(y), n_rows, n_cols, col.numel(), f, _ptr(plan), plan.numel(), tag,
+            _ptr(ws), ws.numel(), _stream(x.device),
+        )
+    _raise(status, "autosage::spmm_csr_fslice")
+    return y
+
+
+def spmm_csr_fslice_impl(crow, col, val, x):
+    """Feature-sliced SpMM: bit-identical to ``spmm_csr`` (per output element
+    an fp32 chain over the row's edges in CSR order), with 32-feature slices
+    of X spread over the XCDs (any column order, any F)."""
+    check_spmm_inputs(crow, col, val, x)
+    _maybe_validate(crow, col)
+    return _spmm_fslice(crow, col, val, x, crow.numel() - 1)
 
 
 def _colslice_workspace_cap() -> int:
@@ -1194,6 +1269,10 @@ _SCHEMAS = {
     "spmm_csr_colslice": (
         "spmm_csr_colslice(Tensor crow, Tensor col, Tensor? val, Tensor x) -> Tensor",
         spmm_csr_colslice_impl,
+    ),
+    "spmm_csr_fslice": (
+        "spmm_csr_fslice(Tensor crow, Tensor col, Tensor? val, Tensor x) -> Tensor",
+        spmm_csr_fslice_impl,
     ),
     "sddmm_csr": ("sddmm_csr(Tensor crow, Tensor col, Tensor query, Tensor key) -> Tensor", sddmm_csr_impl),
     "sddmm_csr_split": (

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 7
+#define AS_ABI_VERSION 8
 
 typedef enum as_status {
   AS_OK = 0,
@@ -104,6 +104,50 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col,
                           int waves_per_block, int64_t hub_threshold, int vec4,
                           int hub_mode, void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/* Feature-sliced exact SpMM.  Replaces the same ops as as_spmm_csr_f32 and
+ * as_spmm_csr_split_f32 (autosage::spmm_csr_cuda, csrc/spmm_csr_vec4.cu:97-176;
+ * autosage::spmm_csr_split_cuda, csrc/launcher_spmm.cu:22-72) with the same
+ * bits: per output element one fp32 accumulator updated in CSR edge order
+ * (fmaf with a weight, acc + x without), the chain of the sequential CPU CSR
+ * product (autosage/ops.py:124-143, csrc/spmm_csr_vec4.cu:42-50).  The
+ * features are cut into 32-wide slices, one XCD per slice (or XCDs sharing
+ * one), so each XCD's L2 caches one slice of X.  An n × n_cols CSR
+ * (n_cols = N for a square graph; x has n_cols rows, y has n rows).
+ *
+ * Plan: built once per graph (crow, col unmodified since), any X, F and
+ * weights.  Holds the rows sorted by degree (longest first, stable) and
+ * the columns as int32.  int32 flags at byte 0 of the plan: bit 0 = a column
+ * outside [0, n_cols) (its edges read row 0 of X instead), bit 1 = a row of
+ * 2^31 or more edges; a plan with flags set gives wrong results and should
+ * be refused by the caller.  The build needs a scratch workspace of
+ * as_spmm_fslice_plan_workspace_bytes(n) bytes (free once the build has run
+ * on the stream); *plan_tag receives the value the SpMM call checks.  No
+ * reference counterpart: the reference bins rows on every call
+ * (csrc/launcher_spmm.cu:49-59). */
+size_t as_spmm_fslice_plan_bytes(int64_t n, int64_t nnz);
+size_t as_spmm_fslice_plan_workspace_bytes(int64_t n);
+int as_spmm_fslice_plan(const int64_t* crow, const int64_t* col, int64_t n,
+                        int64_t n_cols, int64_t nnz, void* plan,
+                        size_t plan_bytes, void* workspace,
+                        size_t workspace_bytes, int64_t* plan_tag,
+                        void* stream);
+
+/* Workspace of as_spmm_csr_fslice_f32: the slice-major copy of X
+ * (ceil(F / 32) · n_cols · 128 bytes). */
+size_t as_spmm_fslice_workspace_bytes(int64_t n_cols, int64_t f);
+
+/* Y = A·X with the plan of as_spmm_fslice_plan; val may be NULL.  Any F and
+ * alignment (float4 lanes when F % 4 == 0 and x, y are 16-byte aligned).
+ * A wrong plan_tag or a plan smaller than as_spmm_fslice_plan_bytes(n, nnz)
+ * returns AS_ERR_INVALID_ARGUMENT; a plan of another graph is not detected
+ * (the caller keys plans by graph). */
+int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val,
+                           const float* x, float* y, int64_t n, int64_t n_cols,
+                           int64_t nnz, int64_t f, const void* plan,
+                           size_t plan_bytes, int64_t plan_tag,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /* Largest row count of as_spmm_csr_split_f32_static. */
 #define AS_STATIC_MAX_ROWS (1 << 22)
