@@ -214,6 +214,12 @@ def _spmm_candidates(crow: torch.Tensor, feature_width: int, config: SchedulerCo
 
 
 COLSLICE = "colslice"  # candidate value of the column-sliced SpMM
+FSLICE = "fslice"  # candidate value of the feature-sliced SpMM (bit-exact)
+# The column-sliced SpMM reassociates each row's sum (fp64 partials, one
+# rounding); the other native schedules keep the reference's CSR-order fp32
+# chain.  The full-graph decision takes the column-sliced one only when it
+# beats the best bit-exact option by more than this fraction.
+_INEXACT_MARGIN = 0.05
 ROUNDED16 = "rounded16"  # candidate value of the bf16 / fp16 SpMM (column slices when the columns ascend)
 ROUNDED16_EDGES = "rounded16:edges"  # the same product with edge slices
 ROUNDED16_ROWS = "rounded16:rows"  # the same product, every row whole (one launch)
@@ -251,6 +257,29 @@ def _colslice_eligible(crow, col, x, config: SchedulerConfig) -> bool:
     return True
 
 
+def _fslice_eligible(crow, col, x, config: SchedulerConfig) -> bool:
+    """Whether the full-graph check should time the feature-sliced SpMM."""
+    return config.full_graph_check and fslice_suits(crow, col, x, config.feature_slices)
+
+
+def fslice_suits(crow, col, x, mode: str) -> bool:
+    """Whether the feature-sliced SpMM is worth running for this graph and X:
+    graphs whose X is beyond the L2s with long rows on average, or with a
+    hub row (``auto``); every graph with edges (``on``); never (``off``)."""
+    if mode == "off" or native_op("spmm_csr_fslice") is None:
+        return False
+    n = crow.numel() - 1
+    if n <= 0 or col.numel() == 0 or x.size(1) == 0:
+        return False
+    if mode == "auto":
+        from ._native import row_counts
+
+        large = x.numel() * x.element_size() >= _COLSLICE_MIN_X_BYTES and col.numel() >= _COLSLICE_MIN_MEAN_DEGREE * n
+        if not large and row_counts(crow, _COLSLICE_HUB_DEGREE, 0)[0] == 0:
+            return False
+    return True
+
+
 def _require_native() -> None:
     """CUDA inputs run on the HIP library: without it the schedulers raise
     instead of quietly running the PyTorch baseline."""
@@ -271,6 +300,8 @@ def _cached_native_available(operation: str, choice: str, candidate) -> bool:
         return native_op(operation) is not None
     if candidate == COLSLICE:
         return native_op(operation + "_colslice") is not None
+    if candidate == FSLICE:
+        return native_op(operation + "_fslice") is not None
     return native_op(operation + ("_split" if candidate is not None else "")) is not None
 
 
@@ -337,6 +368,11 @@ def _run_spmm_choice(choice, candidate, crow, col, val, x) -> torch.Tensor:
         out = _op_call("spmm_csr_colslice", (crow, col, val, x), (val, x))
         if out is None:
             raise RuntimeError("native operator autosage::spmm_csr_colslice is not registered")
+        return out
+    if choice == "autosage" and candidate == FSLICE:
+        out = _op_call("spmm_csr_fslice", (crow, col, val, x), (val, x))
+        if out is None:
+            raise RuntimeError("native operator autosage::spmm_csr_fslice is not registered")
         return out
     if choice == "autosage":
         out = None
@@ -528,7 +564,8 @@ def spmm_csr_auto(
     result = _result_dict("spmm", config, probe, baseline_name, s_crow, s_col, sample_ms)
     if config.full_graph_check:
         colslice = _colslice_eligible(crow, col, x, config)
-        _confirm_spmm_on_full_graph(result, colslice, config, probe, crow, col, val, x)
+        fslice = _fslice_eligible(crow, col, x, config)
+        _confirm_spmm_on_full_graph(result, colslice, config, probe, crow, col, val, x, fslice=fslice)
     output = _run_spmm_choice(result["choice"], result["candidate"], crow, col, val, x)
     if config.cache:
         cache.store(device, graph, result)
@@ -615,17 +652,32 @@ def _full_graph_candidate(crow: torch.Tensor, feature_width: int, config: Schedu
     return [int(tile), int(waves), int(config.hub_threshold or q95)]
 
 
-def _decide_on_full_graph(result: dict[str, Any], options: list[Any], run_option, baseline) -> None:
+def _prefer_exact(options: list[str], times: dict[str, float], inexact: tuple = ()) -> str:
+    """The fastest option, except that an option of ``inexact`` (JSON keys)
+    must beat the fastest of the others by more than ``_INEXACT_MARGIN``."""
+    best_key = min(options, key=lambda k: times[k])
+    exact = [k for k in options if k not in inexact]
+    if best_key in inexact and exact:
+        best_exact = min(exact, key=lambda k: times[k])
+        if times[best_exact] <= times[best_key] * (1.0 + _INEXACT_MARGIN):
+            return best_exact
+    return best_key
+
+
+def _decide_on_full_graph(result: dict[str, Any], options: list[Any], run_option, baseline,
+                          inexact: tuple = ()) -> None:
     """Times each native option on the full graph (1 warmup, best of 3) and
-    the baseline, keeps the fastest native option, and falls back to the
-    baseline only when that is faster.  `result` gets a ``full_graph``
-    record; the sampled probe has only shortlisted."""
+    the baseline, keeps the fastest native option (a reassociating option of
+    ``inexact`` only when it beats the best bit-exact one by more than
+    ``_INEXACT_MARGIN``), and falls back to the baseline only when that is
+    faster.  `result` gets a ``full_graph`` record; the sampled probe has
+    only shortlisted."""
     wall_start = time.perf_counter()
     options = list(dict.fromkeys(json.dumps(o) for o in options))
     times = {
         key: _time_cuda(lambda o=json.loads(key): run_option(o), warmup=1, iterations=3)["best_ms"] for key in options
     }
-    best_key = min(options, key=lambda k: times[k])
+    best_key = _prefer_exact(options, times, tuple(json.dumps(o) for o in inexact))
     best_ms = times[best_key]
     # One baseline call decides when it takes more than twice the best native
     # time; a closer race gets the full warm timing.  The sampled probe has
@@ -655,26 +707,30 @@ def _decide_on_full_graph(result: dict[str, Any], options: list[Any], run_option
 
 
 def _confirm_spmm_on_full_graph(result: dict[str, Any], colslice: bool, config: SchedulerConfig, probe,
-                                crow, col, val, x) -> None:
+                                crow, col, val, x, fslice: bool = False) -> None:
     """SpMM options on the full graph: the sampled probe's best split
     candidate, the preferred candidate at the full graph's q95, the
     whole-graph kernel (candidate None) and, when eligible, the
-    column-sliced SpMM."""
+    feature-sliced and the column-sliced SpMM (the latter taken only when it
+    beats the best bit-exact option by more than ``_INEXACT_MARGIN``)."""
     options: list[Any] = [probe["chosen"]] if probe["chosen"] is not None else []
     if native_op("spmm_csr_split") is not None and config.hub_split:
         options.append(_full_graph_candidate(crow, x.size(1), config))
     options.append(None)
+    if fslice:
+        options.append(FSLICE)
     if colslice:
         options.append(COLSLICE)
     full_baseline, _ = _prepare_spmm_baseline(crow, col, val, x)
     _decide_on_full_graph(result, options, lambda o: _run_spmm_choice("autosage", o, crow, col, val, x),
-                          full_baseline)
+                          full_baseline, inexact=(COLSLICE,))
 
 
 def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dict[str, Any]]:
     """Full-graph calibration (``_auto.py:444-522``) of every shortlisted
-    candidate, the whole-graph kernel and, when eligible, the column-sliced
-    SpMM."""
+    candidate, the whole-graph kernel and, when eligible, the feature-sliced
+    and the column-sliced SpMM (the latter kept only when it beats the best
+    bit-exact option by more than ``_INEXACT_MARGIN``)."""
     crow, col, val, x = _normalize_csr(crow, col, val, x)
     if not x.is_cuda:
         return "baseline", _cpu_info("spmm")
@@ -704,11 +760,18 @@ def calibrate_full(crow, col, val, x, guardrail: float = 0.95) -> tuple[str, dic
         timings.append({"candidate": None, "best_ms": t["best_ms"]})
         if t["best_ms"] < best:
             best, selected = t["best_ms"], None
+    if _fslice_eligible(crow, col, x, config):
+        fslice_op = native_op("spmm_csr_fslice")
+        t = _time_cuda(lambda: fslice_op(crow, col, val, x), warmup=2, iterations=5)
+        timings.append({"candidate": FSLICE, "best_ms": t["best_ms"]})
+        if t["best_ms"] < best:
+            best, selected = t["best_ms"], FSLICE
     if _colslice_eligible(crow, col, x, config):
         colslice_op = native_op("spmm_csr_colslice")
         t = _time_cuda(lambda: colslice_op(crow, col, val, x), warmup=2, iterations=5)
         timings.append({"candidate": COLSLICE, "best_ms": t["best_ms"]})
-        if t["best_ms"] < best:
+        # the reassociating schedule only when it beats every bit-exact one by the margin
+        if t["best_ms"] * (1.0 + _INEXACT_MARGIN) < best:
             best, selected = t["best_ms"], COLSLICE
     choice = "autosage" if best <= guardrail * baseline_timing["best_ms"] else "baseline"
     result = {

@@ -75,6 +75,9 @@ def _spmm(crow, col, val, x, sliced: bool = False):
         # (fp64 partials, within 1e-6 of fp64); the transposed CSR lists its
         # columns in ascending order, so it needs no row-sorted copy
         return torch.ops.autosage.spmm_csr_colslice(crow, col, val, x)
+    if _feature_slices_pay(crow, col, x):
+        # the same bits as the schedules below, XCD-local on large graphs
+        return torch.ops.autosage.spmm_csr_fslice(crow, col, val, x)
     from ._native import row_counts
 
     if row_counts(crow, _HUB_THRESHOLD, 0)[0] == 0:
@@ -82,6 +85,16 @@ def _spmm(crow, col, val, x, sliced: bool = False):
         return torch.ops.autosage.spmm_csr(crow, col, val, x)
     tile = 64 if x.size(1) <= 64 else 128
     return torch.ops.autosage.spmm_csr_split(crow, col, val, x, tile, 2, _HUB_THRESHOLD)
+
+
+def _feature_slices_pay(crow, col, x) -> bool:
+    """The feature-sliced SpMM for a backward product when the forward
+    scheduler would time it (``auto``: X beyond the L2s with long rows, or a
+    hub row) or it is forced on."""
+    from ._auto import fslice_suits
+    from .config import SchedulerConfig
+
+    return fslice_suits(crow, col, x, SchedulerConfig.from_env().feature_slices)
 
 
 def _column_slices_allowed() -> bool:
@@ -218,7 +231,7 @@ def _attention_backward(ctx, grad_out: torch.Tensor):
 
 def register() -> None:
     """Attaches the backward formulas to the registered operators."""
-    for name in ("spmm_csr", "spmm_csr_split"):
+    for name in ("spmm_csr", "spmm_csr_split", "spmm_csr_fslice"):
         torch.library.register_autograd(f"autosage::{name}", _spmm_backward, setup_context=_spmm_setup)
     torch.library.register_autograd("autosage::spmm_csr_colslice", _spmm_backward, setup_context=_spmm_sliced_setup)
     for name in ("sddmm_csr", "sddmm_csr_split"):

@@ -13,6 +13,11 @@ column-sliced SpMM (one column slice per XCD, fp64 accumulation): ``auto``
 times it on the full graph when the graph is large enough to profit, ``on``
 times it on every graph with ascending columns, ``off`` never uses it, which
 keeps SpMM results bit-identical to the sequential CSR product.
+``feature_slices`` (``AUTOSAGE_FEATURE_SLICES`` = ``auto`` | ``on`` | ``off``)
+controls the feature-sliced SpMM (32-feature slices of X per XCD, CSR-order
+fp32 chains, bit-identical to the sequential CSR product): ``auto`` times it
+on the full graph when the graph is large enough to profit, ``on`` on every
+graph, ``off`` never.
 """
 
 from __future__ import annotations
@@ -60,6 +65,7 @@ class SchedulerConfig:
     hub_mode: str = "exact"
     full_graph_check: bool = True
     column_slices: str = "auto"
+    feature_slices: str = "auto"
 
     def __post_init__(self) -> None:
         if not 0 < self.guardrail <= 1:
@@ -80,6 +86,8 @@ class SchedulerConfig:
             raise ValueError("hub_mode must be 'exact' or 'split64'")
         if self.column_slices not in ("auto", "on", "off"):
             raise ValueError("column_slices must be 'auto', 'on' or 'off'")
+        if self.feature_slices not in ("auto", "on", "off"):
+            raise ValueError("feature_slices must be 'auto', 'on' or 'off'")
 
     def tuning_signature(self) -> dict[str, object]:
         return {
@@ -99,6 +107,7 @@ class SchedulerConfig:
             "hub_mode": self.hub_mode,
             "full_graph_check": self.full_graph_check,
             "column_slices": self.column_slices,
+            "feature_slices": self.feature_slices,
         }
 
     @classmethod
@@ -138,6 +147,7 @@ class SchedulerConfig:
             hub_mode=(env("AUTOSAGE_HUB_MODE") or "exact").strip().lower(),
             full_graph_check=_boolean("AUTOSAGE_FULL_CHECK", True),
             column_slices=(env("AUTOSAGE_COLUMN_SLICES") or "auto").strip().lower(),
+            feature_slices=(env("AUTOSAGE_FEATURE_SLICES") or "auto").strip().lower(),
         )
 
 
@@ -146,6 +156,6 @@ _ENV_NAMES = (
     "AUTOSAGE_PROBE_FRAC", "AUTOSAGE_PROBE_MIN_ROWS", "AUTOSAGE_PROBE_ITERS", "AUTOSAGE_PROBE_CAP_MS",
     "AUTOSAGE_MIN_PROBE_ROWS", "AUTOSAGE_MIN_PROBE_NNZ", "AUTOSAGE_HUB_CTA", "AUTOSAGE_VEC4", "AUTOSAGE_CACHE",
     "AUTOSAGE_REPLAY_ONLY", "AUTOSAGE_FTILE", "AUTOSAGE_WPB", "AUTOSAGE_HUB_T", "AUTOSAGE_HUB_MODE",
-    "AUTOSAGE_FULL_CHECK", "AUTOSAGE_COLUMN_SLICES",
+    "AUTOSAGE_FULL_CHECK", "AUTOSAGE_COLUMN_SLICES", "AUTOSAGE_FEATURE_SLICES",
 )
 _FROM_ENV_MEMO: dict = {}

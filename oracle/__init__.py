@@ -37,6 +37,9 @@ How each function is pinned (independent checks in tests/test_oracle.py):
   -> 0, torch autograd of the fp64 softmax within 1e-6).
 * or_row_softmax_f32: KAT (rows sum to 1, single-entry rows = 1.0), torch
   scatter composition within 1e-6 relative, fp64 bound.
+* or_attention_f64: a dense brute force (masked fp64 softmax of Q·Kᵀ·scale
+  times V) on small graphs, and closed forms (zero scores give the mean of
+  the row's V rows; a one-edge row returns that V row).
 * spmm_rounded_16: exact rational sums (fractions.Fraction) rounded the same
   way on random graphs; hand-computed ties (round to even, and the fp32 step
   that decides a tie the exact sum would not), fp16 overflow to inf.
@@ -80,8 +83,9 @@ def _load() -> ctypes.CDLL:
         lib.or_row_softmax_f32.argtypes = [p, p, i64, p]
         lib.or_row_softmax_f64.argtypes = [p, p, i64, p]
         lib.or_row_softmax_backward_f32.argtypes = [p, p, p, i64, p]
+        lib.or_attention_f64.argtypes = [p, p, p, p, p, i64, i64, i64, ctypes.c_double, p]
         for name in ("or_spmm_seq_f32", "or_spmm_f64", "or_bin_rows", "or_sddmm_ref_f32", "or_sddmm_f64",
-                     "or_row_softmax_f32", "or_row_softmax_f64", "or_row_softmax_backward_f32"):
+                     "or_row_softmax_f32", "or_row_softmax_f64", "or_row_softmax_backward_f32", "or_attention_f64"):
             getattr(lib, name).restype = None
         _lib = lib
     return _lib
@@ -222,15 +226,14 @@ def attention_ref(crow, col, query, key, value, scale: float = 1.0) -> np.ndarra
 
 
 def attention_f64(crow, col, query, key, value, scale: float = 1.0) -> np.ndarray:
-    scores = sddmm_f64(crow, col, query, key) * float(scale)
-    probs = row_softmax_f64(crow, scores)
+    """CSR attention in fp64 (``or_attention_f64``): scaled fp64 dot products,
+    fp64 row softmax, fp64 weighted sums of V rows in CSR order."""
     crow_a, col_a = _np(crow, np.int64), _np(col, np.int64)
-    v = _np(value, np.float64)
-    out = np.zeros((crow_a.size - 1, v.shape[1]), dtype=np.float64)
-    for r in range(crow_a.size - 1):
-        s0, s1 = crow_a[r], crow_a[r + 1]
-        if s1 > s0:
-            out[r] = probs[s0:s1] @ v[col_a[s0:s1]]
+    q, k, v = _np(query, np.float32), _np(key, np.float32), _np(value, np.float32)
+    n = crow_a.size - 1
+    out = np.empty((n, v.shape[1]), dtype=np.float64)
+    _load().or_attention_f64(_p(crow_a), _p(col_a), _p(q), _p(k), _p(v), n, q.shape[1], v.shape[1],
+                             float(scale), _p(out))
     return out
 
 

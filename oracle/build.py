@@ -14,7 +14,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 SOURCE = HERE / "csr_oracle.c"
 LIBRARY = HERE / "liboracle.so"
-FLAGS = ["-O2", "-std=c11", "-fPIC", "-shared", "-mfma", "-ffp-contract=off", "-fno-fast-math", "-Wall"]
+FLAGS = ["-O2", "-std=c11", "-fPIC", "-shared", "-mfma", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-Wall"]
 
 
 def build() -> Path:

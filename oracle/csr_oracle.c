@@ -8,11 +8,14 @@
  * Every output element is computed independently in a fixed, documented
  * order; citations are to the AutoSAGE reference tree.
  * Built with -ffp-contract=off: every fused multiply-add below is an explicit
- * fmaf/fma call.
+ * fmaf/fma call.  Built with OpenMP: the loops over rows run in parallel,
+ * one row per thread at a time, so every element is computed by one thread
+ * in the order stated and the results do not depend on the thread count.
  */
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 /* Y[r, f] = sum over edges e of row r, in CSR order, of w_e * X[col_e, f]
  * as one fp32 chain acc = fmaf(w, x, acc) from acc = 0 (w = 1 when val is
@@ -23,6 +26,7 @@
  * y[nrows, f]. */
 void or_spmm_seq_f32(const int64_t* crow, const int64_t* col, const float* val, const float* x, const int64_t* rows,
                      int64_t nrows, int64_t f, float* y) {
+#pragma omp parallel for schedule(dynamic, 64)
   for (int64_t i = 0; i < nrows; ++i) {
     const int64_t r = rows ? rows[i] : i;
     float* out = y + i * f;
@@ -39,6 +43,7 @@ void or_spmm_seq_f32(const int64_t* crow, const int64_t* col, const float* val, 
  * used to bound reassociating kernels. */
 void or_spmm_f64(const int64_t* crow, const int64_t* col, const float* val, const float* x, const int64_t* rows,
                  int64_t nrows, int64_t f, double* y) {
+#pragma omp parallel for schedule(dynamic, 64)
   for (int64_t i = 0; i < nrows; ++i) {
     const int64_t r = rows ? rows[i] : i;
     double* out = y + i * f;
@@ -86,12 +91,14 @@ static float ref_dot(const float* q, const float* k, int64_t f) {
  * (csrc/sddmm_csr_op.cu:19-50 row kernel, :52-83 hub kernel: same dot). */
 void or_sddmm_ref_f32(const int64_t* crow, const int64_t* col, const float* query, const float* key, int64_t n,
                       int64_t f, float* out) {
+#pragma omp parallel for schedule(dynamic, 64)
   for (int64_t r = 0; r < n; ++r)
     for (int64_t e = crow[r]; e < crow[r + 1]; ++e) out[e] = ref_dot(query + r * f, key + col[e] * f, f);
 }
 
 void or_sddmm_f64(const int64_t* crow, const int64_t* col, const float* query, const float* key, int64_t n,
                   int64_t f, double* out) {
+#pragma omp parallel for schedule(dynamic, 64)
   for (int64_t r = 0; r < n; ++r)
     for (int64_t e = crow[r]; e < crow[r + 1]; ++e) {
       const float* a = query + r * f;
@@ -106,6 +113,7 @@ void or_sddmm_f64(const int64_t* crow, const int64_t* col, const float* query, c
  * (scatter_reduce amax), e_i = exp(s_i - m), d = sum of e_i in CSR order
  * (scatter_add), p_i = e_i / d.  Empty rows produce nothing. */
 void or_row_softmax_f32(const int64_t* crow, const float* scores, int64_t n, float* probs) {
+#pragma omp parallel for schedule(dynamic, 64)
   for (int64_t r = 0; r < n; ++r) {
     const int64_t s0 = crow[r], s1 = crow[r + 1];
     if (s0 == s1) continue;
@@ -118,6 +126,7 @@ void or_row_softmax_f32(const int64_t* crow, const float* scores, int64_t n, flo
 }
 
 void or_row_softmax_f64(const int64_t* crow, const double* scores, int64_t n, double* probs) {
+#pragma omp parallel for schedule(dynamic, 64)
   for (int64_t r = 0; r < n; ++r) {
     const int64_t s0 = crow[r], s1 = crow[r + 1];
     if (s0 == s1) continue;
@@ -138,6 +147,7 @@ void or_row_softmax_f64(const int64_t* crow, const double* scores, int64_t n, do
  *   out_e = p_e * (grad_e - t). */
 void or_row_softmax_backward_f32(const int64_t* crow, const float* probs, const float* grad, int64_t n,
                                  float* out) {
+#pragma omp parallel for schedule(dynamic, 64)
   for (int64_t r = 0; r < n; ++r) {
     const int64_t s0 = crow[r], s1 = crow[r + 1];
     if (s0 == s1) continue;
@@ -154,5 +164,50 @@ void or_row_softmax_backward_f32(const int64_t* crow, const float* probs, const 
     }
     const float t = lane[0];
     for (int64_t e = s0; e < s1; ++e) out[e] = probs[e] * (grad[e] - t);
+  }
+}
+
+/* CSR attention in fp64 (autosage/_auto.py:762-780 with the scores scaled):
+ * per row r, s_e = scale * <query[r], key[col_e]> (products and sums in
+ * double, features in order), m = max s_e, p_e = exp(s_e - m) / sum exp,
+ * out[r, j] = sum over the row's edges in CSR order of p_e * value[col_e, j].
+ * Empty rows give zeros.  The near-exact value that bounds the fp32
+ * attention kernels. */
+void or_attention_f64(const int64_t* crow, const int64_t* col, const float* query, const float* key,
+                      const float* value, int64_t n, int64_t f_qk, int64_t f_v, double scale, double* out) {
+#pragma omp parallel
+  {
+    double* scores = NULL;
+    int64_t cap = 0;
+#pragma omp for schedule(dynamic, 64)
+    for (int64_t r = 0; r < n; ++r) {
+      const int64_t s0 = crow[r], s1 = crow[r + 1];
+      double* o = out + r * f_v;
+      for (int64_t j = 0; j < f_v; ++j) o[j] = 0.0;
+      if (s0 == s1) continue;
+      if (s1 - s0 > cap) {
+        free(scores);
+        cap = s1 - s0;
+        scores = (double*)malloc((size_t)cap * sizeof(double));
+      }
+      const float* q = query + r * f_qk;
+      double m = -INFINITY;
+      for (int64_t e = s0; e < s1; ++e) {
+        const float* k = key + col[e] * f_qk;
+        double dot = 0.0;
+        for (int64_t j = 0; j < f_qk; ++j) dot += (double)q[j] * (double)k[j];
+        const double s = scale * dot;
+        scores[e - s0] = s;
+        m = s > m ? s : m;
+      }
+      double d = 0.0;
+      for (int64_t e = s0; e < s1; ++e) d += exp(scores[e - s0] - m);
+      for (int64_t e = s0; e < s1; ++e) {
+        const double p = exp(scores[e - s0] - m) / d;
+        const float* v = value + col[e] * f_v;
+        for (int64_t j = 0; j < f_v; ++j) o[j] += p * (double)v[j];
+      }
+    }
+    free(scores);
   }
 }

@@ -90,6 +90,59 @@ def elementwise_parity(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, *, t
     return counts
 
 
+def elementwise_parity_rows(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, *, tight_rel: float,
+                            tight_abs: float, chunk_rows: int = 65536, label: str = "") -> dict:
+    """``elementwise_parity`` over every element of large outputs, in chunks
+    of rows (bounded host memory); the counts are summed and the worst
+    ratios kept.  Prints one ``[parity]`` line with the totals."""
+    total: dict = {}
+    for start in range(0, got.shape[0], chunk_rows):
+        stop = min(start + chunk_rows, got.shape[0])
+        part = _parity_counts(got[start:stop], ref[start:stop], exact[start:stop], tight_rel=tight_rel,
+                              tight_abs=tight_abs)
+        for key, value in part.items():
+            if key.startswith("worst"):
+                total[key] = max(total.get(key, 0.0), value)
+            elif key.startswith("min_"):
+                if value is not None:
+                    total[key] = value if total.get(key) is None else min(total[key], value)
+                else:
+                    total.setdefault(key, None)
+            else:
+                total[key] = total.get(key, 0) + value
+    print(f"[parity] {label} {total}", flush=True)
+    assert total["neither"] == 0, total
+    return total
+
+
+def _parity_counts(got, ref, exact, *, tight_rel, tight_abs, rtol=1e-5, atol=1e-6) -> dict:
+    got = got.astype(np.float64)
+    ref = ref.astype(np.float64)
+    exact = exact.astype(np.float64)
+    bar_exact = rtol * np.abs(exact) + atol
+    bound = tight_rel * np.abs(exact) + tight_abs
+    near_ref = np.abs(got - ref) <= rtol * np.abs(ref) + atol
+    ref_err = np.abs(ref - exact)
+    got_err = np.abs(got - exact)
+    kernel_ok = (got_err <= bound) & (got_err <= ref_err)
+    ref_misses = ref_err > bar_exact
+    ref_edge = ~ref_misses & (ref_err > bar_exact - bound)
+    case_b = ~near_ref & ref_misses & kernel_ok
+    case_c = ~near_ref & ref_edge & kernel_ok
+    ratio = ref_err / bar_exact
+    return {
+        "elements": int(got.size),
+        "a_within_bar_of_reference": int(near_ref.sum()),
+        "b_reference_off_bar_kernel_within_bound": int(case_b.sum()),
+        "c_reference_at_bar_edge_kernel_within_bound": int(case_c.sum()),
+        "reference_off_bar_total": int(ref_misses.sum()),
+        "worst_reference_error_over_bar": float(ratio.max()) if ratio.size else 0.0,
+        "worst_kernel_error_over_bar": float((got_err / bar_exact).max()) if got.size else 0.0,
+        "min_reference_error_over_bar_in_c": float(ratio[case_c].min()) if case_c.any() else None,
+        "neither": int((~near_ref & ~case_b & ~case_c).sum()),
+    }
+
+
 def assert_spmm_contract(out: torch.Tensor, info: dict, crow, col, val, x) -> None:
     """The contract of the schedule ``spmm_csr_auto`` chose: the exact native
     schedules equal the sequential oracle bit for bit; the column-sliced one

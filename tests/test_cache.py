@@ -1,4 +1,6 @@
-"""Schedule keys and cache file (mirrors the reference tests/test_cache.py)."""
+"""Schedule keys and cache file: the behaviour the reference's
+tests/test_cache.py pins (directory read per call, schema 1, signature
+fields, distinct weighted / dtype keys), plus golden and closed-form checks."""
 
 from __future__ import annotations
 
@@ -15,37 +17,47 @@ from autosage_amd._cache import ScheduleCache, cache_directory, device_signature
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def test_cache_directory_is_resolved_at_call_time(tmp_path, monkeypatch):
-    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
-    assert cache_directory() == tmp_path
-    cache = ScheduleCache()
-    device = {"type": "cpu", "torch": torch.__version__}
-    graph = {"operation": "spmm", "rows": 2}
-    result = {"choice": "baseline"}
-    cache.store(device, graph, result)
-    assert ScheduleCache().lookup(device, graph)["result"] == result
-    payload = json.loads((tmp_path / "schedules.json").read_text(encoding="utf-8"))
-    assert payload["schema_version"] == 1
+def test_cache_follows_the_directory_variable_at_each_call(tmp_path, monkeypatch):
+    """AUTOSAGE_CACHE_DIR is read when a cache is opened, not at import: two
+    directories keep two independent schedule files (schema 1)."""
+    device = {"name": "gfx950", "torch": torch.__version__}
+    graph = {"operation": "spmm", "rows": 5, "nonzeros": 9}
+    for name, choice in (("first", "autosage"), ("second", "baseline")):
+        monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path / name))
+        assert cache_directory() == tmp_path / name
+        assert ScheduleCache().lookup(device, graph) is None
+        ScheduleCache().store(device, graph, {"choice": choice})
+        assert ScheduleCache().lookup(device, graph)["result"] == {"choice": choice}
+    for name in ("first", "second"):
+        stored = json.loads((tmp_path / name / "schedules.json").read_text(encoding="utf-8"))
+        assert stored["schema_version"] == 1
 
 
-def test_graph_signature_preserves_large_integer_counts():
-    crow = torch.tensor([0, 1, 3, 3], dtype=torch.long)
-    col = torch.tensor([0, 1, 2], dtype=torch.long)
-    signature = graph_signature(crow, col, 64, "spmm")
-    assert signature["rows"] == 3
-    assert signature["nonzeros"] == 3
-    assert signature["operation"] == "spmm"
-    assert len(signature["structure_hash"]) == 24
+def test_graph_signature_counts_survive_json():
+    """Row and nonzero counts are plain ints (exact in the JSON cache key)
+    and the structure hash is 24 hex digits."""
+    degrees = [2, 0, 5, 1]
+    crow = torch.tensor([0, 2, 2, 7, 8], dtype=torch.long)
+    col = torch.tensor([1, 3, 0, 1, 2, 3, 3, 0], dtype=torch.long)
+    for width, operation in ((32, "spmm"), (7, "sddmm")):
+        signature = graph_signature(crow, col, width, operation)
+        assert (signature["rows"], signature["nonzeros"]) == (len(degrees), sum(degrees))
+        assert signature["operation"] == operation
+        assert type(signature["rows"]) is int and type(signature["nonzeros"]) is int
+        assert json.loads(json.dumps(signature)) == signature
+        assert len(signature["structure_hash"]) == 24
+        int(signature["structure_hash"], 16)
 
 
-def test_graph_signature_separates_weighted_and_dtype_variants():
-    crow = torch.tensor([0, 1], dtype=torch.long)
-    col = torch.tensor([0], dtype=torch.long)
-    unweighted = graph_signature(crow, col, 64, "spmm", dtype=torch.float32)
-    weighted = graph_signature(crow, col, 64, "spmm", weighted=True, dtype=torch.float32)
-    double = graph_signature(crow, col, 64, "spmm", dtype=torch.float64)
-    assert unweighted != weighted
-    assert unweighted != double
+def test_every_weight_and_dtype_variant_has_its_own_key():
+    crow = torch.tensor([0, 2, 3], dtype=torch.long)
+    col = torch.tensor([0, 1, 1], dtype=torch.long)
+    keys = set()
+    for weighted in (False, True):
+        for dtype in (torch.float32, torch.float64, torch.bfloat16):
+            keys.add(json.dumps(graph_signature(crow, col, 64, "spmm", weighted=weighted, dtype=dtype),
+                                sort_keys=True))
+    assert len(keys) == 6
 
 
 def test_structure_hash_closed_form():

@@ -11,6 +11,7 @@ misaligned X or Y, row shards (n × n_cols) and graphs without edges.
 from __future__ import annotations
 
 import ctypes
+import json
 
 import numpy as np
 import pytest
@@ -222,3 +223,80 @@ def test_fslice_c_abi_checks():
                                      plan.numel() - 1, scratch.data_ptr(), scratch.numel(), ctypes.byref(tag_out),
                                      stream)
     assert status == 4 and tag_out.value == 0
+
+
+def _timed(info) -> dict:
+    return {json.dumps(c["candidate"]): c["best_ms"] for c in info.get("full_graph", {}).get("candidates", [])}
+
+
+def test_scheduler_times_feature_slices_and_prefers_exact(monkeypatch, tmp_path):
+    import autosage_amd
+    from autosage_amd import _auto
+
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    monkeypatch.setenv("AUTOSAGE_FEATURE_SLICES", "on")
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "on")
+    crow, col, val, x = _inputs(128, True, seed=41, rows=8000, degree=40, hubs=6, hub_degree=4000)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    out, info = autosage_amd.spmm_csr_auto(d_crow, d_col, d_val, d_x)
+    timed = _timed(info)
+    assert '"fslice"' in timed and '"colslice"' in timed and "null" in timed, timed
+    exact_best = min(t for k, t in timed.items() if k != '"colslice"')
+    if info["candidate"] == "colslice":
+        # the reassociating schedule only when it beats every exact one by the margin
+        assert timed['"colslice"'] * (1.0 + _auto._INEXACT_MARGIN) < exact_best
+    else:
+        assert info["choice"] == "autosage"
+        assert bitwise_equal(out, oracle.spmm_seq(crow, col, val, x))
+    again, cached = autosage_amd.spmm_csr_auto(d_crow, d_col, d_val, d_x)
+    assert cached["from_cache"] and cached["candidate"] == info["candidate"] and torch.equal(again, out)
+    # off: never timed; column slices off keeps the feature slices (exact)
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path / "b"))
+    monkeypatch.setenv("AUTOSAGE_FEATURE_SLICES", "off")
+    _, info_off = autosage_amd.spmm_csr_auto(d_crow, d_col, d_val, d_x)
+    assert '"fslice"' not in _timed(info_off)
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path / "c"))
+    monkeypatch.setenv("AUTOSAGE_FEATURE_SLICES", "on")
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "off")
+    out_exact, info_exact = autosage_amd.spmm_csr_auto(d_crow, d_col, d_val, d_x)
+    assert '"fslice"' in _timed(info_exact) and '"colslice"' not in _timed(info_exact)
+    if info_exact["choice"] == "autosage":
+        assert bitwise_equal(out_exact, oracle.spmm_seq(crow, col, val, x))
+
+
+def test_calibrate_full_keeps_exactness_margin(monkeypatch, tmp_path):
+    import autosage_amd
+    from autosage_amd import _auto
+
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    monkeypatch.setenv("AUTOSAGE_FEATURE_SLICES", "on")
+    monkeypatch.setenv("AUTOSAGE_COLUMN_SLICES", "on")
+    crow, col, _, x = _inputs(64, False, seed=43, rows=6000, degree=30, hubs=4, hub_degree=3000)
+    d_crow, d_col, d_x = to_dev(crow, col, x)
+    choice, result = autosage_amd.calibrate_full(d_crow, d_col, None, d_x)
+    times = {json.dumps(c["candidate"]): c["best_ms"] for c in result["candidates"]}
+    assert '"fslice"' in times and '"colslice"' in times
+    if result["candidate"] == "colslice":
+        assert times['"colslice"'] * (1.0 + _auto._INEXACT_MARGIN) < min(
+            t for k, t in times.items() if k != '"colslice"')
+    out, replay = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert replay["from_cache"] and replay["candidate"] == result["candidate"]
+    if choice == "autosage" and result["candidate"] != "colslice":
+        assert bitwise_equal(out, oracle.spmm_seq(crow, col, None, x))
+
+
+def test_fslice_gradients_equal_the_exact_schedules():
+    """Autograd through the feature-sliced op: dX = Aᵀ·dY and dval = SDDMM(dY, X)
+    on the exact schedules, the same bits as spmm_csr's gradients."""
+    crow, col, val, x = _inputs(64, True, seed=47, rows=1500)
+    d_crow, d_col = to_dev(crow, col)
+    grads = []
+    for op in (torch.ops.autosage.spmm_csr, torch.ops.autosage.spmm_csr_fslice):
+        d_val = torch.from_numpy(val).cuda().requires_grad_(True)
+        d_x = torch.from_numpy(x).cuda().requires_grad_(True)
+        y = op(d_crow, d_col, d_val, d_x)
+        g = torch.linspace(-1.0, 1.0, y.numel(), device="cuda").view_as(y)
+        y.backward(g)
+        grads.append((y.detach(), d_val.grad, d_x.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)

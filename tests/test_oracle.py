@@ -9,6 +9,8 @@ operand fails at least one check.
 
 from __future__ import annotations
 
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -443,3 +445,37 @@ def test_spmm_rounded_16_ties_and_overflow():
     h = oracle.spmm_rounded_16(crow, col, None, x, torch.float16).float().numpy()[:, 0]
     assert h[3] == np.inf  # 120000 overflows fp16
     assert h[0] == 1.00390625  # fp16 represents 1 + 2^-8 exactly
+
+
+def test_oracle_results_do_not_depend_on_the_thread_count(tmp_path):
+    """The row loops run on OpenMP threads, one row per thread: the same bits
+    with one thread (a child process with OMP_NUM_THREADS=1) as with many."""
+    import subprocess
+    import sys
+
+    crow, col = _graph(3000, 20, seed=31, hubs=3, hub_degree=2000, empty=0.1)
+    rng = np.random.default_rng(32)
+    val = rng.standard_normal(col.size).astype(np.float32)
+    x = rng.standard_normal((3000, 24)).astype(np.float32)
+    q = rng.standard_normal((3000, 8)).astype(np.float32)
+    np.savez(tmp_path / "in.npz", crow=crow, col=col, val=val, x=x, q=q)
+    script = (
+        "import sys, numpy as np; sys.path.insert(0, sys.argv[1]); import oracle; d = np.load(sys.argv[2]);"
+        "np.savez(sys.argv[3], seq=oracle.spmm_seq(d['crow'], d['col'], d['val'], d['x']),"
+        " f64=oracle.spmm_f64(d['crow'], d['col'], d['val'], d['x']),"
+        " dot=oracle.sddmm_ref(d['crow'], d['col'], d['q'], d['q']),"
+        " att=oracle.attention_f64(d['crow'], d['col'], d['q'], d['q'], d['x'], 0.3))"
+    )
+    root = str(Path(oracle.__file__).resolve().parent.parent)
+    env = {**__import__("os").environ, "OMP_NUM_THREADS": "1"}
+    subprocess.run([sys.executable, "-c", script, root, str(tmp_path / "in.npz"), str(tmp_path / "one.npz")],
+                   check=True, env=env)
+    one = np.load(tmp_path / "one.npz")
+    many = {
+        "seq": oracle.spmm_seq(crow, col, val, x),
+        "f64": oracle.spmm_f64(crow, col, val, x),
+        "dot": oracle.sddmm_ref(crow, col, q, q),
+        "att": oracle.attention_f64(crow, col, q, q, x, 0.3),
+    }
+    for name, value in many.items():
+        assert np.array_equal(one[name].view(np.uint8), value.view(np.uint8)), name

@@ -1,11 +1,14 @@
-"""Scheduler configuration and candidate shortlist (mirrors the reference
-tests/test_scheduler.py, plus exact-order checks)."""
+"""Scheduler configuration and candidate shortlist: the behaviour the
+reference's tests/test_scheduler.py pins (valid shortlist, env overrides
+read per call, kernel policy in the signature), checked over more inputs,
+plus exact-order and decision-rule checks."""
 
 from __future__ import annotations
 
 import json
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -15,34 +18,77 @@ from autosage_amd.config import SchedulerConfig
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def test_candidates_only_contain_effective_parameters():
-    crow = torch.tensor([0, 1, 3, 3, 10], dtype=torch.long)
-    candidates = _spmm_candidates(crow, 64, SchedulerConfig(candidate_count=18))
-    assert candidates
-    assert len(candidates) == len(set(candidates))
-    assert all(tile in {64, 128} for tile, _, _ in candidates)
-    assert all(warps in {2, 4, 8} for _, warps, _ in candidates)
-    assert all(threshold > 0 for _, _, threshold in candidates)
+def _crow_of(degrees) -> torch.Tensor:
+    return torch.tensor([0, *np.cumsum(degrees).tolist()], dtype=torch.long)
 
 
-def test_environment_overrides_are_read_for_each_configuration(monkeypatch):
-    monkeypatch.setenv("AUTOSAGE_FTILE", "64")
-    monkeypatch.setenv("AUTOSAGE_WPB", "8")
-    monkeypatch.setenv("AUTOSAGE_HUB_T", "16")
-    first = SchedulerConfig.from_env()
-    monkeypatch.setenv("AUTOSAGE_HUB_T", "32")
-    second = SchedulerConfig.from_env()
-    assert first.hub_threshold == 16
-    assert second.hub_threshold == 32
+@pytest.mark.parametrize("degrees", [[1, 2, 0, 7], [0] * 5 + [40], list(range(50)), [3] * 64 + [900, 2000]])
+@pytest.mark.parametrize("features", [16, 64, 200])
+def test_shortlist_holds_only_runnable_split_settings(degrees, features):
+    """Every shortlisted (feature_tile, waves, hub_threshold) is a setting
+    the split op accepts, each appears once, and the list never outgrows the
+    requested count."""
+    crow = _crow_of(degrees)
+    for count in (1, 3, 6, 18):
+        shortlist = _spmm_candidates(crow, features, SchedulerConfig(candidate_count=count))
+        assert 1 <= len(shortlist) <= count
+        assert len(set(shortlist)) == len(shortlist)
+        for tile, waves, threshold in shortlist:
+            assert tile in (64, 128) and waves in (2, 4, 8)
+            assert isinstance(threshold, int) and threshold >= 1
 
 
-def test_tuning_signature_tracks_kernel_policy(monkeypatch):
-    first = SchedulerConfig.from_env().tuning_signature()
-    monkeypatch.setenv("AUTOSAGE_VEC4", "false")
-    second = SchedulerConfig.from_env().tuning_signature()
-    assert first["vec4"] is True
-    assert second["vec4"] is False
-    assert first != second
+def test_kernel_overrides_follow_the_environment_between_calls(monkeypatch):
+    """AUTOSAGE_FTILE / WPB / HUB_T are parsed again whenever they change."""
+    seen = []
+    for tile, waves, threshold in (("128", "2", "5"), ("64", "8", "77"), ("64", "4", "1")):
+        monkeypatch.setenv("AUTOSAGE_FTILE", tile)
+        monkeypatch.setenv("AUTOSAGE_WPB", waves)
+        monkeypatch.setenv("AUTOSAGE_HUB_T", threshold)
+        config = SchedulerConfig.from_env()
+        seen.append((config.feature_tile, config.warps_per_block, config.hub_threshold))
+    assert seen == [(128, 2, 5), (64, 8, 77), (64, 4, 1)]
+    # the pinned settings are the only candidate left
+    assert _spmm_candidates(_crow_of([4, 9, 2]), 32, SchedulerConfig.from_env()) == [(64, 4, 1)]
+
+
+@pytest.mark.parametrize("word", ["0", "off", "No", "FALSE"])
+def test_vec4_switch_changes_the_signature(monkeypatch, word):
+    """The float4 policy decides which kernels run, so a cached choice made
+    with it on must not replay with it off."""
+    monkeypatch.delenv("AUTOSAGE_VEC4", raising=False)
+    default = SchedulerConfig.from_env().tuning_signature()
+    monkeypatch.setenv("AUTOSAGE_VEC4", word)
+    switched = SchedulerConfig.from_env().tuning_signature()
+    assert (default["vec4"], switched["vec4"]) == (True, False)
+    assert {k for k in default if default[k] != switched[k]} == {"vec4"}
+
+
+def test_feature_slices_is_part_of_the_signature(monkeypatch):
+    assert SchedulerConfig.from_env().tuning_signature()["feature_slices"] == "auto"
+    monkeypatch.setenv("AUTOSAGE_FEATURE_SLICES", " On ")
+    assert SchedulerConfig.from_env().feature_slices == "on"
+    monkeypatch.setenv("AUTOSAGE_FEATURE_SLICES", "maybe")
+    with pytest.raises(ValueError, match="feature_slices"):
+        SchedulerConfig.from_env()
+
+
+def test_exactness_margin_of_the_full_graph_decision():
+    """The reassociating column-sliced SpMM wins only when it beats the best
+    bit-exact option by more than the margin."""
+    from autosage_amd import _auto
+
+    keys = ["null", '"fslice"', '"colslice"']
+    inexact = ('"colslice"',)
+    margin = _auto._INEXACT_MARGIN
+    assert _auto._prefer_exact(keys, {"null": 9.0, '"fslice"': 3.1, '"colslice"': 3.0}, inexact) == '"fslice"'
+    fast = 3.1 / (1.0 + margin) - 0.01
+    assert _auto._prefer_exact(keys, {"null": 9.0, '"fslice"': 3.1, '"colslice"': fast}, inexact) == '"colslice"'
+    assert _auto._prefer_exact(keys, {"null": 2.0, '"fslice"': 3.1, '"colslice"': 3.0}, inexact) == "null"
+    # without a bit-exact option the fastest one is taken
+    assert _auto._prefer_exact(['"colslice"'], {'"colslice"': 5.0}, inexact) == '"colslice"'
+    # and without inexact options the margin plays no part
+    assert _auto._prefer_exact(keys, {"null": 3.0, '"fslice"': 3.1, '"colslice"': 2.0}) == '"colslice"'
 
 
 def test_hub_mode_is_part_of_the_signature(monkeypatch):
