@@ -65,6 +65,11 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_i64, _c_ptr, _c_size,
          _c_ptr],
     ),
+    "as_spmm_fslice_relayout_f32": (_c_int, [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr]),
+    "as_spmm_csr_fslice_sliced_f32": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_i64, _c_ptr],
+    ),
     "as_spmm_csr_split_f32_static": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_int, _c_int,

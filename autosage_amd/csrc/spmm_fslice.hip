@@ -406,9 +406,31 @@ size_t as_spmm_fslice_workspace_bytes(int64_t n_cols, int64_t f) {
                       256);
 }
 
-int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val, const float* x, float* y, int64_t n,
-                           int64_t n_cols, int64_t nnz, int64_t f, const void* plan, size_t plan_bytes,
-                           int64_t plan_tag, void* workspace, size_t workspace_bytes, void* stream) {
+int as_spmm_fslice_relayout_f32(const float* x, int64_t n_cols, int64_t f, void* xs, size_t xs_bytes,
+                                void* stream) {
+  as::clear_error();
+  if (n_cols < 0 || n_cols > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "n_cols exceeds kernel index range");
+  if (f < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "F must be non-negative");
+  if (f >= as::kMaxFeatures) return as::fail(AS_ERR_UNSUPPORTED, "F must be below 2^28");
+  if (n_cols == 0 || f == 0) return AS_OK;
+  if (x == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const size_t need = as_spmm_fslice_workspace_bytes(n_cols, f);
+  if (xs == nullptr || xs_bytes < need)
+    return as::fail(AS_ERR_WORKSPACE, "feature-sliced SpMM needs %zu workspace bytes, got %zu", need,
+                    xs == nullptr ? size_t(0) : xs_bytes);
+  const int ns = as::fslice_count(f);
+  const int vec = f % 4 == 0 && as::aligned(x, 16);
+  const int64_t total = n_cols * ns * as::kSliceLanes;
+  int64_t blocks = (total + as::kBlock - 1) / as::kBlock;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(as::fslice_relayout_kernel, dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0,
+                     static_cast<hipStream_t>(stream), x, static_cast<float*>(xs), n_cols, f, ns, vec);
+  return as::check_launch("spmm_fslice_relayout");
+}
+
+int as_spmm_csr_fslice_sliced_f32(const int64_t* crow, const float* val, const void* xs, size_t xs_bytes, float* y,
+                                  int64_t n, int64_t n_cols, int64_t nnz, int64_t f, const void* plan,
+                                  size_t plan_bytes, int64_t plan_tag, void* stream) {
   as::clear_error();
   if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
   if (n_cols < 0 || n_cols > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "n_cols exceeds kernel index range");
@@ -416,8 +438,8 @@ int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val, const float* x
   if (f >= as::kMaxFeatures) return as::fail(AS_ERR_UNSUPPORTED, "F must be below 2^28");
   if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
   if (n == 0 || f == 0) return AS_OK;
-  if (crow == nullptr || y == nullptr || (n_cols > 0 && x == nullptr))
-    return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (crow == nullptr || y == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (nnz > 0 && n_cols == 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "edges into an empty column space");
   if (plan_tag != as::kFslicePlanTag)
     return as::fail(AS_ERR_INVALID_ARGUMENT, "plan tag %lld is not a feature-sliced plan (%lld)",
                     static_cast<long long>(plan_tag), static_cast<long long>(as::kFslicePlanTag));
@@ -426,36 +448,50 @@ int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val, const float* x
                     "edges (%zu)", plan == nullptr ? size_t(0) : plan_bytes, static_cast<long long>(n),
                     static_cast<long long>(nnz), as::fslice_plan_bytes(n, nnz));
   const size_t need = as_spmm_fslice_workspace_bytes(n_cols, f);
-  if (workspace == nullptr || workspace_bytes < need)
+  if (xs == nullptr || xs_bytes < need)
     return as::fail(AS_ERR_WORKSPACE, "feature-sliced SpMM needs %zu workspace bytes, got %zu", need,
-                    workspace == nullptr ? size_t(0) : workspace_bytes);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (nnz > 0 && n_cols == 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "edges into an empty column space");
+                    xs == nullptr ? size_t(0) : xs_bytes);
   // no edges: every row is empty and the kernel only writes zeros (it reads
   // entry 0 of the padded columns, and would read val[0], which may not exist)
   if (nnz == 0) val = nullptr;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   const as::FslicePlan p = as::fslice_plan_view(const_cast<void*>(plan), n);
   const int ns = as::fslice_count(f);
   const int nsp = as::fslice_padded(ns);
-  float* xs = static_cast<float*>(workspace);
-  const int vec = f % 4 == 0 && as::aligned(x, 16);
-  if (nnz > 0) {
-    const int64_t total = n_cols * ns * as::kSliceLanes;
-    int64_t blocks = (total + as::kBlock - 1) / as::kBlock;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(as::fslice_relayout_kernel, dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s, x,
-                       xs, n_cols, f, ns, vec);
-  }
+  const float* xsf = static_cast<const float*>(xs);
   const int yvec = f % 4 == 0 && as::aligned(y, 16);
   const bool wide = static_cast<uint64_t>(n_cols) * as::kSliceWidth * sizeof(float) > 0xffffffffull;
   if (val != nullptr) {
-    if (wide) as::launch_fslice<true, true>(crow, p.col, val, xs, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
-    else as::launch_fslice<true, false>(crow, p.col, val, xs, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
+    if (wide) as::launch_fslice<true, true>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
+    else as::launch_fslice<true, false>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
   } else {
-    if (wide) as::launch_fslice<false, true>(crow, p.col, val, xs, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
-    else as::launch_fslice<false, false>(crow, p.col, val, xs, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
+    if (wide) as::launch_fslice<false, true>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
+    else as::launch_fslice<false, false>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
   }
   return as::check_launch("spmm_csr_fslice");
+}
+
+int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val, const float* x, float* y, int64_t n,
+                           int64_t n_cols, int64_t nnz, int64_t f, const void* plan, size_t plan_bytes,
+                           int64_t plan_tag, void* workspace, size_t workspace_bytes, void* stream) {
+  as::clear_error();
+  if (n > 0 && f > 0 && nnz > 0 && n_cols > 0 && x == nullptr)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  // the checks of the sliced call first, so that no launch happens on bad arguments
+  if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
+  if (n > 0 && f > 0 && plan_tag != as::kFslicePlanTag)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "plan tag %lld is not a feature-sliced plan (%lld)",
+                    static_cast<long long>(plan_tag), static_cast<long long>(as::kFslicePlanTag));
+  if (n > 0 && f > 0 && nnz >= 0 && (plan == nullptr || plan_bytes < as::fslice_plan_bytes(n, nnz)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "feature-sliced plan of %zu bytes is too small for %lld rows and %lld "
+                    "edges (%zu)", plan == nullptr ? size_t(0) : plan_bytes, static_cast<long long>(n),
+                    static_cast<long long>(nnz), as::fslice_plan_bytes(n, nnz));
+  if (n > 0 && f > 0 && nnz > 0) {
+    const int st = as_spmm_fslice_relayout_f32(x, n_cols, f, workspace, workspace_bytes, stream);
+    if (st != AS_OK) return st;
+  }
+  return as_spmm_csr_fslice_sliced_f32(crow, val, workspace, workspace_bytes, y, n, n_cols, nnz, f, plan, plan_bytes,
+                                       plan_tag, stream);
 }
 
 }  // extern "C"

@@ -149,6 +149,19 @@ int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val,
                            void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* The two launches of as_spmm_csr_fslice_f32 apart: the slice-major copy of
+ * X into `xs` (as_spmm_fslice_workspace_bytes(n_cols, f) bytes), then the
+ * product from it.  A caller that multiplies one X by several graphs, or
+ * times the kernels one by one, copies X once.  Same checks and bits. */
+int as_spmm_fslice_relayout_f32(const float* x, int64_t n_cols, int64_t f,
+                                void* xs, size_t xs_bytes, void* stream);
+int as_spmm_csr_fslice_sliced_f32(const int64_t* crow, const float* val,
+                                  const void* xs, size_t xs_bytes, float* y,
+                                  int64_t n, int64_t n_cols, int64_t nnz,
+                                  int64_t f, const void* plan,
+                                  size_t plan_bytes, int64_t plan_tag,
+                                  void* stream);
+
 /* Largest row count of as_spmm_csr_split_f32_static. */
 #define AS_STATIC_MAX_ROWS (1 << 22)
 
