@@ -379,6 +379,10 @@ def main() -> int:
                              "product with the whole X on this GPU; the line is the slowest shard")
     parser.add_argument("--hub-degree", type=int, default=12_000, help="hubsweep: degree of row 0")
     parser.add_argument("--other-degree", type=int, default=32, help="hubsweep: degree of every other row")
+    parser.add_argument("--ceiling", action="store_true",
+                        help="SpMM fp32 fslice / colslice lines: also time the same schedule on the same graph with "
+                             "every column moved so that all gathers of a slice hit one X row (the all-cached "
+                             "ceiling of the gather path)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gpu-baseline", action="store_true")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -622,6 +626,8 @@ def bench_spmm(args, device) -> dict:
         result["vs_baseline"] = round(result["value"] / a800, 3)
         result["published_context"] = {**published, "autosage_gflops": round(a800, 2),
                                        "vs_baseline_meaning": "value / A800 AutoSAGE GFLOP/s on the same graph"}
+    if args.ceiling and chosen in ("fslice", "colslice") and not half and not args.backward:
+        result["roofline"]["all_cached_ceiling"] = all_cached_ceiling(chosen, crow, col, val, x, args, ms)
     exact = {k_: v_ for k_, v_ in calib.items() if k_ != "colslice"}
     if chosen == "colslice" and exact and not args.backward:
         # the fastest schedule bit-identical to the reference's CPU result
@@ -898,6 +904,26 @@ def plan_record(step, args, crow, col, f, dtype, column_slices: bool, ms: float)
             "note": "slice points and the degree-binned row order are built once per graph (as_spmm_colslice_plan) "
                     "and reused by every call, whatever X; ms_per_step_rebuilding_it times the same step with "
                     "AUTOSAGE_COLSLICE_PLAN=off"}
+
+
+def all_cached_ceiling(variant: str, crow, col, val, x, args, ms: float) -> dict:
+    """The same schedule on the same rows, slices and launches with every
+    gather of a (row, slice) aimed at one X row, so that it hits in cache:
+    for the feature slices every column becomes 0 (all edges read X row 0's
+    slices), for the column slices every column becomes the first column of
+    its slice.  What the gather path allows without misses."""
+    n = crow.numel() - 1
+    if variant == "fslice":
+        cached = torch.zeros_like(col)
+        how = "every column set to 0 (each slice's gathers hit one 128-byte line)"
+    else:
+        starts = torch.tensor([(n * b + 7) // 8 for b in range(8)], device=col.device)
+        cached = starts[torch.searchsorted(starts, col, right=True) - 1].contiguous()
+        how = "every column set to the first column of its slice"
+    op = torch.ops.autosage.spmm_csr_fslice if variant == "fslice" else torch.ops.autosage.spmm_csr_colslice
+    cached_ms, _ = time_steps(lambda: op(crow, cached, val, x), args.steps, args.warmup)
+    return {"ms": round(cached_ms, 4), "frac": round(cached_ms / ms, 4), "how": how,
+            "timing": "this run, same steps and warmup as the line"}
 
 
 def fslice_kernel_times(crow, col, val, x, launches: int) -> dict:
