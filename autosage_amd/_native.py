@@ -1175,10 +1175,13 @@ def row_sorted(crow: torch.Tensor, col: torch.Tensor,
 
 def _row_sorted_weights(col: torch.Tensor, val: Optional[torch.Tensor], perm: Optional[torch.Tensor]):
     """``val`` in the order of ``row_sorted``'s permutation, memoised per live,
-    unmodified (col, val) pair (edge weights usually stay fixed per graph)."""
+    unmodified (col, val, perm) triple (edge weights usually stay fixed per
+    graph)."""
     if val is None or perm is None:
         return val
-    return _SORTED_WEIGHTS_MEMO.get((col, val), None, lambda: val.index_select(0, perm))
+    # keyed on the permutation too: a new one (crow changed in place while
+    # col and val did not) must miss
+    return _SORTED_WEIGHTS_MEMO.get((col, val, perm), None, lambda: val.index_select(0, perm))
 
 
 def row_counts(crow: torch.Tensor, long_from: int, short_below: int) -> tuple[int, int]:

@@ -116,8 +116,16 @@ inline SlicePlan slice_plan_view(void* base, int64_t n) {
   return v;
 }
 
-inline int64_t slice_plan_tag(int64_t min_degree, int light_buckets) {
-  return (int64_t(1) << 48) | (static_cast<int64_t>(light_buckets) << 32) | min_degree;
+// What a plan was built for, checked by the calls that read it: the plan's
+// kind (the SpMM's row-block layout or the attention's whole-graph order),
+// the row blocks of an SpMM plan, the light buckets, whether it is a row
+// shard's plan (columns cut over another row count) and the slicing degree.
+enum : int64_t { kPlanKindSpmm = 1, kPlanKindAttention = 2 };
+inline int64_t slice_plan_tag(int64_t min_degree, int light_buckets, int64_t kind = kPlanKindAttention,
+                              int64_t blocks = 1, bool rect = false) {
+  return (int64_t(1) << 62) | (kind << 56) | ((blocks & 0xff) << 48) |
+         (static_cast<int64_t>(light_buckets & 0xff) << 40) | (static_cast<int64_t>(rect) << 39) |
+         (min_degree & ((int64_t(1) << 39) - 1));
 }
 
 // order: rows of degree >= min_degree in 8 log2-degree buckets, longest

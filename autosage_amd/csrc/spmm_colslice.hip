@@ -1100,7 +1100,9 @@ inline int light_bucket_count(int64_t elem_bytes) {
   return elem_bytes == 2 || AS_COLSLICE_GROUPED_F32 != 0 ? kMaxHeavyBuckets : 1;
 }
 
-inline int64_t plan_tag_of(int64_t min_degree, int light_buckets) { return slice_plan_tag(min_degree, light_buckets); }
+inline int64_t plan_tag_of(int64_t min_degree, int light_buckets, int64_t n, int64_t n_cols, int64_t elem_bytes) {
+  return slice_plan_tag(min_degree, light_buckets, kPlanKindSpmm, row_blocks(n, elem_bytes), n_cols != n);
+}
 
 // n_cols: the column space (rows of X); n for a square graph.  The slice
 // points of all rows in one launch, then the binning of each row block.
@@ -1396,7 +1398,7 @@ int as_spmm_colslice_plan_rect(const int64_t* crow, const int64_t* col, int64_t 
   const as::Slicing slicing = column_slices ? as::kSliceColumns : as::kSliceEdges;
   const int64_t min_degree = as::slicing_degree(slicing, f, e);
   const int light = as::light_bucket_count(e);
-  *plan_tag = as::plan_tag_of(min_degree, light);
+  *plan_tag = as::plan_tag_of(min_degree, light, n, n_cols, e);
   if (n == 0) return AS_OK;
   const int st = as::build_plan(crow, col, n, n_cols, min_degree, light, slicing, e, plan,
                                 static_cast<hipStream_t>(stream));
@@ -1436,10 +1438,11 @@ int as_spmm_csr_colslice_planned_rect(const int64_t* crow, const int64_t* col, c
   if (n == 0 || f == 0) return AS_OK;
   const as::Slicing slicing = column_slices ? as::kSliceColumns : as::kSliceEdges;
   const int64_t min_degree = as::slicing_degree(slicing, f, e);
-  if (plan_tag != as::plan_tag_of(min_degree, as::light_bucket_count(e)))
+  const int64_t want = as::plan_tag_of(min_degree, as::light_bucket_count(e), n, n_cols, e);
+  if (plan_tag != want)
     return as::fail(AS_ERR_INVALID_ARGUMENT,
-                    "the plan was built for other settings (plan tag %lld, these F, dtype and slicing need %lld)",
-                    (long long)plan_tag, (long long)as::plan_tag_of(min_degree, as::light_bucket_count(e)));
+                    "the plan was built for other settings (plan tag %lld, this graph, F, dtype and slicing need "
+                    "%lld)", (long long)plan_tag, (long long)want);
   if (plan == nullptr || plan_bytes < as::colslice_fixed_bytes(n))
     return as::fail(AS_ERR_WORKSPACE, "a column-sliced plan needs %zu bytes, got %zu", as::colslice_fixed_bytes(n),
                     plan_bytes);

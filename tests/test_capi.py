@@ -108,7 +108,20 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     rect_tag = ctypes.c_int64(0)
     assert lib.as_spmm_colslice_plan_rect(None, None, 0, 5, 0, 128, 0, 1, 256, 1 << 20, ctypes.byref(rect_tag),
                                           None) == 0
-    assert rect_tag.value == tags[(0, 128, 1)]
+    # a row shard's plan (columns cut over n_cols rows) has a tag of its own,
+    # which the square call refuses
+    assert rect_tag.value != tags[(0, 128, 1)]
+    assert lib.as_spmm_csr_colslice_planned(fake, fake, None, fake, fake, 4, 4, 128, 0, 1, fake, 1 << 20,
+                                            rect_tag.value, fake, 1 << 20, -1, 0, None) == 1
+    assert lib.as_last_error().startswith(b"the plan was built for other settings")
+    # an attention plan (whole-graph row order) is not an SpMM plan (row
+    # blocks), even where the slicing degree and light buckets agree
+    att_tag = ctypes.c_int64(0)
+    assert lib.as_csr_attention_plan(None, None, 0, 0, 1, 256, 1 << 20, ctypes.byref(att_tag), None) == 0
+    assert att_tag.value not in tags.values()
+    assert lib.as_spmm_csr_colslice_planned(fake, fake, None, fake, fake, 4, 4, 64, 1, 1, fake, 1 << 20,
+                                            att_tag.value, fake, 1 << 20, -1, 0, None) == 1
+    assert lib.as_last_error().startswith(b"the plan was built for other settings")
     assert lib.as_spmm_colslice_plan_rect(None, None, 0, -1, 0, 128, 0, 1, 256, 1 << 20, ctypes.byref(rect_tag),
                                           None) == 1
     assert lib.as_last_error() == b"n_cols exceeds kernel index range"

@@ -475,3 +475,25 @@ def test_colslice_row_blocks_with_empty_blocks_and_feature_tiles(features):
         s_crow, s_col, s_val = shard.shard_csr(d[0], d[1], d[2], r0, r1)
         pieces.append(shard.spmm_csr_shard(s_crow, s_col, s_val, d[3]))
     assert torch.equal(got, torch.cat(pieces))
+
+
+def test_row_sorted_weights_follow_an_in_place_change_of_crow():
+    """A weighted graph whose columns do not ascend runs on its row-sorted
+    copy with the weights permuted the same way.  When crow changes in place
+    (same col and val objects, new row boundaries) the permutation changes,
+    and the permuted weights must follow it."""
+    rng = np.random.default_rng(51)
+    rows, f = 400, 32
+    crow = np.concatenate([[0], np.cumsum(rng.integers(0, 30, size=rows))]).astype(np.int64)
+    nnz = int(crow[-1])
+    col = rng.integers(0, rows, size=nnz).astype(np.int64)  # unsorted, duplicates allowed
+    val = rng.standard_normal(nnz).astype(np.float32)
+    x = rng.standard_normal((rows, f)).astype(np.float32)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    first = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x).cpu().numpy()
+    _assert_fp64_close(first, oracle.spmm_f64(crow, col, val, x))
+    # new row boundaries over the same edges
+    crow2 = np.concatenate([[0], np.sort(rng.integers(0, nnz + 1, size=rows - 1)), [nnz]]).astype(np.int64)
+    d_crow.copy_(torch.from_numpy(crow2))
+    second = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x).cpu().numpy()
+    _assert_fp64_close(second, oracle.spmm_f64(crow2, col, val, x))
