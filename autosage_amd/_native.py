@@ -104,6 +104,7 @@ _SIGNATURES = {
          _c_i64, _c_ptr, _c_size, _c_i64, _c_i64, _c_ptr],
     ),
     "as_spmm_colslice_planned_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int, _c_i64]),
+    "as_spmm_colslice_row_blocks": (_c_i64, [_c_i64, _c_int, ctypes.POINTER(ctypes.c_int64), _c_i64]),
     "as_spmm_csr_colslice_planned": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_i64,
@@ -479,6 +480,29 @@ def spmm_csr_colslice_impl(crow, col, val, x):
     return y
 
 
+def block_sliced_rows(crow: torch.Tensor, f: int, dtype: torch.dtype, column_slices: bool) -> int:
+    """The most rows of slicing degree in one row block of the column-sliced
+    plan: what its partial buffers are sized for.  One device reduction and
+    host sync per live, unmodified crow and settings (memoised)."""
+    lib = library()
+    code = 0 if dtype == torch.float32 else DTYPES_16[dtype]
+    degree = int(lib.as_spmm_colslice_min_degree(int(bool(column_slices)), f, code))
+    n = crow.numel() - 1
+
+    def compute() -> int:
+        begins = (ctypes.c_int64 * 65)()
+        blocks = int(lib.as_spmm_colslice_row_blocks(n, code, begins, 65))
+        if blocks < 1 or blocks > 64:
+            return -1
+        deg = crow[1:] - crow[:-1]
+        long = (deg >= degree).to(torch.int64).cumsum(0)
+        ends = torch.tensor([begins[b] for b in range(blocks + 1)], device=crow.device)
+        at = torch.cat([torch.zeros(1, dtype=torch.int64, device=crow.device), long])[ends]
+        return int((at[1:] - at[:-1]).max().item())
+
+    return _ROW_COUNT_MEMO.get((crow,), ("block_sliced", degree, code), compute)
+
+
 def colslice_plans_enabled() -> bool:
     """Whether the column-sliced SpMM reuses a per-graph plan (slice points
     and binned row order) across calls; ``AUTOSAGE_COLSLICE_PLAN=off`` builds
@@ -536,7 +560,8 @@ def _spmm_colslice_planned(crow, col, val, x, y, column_slices: bool, sliced: in
     code = 0 if x.dtype == torch.float32 else DTYPES_16[x.dtype]
     lib = library()
     plan, tag = colslice_plan(crow, col, f, x.dtype, column_slices, n_cols)
-    needed = lib.as_spmm_colslice_planned_workspace_bytes(n, f, code, sliced)
+    needed = lib.as_spmm_colslice_planned_workspace_bytes(n, f, code, block_sliced_rows(crow, f, x.dtype,
+                                                                                        column_slices))
     ws = _workspace(max(min(needed, _colslice_workspace_cap() - plan.numel()), 0), x.device)
     with _on(x.device):
         if n_cols is None:

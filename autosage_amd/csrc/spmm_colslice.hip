@@ -705,6 +705,53 @@ __device__ __forceinline__ void colslice_slice_block(int64_t mb, const int64_t* 
   }
 }
 
+// Orders one wave's LDS stores before its later loads (lanes read what other
+// lanes of the same wave wrote).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// A sliced fp32 row that found no partial rows in the buffer (the workspace
+// was sized for fewer sliced rows than a chunk has): one wave computes each
+// non-empty slice's fp64 sum with the slice work's own code (slice_wide, into
+// LDS instead of a partial row) and adds them in slice order from 0.0 as the
+// reduction does, then rounds once.  The same operations in the same order,
+// so the same bits as when the row is sliced across waves.  Rows of the
+// cooperative degree never get here (the host keeps chunks within the
+// buffers on graphs that have them).  Called from colslice_overflow_kernel,
+// a launch of its own, so that the step kernel keeps its register budget.  `sums`: this wave's 2·kTile LDS slots,
+// the slice's sum and the running total (kept in LDS, not in registers, so
+// that the slice work around it keeps its register budget).
+template <typename T, int V, bool HAS_VAL, bool OFF32>
+__device__ __forceinline__ void overflow_row_exact(const int64_t* __restrict__ crow, const int64_t* __restrict__ col,
+                                                   const T* __restrict__ val, const T* __restrict__ x,
+                                                   T* __restrict__ y, int64_t F, const int32_t* __restrict__ off,
+                                                   int64_t row, int64_t tile, LdsSum* sums) {
+  constexpr int64_t kTile = 16 * V / static_cast<int64_t>(sizeof(T));
+  const int lane = lane_id();
+  const int64_t rs = uniform_i64(crow[row]);
+  const int64_t deg = uniform_i64(crow[row + 1]) - rs;
+  const int64_t f0 = tile * kTile;
+  const int64_t width = F - f0 < kTile ? F - f0 : kTile;
+  LdsSum* total = sums + kTile;
+  for (int64_t f = lane; f < width; f += kWave) total[f].v = 0.0;
+  for (int s = 0; s < kSpmmSlices; ++s) {
+    int64_t a, b;
+    slice_range<kSpmmSlices>(off, row, s, deg, a, b);
+    a = uniform_i64(a);
+    b = uniform_i64(b);
+    if (a >= b) continue;
+    // addressed by absolute feature index, as for a partial row
+    slice_wide<T, V, HAS_VAL, OFF32>(col, val, x, sums - f0, F, rs + a, rs + b, f0);
+    wave_lds_sync();
+    for (int64_t f = lane; f < width; f += kWave) total[f].v = total[f].v + sums[f].v;
+    wave_lds_sync();
+  }
+  for (int64_t f = lane; f < width; f += kWave) Elem<T>::put(y + row * F + f0 + f, total[f].v);
+}
+
 template <typename T, int V, bool HAS_VAL, bool OFF32>
 __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* __restrict__ crow,
                                                      const int64_t* __restrict__ col, const T* __restrict__ val,
@@ -718,8 +765,15 @@ __device__ __forceinline__ void colslice_short_block(int64_t hb, const int64_t* 
   const int64_t k = hb - tile * tile_blocks;
   const int64_t waves = tile_blocks * kWavesPerBlock;  // short waves per tile
   const int64_t w = k * kWavesPerBlock + wave_in_block();
-  const int64_t fs = first_short(counts, c);
+  // fp32 wide lanes: sliced rows past the partial buffers' capacity, from fs
+  // to counts[0], are left to colslice_overflow_kernel; 16-bit elements sum
+  // them whole here with the short rows (the same bits for their rule)
+  int64_t fs = first_short(counts, c);
   const int64_t end = c.item_begin + c.items;
+  if constexpr (sizeof(T) == 4 && V >= 8) {
+    const int64_t h = counts[0];
+    fs = h < fs ? fs : (h > end ? end : h);
+  }
   int64_t split = end;  // grouped rows: [split, end)
   if constexpr (grouped_lanes<T, V>()) {
     if (grouped.start != nullptr) {
@@ -832,6 +886,51 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(AS_COLSL
   } else {
     colslice_short_block<T, V, HAS_VAL, OFF32>((work - MG) * kSlices + within, crow, col, val, x, y, F, order,
                                                counts, m, grouped);
+  }
+}
+
+// The sliced rows of chunks whose partial buffers held fewer rows than they
+// have: positions [begin, min(counts[0], end)) of each chunk's order, one wave
+// per (row, feature tile), fp32 with wide lanes.  A wave finds the range empty
+// and exits when the workspace was sized for the chunk's sliced rows.
+constexpr int kMaxOverflowChunks = 16;
+struct OverflowChunk {
+  const int64_t* crow;  // the row block's (rebased) row pointer
+  const int32_t* order;
+  const int32_t* counts;
+  const int32_t* off;
+  void* y;
+  int64_t begin;  // first order position past the capacity
+  int64_t end;    // end of the chunk's positions
+};
+struct OverflowChunks {
+  OverflowChunk c[kMaxOverflowChunks];
+  int count;
+};
+
+template <typename T, int V, bool HAS_VAL, bool OFF32>
+__global__ __launch_bounds__(kBlock) void colslice_overflow_kernel(const int64_t* __restrict__ col,
+                                                                   const T* __restrict__ val,
+                                                                   const T* __restrict__ x, int64_t F,
+                                                                   int64_t tiles, OverflowChunks oc) {
+  constexpr int64_t kTile = 16 * V / static_cast<int64_t>(sizeof(T));
+  __shared__ LdsSum sums[kWavesPerBlock * 2 * kTile];
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  LdsSum* mine = sums + wave_in_block() * 2 * kTile;
+  for (int k = 0; k < oc.count; ++k) {
+    const OverflowChunk c = oc.c[k];
+    const int64_t h = uniform_i64(static_cast<int64_t>(c.counts[0]));
+    const int64_t stop = h < c.end ? h : c.end;
+    if (stop <= c.begin) continue;
+    const int64_t items = (stop - c.begin) * tiles;
+    for (int64_t i = wave; i < items; i += waves) {
+      const int64_t pos = c.begin + i / tiles;
+      const int64_t tile = i - (i / tiles) * tiles;
+      const int64_t row = uniform_i64(static_cast<int64_t>(c.order[pos]));
+      overflow_row_exact<T, V, HAS_VAL, OFF32>(c.crow, col, val, x, static_cast<T*>(c.y), F, c.off, row, tile,
+                                               mine);
+    }
   }
 }
 
@@ -1180,17 +1279,26 @@ int colslice_chunks(const int64_t* crow, const int64_t* col, const void* val, co
   const int vr = (f % 2 == 0 && aligned(y, static_cast<size_t>(2 * E))) ? 2 : 1;
 
   // two partial buffers of `capacity` rows each (chunk k writes buffer
-  // k % 2).  fp32: chunks of at most `capacity` rows, so that every sliced
-  // row of a chunk has partial rows.  16-bit: chunks of the preferred size
-  // whatever the workspace; sliced rows past the capacity are summed whole,
-  // with the same bits, so a workspace sized for the sliced rows suffices.
+  // k % 2).  16-bit, and fp32 with wide lanes on graphs without cooperative
+  // rows: chunks of the preferred size whatever the workspace; sliced rows
+  // past the capacity are summed by one wave each (16-bit: whole, fp32: slice
+  // by slice in the sliced rows' order), with the same bits, so a workspace
+  // sized for the sliced rows suffices.  Otherwise (fp32 narrow lanes, or
+  // cooperative rows): chunks of at most `capacity` rows, so that every
+  // sliced row of a chunk has partial rows.
   const int64_t fits = static_cast<int64_t>(partial_bytes / (2 * row_bytes));
+  // fp32 with wide lanes on graphs without cooperative rows: a sliced row
+  // past the capacity is summed by one wave with the same arithmetic
+  // (overflow_row_exact), so chunks need not fit the buffers either and a
+  // workspace sized for the sliced rows keeps one chunk per row block
+  const bool has_mega = nnz <= kMegaMaxNnz && kMegaLevel >= 1 && kMegaLevel < kMaxHeavyBuckets;
+  const bool overflow_exact = E != 4 || (v >= 8 && !has_mega);
   // a graph holds at most nnz / min_degree sliced rows; when they fit one
   // partial buffer the whole graph is one chunk (fewer launches, and short
   // rows run beside the hub rows' slices)
   const int64_t upper = min_degree > 0 && nnz / min_degree < n ? nnz / min_degree : n;
-  if (upper <= chunk && (E != 4 || upper <= fits)) chunk = n;
-  if (E == 4 && (chunk < upper ? chunk : upper) > fits) chunk = fits;
+  if (upper <= chunk && (overflow_exact || upper <= fits)) chunk = n;
+  if (!overflow_exact && (chunk < upper ? chunk : upper) > fits) chunk = fits;
   // blocks of a launch: 8 per group, at most tiles·(P·ceil(c/4) + ceil(c/32))
   // work groups for c rows, and reduce groups at most a quarter of those
   const int64_t max_rows = (kMaxBlocksPerLaunch * 4 / 5 / (kSlices * tiles) - 2) * 32 / (8 * kPhases + 1);
@@ -1268,6 +1376,54 @@ void colslice_pipeline(const StepShape& sh, bool has_val, const std::vector<Chun
   }
 }
 
+// Launches colslice_overflow_kernel for the chunks of `work` whose partial
+// buffers hold fewer rows than the chunk (fp32 wide lanes only; elsewhere
+// the chunks fit their buffers or the step kernel sums the rest).  `upper`:
+// at most this many sliced rows in a chunk (nnz / slicing degree), sizing the grid.
+template <typename T>
+void colslice_overflow(const StepShape& sh, bool has_val, const std::vector<ChunkWork>& work, int64_t upper,
+                       hipStream_t s) {
+  if constexpr (sizeof(T) != 4) {
+    return;
+  } else {
+    if (sh.v < 8 || work.empty()) return;
+    const StepArgs& a0 = work[0].a;
+    OverflowChunks oc{};
+    int64_t potential = 0;
+    auto flush = [&]() {
+      if (oc.count == 0) return;
+      int64_t blocks = (potential * sh.tiles + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock);
+      blocks = blocks < kSlices ? kSlices : (blocks > 2048 ? 2048 : blocks);
+      const dim3 grid(static_cast<unsigned>(blocks)), block(kBlock);
+      const float* v = static_cast<const float*>(a0.val);
+      const float* x = static_cast<const float*>(a0.x);
+#define AS_OVERFLOW(V_, HV_, O_)                                                                                    \
+  hipLaunchKernelGGL((colslice_overflow_kernel<float, V_, HV_, O_>), grid, block, 0, s, a0.col, v, x, a0.f, sh.tiles, \
+                     oc)
+      if (sh.v == 32) {
+        if (has_val) { if (sh.off32) AS_OVERFLOW(32, true, true); else AS_OVERFLOW(32, true, false); }
+        else { if (sh.off32) AS_OVERFLOW(32, false, true); else AS_OVERFLOW(32, false, false); }
+      } else {
+        if (has_val) { if (sh.off32) AS_OVERFLOW(16, true, true); else AS_OVERFLOW(16, true, false); }
+        else { if (sh.off32) AS_OVERFLOW(16, false, true); else AS_OVERFLOW(16, false, false); }
+      }
+#undef AS_OVERFLOW
+      oc.count = 0;
+      potential = 0;
+    };
+    for (const ChunkWork& w : work) {
+      if (w.c.capacity >= w.c.items) continue;
+      const int64_t most = (upper < w.c.items ? upper : w.c.items) - w.c.capacity;
+      if (most <= 0) continue;
+      oc.c[oc.count++] = OverflowChunk{w.a.crow, w.a.order, w.a.counts, w.a.off, w.a.y,
+                                       w.c.item_begin + w.c.capacity, w.c.item_begin + w.c.items};
+      potential += most;
+      if (oc.count == kMaxOverflowChunks) flush();
+    }
+    flush();
+  }
+}
+
 template <typename T>
 int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, const void* x, void* y, int64_t n,
                      int64_t n_cols, int64_t nnz, int64_t f, int64_t min_degree, const PlanView& plan, void* partials,
@@ -1278,6 +1434,7 @@ int colslice_execute(const int64_t* crow, const int64_t* col, const void* val, c
                                     partial_bytes, sliced_rows, grouped_rows, chunk, sh, work);
   if (st != AS_OK) return st;
   colslice_pipeline<T>(sh, val != nullptr, work, 0, work.size(), partials, colslice_row_bytes(f), s);
+  colslice_overflow<T>(sh, val != nullptr, work, min_degree > 0 ? nnz / min_degree : n, s);
   return AS_OK;
 }
 
@@ -1324,10 +1481,13 @@ int colslice_execute_blocks(const int64_t* crow, const int64_t* col, const void*
   const size_t row_bytes = colslice_row_bytes(f);
   if (f <= AS_COLSLICE_FUSE_BLOCKS_MAX_F && same_shape) {
     colslice_pipeline<T>(shapes[0], val != nullptr, work, 0, work.size(), partials, row_bytes, s);
-    return AS_OK;
+  } else {
+    for (size_t b = 0, begin = 0; b < ends.size(); begin = ends[b++])
+      colslice_pipeline<T>(shapes[b], val != nullptr, work, begin, ends[b], partials, row_bytes, s);
   }
-  for (size_t b = 0, begin = 0; b < ends.size(); begin = ends[b++])
-    colslice_pipeline<T>(shapes[b], val != nullptr, work, begin, ends[b], partials, row_bytes, s);
+  // every block shares the lane shape (F, alignments), so the overflow of all
+  // chunks is one launch
+  colslice_overflow<T>(shapes[0], val != nullptr, work, min_degree > 0 ? nnz / min_degree : n, s);
   return AS_OK;
 }
 
@@ -1412,11 +1572,26 @@ int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n, in
                                     plan_tag, stream);
 }
 
+int64_t as_spmm_colslice_row_blocks(int64_t n, int dtype, int64_t* begins, int64_t capacity) {
+  const int64_t e = as::elem_bytes_of(dtype);
+  if (e == 0 || n < 0) return 0;
+  const int64_t blocks = as::row_blocks(n, e);
+  for (int64_t b = 0; b <= blocks && b < capacity && begins != nullptr; ++b) begins[b] = as::block_begin(n, blocks, b);
+  return blocks;
+}
+
 size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype, int64_t sliced_rows) {
   if (n < 0) n = 0;
   if (f < 1) f = 1;
+  // a chunk's rows: the preferred chunk, or a whole row block of the plan
+  // (the planned call runs each block as one chunk when the buffers allow)
+  const int64_t e = as::elem_bytes_of(dtype);
   int64_t rows = as::preferred_chunk_rows(n);
-  if (dtype != AS_DTYPE_F32 && sliced_rows >= 0 && sliced_rows < rows) rows = sliced_rows > 0 ? sliced_rows : 1;
+  if (e != 0) {
+    const int64_t block = as::block_rows_max(n, as::row_blocks(n, e));
+    if (block > rows) rows = block;
+  }
+  if (sliced_rows >= 0 && sliced_rows < rows) rows = sliced_rows > 0 ? sliced_rows : 1;
   return 2 * static_cast<size_t>(rows) * as::colslice_row_bytes(f);
 }
 

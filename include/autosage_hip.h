@@ -236,10 +236,20 @@ int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n,
                           void* stream);
 
 /* Preferred workspace bytes of as_spmm_csr_colslice_planned: the two partial
- * buffers only (for 16-bit types sized by sliced_rows as in
- * as_spmm_rounded_16_workspace_bytes). */
+ * buffers only, of min(sliced_rows, rows of a chunk) partial rows each;
+ * sliced_rows = the most rows of slicing degree that one row block of the
+ * plan holds (as_spmm_colslice_row_blocks), or -1 for a chunk's rows.  The
+ * bits do not depend on it: a sliced row that finds no partial row is summed
+ * by one wavefront with the same operations in the same order (16-bit
+ * elements: whole, by their order-free rule). */
 size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype,
                                                 int64_t sliced_rows);
+
+/* Row blocks of a column-sliced plan for n rows of type dtype: returns their
+ * count B and writes their first rows begins[0..B] (begins[B] = n) when
+ * capacity > B.  Host only. */
+int64_t as_spmm_colslice_row_blocks(int64_t n, int dtype, int64_t* begins,
+                                    int64_t capacity);
 
 /* as_spmm_csr_colslice_f32 (dtype AS_DTYPE_F32, column_slices != 0) or
  * as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16) with the slice

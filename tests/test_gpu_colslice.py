@@ -9,6 +9,8 @@ It is deterministic: repeated and chunked calls give identical bits.
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -497,3 +499,54 @@ def test_row_sorted_weights_follow_an_in_place_change_of_crow():
     d_crow.copy_(torch.from_numpy(crow2))
     second = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x).cpu().numpy()
     _assert_fp64_close(second, oracle.spmm_f64(crow2, col, val, x))
+
+
+@pytest.mark.parametrize("features", [64, 128, 200])
+def test_fp32_partial_buffers_smaller_than_the_sliced_rows(features):
+    """fp32 with a workspace sized below a block's sliced rows (a graph of more
+    than 2^24 edges, so no cooperative rows): the sliced rows past the
+    capacity are summed one wave each with the sliced rows' own arithmetic,
+    so every workspace size gives the bits of the full one, weighted or not."""
+    rows = 120_000
+    crow, col = case_graph(rows, 150, seed=features, hubs=30, hub_degree=20_000, empty=0.02)
+    assert col.size > (1 << 24)
+    rng = np.random.default_rng(features)
+    val = rng.standard_normal(col.size).astype(np.float32)
+    x = rng.standard_normal((rows, features)).astype(np.float32)
+    d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+    n, f = x.shape
+    lib = _native.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    plan, tag = _native.colslice_plan(d_crow, d_col, f, torch.float32, True)
+    most = _native.block_sliced_rows(d_crow, f, torch.float32, True)
+    degree = lib.as_spmm_colslice_min_degree(1, f, 0)
+    begins = (ctypes.c_int64 * 65)()
+    blocks = lib.as_spmm_colslice_row_blocks(n, 0, begins, 65)
+    want_most = max(int((np.diff(crow)[begins[b]:begins[b + 1]] >= degree).sum()) for b in range(blocks))
+    assert blocks >= 2 and most == want_most
+    row_bytes = lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, 1) // 2
+    sliced, grouped = _native.colslice_row_counts(d_crow, f, torch.float32)
+    for weights in (None, d_val):
+        outs = []
+        for rows_per_buffer in (-1, most, most // 3, 1):
+            ws_bytes = (lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, -1) if rows_per_buffer < 0
+                        else 2 * rows_per_buffer * row_bytes)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+            y = torch.empty_like(d_x)
+            status = lib.as_spmm_csr_colslice_planned(
+                d_crow.data_ptr(), d_col.data_ptr(), None if weights is None else weights.data_ptr(), d_x.data_ptr(),
+                y.data_ptr(), n, col.size, f, 0, 1, plan.data_ptr(), plan.numel(), tag, ws.data_ptr(), ws.numel(),
+                sliced, grouped, stream)
+            assert status == 0, lib.as_last_error()
+            outs.append(y)
+        torch.cuda.synchronize()
+        for y in outs[1:]:
+            assert torch.equal(y, outs[0])
+        picked = np.concatenate([np.argsort(-np.diff(crow))[:6], rng.choice(rows, 300, replace=False)])
+        exact = oracle.spmm_f64(crow, col, None if weights is None else val, x, rows=picked)
+        _assert_fp64_close(outs[-1][torch.from_numpy(picked).cuda()].cpu().numpy(), exact)
+    # the op sizes its workspace for the sliced rows of the largest block (a
+    # block's rows at most)
+    block_rows = max(begins[b + 1] - begins[b] for b in range(blocks))
+    assert lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, -1) >= 2 * block_rows * row_bytes
+    assert lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, most) == 2 * min(most, block_rows) * row_bytes
