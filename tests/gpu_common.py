@@ -42,7 +42,8 @@ def mismatch_report(gpu: torch.Tensor, ref: np.ndarray) -> str:
 
 
 def elementwise_parity(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, *, tight_rel: float,
-                       tight_abs: float, rtol: float = 1e-5, atol: float = 1e-6) -> dict:
+                       tight_abs: float, rtol: float = 1e-5, atol: float = 1e-6,
+                       accept_both_within_bar: bool = False) -> dict:
     """Per-element parity of a reassociating kernel with the reference's fp32
     result ``ref``, against the exact (fp64) result ``exact``.  With
     bar(v) = rtol·|v| + atol and the kernel's bound δ = tight_rel·|exact| +
@@ -57,6 +58,13 @@ def elementwise_parity(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, *, t
         |ref − exact|.  If |got − exact| <= δ and (a) fails, the triangle
         inequality puts |ref − exact| above roughly bar − δ, so (c) is the
         boundary band that (a) and (b) leave between them.
+
+    With ``accept_both_within_bar`` a fourth case counts:
+
+    (d) |ref − exact| <= bar(exact) and |got − exact| <= δ: both results are
+        within the bar of the exact one, on opposite sides of it, so neither
+        is the more correct (used for gradients, where the reference's
+        autograd and the kernel sum the same terms in unrelated orders).
 
     Returns the counts (and the largest |ref − exact| / bar(exact) among the
     elements of (b) and (c)); raises AssertionError naming them when an
@@ -73,7 +81,8 @@ def elementwise_parity(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, *, t
     ref_edge = ~ref_misses & (ref_err > bar_exact - bound)
     case_b = ~near_ref & ref_misses & kernel_ok
     case_c = ~near_ref & ref_edge & kernel_ok
-    neither = ~near_ref & ~case_b & ~case_c
+    case_d = ~near_ref & ~case_b & ~case_c & ~ref_misses & (got_err <= bound)
+    neither = ~near_ref & ~case_b & ~case_c & ~(case_d if accept_both_within_bar else np.zeros_like(case_d))
     ratio = ref_err / bar_exact
     counts = {
         "elements": int(got.size),
@@ -83,8 +92,11 @@ def elementwise_parity(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, *, t
         "reference_off_bar_total": int(ref_misses.sum()),
         "worst_reference_error_over_bar": float(ratio.max()) if ratio.size else 0.0,
         "min_reference_error_over_bar_in_c": float(ratio[case_c].min()) if case_c.any() else None,
+        "worst_kernel_error_over_bar": float((got_err / bar_exact).max()) if got.size else 0.0,
         "neither": int(neither.sum()),
     }
+    if accept_both_within_bar:
+        counts["d_both_within_bar_of_exact"] = int(case_d.sum())
     print(f"[parity] {counts}", flush=True)
     assert counts["neither"] == 0, counts
     return counts

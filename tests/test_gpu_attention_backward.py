@@ -3,7 +3,10 @@
 The reference registers no autograd; these gradients are checked against the
 oracle's restatement of the softmax backward (bit for bit: the kernel has no
 ``exp``) and against torch autograd of an fp64 composition of the attention
-(SDDMM, row softmax, SpMM) on the CPU.
+(SDDMM, row softmax, SpMM) on the CPU: every gradient element within
+1e-5·|fp64| + 1e-6, and within that bar of the reference's own fp32 autograd
+gradient or, where not, both on opposite sides of the fp64 gradient within its
+bar, or the reference off the bar and the kernel closer.
 """
 
 from __future__ import annotations
@@ -13,7 +16,7 @@ import pytest
 import torch
 
 import oracle
-from tests.gpu_common import case_graph, require_gpu, to_dev
+from tests.gpu_common import case_graph, elementwise_parity, require_gpu, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -58,18 +61,47 @@ def test_softmax_op_autograd():
     assert np.array_equal(d_s.grad.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
-def _attention_fp64(crow, col, q, k, v, scale):
-    """out = softmax_row(scale·<q[row], k[col]>)·v in fp64 with torch autograd."""
+def _attention_torch(crow, col, q, k, v, scale, dtype=torch.float64):
+    """out = softmax_row(scale·<q[row], k[col]>)·v with torch autograd on the
+    CPU: in fp64 the near-exact gradients, in fp32 the reference's own
+    (its composition, autosage/_auto.py:744-780, has no custom backward)."""
     n = crow.size - 1
     rows = torch.repeat_interleave(torch.arange(n), torch.from_numpy(np.diff(crow)))
     c = torch.from_numpy(col)
-    q64, k64, v64 = (torch.from_numpy(a).double().requires_grad_(True) for a in (q, k, v))
-    s = (q64[rows] * k64[c]).sum(1) * scale
-    m = torch.full((n,), -torch.inf, dtype=torch.float64).scatter_reduce(0, rows, s.detach(), "amax")
+    qq, kk, vv = (torch.from_numpy(a).to(dtype).requires_grad_(True) for a in (q, k, v))
+    s = (qq[rows] * kk[c]).sum(1) * scale
+    m = torch.full((n,), -torch.inf, dtype=dtype).scatter_reduce(0, rows, s.detach(), "amax")
     ex = (s - m[rows]).exp()
-    p = ex / torch.zeros(n, dtype=torch.float64).index_add(0, rows, ex)[rows]
-    out = torch.zeros(n, v.shape[1], dtype=torch.float64).index_add(0, rows, p[:, None] * v64[c])
-    return out, (q64, k64, v64)
+    p = ex / torch.zeros(n, dtype=dtype).index_add(0, rows, ex)[rows]
+    out = torch.zeros(n, v.shape[1], dtype=dtype).index_add(0, rows, p[:, None] * vv[c])
+    return out, (qq, kk, vv)
+
+
+def _attention_fp64(crow, col, q, k, v, scale):
+    return _attention_torch(crow, col, q, k, v, scale, torch.float64)
+
+
+RTOL = 1e-5
+ATOL = 1e-6
+
+
+def _assert_gradients_per_element(got_grads, crow, col, q, k, v, g, scale, label):
+    """Every element of dQ, dK, dV within 1e-5·|want| + 1e-6 of the fp64
+    autograd gradient, and within that bar of the reference's fp32 autograd
+    gradient or arbitrated against fp64 (``elementwise_parity`` with case (d):
+    the reference's autograd sums each gradient's terms in its own order, so
+    two results on opposite sides of the exact one, both within its bar,
+    count as agreeing)."""
+    exact_out, exact = _attention_torch(crow, col, q, k, v, scale, torch.float64)
+    exact_out.backward(torch.from_numpy(g).double())
+    ref_out, ref = _attention_torch(crow, col, q, k, v, scale, torch.float32)
+    ref_out.backward(torch.from_numpy(g))
+    for name, got, e_leaf, r_leaf in zip("QKV", got_grads, exact, ref):
+        want = e_leaf.grad.numpy()
+        err = np.abs(got.astype(np.float64) - want)
+        assert np.all(err <= RTOL * np.abs(want) + ATOL), (label, name, float(np.max(err / (RTOL * np.abs(want) + ATOL))))
+        elementwise_parity(got, r_leaf.grad.numpy(), want, tight_rel=RTOL, tight_abs=ATOL,
+                           accept_both_within_bar=True)
 
 
 @pytest.mark.parametrize("variant", ["fused", "colslice", "stages"])
@@ -93,13 +125,10 @@ def test_attention_gradients(variant):
         p = torch.ops.autosage.csr_row_softmax(d_crow, s)
         out = torch.ops.autosage.spmm_csr(d_crow, d_col, p, d_v)
     out.backward(torch.from_numpy(g).cuda())
-    ref, leaves = _attention_fp64(crow, col, q, k, v, scale)
-    ref.backward(torch.from_numpy(g).double())
+    ref, _ = _attention_fp64(crow, col, q, k, v, scale)
     assert np.max(np.abs(out.detach().cpu().numpy() - ref.detach().numpy())) <= 1e-5 * np.max(np.abs(ref.detach().numpy()))
-    for got, leaf in zip((d_q, d_k, d_v), leaves):
-        want = leaf.grad.numpy()
-        err = np.max(np.abs(got.grad.cpu().numpy() - want))
-        assert err <= 2e-5 * np.max(np.abs(want)), (variant, err, np.max(np.abs(want)))
+    _assert_gradients_per_element([t.grad.cpu().numpy() for t in (d_q, d_k, d_v)], crow, col, q, k, v, g, scale,
+                                  variant)
 
 
 def test_colslice_attention_backward_schedules(monkeypatch):
@@ -148,9 +177,9 @@ def _symmetric_hub_graph(n, seed):
 def test_two_pass_attention_backward(fqk, fv):
     """The column-sliced op's backward runs the two native passes: on a graph
     with out- and in-degree hubs (both passes slice rows), empty rows and
-    columns out of order, every gradient is within 2e-5 of the fp64 autograd
-    gradients (max-norm), and a second run gives the same bits.  The
-    comparison with the recomputing chain is in the schedules test above."""
+    columns out of order, every gradient element meets the per-element bars,
+    and a second run gives the same bits.  The comparison with the
+    recomputing chain is in the schedules test above."""
     n = 2500
     crow, col, rng = _symmetric_hub_graph(n, seed=fqk + fv)
     q = (rng.standard_normal((n, fqk)) * 0.25).astype(np.float32)
@@ -161,12 +190,8 @@ def test_two_pass_attention_backward(fqk, fv):
     leaves = [torch.from_numpy(a).cuda().requires_grad_(True) for a in (q, k, v)]
     out = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *leaves, 0.125)
     out.backward(torch.from_numpy(g).cuda())
-    ref, ref_leaves = _attention_fp64(crow, col, q, k, v, 0.125)
-    ref.backward(torch.from_numpy(g).double())
-    for got, leaf in zip(leaves, ref_leaves):
-        want = leaf.grad.numpy()
-        err = np.max(np.abs(got.grad.cpu().numpy() - want))
-        assert err <= 2e-5 * np.max(np.abs(want)), (err, np.max(np.abs(want)))
+    _assert_gradients_per_element([t.grad.cpu().numpy() for t in leaves], crow, col, q, k, v, g, 0.125,
+                                  f"two-pass {fqk}/{fv}")
     # deterministic
     again = [torch.from_numpy(a).cuda().requires_grad_(True) for a in (q, k, v)]
     torch.ops.autosage.csr_attention_colslice(d_crow, d_col, *again, 0.125).backward(torch.from_numpy(g).cuda())

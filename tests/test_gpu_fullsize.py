@@ -201,3 +201,115 @@ def test_config5_attention():
     print(f"[parity] colslice attention cfg5 worst |got - fp64| / bar = {worst:.4f}", flush=True)
     assert worst <= 1.0
     elementwise_parity_rows(got_s, ref, exact, tight_rel=RTOL, tight_abs=ATOL, label="colslice attention cfg5")
+
+
+def _edges_of(crow: np.ndarray, rows: np.ndarray):
+    """(edge ids of `rows` in CSR order, the position in `rows` of each edge's row)."""
+    starts, ends = crow[rows], crow[rows + 1]
+    counts = ends - starts
+    owner = np.repeat(np.arange(rows.size), counts)
+    offsets = np.arange(counts.sum()) - np.repeat(np.cumsum(counts) - counts, counts)
+    return np.repeat(starts, counts) + offsets, owner
+
+
+def _row_softmax_stats(crow, col, q, k, v, g, rows, scale, chunk=1 << 20):
+    """fp64 per-row softmax statistics of the attention for `rows`: the max
+    score m, the denominator d and t = sum_e p_e·<g_row, v_col>."""
+    edges, owner = _edges_of(crow, rows)
+    m = np.full(rows.size, -np.inf)
+    s = np.empty(edges.size)
+    dp = np.empty(edges.size)
+    for a in range(0, edges.size, chunk):
+        e, o = edges[a:a + chunk], owner[a:a + chunk]
+        s[a:a + chunk] = scale * np.einsum("ij,ij->i", q[rows[o]].astype(np.float64), k[col[e]].astype(np.float64))
+        dp[a:a + chunk] = np.einsum("ij,ij->i", g[rows[o]].astype(np.float64), v[col[e]].astype(np.float64))
+    np.maximum.at(m, owner, s)
+    ex = np.exp(s - m[owner])
+    d = np.bincount(owner, weights=ex, minlength=rows.size)
+    t = np.bincount(owner, weights=ex / d[owner] * dp, minlength=rows.size)
+    return m, d, t
+
+
+def _attention_grad_samples(crow, col, crow_t, col_t, perm, q, k, v, g, rows, cols, scale):
+    """fp64 dQ of `rows` and dK, dV of `cols` of out = softmax_row(scale·QKᵀ)·V
+    with upstream gradient g, each with the sum of its terms' magnitudes
+    (want, magnitude): dQ[r] = scale·sum_e ds_e·K[c_e], dK[c] = scale·sum_e
+    ds_e·Q[r_e], dV[c] = sum_e p_e·g[r_e], ds_e = p_e·(<g_r, V_c> - t_r)."""
+    f64 = lambda a: a.astype(np.float64)
+    m, d, t = _row_softmax_stats(crow, col, q, k, v, g, rows, scale)
+    edges, owner = _edges_of(crow, rows)
+    r, c = rows[owner], col[edges]
+    p = np.exp(scale * np.einsum("ij,ij->i", f64(q[r]), f64(k[c])) - m[owner]) / d[owner]
+    ds = p * (np.einsum("ij,ij->i", f64(g[r]), f64(v[c])) - t[owner])
+    dq = np.zeros((rows.size, q.shape[1]))
+    dq_mag = np.zeros_like(dq)
+    np.add.at(dq, owner, scale * ds[:, None] * f64(k[c]))
+    np.add.at(dq_mag, owner, np.abs(scale * ds[:, None] * f64(k[c])))
+    # the edges into the sampled columns and the softmax of every row they sit in
+    in_edges, in_owner = _edges_of(crow_t, cols)
+    e_ids, e_rows = perm[in_edges], col_t[in_edges]
+    involved, where = np.unique(e_rows, return_inverse=True)
+    m2, d2, t2 = _row_softmax_stats(crow, col, q, k, v, g, involved, scale)
+    cc = cols[in_owner]
+    p2 = np.exp(scale * np.einsum("ij,ij->i", f64(q[e_rows]), f64(k[cc])) - m2[where]) / d2[where]
+    ds2 = p2 * (np.einsum("ij,ij->i", f64(g[e_rows]), f64(v[cc])) - t2[where])
+    dk = np.zeros((cols.size, k.shape[1]))
+    dk_mag = np.zeros_like(dk)
+    dv = np.zeros((cols.size, v.shape[1]))
+    dv_mag = np.zeros_like(dv)
+    np.add.at(dk, in_owner, scale * ds2[:, None] * f64(q[e_rows]))
+    np.add.at(dk_mag, in_owner, np.abs(scale * ds2[:, None] * f64(q[e_rows])))
+    np.add.at(dv, in_owner, p2[:, None] * f64(g[e_rows]))
+    np.add.at(dv_mag, in_owner, np.abs(p2[:, None] * f64(g[e_rows])))
+    assert np.array_equal(col[e_ids], cc)
+    return (dq, dq_mag), (dk, dk_mag), (dv, dv_mag)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config5_attention_gradients_sampled(dtype):
+    """The attention backward at full size (cfg5: 2.45M rows, 124M edges), on
+    sampled rows (dQ) and columns (dK, dV), the longest ones included,
+    against fp64.  fp32: every sampled element within 1e-5·|want| + 1e-6, or,
+    where the sum nearly cancels, within 1e-5 of the sum of its terms'
+    magnitudes; bf16 (inputs, upstream gradient and gradients in bf16): within
+    a unit of the type's rounding plus 2e-5 of the largest element."""
+    from autosage_amd._autograd import csr_transpose
+
+    w = synth.config5(seed=0)
+    n = w.rows
+    scale = 0.125
+    rng = np.random.default_rng(55)
+    g32 = rng.standard_normal(w.dense["v"].shape).astype(np.float32)
+    d_crow, d_col = dev(w.crow), dev(w.col)
+    leaves = [dev(w.dense[name]).to(dtype).requires_grad_(True) for name in ("q", "k", "v")]
+    d_g = dev(g32).to(dtype)
+    op = torch.ops.autosage.csr_attention if dtype == torch.float32 else torch.ops.autosage.csr_attention_colslice
+    _step(f"cfg5 attention backward {dtype}")
+    op(d_crow, d_col, *leaves, scale).backward(d_g)
+    # the values the kernels saw (16-bit: converted exactly)
+    q, k, v = (t.detach().float().cpu().numpy() for t in leaves)
+    g = d_g.float().cpu().numpy()
+    deg = np.diff(w.crow)
+    rows = np.unique(np.concatenate([np.argsort(deg)[-8:], rng.choice(n, 1500, replace=False)]))
+    crow_t, col_t, perm = (t.cpu().numpy() for t in csr_transpose(d_crow, d_col))
+    in_deg = np.diff(crow_t)
+    cols = np.unique(np.concatenate([np.argsort(in_deg)[-4:], rng.choice(n, 300, replace=False)]))
+    _step(f"cfg5 fp64 gradients of {rows.size} rows and {cols.size} columns")
+    wants = _attention_grad_samples(w.crow, w.col, crow_t, col_t, perm, q, k, v, g, rows, cols, scale)
+    picks = (rows, cols, cols)
+    for name, leaf, (want, mag), pick in zip("QKV", leaves, wants, picks):
+        got = leaf.grad[torch.from_numpy(pick).cuda()].double().cpu().numpy()
+        err = np.abs(got - want)
+        if dtype == torch.float32:
+            plain = err <= RTOL * np.abs(want) + ATOL
+            bound = err <= RTOL * mag + ATOL
+            print(f"[parity] cfg5 d{name} fp32: {got.size} sampled elements, {int(plain.sum())} within "
+                  f"1e-5·|want| + 1e-6, all within 1e-5·sum|terms| + 1e-6: {bool(bound.all())}, worst "
+                  f"err / (1e-5·|want| + 1e-6) = {float(np.max(err / (RTOL * np.abs(want) + ATOL))):.3f}, worst "
+                  f"err / (1e-5·sum|terms| + 1e-6) = {float(np.max(err / (RTOL * mag + ATOL))):.3f}", flush=True)
+            assert bound.all(), (name, float(np.max(err - RTOL * mag - ATOL)))
+        else:
+            bar = 2.0 ** -8 * np.abs(want) + 2e-5 * np.max(np.abs(want))
+            print(f"[parity] cfg5 d{name} bf16: {got.size} sampled elements, worst err / bar = "
+                  f"{float(np.max(err / bar)):.3f}", flush=True)
+            assert np.all(err <= bar), (name, float(np.max(err - bar)))
