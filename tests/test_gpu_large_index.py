@@ -1,5 +1,6 @@
 """GPU parity on a graph of 2^24 + 1000 rows: the 64-bit address forms of the
-column-sliced and 16-bit kernels.
+column-sliced and 16-bit kernels (and, on 2^25 + 1000 rows, of the
+feature-sliced SpMM).
 
 Below 2^24 rows (and 4 GiB of features) the gather offsets of these kernels
 are 32-bit (``off32`` / ``OFF32``); this graph is past that limit, so the
@@ -119,3 +120,47 @@ def test_rounded_sddmm_past_32_bit_offsets(graph, dtype):
         got = torch.ops.autosage.sddmm_csr_split(d_crow, d_col, q, k, waves, threshold).cpu()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (waves, threshold)
     del q, k
+
+
+N_WIDE = (1 << 25) + 1000
+
+
+def test_fslice_past_32_bit_offsets():
+    """The feature-sliced SpMM on 2^25 + 1000 rows: the slice-major copy of X
+    is then past 4 GiB (2^25 columns of 128 bytes per slice), so the kernel
+    takes its 64-bit gather offsets.  1,000 rows hold edges (up to 2,500,
+    columns over the whole range, above 2^25 included); exact values, so the
+    rows with edges equal the sequential oracle on the compacted sub-graph bit
+    for bit, weighted and not, and the other rows stay zero."""
+    from autosage_amd import _native
+
+    rng = np.random.default_rng(99)
+    rows = np.sort(rng.choice(N_WIDE, size=1000, replace=False))
+    deg = np.concatenate([rng.integers(1, 64, 700), rng.integers(64, 1024, 250), rng.integers(1024, 2500, 50)])
+    rng.shuffle(deg)
+    counts = np.zeros(N_WIDE, dtype=np.int64)
+    counts[rows] = deg
+    crow = np.zeros(N_WIDE + 1, dtype=np.int64)
+    np.cumsum(counts, out=crow[1:])
+    col = np.concatenate([np.sort(rng.choice(N_WIDE, size=d, replace=False)) for d in deg]).astype(np.int64)
+    assert col.max() >= (1 << 25)
+    val = rng.integers(-16, 17, col.size).astype(np.float32) / 8.0
+    uniq, inv = np.unique(col, return_inverse=True)
+    sub_crow = np.concatenate([[0], np.cumsum(counts[rows])]).astype(np.int64)
+    features = 32
+    lib = _native.library()
+    assert lib.as_spmm_fslice_workspace_bytes(N_WIDE, features) > 0xFFFFFFFF
+    d_crow, d_col, d_val = (torch.from_numpy(a).cuda() for a in (crow, col, val))
+    del counts, crow
+    x = _device_values(N_WIDE, features, torch.float32)
+    x_sub = _values(uniq, features)
+    d_rows = torch.from_numpy(rows).cuda()
+    empty = torch.from_numpy(np.setdiff1d(rng.integers(0, N_WIDE, 1000), rows)).cuda()
+    for weights, h_val in ((d_val, val), (None, None)):
+        y = torch.ops.autosage.spmm_csr_fslice(d_crow, d_col, weights, x)
+        want = oracle.spmm_seq(sub_crow, inv.astype(np.int64), h_val, x_sub)
+        got = y.index_select(0, d_rows).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), weights is None
+        assert torch.count_nonzero(y.index_select(0, empty)).item() == 0
+        del y
+    del x
