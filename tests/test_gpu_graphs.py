@@ -28,17 +28,22 @@ def test_native_ops_replay_in_a_hip_graph():
     x = rng.standard_normal((6000, 128)).astype(np.float32)
     q = rng.standard_normal((6000, 64)).astype(np.float32)
     k = rng.standard_normal((6000, 64)).astype(np.float32)
-    d_crow, d_col, d_x, d_q, d_k = to_dev(crow, col, x, q, k)
+    w = rng.standard_normal(col.size).astype(np.float32)
+    d_crow, d_col, d_x, d_q, d_k, d_w = to_dev(crow, col, x, q, k, w)
     ops = torch.ops.autosage
     calls = [
         lambda: ops.spmm_csr(d_crow, d_col, None, d_x),
         lambda: ops.spmm_csr_split(d_crow, d_col, None, d_x, 128, 2, 1024),
+        # the feature-sliced SpMM: relayout of X and product on the graph's
+        # plan (built by the eager call), weighted and not
+        lambda: ops.spmm_csr_fslice(d_crow, d_col, None, d_x),
+        lambda: ops.spmm_csr_fslice(d_crow, d_col, d_w, d_x),
         lambda: ops.spmm_csr_colslice(d_crow, d_col, None, d_x),
         lambda: ops.sddmm_csr_split(d_crow, d_col, d_q, d_k, 4, 1024),
         lambda: ops.csr_attention(d_crow, d_col, d_q, d_k, d_x, 0.125),
         lambda: ops.csr_attention_colslice(d_crow, d_col, d_q, d_k, d_x, 0.125),
     ]
-    _replay_matches_eager(calls, lambda: (d_x.mul_(2.0), d_q.mul_(0.5)))
+    _replay_matches_eager(calls, lambda: (d_x.mul_(2.0), d_q.mul_(0.5), d_w.mul_(-1.5)))
 
 
 def test_16_bit_ops_replay_in_a_hip_graph():
