@@ -29,7 +29,7 @@ from . import _env
 from ._memo import GraphMemo
 
 LIBRARY_NAME = "libautosage_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 HUB_EXACT = 0
 HUB_SPLIT64 = 1
 # 16-bit feature types of as_spmm_csr_rounded_16 (AS_DTYPE_BF16 / AS_DTYPE_F16)
@@ -52,12 +52,12 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_i64, _c_int, _c_int,
          _c_ptr, _c_size, _c_ptr],
     ),
-    "as_spmm_fslice_plan_bytes": (_c_size, [_c_i64, _c_i64]),
+    "as_spmm_fslice_plan_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "as_spmm_fslice_plan_workspace_bytes": (_c_size, [_c_i64]),
     "as_spmm_fslice_plan": (
         _c_int,
-        [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr, _c_size, ctypes.POINTER(ctypes.c_int64),
-         _c_ptr],
+        [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size, _c_ptr, _c_size,
+         ctypes.POINTER(ctypes.c_int64), _c_ptr],
     ),
     "as_spmm_fslice_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "as_spmm_csr_fslice_f32": (
@@ -387,23 +387,58 @@ FSLICE_FLAG_BAD_COLUMN = 1
 FSLICE_FLAG_LONG_ROW = 2
 
 
-def fslice_plan(crow: torch.Tensor, col: torch.Tensor, n_cols: int) -> tuple[torch.Tensor, int]:
+# Column phases of the feature-sliced SpMM (the same bits for any count):
+# two where one slice of X (n_cols x 128 bytes) is well beyond an XCD's 4 MB
+# L2, the rows are long enough to cut, and the columns ascend in every row
+# (otherwise a cut narrows no gather window).  On the 233k-row skewed graph
+# two phases take F = 128 from 3.15 to 2.82 ms; three or more cost more than
+# they save.  AUTOSAGE_FSLICE_PHASES = 1 .. 8 forces a count.
+FSLICE_MAX_PHASES = 8
+_FSLICE_PHASE_MIN_COLS = 1 << 16
+_FSLICE_PHASE_MIN_MEAN_DEGREE = 32
+
+
+def fslice_phases(crow: torch.Tensor, col: torch.Tensor, n_cols: int) -> int:
+    """The column-phase count the feature-sliced SpMM uses for this graph."""
+    forced = _env.get("AUTOSAGE_FSLICE_PHASES", "auto").strip().lower()
+    if forced != "auto":
+        try:
+            phases = int(forced)
+        except ValueError:
+            phases = 0
+        if not 1 <= phases <= FSLICE_MAX_PHASES:
+            raise ValueError(f"AUTOSAGE_FSLICE_PHASES must be auto or an integer in [1, {FSLICE_MAX_PHASES}]")
+        return phases
+    n = crow.numel() - 1
+    if n_cols < _FSLICE_PHASE_MIN_COLS or col.numel() < _FSLICE_PHASE_MIN_MEAN_DEGREE * max(n, 1):
+        return 1
+    if not columns_ascending(crow, col, None if n_cols == n else int(n_cols)):
+        return 1
+    return 2
+
+
+def fslice_plan(crow: torch.Tensor, col: torch.Tensor, n_cols: int,
+                phases: Optional[int] = None) -> tuple[torch.Tensor, int]:
     """(plan, tag) of the feature-sliced SpMM for this graph: the rows sorted
-    by degree and the columns as int32, built on the device once per live,
-    unmodified (crow, col) pair and column count, then reused whatever X, F
-    and the weights.  The build synchronises the stream once and raises on a
+    by degree, the columns as int32 and each column phase's row tasks, built
+    on the device once per live, unmodified (crow, col) pair, column count and
+    phase count (``fslice_phases`` when None), then reused whatever X, F and
+    the weights.  The build synchronises the stream once and raises on a
     column outside [0, n_cols) or a row of 2^31 or more edges."""
     lib = library()
+    if phases is None:
+        phases = fslice_phases(crow, col, n_cols)
 
     def compute() -> tuple[torch.Tensor, int]:
         n = crow.numel() - 1
         nnz = col.numel()
-        plan = _workspace(lib.as_spmm_fslice_plan_bytes(n, nnz), crow.device)
+        plan = _workspace(lib.as_spmm_fslice_plan_bytes(n, nnz, phases), crow.device)
         scratch = _workspace(lib.as_spmm_fslice_plan_workspace_bytes(n), crow.device)
         tag = ctypes.c_int64(0)
         with _on(crow.device):
-            status = lib.as_spmm_fslice_plan(_ptr(crow), _ptr(col), n, int(n_cols), nnz, _ptr(plan), plan.numel(),
-                                             _ptr(scratch), scratch.numel(), ctypes.byref(tag), _stream(crow.device))
+            status = lib.as_spmm_fslice_plan(_ptr(crow), _ptr(col), n, int(n_cols), nnz, int(phases), _ptr(plan),
+                                             plan.numel(), _ptr(scratch), scratch.numel(), ctypes.byref(tag),
+                                             _stream(crow.device))
             _raise(status, "autosage feature-sliced plan")
             flags = int(plan[:4].view(torch.int32).item())  # synchronises the stream
         del scratch
@@ -411,7 +446,7 @@ def fslice_plan(crow: torch.Tensor, col: torch.Tensor, n_cols: int) -> tuple[tor
         _check(not flags & FSLICE_FLAG_LONG_ROW, "rows of 2^31 or more edges are not supported")
         return plan, int(tag.value)
 
-    return _FSLICE_PLAN_MEMO.get((crow, col), int(n_cols), compute)
+    return _FSLICE_PLAN_MEMO.get((crow, col), (int(n_cols), int(phases)), compute)
 
 
 def _spmm_fslice(crow, col, val, x, n_rows: int) -> torch.Tensor:

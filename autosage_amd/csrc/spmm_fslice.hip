@@ -37,10 +37,26 @@
 // with per-edge index loads.  U = 40 edges in flight per lane (2 waves per
 // SIMD) beat 16-32 at 3-4 waves: long rows are latency chains.
 //
+// Column phases.  Each XCD still gathers from a window of N x 128 bytes
+// (29.8 MB on the 233k-row graph) against its 4 MB L2.  Where the columns of
+// every row ascend, the product can run as P launches: launch p takes every
+// row's edges whose column lies in the p-th of P equal column ranges, and
+// continues the row's fp32 chain from Y (launch 0 starts it from 0 and writes
+// every row).  A row's edges in range p follow those in range p - 1 in CSR
+// order, so each output is the same chain and the same bits; the gather
+// window is P times smaller.  Any split point gives the same bits (a row's
+// edges are cut into consecutive runs, summed in order); only the locality
+// depends on the columns ascending.  On the skewed graph, two phases take
+// F = 128 from 3.15 to 2.82 ms; more phases pay more than they gain (each
+// launch waits for its longest chains, and every (row, phase) pays its own
+// dependent start).
+//
 // Plan (per graph, X-independent): a header (int32 flags: bit 0 = a column
 // outside [0, n_cols), clamped to 0 so no access leaves X; bit 1 = a row of
-// 2^31 or more edges), the row order, and the columns as int32 padded with
-// kColPad zeros.
+// 2^31 or more edges), the row order, the columns as int32 padded with
+// kColPad zeros, and per phase one 16-byte task per position of the order
+// (row, the row's edge count in the phase, the phase's first edge), so that a
+// wave reaches its edges with one load.
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include "as_device.h"
@@ -64,25 +80,39 @@ constexpr int kFsliceUnroll = 40;               // edges in flight per lane (a m
 constexpr int64_t kSuperblock = 4;
 constexpr int64_t kColPad = 64;
 constexpr int64_t kHeaderBytes = 256;
-constexpr int64_t kFslicePlanTag = (int64_t(3) << 48) | 1;
+constexpr int64_t kFslicePlanTag = (int64_t(3) << 48) | 1;  // | phases << 8
+constexpr int kMaxPhases = 8;
 enum : int32_t { kFlagBadColumn = 1, kFlagLongRow = 2 };
 
 struct FslicePlan {
   int32_t* flags;
   int32_t* order;
   int32_t* col;
+  int4* tasks;  // [phases][n]: row, edge count in the phase, first edge (low, high words)
 };
 
 size_t fslice_order_bytes(int64_t n) { return align_up(static_cast<size_t>(n > 0 ? n : 1) * sizeof(int32_t), 256); }
 size_t fslice_col_bytes(int64_t nnz) { return align_up(static_cast<size_t>(nnz + kColPad) * sizeof(int32_t), 256); }
-size_t fslice_plan_bytes(int64_t n, int64_t nnz) {
-  return kHeaderBytes + fslice_order_bytes(n) + fslice_col_bytes(nnz);
+size_t fslice_task_bytes(int64_t n, int phases) {
+  return align_up(static_cast<size_t>(n > 0 ? n : 1) * static_cast<size_t>(phases) * sizeof(int4), 256);
+}
+size_t fslice_plan_bytes(int64_t n, int64_t nnz, int phases) {
+  return kHeaderBytes + fslice_order_bytes(n) + fslice_col_bytes(nnz) + fslice_task_bytes(n, phases);
 }
 
-FslicePlan fslice_plan_view(void* base, int64_t n) {
+FslicePlan fslice_plan_view(void* base, int64_t n, int64_t nnz) {
   char* p = static_cast<char*>(base);
   return FslicePlan{reinterpret_cast<int32_t*>(p), reinterpret_cast<int32_t*>(p + kHeaderBytes),
-                    reinterpret_cast<int32_t*>(p + kHeaderBytes + fslice_order_bytes(n))};
+                    reinterpret_cast<int32_t*>(p + kHeaderBytes + fslice_order_bytes(n)),
+                    reinterpret_cast<int4*>(p + kHeaderBytes + fslice_order_bytes(n) + fslice_col_bytes(nnz))};
+}
+
+int64_t fslice_tag(int phases) { return kFslicePlanTag | (static_cast<int64_t>(phases) << 8); }
+// The phase count of a feature-sliced plan tag, or 0 if it is not one.
+int fslice_tag_phases(int64_t tag) {
+  const int phases = static_cast<int>((tag >> 8) & 0xff);
+  if (phases < 1 || phases > kMaxPhases || tag != fslice_tag(phases)) return 0;
+  return phases;
 }
 
 // Slices of F features, and the slice count the XCDs are folded onto: a
@@ -136,6 +166,41 @@ __global__ __launch_bounds__(kBlock) void fslice_columns_kernel(const int64_t* _
   if (bad) atomicOr(flags, kFlagBadColumn);
 }
 
+// The tasks of position i of the order: the row's edges cut at the first
+// column >= p * n_cols / phases (a lower bound over the row's columns; for
+// columns that do not ascend it is some cut, kept monotone, which changes
+// the locality and not the bits).
+__global__ __launch_bounds__(kBlock) void fslice_tasks_kernel(const int64_t* __restrict__ crow,
+                                                              const int64_t* __restrict__ col,
+                                                              const int32_t* __restrict__ order, int64_t n,
+                                                              int64_t n_cols, int phases, int4* __restrict__ tasks) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int32_t row = order[i];
+  const int64_t rs = crow[row];
+  const int64_t re = crow[row + 1];
+  const int64_t deg = re > rs ? re - rs : 0;
+  int64_t lo = 0;
+  for (int p = 0; p < phases; ++p) {
+    int64_t hi = deg;
+    if (p + 1 < phases) {
+      const int64_t bound = n_cols * (p + 1) / phases;
+      int64_t a = lo, b = deg;  // first edge in [lo, deg) with col >= bound
+      while (a < b) {
+        const int64_t m = a + (b - a) / 2;
+        if (col[rs + m] < bound) a = m + 1;
+        else b = m;
+      }
+      hi = a;
+    }
+    const int64_t first = rs + lo;
+    tasks[static_cast<int64_t>(p) * n + i] =
+        make_int4(row, static_cast<int>(hi - lo), static_cast<int>(static_cast<uint32_t>(first)),
+                  static_cast<int>(static_cast<uint64_t>(first) >> 32));
+    lo = hi;
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void fslice_flags_clear_kernel(int32_t* __restrict__ flags) {
   if (threadIdx.x == 0) flags[0] = 0;
 }
@@ -175,14 +240,17 @@ __device__ __forceinline__ int group_lane(int v) {
   return __builtin_amdgcn_ds_swizzle(v, 0x18 | (I << 5));
 }
 
+// One phase: `tasks` are that phase's; `chain` = 1 continues every row that
+// has edges in the phase from Y (phases after the first), 0 starts every row
+// from zero and writes it (the first phase, which also writes empty rows).
 template <bool HAS_VAL, bool WIDE>
-__global__ __launch_bounds__(kBlock) void fslice_spmm_kernel(const int64_t* __restrict__ crow,
+__global__ __launch_bounds__(kBlock) void fslice_spmm_kernel(const int4* __restrict__ tasks,
                                                              const int32_t* __restrict__ colp,
                                                              const float* __restrict__ val,
                                                              const float* __restrict__ xs, float* __restrict__ y,
-                                                             const int32_t* __restrict__ order, int64_t n,
-                                                             int64_t n_cols, int64_t F, int ns, int nsp,
-                                                             int64_t blocks, int64_t group_base, int yvec) {
+                                                             int64_t n, int64_t n_cols, int64_t F, int ns, int nsp,
+                                                             int64_t blocks, int64_t group_base, int yvec,
+                                                             int chain) {
   constexpr int U = kFsliceUnroll;
   constexpr int NG = U / 8;
   const int xcd = static_cast<int>(blockIdx.x & (kXcds - 1));
@@ -207,9 +275,10 @@ __global__ __launch_bounds__(kBlock) void fslice_spmm_kernel(const int64_t* __re
   int64_t rs = 0;
   int deg = 0;
   if (valid) {
-    row = order[idx];
-    rs = crow[row];
-    deg = static_cast<int>(crow[row + 1] - rs);
+    const int4 t = tasks[idx];
+    row = t.x;
+    deg = t.y;
+    rs = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(t.w)) << 32) | static_cast<uint32_t>(t.z));
   }
   int kmin = valid ? deg : 0x7fffffff;
   int kmax = deg;
@@ -231,6 +300,19 @@ __global__ __launch_bounds__(kBlock) void fslice_spmm_kernel(const int64_t* __re
   const int32_t* cp = colp + base;
   const float* vp = HAS_VAL ? val + base : nullptr;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int64_t f0 = static_cast<int64_t>(s) * kSliceWidth + j * 4;
+  // a row continued from an earlier phase: its chain so far is in Y
+  const bool resume = chain && valid && deg > 0 && f0 < F;
+  if (resume) {
+    if (yvec) {
+      const FVec<4> o = load_vec<4>(y + row * F + f0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = o.v[t];
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = f0 + t < F ? y[row * F + f0 + t] : 0.f;
+    }
+  }
   int cn[NG];
   float wn[NG];
 #pragma unroll
@@ -318,8 +400,7 @@ __global__ __launch_bounds__(kBlock) void fslice_spmm_kernel(const int64_t* __re
       }
     }
   }
-  if (valid) {
-    const int64_t f0 = static_cast<int64_t>(s) * kSliceWidth + j * 4;
+  if (valid && (!chain || deg > 0)) {
     if (yvec) {
       if (f0 < F) {
         FVec<4> o;
@@ -337,9 +418,8 @@ __global__ __launch_bounds__(kBlock) void fslice_spmm_kernel(const int64_t* __re
 }
 
 template <bool HAS_VAL, bool WIDE>
-void launch_fslice(const int64_t* crow, const int32_t* colp, const float* val, const float* xs, float* y,
-                   const int32_t* order, int64_t n, int64_t n_cols, int64_t f, int ns, int nsp, int yvec,
-                   hipStream_t s) {
+void launch_fslice(const int4* tasks, const int32_t* colp, const float* val, const float* xs, float* y, int64_t n,
+                   int64_t n_cols, int64_t f, int ns, int nsp, int yvec, int chain, hipStream_t s) {
   const int64_t blocks = (n + kRowsPerGroup - 1) / kRowsPerGroup;
   // nsp <= 8: q runs over the runs of every XCD of a slice (blocks past the
   // last one are whole workgroups of invalid rows, which store nothing)
@@ -351,7 +431,7 @@ void launch_fslice(const int64_t* crow, const int32_t* colp, const float* val, c
   for (int64_t g0 = 0; g0 < groups; g0 += kMaxGroups) {
     const int64_t ng = groups - g0 < kMaxGroups ? groups - g0 : kMaxGroups;
     hipLaunchKernelGGL((fslice_spmm_kernel<HAS_VAL, WIDE>), dim3(static_cast<unsigned>(ng * kXcds)), dim3(kBlock),
-                       0, s, crow, colp, val, xs, y, order, n, n_cols, f, ns, nsp, blocks, g0, yvec);
+                       0, s, tasks, colp, val, xs, y, n, n_cols, f, ns, nsp, blocks, g0, yvec, chain);
   }
 }
 
@@ -361,30 +441,34 @@ void launch_fslice(const int64_t* crow, const int32_t* colp, const float* val, c
 
 extern "C" {
 
-size_t as_spmm_fslice_plan_bytes(int64_t n, int64_t nnz) {
-  return as::fslice_plan_bytes(n < 0 ? 0 : n, nnz < 0 ? 0 : nnz);
+size_t as_spmm_fslice_plan_bytes(int64_t n, int64_t nnz, int64_t phases) {
+  if (phases < 1 || phases > as::kMaxPhases) return 0;
+  return as::fslice_plan_bytes(n < 0 ? 0 : n, nnz < 0 ? 0 : nnz, static_cast<int>(phases));
 }
 
 size_t as_spmm_fslice_plan_workspace_bytes(int64_t n) { return as::fslice_build_bytes(n < 0 ? 0 : n); }
 
-int as_spmm_fslice_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t n_cols, int64_t nnz, void* plan,
-                        size_t plan_bytes, void* workspace, size_t workspace_bytes, int64_t* plan_tag,
-                        void* stream) {
+int as_spmm_fslice_plan(const int64_t* crow, const int64_t* col, int64_t n, int64_t n_cols, int64_t nnz,
+                        int64_t phases, void* plan, size_t plan_bytes, void* workspace, size_t workspace_bytes,
+                        int64_t* plan_tag, void* stream) {
   as::clear_error();
+  if (phases < 1 || phases > as::kMaxPhases)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "phases must be in [1, %d]", as::kMaxPhases);
+  const int ph = static_cast<int>(phases);
   if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
   if (n_cols < 0 || n_cols > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "n_cols exceeds kernel index range");
   if (nnz < 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "nnz must be non-negative");
   if (plan_tag == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "plan_tag must not be NULL");
-  if (plan == nullptr || plan_bytes < as::fslice_plan_bytes(n, nnz))
-    return as::fail(AS_ERR_WORKSPACE, "feature-sliced plan needs %zu bytes, got %zu", as::fslice_plan_bytes(n, nnz),
-                    plan == nullptr ? size_t(0) : plan_bytes);
+  if (plan == nullptr || plan_bytes < as::fslice_plan_bytes(n, nnz, ph))
+    return as::fail(AS_ERR_WORKSPACE, "feature-sliced plan needs %zu bytes, got %zu",
+                    as::fslice_plan_bytes(n, nnz, ph), plan == nullptr ? size_t(0) : plan_bytes);
   if (workspace == nullptr || workspace_bytes < as::fslice_build_bytes(n))
     return as::fail(AS_ERR_WORKSPACE, "feature-sliced plan build needs %zu workspace bytes, got %zu",
                     as::fslice_build_bytes(n), workspace == nullptr ? size_t(0) : workspace_bytes);
   if (n > 0 && crow == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "null crow pointer");
   if (nnz > 0 && col == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "null col pointer");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const as::FslicePlan p = as::fslice_plan_view(plan, n);
+  const as::FslicePlan p = as::fslice_plan_view(plan, n, nnz);
   hipLaunchKernelGGL(as::fslice_flags_clear_kernel, dim3(1), dim3(64), 0, s, p.flags);
   if (n > 0) {
     const size_t rows = as::align_up(static_cast<size_t>(n) * sizeof(uint32_t), 256);
@@ -400,13 +484,15 @@ int as_spmm_fslice_plan(const int64_t* crow, const int64_t* col, int64_t n, int6
     const hipError_t e = rocprim::radix_sort_pairs_desc(temp, temp_bytes, keys_in, keys_out, rows_in, p.order,
                                                         static_cast<unsigned>(n), 0, 32, s);
     if (e != hipSuccess) return as::fail(AS_ERR_LAUNCH, "feature-sliced plan: degree sort failed: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(as::fslice_tasks_kernel, dim3(static_cast<unsigned>((n + as::kBlock - 1) / as::kBlock)),
+                       dim3(as::kBlock), 0, s, crow, col, p.order, n, n_cols, ph, p.tasks);
   }
   const int64_t total = nnz + as::kColPad;
   int64_t blocks = (total + as::kBlock - 1) / as::kBlock;
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(as::fslice_columns_kernel, dim3(static_cast<unsigned>(blocks)), dim3(as::kBlock), 0, s, col,
                      nnz, n_cols, p.col, p.flags);
-  *plan_tag = as::kFslicePlanTag;
+  *plan_tag = as::fslice_tag(ph);
   return as::check_launch("spmm_fslice_plan");
 }
 
@@ -451,13 +537,14 @@ int as_spmm_csr_fslice_sliced_f32(const int64_t* crow, const float* val, const v
   if (n == 0 || f == 0) return AS_OK;
   if (crow == nullptr || y == nullptr) return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (nnz > 0 && n_cols == 0) return as::fail(AS_ERR_INVALID_ARGUMENT, "edges into an empty column space");
-  if (plan_tag != as::kFslicePlanTag)
-    return as::fail(AS_ERR_INVALID_ARGUMENT, "plan tag %lld is not a feature-sliced plan (%lld)",
-                    static_cast<long long>(plan_tag), static_cast<long long>(as::kFslicePlanTag));
-  if (plan == nullptr || plan_bytes < as::fslice_plan_bytes(n, nnz))
-    return as::fail(AS_ERR_INVALID_ARGUMENT, "feature-sliced plan of %zu bytes is too small for %lld rows and %lld "
-                    "edges (%zu)", plan == nullptr ? size_t(0) : plan_bytes, static_cast<long long>(n),
-                    static_cast<long long>(nnz), as::fslice_plan_bytes(n, nnz));
+  const int phases = as::fslice_tag_phases(plan_tag);
+  if (phases == 0)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "plan tag %lld is not a feature-sliced plan",
+                    static_cast<long long>(plan_tag));
+  if (plan == nullptr || plan_bytes < as::fslice_plan_bytes(n, nnz, phases))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "feature-sliced plan of %zu bytes is too small for %lld rows, %lld "
+                    "edges and %d phases (%zu)", plan == nullptr ? size_t(0) : plan_bytes, static_cast<long long>(n),
+                    static_cast<long long>(nnz), phases, as::fslice_plan_bytes(n, nnz, phases));
   const size_t need = as_spmm_fslice_workspace_bytes(n_cols, f);
   if (xs == nullptr || xs_bytes < need)
     return as::fail(AS_ERR_WORKSPACE, "feature-sliced SpMM needs %zu workspace bytes, got %zu", need,
@@ -466,18 +553,23 @@ int as_spmm_csr_fslice_sliced_f32(const int64_t* crow, const float* val, const v
   // entry 0 of the padded columns, and would read val[0], which may not exist)
   if (nnz == 0) val = nullptr;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const as::FslicePlan p = as::fslice_plan_view(const_cast<void*>(plan), n);
+  const as::FslicePlan p = as::fslice_plan_view(const_cast<void*>(plan), n, nnz);
   const int ns = as::fslice_count(f);
   const int nsp = as::fslice_padded(ns);
   const float* xsf = static_cast<const float*>(xs);
   const int yvec = f % 4 == 0 && as::aligned(y, 16);
   const bool wide = static_cast<uint64_t>(n_cols) * as::kSliceWidth * sizeof(float) > 0xffffffffull;
-  if (val != nullptr) {
-    if (wide) as::launch_fslice<true, true>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
-    else as::launch_fslice<true, false>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
-  } else {
-    if (wide) as::launch_fslice<false, true>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
-    else as::launch_fslice<false, false>(crow, p.col, val, xsf, y, p.order, n, n_cols, f, ns, nsp, yvec, s);
+  // one launch per phase, in order: phase q continues the chains phase q - 1 left in Y
+  for (int q = 0; q < phases; ++q) {
+    const int4* t = p.tasks + static_cast<int64_t>(q) * n;
+    const int chain = q > 0;
+    if (val != nullptr) {
+      if (wide) as::launch_fslice<true, true>(t, p.col, val, xsf, y, n, n_cols, f, ns, nsp, yvec, chain, s);
+      else as::launch_fslice<true, false>(t, p.col, val, xsf, y, n, n_cols, f, ns, nsp, yvec, chain, s);
+    } else {
+      if (wide) as::launch_fslice<false, true>(t, p.col, val, xsf, y, n, n_cols, f, ns, nsp, yvec, chain, s);
+      else as::launch_fslice<false, false>(t, p.col, val, xsf, y, n, n_cols, f, ns, nsp, yvec, chain, s);
+    }
   }
   return as::check_launch("spmm_csr_fslice");
 }
@@ -490,13 +582,14 @@ int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val, const float* x
     return as::fail(AS_ERR_INVALID_ARGUMENT, "null pointer argument");
   // the checks of the sliced call first, so that no launch happens on bad arguments
   if (n < 0 || n > INT32_MAX) return as::fail(AS_ERR_INVALID_ARGUMENT, "N exceeds kernel index range");
-  if (n > 0 && f > 0 && plan_tag != as::kFslicePlanTag)
-    return as::fail(AS_ERR_INVALID_ARGUMENT, "plan tag %lld is not a feature-sliced plan (%lld)",
-                    static_cast<long long>(plan_tag), static_cast<long long>(as::kFslicePlanTag));
-  if (n > 0 && f > 0 && nnz >= 0 && (plan == nullptr || plan_bytes < as::fslice_plan_bytes(n, nnz)))
-    return as::fail(AS_ERR_INVALID_ARGUMENT, "feature-sliced plan of %zu bytes is too small for %lld rows and %lld "
-                    "edges (%zu)", plan == nullptr ? size_t(0) : plan_bytes, static_cast<long long>(n),
-                    static_cast<long long>(nnz), as::fslice_plan_bytes(n, nnz));
+  const int phases = as::fslice_tag_phases(plan_tag);
+  if (n > 0 && f > 0 && phases == 0)
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "plan tag %lld is not a feature-sliced plan",
+                    static_cast<long long>(plan_tag));
+  if (n > 0 && f > 0 && nnz >= 0 && (plan == nullptr || plan_bytes < as::fslice_plan_bytes(n, nnz, phases)))
+    return as::fail(AS_ERR_INVALID_ARGUMENT, "feature-sliced plan of %zu bytes is too small for %lld rows, %lld "
+                    "edges and %d phases (%zu)", plan == nullptr ? size_t(0) : plan_bytes, static_cast<long long>(n),
+                    static_cast<long long>(nnz), phases, as::fslice_plan_bytes(n, nnz, phases));
   if (n > 0 && f > 0 && nnz > 0) {
     const int st = as_spmm_fslice_relayout_f32(x, n_cols, f, workspace, workspace_bytes, stream);
     if (st != AS_OK) return st;

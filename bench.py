@@ -982,15 +982,17 @@ def fslice_kernel_times(crow, col, val, x, launches: int) -> dict:
 
 def fslice_plan_record(args, crow, col, val, x) -> dict:
     """What the feature-sliced SpMM keeps per graph: its plan (rows sorted by
-    degree, int32 columns) is built once per graph and reused by every call.
-    Records the build time (median of 5 after a warmup, HIP events on the
-    launch stream) and the step time with the plan rebuilt in every call."""
+    degree, int32 columns, each column phase's row tasks) is built once per
+    graph and reused by every call.  Records the phase count, the build time
+    (median of 5 after a warmup, HIP events on the launch stream) and the step
+    time with the plan rebuilt in every call."""
     from autosage_amd import _native
 
     lib = _native.library()
     n, f, nnz = crow.numel() - 1, x.size(1), col.numel()
     n_cols = x.size(0)
-    plan = torch.empty(lib.as_spmm_fslice_plan_bytes(n, nnz), dtype=torch.uint8, device=crow.device)
+    phases = _native.fslice_phases(crow, col, n_cols)
+    plan = torch.empty(lib.as_spmm_fslice_plan_bytes(n, nnz, phases), dtype=torch.uint8, device=crow.device)
     scratch = torch.empty(lib.as_spmm_fslice_plan_workspace_bytes(n), dtype=torch.uint8, device=crow.device)
     xs = torch.empty(lib.as_spmm_fslice_workspace_bytes(n_cols, f), dtype=torch.uint8, device=crow.device)
     y = torch.empty(n, f, dtype=x.dtype, device=x.device)
@@ -999,7 +1001,7 @@ def fslice_plan_record(args, crow, col, val, x) -> dict:
     vptr = None if val is None else val.data_ptr()
 
     def build():
-        status = lib.as_spmm_fslice_plan(crow.data_ptr(), col.data_ptr(), n, n_cols, nnz, plan.data_ptr(),
+        status = lib.as_spmm_fslice_plan(crow.data_ptr(), col.data_ptr(), n, n_cols, nnz, phases, plan.data_ptr(),
                                          plan.numel(), scratch.data_ptr(), scratch.numel(), ctypes.byref(tag), stream)
         if status != 0:
             raise RuntimeError(lib.as_last_error().decode())
@@ -1021,11 +1023,12 @@ def fslice_plan_record(args, crow, col, val, x) -> dict:
         end.synchronize()
         times.append(start.elapsed_time(end))
     rebuilding, _ = time_steps(rebuilt_step, max(5, args.steps // 2), 2)
-    return {"reused": True, "build_ms": round(statistics.median(times[1:]), 4),
+    return {"reused": True, "phases": phases, "build_ms": round(statistics.median(times[1:]), 4),
             "plan_bytes": plan.numel(), "ms_per_step_rebuilding_it": round(rebuilding, 4),
-            "note": "the rows sorted by degree (rocPRIM radix sort) and the columns as int32 are built once per "
-                    "graph (as_spmm_fslice_plan) and reused by every call, whatever X and the weights; "
-                    "ms_per_step_rebuilding_it times the C entry with the plan rebuilt before every call"}
+            "note": "the rows sorted by degree (rocPRIM radix sort), the columns as int32 and each column phase's "
+                    "row tasks are built once per graph (as_spmm_fslice_plan) and reused by every call, whatever X "
+                    "and the weights; a call runs one product launch per phase; ms_per_step_rebuilding_it times the "
+                    "C entry with the plan rebuilt before every call"}
 
 
 def bench_hubsweep(args, device) -> dict:

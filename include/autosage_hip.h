@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AS_ABI_VERSION 8
+#define AS_ABI_VERSION 9
 
 typedef enum as_status {
   AS_OK = 0,
@@ -116,8 +116,14 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col,
  * (n_cols = N for a square graph; x has n_cols rows, y has n rows).
  *
  * Plan: built once per graph (crow, col unmodified since), any X, F and
- * weights.  Holds the rows sorted by degree (longest first, stable) and
- * the columns as int32.  int32 flags at byte 0 of the plan: bit 0 = a column
+ * weights.  Holds the rows sorted by degree (longest first, stable), the
+ * columns as int32, and for each of `phases` (1 to 8) column phases one
+ * 16-byte task per row: the row's edges whose column lies in the phase's
+ * equal share of [0, n_cols) (found by a lower bound over the row's
+ * columns).  The product runs one launch per phase, each continuing the
+ * rows' fp32 chains in Y, so every phase count gives the same bits; with
+ * columns ascending in every row each launch gathers from a 1/phases window
+ * of X (for other column orders the cut is arbitrary, the bits the same).  int32 flags at byte 0 of the plan: bit 0 = a column
  * outside [0, n_cols) (its edges read row 0 of X instead), bit 1 = a row of
  * 2^31 or more edges; a plan with flags set gives wrong results and should
  * be refused by the caller.  The build needs a scratch workspace of
@@ -125,11 +131,11 @@ int as_spmm_csr_split_f32(const int64_t* crow, const int64_t* col,
  * on the stream); *plan_tag receives the value the SpMM call checks.  No
  * reference counterpart: the reference bins rows on every call
  * (csrc/launcher_spmm.cu:49-59). */
-size_t as_spmm_fslice_plan_bytes(int64_t n, int64_t nnz);
+size_t as_spmm_fslice_plan_bytes(int64_t n, int64_t nnz, int64_t phases);
 size_t as_spmm_fslice_plan_workspace_bytes(int64_t n);
 int as_spmm_fslice_plan(const int64_t* crow, const int64_t* col, int64_t n,
-                        int64_t n_cols, int64_t nnz, void* plan,
-                        size_t plan_bytes, void* workspace,
+                        int64_t n_cols, int64_t nnz, int64_t phases,
+                        void* plan, size_t plan_bytes, void* workspace,
                         size_t workspace_bytes, int64_t* plan_tag,
                         void* stream);
 
@@ -139,8 +145,8 @@ size_t as_spmm_fslice_workspace_bytes(int64_t n_cols, int64_t f);
 
 /* Y = A·X with the plan of as_spmm_fslice_plan; val may be NULL.  Any F and
  * alignment (float4 lanes when F % 4 == 0 and x, y are 16-byte aligned).
- * A wrong plan_tag or a plan smaller than as_spmm_fslice_plan_bytes(n, nnz)
- * returns AS_ERR_INVALID_ARGUMENT; a plan of another graph is not detected
+ * A wrong plan_tag (it carries the phase count) or a plan smaller than
+ * as_spmm_fslice_plan_bytes(n, nnz, phases) returns AS_ERR_INVALID_ARGUMENT; a plan of another graph is not detected
  * (the caller keys plans by graph). */
 int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val,
                            const float* x, float* y, int64_t n, int64_t n_cols,

@@ -219,10 +219,21 @@ def test_fslice_c_abi_checks():
     # the plan builder refuses short buffers before launching anything
     tag_out = ctypes.c_int64(0)
     scratch = torch.empty(lib.as_spmm_fslice_plan_workspace_bytes(n), dtype=torch.uint8, device="cuda")
-    status = lib.as_spmm_fslice_plan(d_crow.data_ptr(), d_col.data_ptr(), n, n, col.size, plan.data_ptr(),
+    status = lib.as_spmm_fslice_plan(d_crow.data_ptr(), d_col.data_ptr(), n, n, col.size, 1, plan.data_ptr(),
                                      plan.numel() - 1, scratch.data_ptr(), scratch.numel(), ctypes.byref(tag_out),
                                      stream)
     assert status == 4 and tag_out.value == 0
+    for phases in (0, 9):
+        status = lib.as_spmm_fslice_plan(d_crow.data_ptr(), d_col.data_ptr(), n, n, col.size, phases,
+                                         plan.data_ptr(), plan.numel(), scratch.data_ptr(), scratch.numel(),
+                                         ctypes.byref(tag_out), stream)
+        assert status == 1 and b"phases must be in [1, 8]" in lib.as_last_error()
+    assert lib.as_spmm_fslice_plan_bytes(n, col.size, 0) == 0
+    # the tag carries the phase count: a one-phase plan under a two-phase tag is too small
+    plan_bytes_2 = lib.as_spmm_fslice_plan_bytes(n, col.size, 2)
+    assert plan_bytes_2 > lib.as_spmm_fslice_plan_bytes(n, col.size, 1)
+    two_phase_tag = (tag & ~(0xFF << 8)) | (2 << 8)
+    assert call(plan_tag=two_phase_tag) == 1 and b"too small" in lib.as_last_error()
 
 
 def _timed(info) -> dict:
@@ -300,3 +311,77 @@ def test_fslice_gradients_equal_the_exact_schedules():
         grads.append((y.detach(), d_val.grad, d_x.grad))
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+def _shuffled_within_rows(crow, col, seed):
+    rng = np.random.default_rng(seed)
+    out = col.copy()
+    for r in range(crow.size - 1):
+        seg = out[crow[r]:crow[r + 1]]
+        rng.shuffle(seg)
+    return out
+
+
+@pytest.mark.parametrize("phases", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("ascending", [True, False])
+def test_fslice_column_phases_keep_the_bits(phases, ascending, monkeypatch):
+    """Every phase count gives the sequential product's bits: a row's edges
+    are cut into consecutive runs (at the phase's column bound when the
+    columns ascend, at some point when they do not) and each launch continues
+    the row's fp32 chain from Y.  Weighted and not, F = 96 (three slices, a
+    chain read back through the float4 path) and F = 33 (a partial slice, the
+    element path), hub rows, empty rows."""
+    monkeypatch.setenv("AUTOSAGE_FSLICE_PHASES", str(phases))
+    for features, weighted in ((96, True), (33, False)):
+        crow, col, val, x = _inputs(features, weighted, seed=40 + phases, rows=2500, degree=14, hubs=4,
+                                    hub_degree=2200, empty=0.1)
+        if not ascending:
+            col = _shuffled_within_rows(crow, col, seed=phases)
+        d_crow, d_col, d_val, d_x = to_dev(crow, col, val, x)
+        assert _native.fslice_phases(d_crow, d_col, crow.size - 1) == phases
+        got = torch.ops.autosage.spmm_csr_fslice(d_crow, d_col, d_val, d_x)
+        want = oracle.spmm_seq(crow, col, val, x)
+        assert bitwise_equal(got, want), (features, weighted, mismatch_report(got, want))
+
+
+def test_fslice_phase_tasks_cut_rows_at_the_column_bounds():
+    """The plan's tasks: for position i of the order and phase p, the row's
+    edges [first, first + count) are exactly those with a column in
+    [p·N/P, (p+1)·N/P) when the columns ascend, and the phases of a row tile
+    its edges in order."""
+    crow, col, _, _ = _inputs(32, False, seed=61, rows=3000, degree=20, hubs=2, hub_degree=2900, empty=0.1)
+    d_crow, d_col = to_dev(crow, col)
+    n, nnz, phases = crow.size - 1, col.size, 3
+    plan, tag = _native.fslice_plan(d_crow, d_col, n, phases=phases)
+    assert (tag >> 8) & 0xFF == phases
+    align = lambda b: (b + 255) // 256 * 256
+    start = 256 + align(4 * n) + align(4 * (nnz + 64))
+    tasks = plan[start:start + 16 * n * phases].view(torch.int32).view(phases, n, 4).cpu().numpy().astype(np.int64)
+    order = plan[256:256 + 4 * n].view(torch.int32).cpu().numpy()
+    for i in range(0, n, 7):
+        row = order[i]
+        edge = crow[row]
+        for p in range(phases):
+            r, count, lo, hi = tasks[p, i]
+            first = lo & 0xFFFFFFFF | (hi << 32)
+            assert r == row and first == edge, (i, p)
+            cols = col[first:first + count]
+            assert np.all(cols >= p * n // phases) and np.all(cols < (p + 1) * n // phases), (i, p)
+            edge += count
+        assert edge == crow[row + 1]
+
+
+def test_fslice_phase_rule():
+    """Two phases where a slice of X is well beyond an XCD's L2 (at least
+    65,536 columns), rows average at least 32 edges and the columns ascend;
+    one otherwise."""
+    n, degree = 70_000, 40
+    crow, col = case_graph(n, degree, seed=3)
+    d_crow, d_col = to_dev(crow, col)
+    assert _native.fslice_phases(d_crow, d_col, n) == 2
+    d_shuffled = to_dev(_shuffled_within_rows(crow, col, seed=1))[0]
+    assert _native.fslice_phases(d_crow, d_shuffled, n) == 1
+    small_crow, small_col = case_graph(5000, degree, seed=4)
+    assert _native.fslice_phases(*to_dev(small_crow, small_col), 5000) == 1
+    sparse_crow, sparse_col = case_graph(n, 8, seed=5)
+    assert _native.fslice_phases(*to_dev(sparse_crow, sparse_col), n) == 1
