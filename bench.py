@@ -933,8 +933,9 @@ def all_cached_ceiling(variant: str, crow, col, val, x, args, ms: float) -> dict
 
 def fslice_kernel_times(crow, col, val, x, launches: int) -> dict:
     """The two kernels of the feature-sliced SpMM timed one by one in this
-    run: ``launches`` back-to-back launches of each, bracketed by HIP events
-    recorded on the stream the library launches on (torch's current stream),
+    run: ``launches`` back-to-back calls of each (a product call is one launch
+    per column phase), bracketed by HIP events recorded on the stream the
+    library launches on (torch's current stream),
     after two warmup launches."""
     from autosage_amd import _native
 
@@ -974,8 +975,11 @@ def fslice_kernel_times(crow, col, val, x, launches: int) -> dict:
     relayout()
     product_ms = per_launch(product)
     relayout_ms = per_launch(relayout)
-    return {"timing": f"HIP events on the launch stream around {launches} launches of the kernel alone, this run",
-            "dominant": {"name": "fslice_spmm_kernel", "ms": product_ms},
+    phases = (tag >> 8) & 0xFF
+    return {"timing": f"HIP events on the launch stream around {launches} calls of the product alone "
+                      f"({phases} launch{'es' if phases > 1 else ''} of the kernel per call, one per column phase), "
+                      f"this run",
+            "dominant": {"name": "fslice_spmm_kernel", "ms": product_ms, "launches_per_call": phases},
             "others": [{"name": "fslice_relayout_kernel", "ms": relayout_ms,
                         "bytes_per_launch": 2 * n_cols * ((f + 31) // 32) * 128}]}
 
