@@ -108,6 +108,33 @@ def test_config3_skewed_spmm(features, monkeypatch):
     assert counts["worst_reference_error_over_bar"] > 1.0 > 0.1 > counts["worst_kernel_error_over_bar"]
 
 
+def test_config3_backward_dx_is_the_sequential_transposed_product():
+    """cfg3 at F = 128 through autograd: dX = Aᵀ·dY runs on the feature-sliced
+    SpMM over the transposed graph (whose columns ascend, so it runs in two
+    column phases) and equals the sequential CPU product over Aᵀ on every
+    output, weighted (dval is not asked for) and not."""
+    from autosage_amd import _native
+    from autosage_amd._autograd import csr_transpose
+
+    w = synth.config3(seed=0, features=128)
+    n = w.rows
+    d_crow, d_col = dev(w.crow), dev(w.col)
+    rng = np.random.default_rng(21)
+    g = rng.standard_normal((n, 128)).astype(np.float32)
+    val = rng.standard_normal(w.nnz).astype(np.float32)
+    crow_t, col_t, perm = csr_transpose(d_crow, d_col)
+    assert _native.fslice_phases(crow_t, col_t, n) == 2
+    h_crow_t, h_col_t, h_perm = (t.cpu().numpy() for t in (crow_t, col_t, perm))
+    for weights in (None, val):
+        x = dev(w.dense["x"]).requires_grad_(True)
+        d_val = None if weights is None else dev(weights)
+        _step(f"cfg3 backward dX weighted={weights is not None}")
+        torch.ops.autosage.spmm_csr_fslice(d_crow, d_col, d_val, x).backward(dev(g))
+        want = oracle.spmm_seq(h_crow_t, h_col_t, None if weights is None else weights[h_perm], g)
+        assert bitwise_equal(x.grad, want), mismatch_report(x.grad, want)
+        del x
+
+
 def test_config3_shuffled_columns():
     """cfg3 at F = 128 with the columns of every row in a random order (what
     ``edge_index_to_csr`` gives for an edge list not sorted by source):
