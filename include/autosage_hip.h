@@ -146,7 +146,8 @@ size_t as_spmm_fslice_workspace_bytes(int64_t n_cols, int64_t f);
 /* Y = A·X with the plan of as_spmm_fslice_plan; val may be NULL.  Any F and
  * alignment (float4 lanes when F % 4 == 0 and x, y are 16-byte aligned).
  * A wrong plan_tag (it carries the phase count) or a plan smaller than
- * as_spmm_fslice_plan_bytes(n, nnz, phases) returns AS_ERR_INVALID_ARGUMENT; a plan of another graph is not detected
+ * as_spmm_fslice_plan_bytes(n, nnz, phases) returns AS_ERR_INVALID_ARGUMENT; a plan of
+ * another graph is not detected
  * (the caller keys plans by graph). */
 int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val,
                            const float* x, float* y, int64_t n, int64_t n_cols,
@@ -155,9 +156,9 @@ int as_spmm_csr_fslice_f32(const int64_t* crow, const float* val,
                            void* workspace, size_t workspace_bytes,
                            void* stream);
 
-/* The two launches of as_spmm_csr_fslice_f32 apart: the slice-major copy of
- * X into `xs` (as_spmm_fslice_workspace_bytes(n_cols, f) bytes), then the
- * product from it.  A caller that multiplies one X by several graphs, or
+/* The two steps of as_spmm_csr_fslice_f32 apart: the slice-major copy of X
+ * into `xs` (as_spmm_fslice_workspace_bytes(n_cols, f) bytes), then the
+ * product from it (one launch per column phase of the plan).  A caller that multiplies one X by several graphs, or
  * times the kernels one by one, copies X once.  Same checks and bits. */
 int as_spmm_fslice_relayout_f32(const float* x, int64_t n_cols, int64_t f,
                                 void* xs, size_t xs_bytes, void* stream);
