@@ -247,7 +247,7 @@ def host_description() -> dict:
 
 
 def _host_threads() -> int:
-    """All cores this process may run on (BASELINE.md section 3 plan)."""
+    """All cores this process may run on (the CPU baseline runs on every one)."""
     threads = max(1, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
     return threads
@@ -274,7 +274,7 @@ def cpu_baseline_spmm(crow: np.ndarray, col: np.ndarray, val, x: np.ndarray, wor
     (autosage/ops.py:124-143), on the FULL graph, timed on this host's cores.
     The CSR tensor is built outside the timed region; cfg3-sized graphs take
     1 warmup and the median of 5 calls, smaller ones 2 warmups and the
-    median of 15 (the BASELINE.md section 3 plan)."""
+    median of 15."""
     threads = _host_threads()
     n, f = x.shape
     nnz = int(crow[-1])
@@ -437,7 +437,7 @@ def main() -> int:
 
 
 # Published context for the reference's reproducible synthetic workloads
-# (1x A800): same graphs, other hardware.
+# (the reference's own results on 1x A800): same graphs, other hardware.
 PUBLISHED = {
     ("er", 64): {"baseline_ms": 1.5227, "autosage_ms": 0.3226,
                  "source": "artifacts/results/spmm/synth_er.csv:2-3 (1x A800-SXM4-40GB)"},
