@@ -1,8 +1,9 @@
 """Seeded random sweep over graph shapes, feature widths, weights and types,
 every op against its oracle at its own bar:
 
-* ``spmm_csr`` / ``spmm_csr_split`` (fp32): bit-identical to the sequential
-  CSR product (``oracle.spmm_seq``);
+* ``spmm_csr`` / ``spmm_csr_split`` / ``spmm_csr_fslice`` (fp32, the latter
+  in 1 to 4 column phases): bit-identical to the sequential CSR product
+  (``oracle.spmm_seq``);
 * ``spmm_csr_colslice`` (fp32, ascending columns): |gpu − fp64| ≤
   1e-6·|fp64| + 1e-9;
 * ``sddmm_csr`` / ``sddmm_csr_split`` (fp32): bit-identical to the reference
@@ -52,7 +53,7 @@ def _case(seed: int):
 
 
 @pytest.mark.parametrize("seed", range(CASES))
-def test_random_case(seed):
+def test_random_case(seed, monkeypatch):
     crow, col, val, x, q = _case(seed)
     d_crow, d_col, d_x, d_q = to_dev(crow, col, x, q)
     d_val = None if val is None else torch.from_numpy(val).cuda()
@@ -62,6 +63,9 @@ def test_random_case(seed):
     assert np.array_equal(torch.ops.autosage.spmm_csr(d_crow, d_col, d_val, d_x).cpu().numpy(), want), tag
     assert np.array_equal(torch.ops.autosage.spmm_csr_split(d_crow, d_col, d_val, d_x, 64, 2, 256).cpu().numpy(),
                           want), tag
+    monkeypatch.setenv("AUTOSAGE_FSLICE_PHASES", str(1 + seed % 4))
+    assert np.array_equal(torch.ops.autosage.spmm_csr_fslice(d_crow, d_col, d_val, d_x).cpu().numpy(), want), \
+        (tag, 1 + seed % 4)
     # column slices (the generator's columns ascend)
     exact = oracle.spmm_f64(crow, col, val, x)
     got = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, d_val, d_x).cpu().numpy().astype(np.float64)
