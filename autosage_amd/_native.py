@@ -103,7 +103,7 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size,
          _c_i64, _c_ptr, _c_size, _c_i64, _c_i64, _c_ptr],
     ),
-    "as_spmm_colslice_planned_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int, _c_i64]),
+    "as_spmm_colslice_planned_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_i64]),
     "as_spmm_colslice_row_blocks": (_c_i64, [_c_i64, _c_int, ctypes.POINTER(ctypes.c_int64), _c_i64]),
     "as_spmm_csr_colslice_planned": (
         _c_int,
@@ -595,8 +595,8 @@ def _spmm_colslice_planned(crow, col, val, x, y, column_slices: bool, sliced: in
     code = 0 if x.dtype == torch.float32 else DTYPES_16[x.dtype]
     lib = library()
     plan, tag = colslice_plan(crow, col, f, x.dtype, column_slices, n_cols)
-    needed = lib.as_spmm_colslice_planned_workspace_bytes(n, f, code, block_sliced_rows(crow, f, x.dtype,
-                                                                                        column_slices))
+    needed = lib.as_spmm_colslice_planned_workspace_bytes(n, col.numel(), f, code,
+                                                          block_sliced_rows(crow, f, x.dtype, column_slices))
     ws = _workspace(max(min(needed, _colslice_workspace_cap() - plan.numel()), 0), x.device)
     with _on(x.device):
         if n_cols is None:

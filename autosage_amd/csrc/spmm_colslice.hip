@@ -1580,7 +1580,8 @@ int64_t as_spmm_colslice_row_blocks(int64_t n, int dtype, int64_t* begins, int64
   return blocks;
 }
 
-size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype, int64_t sliced_rows) {
+size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t nnz, int64_t f, int dtype,
+                                                int64_t sliced_rows) {
   if (n < 0) n = 0;
   if (f < 1) f = 1;
   // a chunk's rows: the preferred chunk, or a whole row block of the plan
@@ -1591,7 +1592,15 @@ size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype,
     const int64_t block = as::block_rows_max(n, as::row_blocks(n, e));
     if (block > rows) rows = block;
   }
-  if (sliced_rows >= 0 && sliced_rows < rows) rows = sliced_rows > 0 ? sliced_rows : 1;
+  // Buffers of fewer rows than a chunk keep one chunk per row block only where
+  // the sliced rows past them are summed with the same bits (16-bit; fp32
+  // with 16-byte lanes, F % 4 == 0 and X aligned, on graphs without
+  // cooperative hub rows, i.e. of more than 2^24 edges).  Elsewhere the
+  // chunks are cut to the buffers, so buffers sized for the sliced rows
+  // would cut a graph of few sliced rows into as many launches as it has
+  // rows: there they hold a chunk's rows.
+  const bool capped = sliced_rows >= 0 && (e != 4 || (f % 4 == 0 && nnz > as::kMegaMaxNnz));
+  if (capped && sliced_rows < rows) rows = sliced_rows > 0 ? sliced_rows : 1;
   return 2 * static_cast<size_t>(rows) * as::colslice_row_bytes(f);
 }
 

@@ -243,13 +243,18 @@ int as_spmm_colslice_plan(const int64_t* crow, const int64_t* col, int64_t n,
                           void* stream);
 
 /* Preferred workspace bytes of as_spmm_csr_colslice_planned: the two partial
- * buffers only, of min(sliced_rows, rows of a chunk) partial rows each;
- * sliced_rows = the most rows of slicing degree that one row block of the
- * plan holds (as_spmm_colslice_row_blocks), or -1 for a chunk's rows.  The
- * bits do not depend on it: a sliced row that finds no partial row is summed
+ * buffers only, of min(sliced_rows, rows of a chunk) partial rows each for
+ * 16-bit elements, and for fp32 with F % 4 == 0 on graphs of more than 2^24
+ * edges; of a chunk's rows otherwise (fp32 chunks are cut to buffers that
+ * cannot hold their sliced rows there, see below).  sliced_rows = the most
+ * rows of slicing degree that one row block of the plan holds
+ * (as_spmm_colslice_row_blocks), or -1 for a chunk's rows.  The bits do not
+ * depend on the workspace: a sliced row that finds no partial row is summed
  * by one wavefront with the same operations in the same order (16-bit
- * elements: whole, by their order-free rule). */
-size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t f, int dtype,
+ * elements: whole, by their order-free rule; fp32 cooperative hub rows and
+ * narrow lanes: the chunk is cut instead). */
+size_t as_spmm_colslice_planned_workspace_bytes(int64_t n, int64_t nnz,
+                                                int64_t f, int dtype,
                                                 int64_t sliced_rows);
 
 /* Row blocks of a column-sliced plan for n rows of type dtype: returns their

@@ -138,8 +138,14 @@ def test_argument_errors_are_reported_without_a_launch(lib):
             assert lib.as_spmm_colslice_group_degree(f, code) == lib.as_spmm_rounded_16_group_degree(f)
     assert lib.as_spmm_colslice_group_degree(64, 3) == 0
     # two partial buffers of a chunk's rows (all 1,000 rows here: chunks hold at least 32,768), 8 slices of F fp64
-    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 0, -1) == 2 * 1000 * 8 * 128 * 8
-    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 128, 1, 10) == 2 * 10 * 8 * 128 * 8
+    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 50_000, 128, 0, -1) == 2 * 1000 * 8 * 128 * 8
+    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 50_000, 128, 1, 10) == 2 * 10 * 8 * 128 * 8
+    # fp32 keeps a chunk's rows where its chunks would be cut to the buffers: graphs of at most 2^24 edges
+    # (cooperative hub rows) and F not a multiple of 4 (narrow lanes); a 20,000-row graph with one sliced
+    # row would otherwise run as 20,000 one-row launches
+    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 50_000, 128, 0, 10) == 2 * 1000 * 8 * 128 * 8
+    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 1 << 25, 130, 0, 10) == 2 * 1000 * 8 * 130 * 8
+    assert lib.as_spmm_colslice_planned_workspace_bytes(1000, 1 << 25, 128, 0, 10) == 2 * 10 * 8 * 128 * 8
     # attention plans: fp32 and 16-bit tags differ (light buckets), and the
     # forward and the backward refuse a tag of other settings before any device work
     att = {}

@@ -363,7 +363,8 @@ def test_planned_call_rejects_a_plan_of_other_settings():
     _, tag128 = _native.colslice_plan(d_crow, d_col, 128, torch.float32, True)
     assert tag64 != tag128
     y = torch.empty_like(d_x)
-    ws = torch.empty(lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, -1), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(lib.as_spmm_colslice_planned_workspace_bytes(n, col.size, f, 0, -1), dtype=torch.uint8,
+                     device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     args = (d_crow.data_ptr(), d_col.data_ptr(), 0, d_x.data_ptr(), y.data_ptr(), n, col.size, f, 0, 1,
             plan64.data_ptr(), plan64.numel())
@@ -524,12 +525,12 @@ def test_fp32_partial_buffers_smaller_than_the_sliced_rows(features):
     blocks = lib.as_spmm_colslice_row_blocks(n, 0, begins, 65)
     want_most = max(int((np.diff(crow)[begins[b]:begins[b + 1]] >= degree).sum()) for b in range(blocks))
     assert blocks >= 2 and most == want_most
-    row_bytes = lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, 1) // 2
+    row_bytes = lib.as_spmm_colslice_planned_workspace_bytes(n, col.size, f, 0, 1) // 2
     sliced, grouped = _native.colslice_row_counts(d_crow, f, torch.float32)
     for weights in (None, d_val):
         outs = []
         for rows_per_buffer in (-1, most, most // 3, 1):
-            ws_bytes = (lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, -1) if rows_per_buffer < 0
+            ws_bytes = (lib.as_spmm_colslice_planned_workspace_bytes(n, col.size, f, 0, -1) if rows_per_buffer < 0
                         else 2 * rows_per_buffer * row_bytes)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
             y = torch.empty_like(d_x)
@@ -548,5 +549,37 @@ def test_fp32_partial_buffers_smaller_than_the_sliced_rows(features):
     # the op sizes its workspace for the sliced rows of the largest block (a
     # block's rows at most)
     block_rows = max(begins[b + 1] - begins[b] for b in range(blocks))
-    assert lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, -1) >= 2 * block_rows * row_bytes
-    assert lib.as_spmm_colslice_planned_workspace_bytes(n, f, 0, most) == 2 * min(most, block_rows) * row_bytes
+    assert lib.as_spmm_colslice_planned_workspace_bytes(n, col.size, f, 0, -1) >= 2 * block_rows * row_bytes
+    capped = lib.as_spmm_colslice_planned_workspace_bytes(n, col.size, f, 0, most)
+    if f % 4 == 0:
+        assert capped == 2 * min(most, block_rows) * row_bytes
+    else:
+        # narrow lanes cut chunks to the buffers: a block's rows, not its sliced rows
+        assert capped >= 2 * block_rows * row_bytes
+
+
+def test_few_sliced_rows_keep_one_chunk():
+    """The reference hub sweep's graph (20,000 rows, one of 12,000 edges, the
+    rest of 32; 652k edges, so cooperative hub rows): the op sizes its fp32
+    partial buffers for a chunk's rows, not for its one sliced row, so the
+    graph runs as one chunk (buffers of one row would cut it into 20,000
+    one-row launches, about 150 ms).  Within 1e-6 of fp64, and well under a
+    millisecond per call."""
+    from autosage_amd import synth
+
+    d_crow, d_col = synth.hub_sweep_graph()
+    rows = d_crow.numel() - 1
+    x = torch.randn(rows, 128, device="cuda")
+    y = torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, None, x)
+    h_crow, h_col = d_crow.cpu().numpy(), d_col.cpu().numpy()
+    _assert_fp64_close(y.cpu().numpy(), oracle.spmm_f64(h_crow, h_col, None, x.cpu().numpy()))
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(5):
+        torch.ops.autosage.spmm_csr_colslice(d_crow, d_col, None, x)
+    end.record()
+    end.synchronize()
+    per_call = start.elapsed_time(end) / 5
+    print(f"[colslice] hub sweep graph: {per_call:.4f} ms per call", flush=True)
+    assert per_call < 5.0, per_call
