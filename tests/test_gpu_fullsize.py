@@ -57,7 +57,7 @@ def test_config2_weighted_spmm():
 
 
 @pytest.mark.parametrize("features", [64, 128, 256])
-def test_config3_skewed_spmm(features, monkeypatch):
+def test_config3_skewed_spmm(features, monkeypatch, tmp_path):
     w = synth.config3(seed=0, features=features)
     x = w.dense["x"]
     d_crow, d_col, d_x = dev(w.crow), dev(w.col), dev(x)
@@ -74,6 +74,17 @@ def test_config3_skewed_spmm(features, monkeypatch):
     fslice = torch.ops.autosage.spmm_csr_fslice(d_crow, d_col, None, d_x)
     assert torch.equal(fslice, whole)
     del fslice
+    # the scheduler's step (the bench line): cold, then replayed from its cache,
+    # the same bits as the sequential product
+    import autosage_amd
+
+    monkeypatch.setenv("AUTOSAGE_CACHE_DIR", str(tmp_path))
+    auto, info = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert info["candidate"] == "fslice", info.get("candidate")
+    assert torch.equal(auto, whole)
+    again, cached = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert cached["from_cache"] and torch.equal(again, whole)
+    del auto, again
     # reassociating hub mode: hub rows within 1e-6 of fp64, light rows exact
     monkeypatch.setenv("AUTOSAGE_HUB_MODE", "split64")
     s64 = torch.ops.autosage.spmm_csr_split(d_crow, d_col, None, d_x, 128, 4, q95).cpu().numpy()
