@@ -351,3 +351,75 @@ def test_config5_attention_gradients_sampled(dtype):
             print(f"[parity] cfg5 d{name} bf16: {got.size} sampled elements, worst err / bar = "
                   f"{float(np.max(err / bar)):.3f}", flush=True)
             assert np.all(err <= bar), (name, float(np.max(err - bar)))
+
+
+def _round16(values: np.ndarray, dtype) -> np.ndarray:
+    """fp64 -> fp32 -> dtype, round to nearest even both times, back to fp64."""
+    return torch.from_numpy(values).to(torch.float32).to(dtype).to(torch.float64).numpy()
+
+
+def test_config3_bf16_spmm_every_schedule():
+    """cfg3 at F = 128 in bf16: every 16-bit schedule (rows whole, edge
+    slices, column slices) and ``spmm_csr_auto`` equal the rounded oracle
+    (fp64 sum of the exact products, rounded to fp32 and then to bf16) on
+    every output; the sums are exact in fp64 here, so the order is free."""
+    import autosage_amd
+    from autosage_amd import _native
+
+    w = synth.config3(seed=0, features=128)
+    x16 = torch.from_numpy(w.dense["x"]).to(torch.bfloat16)
+    d_crow, d_col, d_x = dev(w.crow), dev(w.col), x16.cuda()
+    _step("cfg3 bf16 oracle (fp64 sums, all rows)")
+    want = oracle.spmm_rounded_16(w.crow, w.col, None, x16, torch.bfloat16).view(torch.int16)
+    outs = {
+        "rows": _native.spmm_rows_16_impl(d_crow, d_col, None, d_x),
+        "edges": _native.spmm_rounded_16_impl(d_crow, d_col, None, d_x, column_slices=False),
+        "columns": _native.spmm_rounded_16_impl(d_crow, d_col, None, d_x, column_slices=True),
+        "op": torch.ops.autosage.spmm_csr(d_crow, d_col, None, d_x),
+    }
+    for name, got in outs.items():
+        assert torch.equal(got.cpu().view(torch.int16), want), name
+    auto, info = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
+    assert torch.equal(auto.cpu().view(torch.int16), want), info.get("candidate")
+
+
+def test_config4_bf16_sddmm():
+    """cfg4 at F = 64 in bf16: the edge-block SDDMM (the op's schedule) and a
+    degree split equal the rounded oracle on every edge."""
+    w = synth.config4(seed=0, features=64)
+    q16 = torch.from_numpy(w.dense["q"]).to(torch.bfloat16)
+    k16 = torch.from_numpy(w.dense["k"]).to(torch.bfloat16)
+    d_crow, d_col, d_q, d_k = dev(w.crow), dev(w.col), q16.cuda(), k16.cuda()
+    _step("cfg4 bf16 oracle (fp64 dots, all edges)")
+    want = oracle.sddmm_rounded_16(w.crow, w.col, q16, k16, torch.bfloat16).view(torch.int16)
+    got = torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, d_k).cpu().view(torch.int16)
+    assert torch.equal(got, want)
+    got = torch.ops.autosage.sddmm_csr_split(d_crow, d_col, d_q, d_k, 4, 1024).cpu().view(torch.int16)
+    assert torch.equal(got, want)
+
+
+def test_config5_bf16_attention():
+    """cfg5 in bf16 (``csr_attention_colslice``, one kernel with fp32 inside):
+    every one of the 313M outputs lies between the rounded ends of
+    [exact − ε, exact + ε], ε = 1e-5·|exact| + 1e-6, against the fp64
+    attention of the same bf16 inputs (rounding is monotone)."""
+    w = synth.config5(seed=0)
+    q, k, v = (torch.from_numpy(w.dense[name]).to(torch.bfloat16) for name in ("q", "k", "v"))
+    d_crow, d_col = dev(w.crow), dev(w.col)
+    got = torch.ops.autosage.csr_attention_colslice(d_crow, d_col, q.cuda(), k.cuda(), v.cuda(), 0.125)
+    got = got.cpu().to(torch.float64).numpy()
+    _step("cfg5 bf16 fp64 attention, all rows")
+    exact = oracle.attention_f64(w.crow, w.col, q.float().numpy(), k.float().numpy(), v.float().numpy(), scale=0.125)
+    bad = 0
+    same = 0
+    for start in range(0, exact.shape[0], 262144):
+        part = slice(start, start + 262144)
+        e = exact[part]
+        eps = RTOL * np.abs(e) + ATOL
+        lo, hi = _round16(e - eps, torch.bfloat16), _round16(e + eps, torch.bfloat16)
+        g = got[part]
+        bad += int(((g < lo) | (g > hi)).sum())
+        same += int((g == _round16(e, torch.bfloat16)).sum())
+    print(f"[parity] cfg5 bf16 attention: {got.size} outputs, {bad} outside the rounded bar, "
+          f"{same / got.size:.4f} equal to round(exact)", flush=True)
+    assert bad == 0
