@@ -28,7 +28,7 @@ from tests.gpu_common import require_gpu, to_dev
 
 pytestmark = pytest.mark.gpu
 
-CASES = 100
+CASES = 200
 
 
 @pytest.fixture(scope="module", autouse=True)
