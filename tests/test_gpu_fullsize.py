@@ -358,19 +358,22 @@ def _round16(values: np.ndarray, dtype) -> np.ndarray:
     return torch.from_numpy(values).to(torch.float32).to(dtype).to(torch.float64).numpy()
 
 
-def test_config3_bf16_spmm_every_schedule():
-    """cfg3 at F = 128 in bf16: every 16-bit schedule (rows whole, edge
-    slices, column slices) and ``spmm_csr_auto`` equal the rounded oracle
-    (fp64 sum of the exact products, rounded to fp32 and then to bf16) on
-    every output; the sums are exact in fp64 here, so the order is free."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_config3_16bit_spmm_every_schedule(dtype):
+    """cfg3 at F = 128 in bf16 and fp16: every 16-bit schedule (rows whole,
+    edge slices, column slices) and ``spmm_csr_auto`` equal the rounded oracle
+    (fp64 sum of the exact products, rounded to fp32 and then to the type) on
+    every output; the sums are exact in fp64 here, so the order is free.  Then
+    dX = Aᵀ·dY through autograd equals the rounded oracle over Aᵀ."""
     import autosage_amd
     from autosage_amd import _native
+    from autosage_amd._autograd import csr_transpose
 
     w = synth.config3(seed=0, features=128)
-    x16 = torch.from_numpy(w.dense["x"]).to(torch.bfloat16)
+    x16 = torch.from_numpy(w.dense["x"]).to(dtype)
     d_crow, d_col, d_x = dev(w.crow), dev(w.col), x16.cuda()
-    _step("cfg3 bf16 oracle (fp64 sums, all rows)")
-    want = oracle.spmm_rounded_16(w.crow, w.col, None, x16, torch.bfloat16).view(torch.int16)
+    _step(f"cfg3 {dtype} oracle (fp64 sums, all rows)")
+    want = oracle.spmm_rounded_16(w.crow, w.col, None, x16, dtype).view(torch.int16)
     outs = {
         "rows": _native.spmm_rows_16_impl(d_crow, d_col, None, d_x),
         "edges": _native.spmm_rounded_16_impl(d_crow, d_col, None, d_x, column_slices=False),
@@ -381,17 +384,27 @@ def test_config3_bf16_spmm_every_schedule():
         assert torch.equal(got.cpu().view(torch.int16), want), name
     auto, info = autosage_amd.spmm_csr_auto(d_crow, d_col, None, d_x)
     assert torch.equal(auto.cpu().view(torch.int16), want), info.get("candidate")
+    del auto, outs
+    # the backward: dX = Aᵀ·dY on the 16-bit kernels
+    g16 = torch.from_numpy(np.random.default_rng(8).standard_normal((w.rows, 128)).astype(np.float32)).to(dtype)
+    leaf = d_x.clone().requires_grad_(True)
+    torch.ops.autosage.spmm_csr(d_crow, d_col, None, leaf).backward(g16.cuda())
+    crow_t, col_t, _ = csr_transpose(d_crow, d_col)
+    _step(f"cfg3 {dtype} backward oracle")
+    want_dx = oracle.spmm_rounded_16(crow_t.cpu().numpy(), col_t.cpu().numpy(), None, g16, dtype).view(torch.int16)
+    assert torch.equal(leaf.grad.cpu().view(torch.int16), want_dx)
 
 
-def test_config4_bf16_sddmm():
-    """cfg4 at F = 64 in bf16: the edge-block SDDMM (the op's schedule) and a
-    degree split equal the rounded oracle on every edge."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_config4_16bit_sddmm(dtype):
+    """cfg4 at F = 64 in bf16 and fp16: the edge-block SDDMM (the op's
+    schedule) and a degree split equal the rounded oracle on every edge."""
     w = synth.config4(seed=0, features=64)
-    q16 = torch.from_numpy(w.dense["q"]).to(torch.bfloat16)
-    k16 = torch.from_numpy(w.dense["k"]).to(torch.bfloat16)
+    q16 = torch.from_numpy(w.dense["q"]).to(dtype)
+    k16 = torch.from_numpy(w.dense["k"]).to(dtype)
     d_crow, d_col, d_q, d_k = dev(w.crow), dev(w.col), q16.cuda(), k16.cuda()
-    _step("cfg4 bf16 oracle (fp64 dots, all edges)")
-    want = oracle.sddmm_rounded_16(w.crow, w.col, q16, k16, torch.bfloat16).view(torch.int16)
+    _step(f"cfg4 {dtype} oracle (fp64 dots, all edges)")
+    want = oracle.sddmm_rounded_16(w.crow, w.col, q16, k16, dtype).view(torch.int16)
     got = torch.ops.autosage.sddmm_csr(d_crow, d_col, d_q, d_k).cpu().view(torch.int16)
     assert torch.equal(got, want)
     got = torch.ops.autosage.sddmm_csr_split(d_crow, d_col, d_q, d_k, 4, 1024).cpu().view(torch.int16)
